@@ -1,0 +1,360 @@
+// norm.hip - fused residual add + RMSNorm for gfx950, with bf16 or FP8 e4m3
+// output.
+//
+// Arithmetic (bit-for-bit the reference's, kernels_phase2.cu:51-132 and the
+// residual epilogue forward_gpu.cu:992-994):
+//   x      = bf16(float(res) + mult * float(branch))        (two roundings, no FMA)
+//   r      = 1 / sqrt(float(sum(x^2) in double / cols) + eps)
+//   y      = bf16((x * r) * w)
+// Each x^2 of a bf16 value is exact in f32; the row sum is accumulated in f64
+// per lane, then reduced across lanes with DPP (g4_wave.h) and across the
+// row's waves through LDS in a fixed order.
+//
+// Layout: one row is 4096 bf16 = 512 16-byte vectors. WPR waves share a row
+// (WPR = 1: 8 vectors per lane held in VGPRs; WPR = 4: 2 per lane) and a
+// 256-thread workgroup holds 4 / WPR rows. Every wave-wide load is 1 KiB
+// contiguous. All loads of a lane (x, branch, gamma) are issued before any
+// store, so an in-place residual (res_out == res) does not serialise them.
+//
+// FP8 output (granite4_add_rmsnorm_fp8): the per-tensor scale depends on the
+// maximum over the whole [rows][cols] tensor, so two launches run back to
+// back: pass 1 writes res' and folds each workgroup's max |y| into work[0]
+// with one atomicMax on the f32 bit pattern (non-negative floats order as
+// unsigned integers); pass 2 re-reads res' (2 B / element, usually still in
+// the 256 MB Infinity Cache), recomputes r and y exactly as pass 1 did, and
+// writes the codes. The last workgroup of pass 2 (atomic counter in work[1])
+// zeroes the workspace for the next call.
+#include "g4_common.h"
+#include "g4_math.h"
+#include "g4_wave.h"
+#include "granite4_layerops.h"
+
+#include <cstdlib>
+
+namespace g4 {
+namespace {
+
+enum : int { kOutBf16 = 0, kOutAmax = 1, kOutFp8 = 2 };
+
+struct NormArgs {
+  const uint16_t* x;       // residual stream (or the plain RMSNorm input)
+  const uint16_t* branch;  // NULL: no residual add
+  float mult;
+  const uint16_t* w;
+  float eps;
+  int rows, cols;
+  uint16_t* res_out;  // NULL: res' not stored
+  uint16_t* normed;   // kOutBf16
+  uint8_t* codes;     // kOutFp8
+  float* scale_out;   // kOutFp8
+  uint32_t* work;     // kOutAmax / kOutFp8: [0] amax bits, [1] done counter
+};
+
+__device__ __forceinline__ void fp8_finish(const NormArgs& a, float s) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __threadfence();
+    const uint32_t prev = atomicAdd(&a.work[1], 1u);
+    if (prev == gridDim.x - 1) {
+      atomicExch(&a.work[0], 0u);
+      atomicExch(&a.work[1], 0u);
+    }
+  }
+}
+
+__device__ __forceinline__ void block_amax(const NormArgs& a, float m) {
+  __shared__ float s_max[kBlock / 64];
+  m = wave_max(m);
+  if ((threadIdx.x & 63) == 0) s_max[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float b = s_max[0];
+    for (int i = 1; i < kBlock / 64; ++i) b = fmaxf(b, s_max[i]);
+    if (b > 0.0f) atomicMax(&a.work[0], __builtin_bit_cast(uint32_t, b));
+  }
+}
+
+struct Fp8Scale {
+  float s, inv;
+  bool fast;
+};
+
+__device__ __forceinline__ Fp8Scale fp8_scale_from_work(const uint32_t* work) {
+  const float amax = __builtin_bit_cast(float, __atomic_load_n(work, __ATOMIC_RELAXED));
+  Fp8Scale f;
+  f.s = fp8_scale_for(amax);
+  f.fast = fp8_fast_scale(f.s);
+  f.inv = f.fast ? 1.0f / f.s : 0.0f;
+  return f;
+}
+
+template <int VPL, int WPR, int MODE>
+__global__ __launch_bounds__(kBlock) void norm_kernel(NormArgs a) {
+  constexpr int RPB = 4 / WPR;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * RPB + wave / WPR;
+  const int part = wave % WPR;
+  const bool live = row < a.rows;
+  const int nvec = a.cols >> 3;
+  const size_t base = live ? static_cast<size_t>(row) * static_cast<size_t>(a.cols) : 0;
+
+  V8 xv[VPL], bv[VPL], wv[VPL];
+  bool ok[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int vi = (j * WPR + part) * 64 + lane;
+    ok[j] = live && vi < nvec;
+    xv[j] = V8{{0u, 0u, 0u, 0u}};
+    bv[j] = V8{{0u, 0u, 0u, 0u}};
+    wv[j] = V8{{0u, 0u, 0u, 0u}};
+    if (ok[j]) {
+      xv[j] = ld8(a.x + base + 8 * vi);
+      if (a.branch != nullptr) bv[j] = ld8(a.branch + base + 8 * vi);
+      wv[j] = ld8(a.w + 8 * vi);
+    }
+  }
+  double ss = 0.0;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    if (a.branch != nullptr) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = lo_bf16(xv[j].w[e]) + a.mult * lo_bf16(bv[j].w[e]);
+        const float hi = hi_bf16(xv[j].w[e]) + a.mult * hi_bf16(bv[j].w[e]);
+        xv[j].w[e] = pack_bf16(lo, hi);
+      }
+      if (ok[j] && a.res_out != nullptr) {
+        const int vi = (j * WPR + part) * 64 + lane;
+        st8(a.res_out + base + 8 * vi, xv[j]);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = lo_bf16(xv[j].w[e]), hi = hi_bf16(xv[j].w[e]);
+      ss += static_cast<double>(lo * lo);
+      ss += static_cast<double>(hi * hi);
+    }
+  }
+  ss = wave_sum(ss);
+  if (WPR > 1) {
+    __shared__ double s_part[kBlock / 64];
+    if (lane == 0) s_part[wave] = ss;
+    __syncthreads();
+    const int w0 = (wave / WPR) * WPR;
+    ss = s_part[w0];
+#pragma unroll
+    for (int k = 1; k < WPR; ++k) ss += s_part[w0 + k];
+  }
+  const float r = 1.0f / sqrtf(static_cast<float>(ss / a.cols) + a.eps);
+
+  if (MODE == kOutBf16) {
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      if (!ok[j]) continue;
+      V8 y;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        y.w[e] = pack_bf16(lo_bf16(xv[j].w[e]) * r * lo_bf16(wv[j].w[e]),
+                           hi_bf16(xv[j].w[e]) * r * hi_bf16(wv[j].w[e]));
+      const int vi = (j * WPR + part) * 64 + lane;
+      st8(a.normed + base + 8 * vi, y);
+    }
+    return;
+  }
+  if (MODE == kOutAmax) {
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t yl = f32_to_bf16(lo_bf16(xv[j].w[e]) * r * lo_bf16(wv[j].w[e]));
+        const uint32_t yh = f32_to_bf16(hi_bf16(xv[j].w[e]) * r * hi_bf16(wv[j].w[e]));
+        m = fmaxf(m, bf16_to_f32(yl & 0x7fffu));
+        m = fmaxf(m, bf16_to_f32(yh & 0x7fffu));
+      }
+    }
+    block_amax(a, m);
+    return;
+  }
+  // kOutFp8
+  const Fp8Scale f = fp8_scale_from_work(a.work);
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    if (!ok[j]) continue;
+    uint32_t c[2] = {0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float yl = bf16_to_f32(f32_to_bf16(lo_bf16(xv[j].w[e]) * r * lo_bf16(wv[j].w[e])));
+      const float yh = bf16_to_f32(f32_to_bf16(hi_bf16(xv[j].w[e]) * r * hi_bf16(wv[j].w[e])));
+      const uint32_t pair = fp8_encode_scaled(yl, f.s, f.inv, f.fast) |
+                            (fp8_encode_scaled(yh, f.s, f.inv, f.fast) << 8);
+      c[e >> 1] |= pair << (16 * (e & 1));
+    }
+    const int vi = (j * WPR + part) * 64 + lane;
+    *reinterpret_cast<uint2*>(a.codes + base + 8 * vi) = make_uint2(c[0], c[1]);
+  }
+  fp8_finish(a, f.s);
+}
+
+// Any-shape fallback: one workgroup per row, element loops, two passes over
+// the row (the second re-reads it from cache). Same arithmetic and reduction
+// order as above at the wave level.
+template <int MODE>
+__global__ __launch_bounds__(kBlock) void norm_generic_kernel(NormArgs a) {
+  const int row = blockIdx.x;
+  const size_t base = static_cast<size_t>(row) * static_cast<size_t>(a.cols);
+  auto load_x = [&](int c) {
+    const float x = bf16_to_f32(a.x[base + c]);
+    if (a.branch == nullptr) return x;
+    return bf16_to_f32(f32_to_bf16(x + a.mult * bf16_to_f32(a.branch[base + c])));
+  };
+  double ss = 0.0;
+  for (int c = threadIdx.x; c < a.cols; c += kBlock) {
+    const float x = load_x(c);
+    if (a.branch != nullptr && a.res_out != nullptr) a.res_out[base + c] = f32_to_bf16(x);
+    ss += static_cast<double>(x * x);
+  }
+  __shared__ double s_part[kBlock / 64];
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  ss = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
+  const float r = 1.0f / sqrtf(static_cast<float>(ss / a.cols) + a.eps);
+  // The same thread reads back what it wrote above, so res_out aliasing res
+  // needs no extra barrier: recompute from the inputs when res' was not stored.
+  auto x_again = [&](int c) {
+    if (a.branch != nullptr && a.res_out != nullptr) return bf16_to_f32(a.res_out[base + c]);
+    return load_x(c);
+  };
+  if (MODE == kOutBf16) {
+    for (int c = threadIdx.x; c < a.cols; c += kBlock)
+      a.normed[base + c] = static_cast<uint16_t>(f32_to_bf16(x_again(c) * r * bf16_to_f32(a.w[c])));
+    return;
+  }
+  if (MODE == kOutAmax) {
+    float m = 0.0f;
+    for (int c = threadIdx.x; c < a.cols; c += kBlock)
+      m = fmaxf(m, bf16_to_f32(f32_to_bf16(x_again(c) * r * bf16_to_f32(a.w[c])) & 0x7fffu));
+    block_amax(a, m);
+    return;
+  }
+  const Fp8Scale f = fp8_scale_from_work(a.work);
+  for (int c = threadIdx.x; c < a.cols; c += kBlock) {
+    const float y = bf16_to_f32(f32_to_bf16(x_again(c) * r * bf16_to_f32(a.w[c])));
+    a.codes[base + c] = static_cast<uint8_t>(fp8_encode_scaled(y, f.s, f.inv, f.fast));
+  }
+  fp8_finish(a, f.s);
+}
+
+// Waves per row: more waves per row when there are too few rows to fill the
+// 1024 SIMDs. G4_NORM_WPR=1|4 overrides (benchmark sweeps).
+int pick_wpr(int rows) {
+  static const int forced = [] {
+    const char* e = std::getenv("G4_NORM_WPR");
+    return e ? std::atoi(e) : 0;
+  }();
+  if (forced == 1 || forced == 4) return forced;
+  return rows <= 2048 ? 4 : 1;
+}
+
+template <int MODE>
+int launch_norm(const NormArgs& a, const char* what) {
+  const int nvec = a.cols / 8;
+  const bool vec = (a.cols % 8) == 0;
+  const int wpr = pick_wpr(a.rows);
+  const hipStream_t st = stream();
+  if (vec && wpr == 4 && nvec <= 4 * 64 * 4) {
+    const unsigned grid = static_cast<unsigned>(a.rows);
+    if (nvec <= 256) hipLaunchKernelGGL((norm_kernel<1, 4, MODE>), grid, kBlock, 0, st, a);
+    else if (nvec <= 512) hipLaunchKernelGGL((norm_kernel<2, 4, MODE>), grid, kBlock, 0, st, a);
+    else hipLaunchKernelGGL((norm_kernel<4, 4, MODE>), grid, kBlock, 0, st, a);
+  } else if (vec && nvec <= 8 * 64) {
+    const unsigned grid = static_cast<unsigned>((a.rows + 3) / 4);
+    if (nvec <= 64) hipLaunchKernelGGL((norm_kernel<1, 1, MODE>), grid, kBlock, 0, st, a);
+    else if (nvec <= 128) hipLaunchKernelGGL((norm_kernel<2, 1, MODE>), grid, kBlock, 0, st, a);
+    else if (nvec <= 256) hipLaunchKernelGGL((norm_kernel<4, 1, MODE>), grid, kBlock, 0, st, a);
+    else hipLaunchKernelGGL((norm_kernel<8, 1, MODE>), grid, kBlock, 0, st, a);
+  } else {
+    hipLaunchKernelGGL((norm_generic_kernel<MODE>), static_cast<unsigned>(a.rows), kBlock, 0, st,
+                       a);
+  }
+  return launch_status(what);
+}
+
+bool norm_args_ok(const void* x, const void* w, float eps, int rows, int cols) {
+  return x != nullptr && w != nullptr && std::isfinite(eps) && eps >= 0.0f && rows > 0 &&
+         cols > 0 && fits_int(static_cast<long long>(rows) * cols);
+}
+
+int rmsnorm_ref_api(const uint16_t* d_x, const uint16_t* d_w, float eps, int rows, int cols,
+                    uint16_t* d_out, int max_rows, const char* what) {
+  // kernels_phase2.cu:910-936: eps must be finite and > 0.
+  if (!norm_args_ok(d_x, d_w, eps, rows, cols) || eps <= 0.0f || d_out == nullptr ||
+      rows > max_rows) {
+    std::fprintf(stderr, "granite4: %s: invalid arguments\n", what);
+    return -1;
+  }
+  NormArgs a{d_x, nullptr, 1.0f, d_w, eps, rows, cols, nullptr, d_out, nullptr, nullptr, nullptr};
+  return launch_norm<kOutBf16>(a, what);
+}
+
+}  // namespace
+}  // namespace g4
+
+using namespace g4;
+
+extern "C" {
+
+int granite4_kernel_rmsnorm(const uint16_t* d_x, const uint16_t* d_w, float eps, int rows,
+                            int cols, uint16_t* d_out) {
+  return rmsnorm_ref_api(d_x, d_w, eps, rows, cols, d_out, INT_MAX, "granite4_kernel_rmsnorm");
+}
+
+int granite4_kernel_rmsnorm_batched(const uint16_t* d_x, const uint16_t* d_w, float eps,
+                                    int rows, int cols, uint16_t* d_out) {
+  return rmsnorm_ref_api(d_x, d_w, eps, rows, cols, d_out, kMaxVerifyRows,
+                         "granite4_kernel_rmsnorm_batched");
+}
+
+int granite4_add_rmsnorm(const uint16_t* d_res, const uint16_t* d_branch, float resid_mult,
+                         const uint16_t* d_w, float eps, int rows, int cols, uint16_t* d_res_out,
+                         uint16_t* d_normed) {
+  if (!norm_args_ok(d_res, d_w, eps, rows, cols) || !std::isfinite(resid_mult) ||
+      d_normed == nullptr) {
+    std::fprintf(stderr, "granite4: granite4_add_rmsnorm: invalid arguments\n");
+    return -1;
+  }
+  NormArgs a{d_res, d_branch, resid_mult, d_w, eps, rows, cols,
+             d_branch != nullptr ? d_res_out : nullptr, d_normed, nullptr, nullptr, nullptr};
+  return launch_norm<kOutBf16>(a, "granite4_add_rmsnorm");
+}
+
+int granite4_add_rmsnorm_fp8(const uint16_t* d_res, const uint16_t* d_branch, float resid_mult,
+                             const uint16_t* d_w, float eps, int rows, int cols,
+                             uint16_t* d_res_out, uint8_t* d_codes, float* d_scale,
+                             void* d_work) {
+  if (!norm_args_ok(d_res, d_w, eps, rows, cols) || !std::isfinite(resid_mult) ||
+      d_codes == nullptr || d_scale == nullptr || d_work == nullptr) {
+    std::fprintf(stderr, "granite4: granite4_add_rmsnorm_fp8: invalid arguments\n");
+    return -1;
+  }
+  uint32_t* work = static_cast<uint32_t*>(d_work);
+  uint16_t* res_out = d_branch != nullptr ? d_res_out : nullptr;
+  NormArgs p1{d_res, d_branch, resid_mult, d_w, eps, rows, cols,
+              res_out, nullptr, nullptr, nullptr, work};
+  if (launch_norm<kOutAmax>(p1, "granite4_add_rmsnorm_fp8 (amax)") != 0) return -1;
+  // Pass 2 reads the stored residual when there is one (it may alias d_res).
+  NormArgs p2 = p1;
+  if (res_out != nullptr) {
+    p2.x = res_out;
+    p2.branch = nullptr;
+  }
+  p2.res_out = nullptr;
+  p2.codes = d_codes;
+  p2.scale_out = d_scale;
+  return launch_norm<kOutFp8>(p2, "granite4_add_rmsnorm_fp8 (encode)");
+}
+
+}  // extern "C"

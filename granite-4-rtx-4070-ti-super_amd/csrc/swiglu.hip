@@ -1,0 +1,228 @@
+// swiglu.hip - SwiGLU activation for gfx950, bf16 or FP8 e4m3 output.
+//
+// act = bf16(g * (1 / (1 + exp(-g))) * u), g = gu[r][i], u = gu[r][I + i]
+// (prefill_gemm.cu:1194-1203; the decode epilogue kernels_phase2.cu:643-651
+// has the same operation order). exp is the hardware base-2 exponential on a
+// pre-scaled argument and the reciprocal the hardware v_rcp_f32: both are
+// within a few f32 ulp, so act is within one bf16 ulp of the reference's
+// evaluation (the bar the parity tests hold it to).
+//
+// Streaming layout: one lane owns one 16-byte vector (8 values) of the gate
+// half and the matching vector of the up half; a grid-stride loop over
+// [rows][I / 8] vectors with two vectors in flight per lane. HBM-bound: 4 B
+// read + 2 B (bf16) or 1 B (FP8) written per element.
+//
+// FP8 output uses the same two-launch scheme as the add+RMSNorm kernel
+// (norm.hip): pass 1 folds max |act| into work[0], pass 2 recomputes act and
+// writes the codes; the last workgroup of pass 2 zeroes the workspace.
+#include "g4_common.h"
+#include "g4_math.h"
+#include "g4_wave.h"
+#include "granite4_layerops.h"
+
+namespace g4 {
+namespace {
+
+enum : int { kOutBf16 = 0, kOutAmax = 1, kOutFp8 = 2 };
+
+struct SwArgs {
+  const void* gu;  // bf16 [rows][2I] (or f32 for the reference's prefill_silu_mul)
+  int rows, I;
+  uint16_t* act;     // bf16 output (kOutBf16) or optional copy (kOutAmax)
+  uint8_t* codes;    // kOutFp8
+  float* scale_out;  // kOutFp8
+  uint32_t* work;
+};
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  const float e = __expf(-g);
+  const float sig = __builtin_amdgcn_rcpf(1.0f + e);
+  return g * sig * u;
+}
+
+template <bool F32IN>
+__device__ __forceinline__ void load_gu(const SwArgs& a, long long v, int nv, float* g,
+                                        float* u, long long* out_off) {
+  const long long r = v / nv;
+  const long long c = v - r * nv;
+  const long long row = r * 2LL * a.I;
+  *out_off = r * a.I + 8 * c;
+  if (F32IN) {
+    const float* p = static_cast<const float*>(a.gu) + row + 8 * c;
+    const float4 g0 = *reinterpret_cast<const float4*>(p);
+    const float4 g1 = *reinterpret_cast<const float4*>(p + 4);
+    const float4 u0 = *reinterpret_cast<const float4*>(p + a.I);
+    const float4 u1 = *reinterpret_cast<const float4*>(p + a.I + 4);
+    g[0] = g0.x; g[1] = g0.y; g[2] = g0.z; g[3] = g0.w;
+    g[4] = g1.x; g[5] = g1.y; g[6] = g1.z; g[7] = g1.w;
+    u[0] = u0.x; u[1] = u0.y; u[2] = u0.z; u[3] = u0.w;
+    u[4] = u1.x; u[5] = u1.y; u[6] = u1.z; u[7] = u1.w;
+  } else {
+    const uint16_t* p = static_cast<const uint16_t*>(a.gu) + row + 8 * c;
+    const V8 gv = ld8(p);
+    const V8 uv = ld8(p + a.I);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      g[e] = v8_get(gv, e);
+      u[e] = v8_get(uv, e);
+    }
+  }
+}
+
+template <int MODE, bool F32IN>
+__global__ __launch_bounds__(kBlock) void swiglu_kernel(SwArgs a) {
+  const int nv = a.I >> 3;
+  const long long total = static_cast<long long>(a.rows) * nv;
+  const long long step = static_cast<long long>(gridDim.x) * kBlock;
+  float s = 0.0f, inv = 0.0f;
+  bool fast = false;
+  if (MODE == kOutFp8) {
+    const float amax = __builtin_bit_cast(float, __atomic_load_n(a.work, __ATOMIC_RELAXED));
+    s = fp8_scale_for(amax);
+    fast = fp8_fast_scale(s);
+    inv = fast ? 1.0f / s : 0.0f;
+  }
+  float m = 0.0f;
+  for (long long v0 = static_cast<long long>(blockIdx.x) * kBlock + threadIdx.x; v0 < total;
+       v0 += 2 * step) {
+    const long long v1 = v0 + step;
+    float g[2][8], u[2][8];
+    long long off[2];
+    load_gu<F32IN>(a, v0, nv, g[0], u[0], &off[0]);
+    const bool has1 = v1 < total;
+    if (has1) load_gu<F32IN>(a, v1, nv, g[1], u[1], &off[1]);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      if (k == 1 && !has1) break;
+      uint32_t w[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        w[e] = pack_bf16(silu_mul(g[k][2 * e], u[k][2 * e]),
+                         silu_mul(g[k][2 * e + 1], u[k][2 * e + 1]));
+      if (MODE == kOutBf16 || (MODE == kOutAmax && a.act != nullptr))
+        st8(a.act + off[k], V8{{w[0], w[1], w[2], w[3]}});
+      if (MODE == kOutAmax) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          m = fmaxf(m, fmaxf(bf16_to_f32(w[e] & 0x7fffu), bf16_to_f32((w[e] >> 16) & 0x7fffu)));
+      }
+      if (MODE == kOutFp8) {
+        uint32_t c[2] = {0u, 0u};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t pair = fp8_encode_scaled(lo_bf16(w[e]), s, inv, fast) |
+                                (fp8_encode_scaled(hi_bf16(w[e]), s, inv, fast) << 8);
+          c[e >> 1] |= pair << (16 * (e & 1));
+        }
+        *reinterpret_cast<uint2*>(a.codes + off[k]) = make_uint2(c[0], c[1]);
+      }
+    }
+  }
+  if (MODE == kOutAmax) {
+    __shared__ float s_max[kBlock / 64];
+    m = wave_max(m);
+    if ((threadIdx.x & 63) == 0) s_max[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float b = s_max[0];
+      for (int i = 1; i < kBlock / 64; ++i) b = fmaxf(b, s_max[i]);
+      if (b > 0.0f) atomicMax(&a.work[0], __builtin_bit_cast(uint32_t, b));
+    }
+  }
+  if (MODE == kOutFp8) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      __threadfence();
+      const uint32_t prev = atomicAdd(&a.work[1], 1u);
+      if (prev == gridDim.x - 1) {
+        atomicExch(&a.work[0], 0u);
+        atomicExch(&a.work[1], 0u);
+      }
+    }
+  }
+}
+
+// Element-wise fallback for I not a multiple of 8 (bf16 / f32 in, bf16 out).
+template <bool F32IN>
+__global__ __launch_bounds__(kBlock) void swiglu_scalar_kernel(SwArgs a) {
+  const long long total = static_cast<long long>(a.rows) * a.I;
+  for (long long i = static_cast<long long>(blockIdx.x) * kBlock + threadIdx.x; i < total;
+       i += static_cast<long long>(gridDim.x) * kBlock) {
+    const long long r = i / a.I, c = i - r * a.I;
+    float g, u;
+    if (F32IN) {
+      const float* p = static_cast<const float*>(a.gu) + r * 2 * a.I + c;
+      g = p[0];
+      u = p[a.I];
+    } else {
+      const uint16_t* p = static_cast<const uint16_t*>(a.gu) + r * 2 * a.I + c;
+      g = bf16_to_f32(p[0]);
+      u = bf16_to_f32(p[a.I]);
+    }
+    a.act[i] = static_cast<uint16_t>(f32_to_bf16(silu_mul(g, u)));
+  }
+}
+
+unsigned grid_for(long long vectors) {
+  const long long want = (vectors + 2LL * kBlock - 1) / (2LL * kBlock);
+  return static_cast<unsigned>(want < kPersistBlocks ? (want > 0 ? want : 1) : kPersistBlocks);
+}
+
+bool sw_args_ok(const void* gu, int rows, int I) {
+  return gu != nullptr && rows > 0 && I > 0 && static_cast<long long>(rows) * 2 * I < (1LL << 40);
+}
+
+}  // namespace
+}  // namespace g4
+
+using namespace g4;
+
+extern "C" {
+
+int granite4_swiglu(const uint16_t* d_gu, int rows, int I, uint16_t* d_act) {
+  if (!sw_args_ok(d_gu, rows, I) || d_act == nullptr) {
+    std::fprintf(stderr, "granite4: granite4_swiglu: invalid arguments\n");
+    return -1;
+  }
+  SwArgs a{d_gu, rows, I, d_act, nullptr, nullptr, nullptr};
+  if (I % 8 == 0)
+    hipLaunchKernelGGL((swiglu_kernel<kOutBf16, false>),
+                       grid_for(static_cast<long long>(rows) * (I / 8)), kBlock, 0, stream(), a);
+  else
+    hipLaunchKernelGGL((swiglu_scalar_kernel<false>), kPersistBlocks, kBlock, 0, stream(), a);
+  return launch_status("granite4_swiglu");
+}
+
+int granite4_prefill_silu_mul(const float* gu, int I, int rows, uint16_t* act) {
+  if (!sw_args_ok(gu, rows, I) || act == nullptr) {
+    std::fprintf(stderr, "granite4: granite4_prefill_silu_mul: invalid arguments\n");
+    return -1;
+  }
+  SwArgs a{gu, rows, I, act, nullptr, nullptr, nullptr};
+  if (I % 8 == 0)
+    hipLaunchKernelGGL((swiglu_kernel<kOutBf16, true>),
+                       grid_for(static_cast<long long>(rows) * (I / 8)), kBlock, 0, stream(), a);
+  else
+    hipLaunchKernelGGL((swiglu_scalar_kernel<true>), kPersistBlocks, kBlock, 0, stream(), a);
+  return launch_status("granite4_prefill_silu_mul");
+}
+
+int granite4_swiglu_fp8(const uint16_t* d_gu, int rows, int I, uint8_t* d_codes,
+                        float* d_scale, void* d_work, uint16_t* d_act) {
+  if (!sw_args_ok(d_gu, rows, I) || I % 8 != 0 || d_codes == nullptr || d_scale == nullptr ||
+      d_work == nullptr) {
+    std::fprintf(stderr, "granite4: granite4_swiglu_fp8: invalid arguments (I %% 8 == 0)\n");
+    return -1;
+  }
+  uint32_t* work = static_cast<uint32_t*>(d_work);
+  const unsigned grid = grid_for(static_cast<long long>(rows) * (I / 8));
+  SwArgs p1{d_gu, rows, I, d_act, nullptr, nullptr, work};
+  hipLaunchKernelGGL((swiglu_kernel<kOutAmax, false>), grid, kBlock, 0, stream(), p1);
+  if (launch_status("granite4_swiglu_fp8 (amax)") != 0) return -1;
+  SwArgs p2{d_gu, rows, I, nullptr, d_codes, d_scale, work};
+  hipLaunchKernelGGL((swiglu_kernel<kOutFp8, false>), grid, kBlock, 0, stream(), p2);
+  return launch_status("granite4_swiglu_fp8 (encode)");
+}
+
+}  // extern "C"

@@ -1,0 +1,350 @@
+/*
+ * granite4_layerops.h - C ABI of the MI355X (gfx950) non-GEMM layer ops of the
+ * Granite 4.2 8B engine: embedding gather, residual add + RMSNorm (bf16 or
+ * FP8 e4m3 output), SwiGLU (bf16 or FP8), RoPE on Q/K fused with the
+ * quantised write into the paged KV arena.
+ *
+ * Conventions (the reference engine's, kernels_phase2.cu:822-836,
+ * engine/CMakeLists.txt:39-48):
+ *   - every pointer is device memory owned by the caller, except where a
+ *     function says it allocates (granite4_rope_tables_build);
+ *   - return 0 on success, -1 on invalid arguments or a launch error, with a
+ *     diagnostic on stderr; outputs are untouched when -1 comes from argument
+ *     validation;
+ *   - launches are asynchronous on the calling host thread's current stream
+ *     (hipStreamPerThread unless granite4_set_stream chose another), never
+ *     synchronise and never allocate, so a caller may capture them in a HIP
+ *     graph;
+ *   - decode variants read the position from device memory (d_pos).
+ *
+ * Shapes of the Granite 4.2 8B model: H = 4096, I = 12800, Hq = 32, Hk = 8,
+ * d = 128, 16-token KV pages.
+ *
+ * KV arena (per layer, forward_gpu.cu:1315-1343): K and V are
+ * [Hk][stride][row bytes] with row bytes 256 (bf16), 128 (int8), 64 (int4),
+ * 80 (K5: 64 nibble bytes + 16-byte high-bit plane; V stays int4). Scales
+ * are f32 [Hk][stride][d / group]; group = d reproduces the reference's one
+ * scale per (head, token) row, group = 32 is the group-32 format. Logical
+ * position p lives in arena row d_pt[p] (d_pt == NULL: row p), with
+ * d_pt[p] = block_table[p / 16] * 16 + p % 16 (kv_pool.cc:285-297).
+ * A row index outside [0, stride) or a position outside the cos/sin table is
+ * skipped by the kernels (no write) instead of faulting.
+ */
+#ifndef GRANITE4_LAYEROPS_H
+#define GRANITE4_LAYEROPS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------------------
+ * Stream selection (the reference builds with the per-thread default stream;
+ * this keeps that default and lets a caller such as a PyTorch harness name
+ * its own stream). `stream` is a hipStream_t; NULL restores the default.
+ * ------------------------------------------------------------------------- */
+int granite4_set_stream(void* stream);
+void* granite4_get_stream(void);
+
+/* Library / device identification for harnesses: writes the gfx arch name of
+ * the current device (e.g. "gfx950") into buf; 0 on success. */
+int granite4_device_arch(char* buf, int buf_len);
+
+/* ===========================================================================
+ * Entry points with the reference's names and signatures (drop-in).
+ * ========================================================================= */
+
+/* kernels_phase2.cu:868. Builds cos/sin [max_pos][head_dim/2] f32 tables on
+ * the host in double (kernel_math.h:191-206), allocates them with hipMalloc
+ * and uploads them; the caller frees both (hipFree or
+ * granite4_rope_tables_free). Synchronous. */
+int granite4_rope_tables_build(double theta, int head_dim, int max_pos, float** d_cos,
+                               float** d_sin);
+/* Frees tables from granite4_rope_tables_build (no reference counterpart). */
+int granite4_rope_tables_free(float* d_cos, float* d_sin);
+
+/* kernels_phase2.cu:910 / :922. y = bf16(x * rsqrt(mean(x^2) + eps) * w) per
+ * row; the _batched form also requires rows <= 16 (kMaxVerifyRows). */
+int granite4_kernel_rmsnorm(const uint16_t* d_x, const uint16_t* d_w, float eps, int rows,
+                            int cols, uint16_t* d_out);
+int granite4_kernel_rmsnorm_batched(const uint16_t* d_x, const uint16_t* d_w, float eps,
+                                    int rows, int cols, uint16_t* d_out);
+
+/* kernels_phase2.cu:938. Row r of x ([rows][head_dim]) is rotated with table
+ * row r (the row index is the position). */
+int granite4_kernel_rope(const uint16_t* d_x, const float* d_cos, const float* d_sin, int rows,
+                         int head_dim, uint16_t* d_out);
+
+/* forward_gpu.cu:3814. Every head of x ([heads][d]) rotated with one table row
+ * (d_cos_row / d_sin_row point at that position's d/2 entries). */
+int granite4_kernel_rope_at_pos(const uint16_t* d_x, const float* d_cos_row,
+                                const float* d_sin_row, int heads, int d, uint16_t* d_out);
+
+/* forward_gpu.cu:3829. Row r ([rows][heads][d]) rotated with table row r of
+ * d_cos / d_sin; rows <= 16. */
+int granite4_kernel_rope_at_pos_batched(const uint16_t* d_x, const float* d_cos,
+                                        const float* d_sin, int rows, int heads, int d,
+                                        uint16_t* d_out);
+
+/* kernels_phase2.cu:1087 / :1107 / :1133 / :1159. Append `rows` consecutive
+ * positions base_pos.. of already-rotated K and raw V ([rows][Hk][d] bf16) to
+ * the caches through d_pt; rows <= 16, stride >= base_pos + rows. Quantised
+ * forms store one f32 scale per (head, row); k5v4 needs d == 128. */
+int granite4_kernel_kv_append_batched(const uint16_t* d_src_k, const uint16_t* d_src_v,
+                                      uint16_t* d_cache_k, uint16_t* d_cache_v, int base_pos,
+                                      int rows, int stride, int Hk, int d, const int* d_pt);
+int granite4_kernel_kv_append_int8_batched(const uint16_t* d_src_k, const uint16_t* d_src_v,
+                                           int8_t* d_cache_k, int8_t* d_cache_v,
+                                           float* d_cache_k_scale, float* d_cache_v_scale,
+                                           int base_pos, int rows, int stride, int Hk, int d,
+                                           const int* d_pt);
+int granite4_kernel_kv_append_int4_batched(const uint16_t* d_src_k, const uint16_t* d_src_v,
+                                           uint8_t* d_cache_k, uint8_t* d_cache_v,
+                                           float* d_cache_k_scale, float* d_cache_v_scale,
+                                           int base_pos, int rows, int stride, int Hk, int d,
+                                           const int* d_pt);
+int granite4_kernel_kv_append_k5v4_batched(const uint16_t* d_src_k, const uint16_t* d_src_v,
+                                           uint8_t* d_cache_k, uint8_t* d_cache_v,
+                                           float* d_cache_k_scale, float* d_cache_v_scale,
+                                           int base_pos, int rows, int stride, int Hk, int d,
+                                           const int* d_pt);
+
+/* forward_gpu.cu:3847. RoPE q and k of `rows` verify rows (table row r of
+ * d_cos / d_sin for row r) into d_q_rot / d_k_rot, then append rotated K and
+ * raw V at positions base_pos.. (bf16 cache); rows <= 16. */
+int granite4_kernel_verify_qkv_stage(const uint16_t* d_q, const uint16_t* d_k,
+                                     const uint16_t* d_v, const float* d_cos,
+                                     const float* d_sin, int base_pos, int rows, int Hq, int Hk,
+                                     int d, int cache_stride, uint16_t* d_q_rot,
+                                     uint16_t* d_k_rot, uint16_t* d_cache_k,
+                                     uint16_t* d_cache_v, const int* d_pt);
+
+/* C-linkage twins of the reference's C++ `granite4::prefill_*` launchers
+ * (prefill_gemm.h:41-105); the C++ wrappers at the end of this header keep the
+ * reference's names. */
+
+/* prefill_gemm.cu:1300. out[r] = bf16(mult * emb[d_tokens[start + r]]). */
+int granite4_prefill_embed_rows(const int32_t* d_tokens, int start, int rows,
+                                const uint16_t* emb, float mult, uint16_t* out, int H);
+
+/* prefill_gemm.cu:1311 / :1331 / :1356 / :1378. qkv is token-major
+ * [rows][(Hq + 2 Hk) d]; row r sits at position base_pos + r. q is rotated
+ * into q_rot [rows][Hq d]; k is rotated and, with v, written through d_pt.
+ * The quantised forms quantise the f32 rotated K (not its bf16 rounding),
+ * one scale per (head, row), and need d == 128. */
+int granite4_prefill_rope_split_append(const uint16_t* qkv, const float* cos_tbl,
+                                       const float* sin_tbl, int base_pos, int rows, int Hq,
+                                       int Hk, int d, int stride, uint16_t* q_rot,
+                                       uint16_t* cache_k, uint16_t* cache_v, const int* d_pt);
+int granite4_prefill_rope_split_append_int8(const uint16_t* qkv, const float* cos_tbl,
+                                            const float* sin_tbl, int base_pos, int rows,
+                                            int Hq, int Hk, int d, int stride, uint16_t* q_rot,
+                                            int8_t* cache_k, int8_t* cache_v,
+                                            float* cache_k_scale, float* cache_v_scale,
+                                            const int* d_pt);
+int granite4_prefill_rope_split_append_int4(const uint16_t* qkv, const float* cos_tbl,
+                                            const float* sin_tbl, int base_pos, int rows,
+                                            int Hq, int Hk, int d, int stride, uint16_t* q_rot,
+                                            uint8_t* cache_k, uint8_t* cache_v,
+                                            float* cache_k_scale, float* cache_v_scale,
+                                            const int* d_pt);
+int granite4_prefill_rope_split_append_k5v4(const uint16_t* qkv, const float* cos_tbl,
+                                            const float* sin_tbl, int base_pos, int rows,
+                                            int Hq, int Hk, int d, int stride, uint16_t* q_rot,
+                                            uint8_t* cache_k, uint8_t* cache_v,
+                                            float* cache_k_scale, float* cache_v_scale,
+                                            const int* d_pt);
+
+/* prefill_gemm.cu:1468. act[r][i] = bf16(g * sigmoid(g) * u) with f32
+ * gu [rows][2I] (gate at [r][i], up at [r][I + i]). */
+int granite4_prefill_silu_mul(const float* gu, int I, int rows, uint16_t* act);
+
+/* Multi-session descriptor (forward_gpu_api.h:163-182), layout-identical. */
+#define GRANITE4_MAX_VERIFY_ROWS 16
+#define GRANITE4_MAX_TREE_DEPTH 8
+typedef struct GpuMultiRows {
+  int n;
+  int pos[GRANITE4_MAX_VERIFY_ROWS];
+  const int* pt[GRANITE4_MAX_VERIFY_ROWS];
+  int32_t* tok[GRANITE4_MAX_VERIFY_ROWS];
+  int grp[GRANITE4_MAX_VERIFY_ROWS];
+  int tree;
+  int slot[GRANITE4_MAX_VERIFY_ROWS];
+  int tbase[GRANITE4_MAX_VERIFY_ROWS];
+  int tail[GRANITE4_MAX_VERIFY_ROWS][GRANITE4_MAX_TREE_DEPTH];
+} GpuMultiRows;
+
+/* forward_gpu.cu:3891 / :3907 / :3914 (C-linkage twins of gpu_multi_rope,
+ * gpu_multi_rope_append, gpu_multi_kv_append). Row r is position
+ * d_rows->pos[r]; its KV goes to arena row d_rows->pt[r][slot] with slot =
+ * tree ? d_rows->slot[r] : pos[r]. bits: 16 / 8 / 4 / 5 (K5V4). The multi
+ * forms quantise the bf16-rounded rotated K, as the reference's decode path. */
+int granite4_multi_rope(const uint16_t* x, const float* cos_tbl, const float* sin_tbl,
+                        const GpuMultiRows* d_rows, int rows, int heads, int d, uint16_t* out);
+int granite4_multi_rope_append(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                               const float* cos_tbl, const float* sin_tbl,
+                               const GpuMultiRows* d_rows, int rows, int Hq, int Hk, int d,
+                               int bits, void* cache_k, void* cache_v, float* k_scale,
+                               float* v_scale, int stride, uint16_t* q_rot);
+int granite4_multi_kv_append(const uint16_t* k, const uint16_t* v, int bits, void* cache_k,
+                             void* cache_v, float* k_scale, float* v_scale,
+                             const GpuMultiRows* d_rows, int rows, int stride, int Hk, int d);
+
+/* ===========================================================================
+ * Fused entry points the MI355X build adds (no single reference function;
+ * each cites the reference pieces it fuses).
+ * ========================================================================= */
+
+/* Non-allocating twin of granite4_rope_tables_build: fills caller-owned
+ * device tables [max_pos][head_dim / 2]. Synchronous. */
+int granite4_rope_tables_fill(double theta, int head_dim, int max_pos, float* d_cos,
+                              float* d_sin);
+
+/* Embedding gather with a bounds check (forward_gpu.cu:84-101,
+ * prefill_gemm.cu:292-301): out[r] = bf16(mult * emb[tokens[r]]); a token
+ * outside [0, vocab) writes a zero row. */
+int granite4_embed_rows(const int32_t* d_tokens, int rows, const uint16_t* emb, int vocab,
+                        int H, float mult, uint16_t* out);
+/* Decode form: one row, token d_tokens[*d_pos] (embed_v8_kernel). */
+int granite4_embed_at_pos(const int32_t* d_tokens, const int* d_pos, const uint16_t* emb,
+                          int vocab, int H, float mult, uint16_t* out);
+
+/* Residual add + RMSNorm (forward_gpu.cu:992-994 epilogue + rmsnorm_kernel
+ * kernels_phase2.cu:51-132):
+ *   res'   = bf16(float(res) + resid_mult * float(branch))   (written to d_res_out)
+ *   normed = bf16(float(res') * rsqrt(mean(res'^2) + eps) * float(w))
+ * d_branch == NULL skips the add (normed = rmsnorm(res)); d_res_out may alias
+ * d_res; d_res_out == NULL skips that write. */
+int granite4_add_rmsnorm(const uint16_t* d_res, const uint16_t* d_branch, float resid_mult,
+                         const uint16_t* d_w, float eps, int rows, int cols, uint16_t* d_res_out,
+                         uint16_t* d_normed);
+
+/* As granite4_add_rmsnorm, with the normed output as FP8 e4m3 codes under one
+ * per-tensor scale: scale = float(amax / 448) over all |normed| (bf16 values),
+ * code = RNE_e4m3(normed / scale) (the reference's weight quantiser
+ * gpu_pack.cc:44-51, 296-308 applied to the bf16 normed tensor). Two launches
+ * (amax, then encode). d_work: caller-owned device workspace of at least
+ * GRANITE4_FP8_WORK_BYTES, zero-filled once before first use; every call
+ * leaves it zeroed again. Calls that share one workspace must be ordered on
+ * one stream. */
+#define GRANITE4_FP8_WORK_BYTES 256
+int granite4_add_rmsnorm_fp8(const uint16_t* d_res, const uint16_t* d_branch, float resid_mult,
+                             const uint16_t* d_w, float eps, int rows, int cols,
+                             uint16_t* d_res_out, uint8_t* d_codes, float* d_scale,
+                             void* d_work);
+
+/* SwiGLU from bf16 gate|up rows gu [rows][2I] (gate at [r][i], up at
+ * [r][I + i]; prefill_gemm.cu:1194-1203 with bf16 inputs):
+ * act = bf16(g * (1 / (1 + exp(-g))) * u). */
+int granite4_swiglu(const uint16_t* d_gu, int rows, int I, uint16_t* d_act);
+
+/* SwiGLU with FP8 requantisation of act (per-tensor scale, as
+ * granite4_add_rmsnorm_fp8). d_act (may be NULL) also receives the bf16 act. */
+int granite4_swiglu_fp8(const uint16_t* d_gu, int rows, int I, uint8_t* d_codes,
+                        float* d_scale, void* d_work, uint16_t* d_act);
+
+/* RoPE of q / k fused with the KV write (rope_append_multi_kernel
+ * forward_gpu.cu:598-729 and rope_split_append_*_kernel prefill_gemm.cu:
+ * 306-624, generalised).
+ *   q, k, v      bf16 rows with element strides q_stride / k_stride / v_stride
+ *                (prefill: one qkv buffer, q = qkv, k = qkv + Hq d,
+ *                v = qkv + (Hq + Hk) d, all strides (Hq + 2 Hk) d); q may be
+ *                NULL (no query heads).
+ *   position     row r uses RoPE position d_pos_rows[r] when given, else
+ *                base_pos + r; its arena row is d_arena_rows[r] when given,
+ *                else d_pt[pos] (d_pt NULL: pos).
+ *   bits / group 16, 8, 4 or 5 (K5V4); group 32, 64 or 128 (= d) elements per
+ *                scale.
+ *   k_round_bf16 1: quantise the bf16-rounded rotated K (decode / multi
+ *                semantics); 0: the f32 value (prefill semantics).
+ *   rotate_k     0: K is already rotated (the kv_append kernels).
+ * d must be 128. max_pos bounds the cos/sin tables. */
+int granite4_rope_append(const uint16_t* q, long q_stride, const uint16_t* k, long k_stride,
+                         const uint16_t* v, long v_stride, const float* cos_tbl,
+                         const float* sin_tbl, int max_pos, int rows, int Hq, int Hk, int d,
+                         int base_pos, const int* d_pos_rows, const int* d_pt,
+                         const int* d_arena_rows, int bits, int group, int k_round_bf16,
+                         int rotate_k, uint16_t* q_rot, long q_rot_stride, void* cache_k,
+                         void* cache_v, float* k_scale, float* v_scale, int stride);
+
+/* Decode form (rope_at_pos_qk_kernel forward_gpu.cu:857-886 + the
+ * kv_append_* kernels :104-277 in one launch): one row at position *d_pos,
+ * separate q [Hq d], k, v [Hk d]; K quantised from its bf16 rounding. */
+int granite4_rope_append_at_pos(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                const float* cos_tbl, const float* sin_tbl, int max_pos,
+                                const int* d_pos, const int* d_pt, int Hq, int Hk, int d,
+                                int bits, int group, uint16_t* q_rot, void* cache_k,
+                                void* cache_v, float* k_scale, float* v_scale, int stride);
+
+/* Host-side paged-pool index math (kv_pool.cc:285-297): out[p] =
+ * block_table[p / page] * page + p % page for p < n. Pure host code. */
+int granite4_row_table(const int32_t* block_table, int n, int page, int32_t* out);
+
+/* Host-side self-test of the device FP8 / KV arithmetic: runs the exact
+ * inline code the kernels use, on the CPU (no GPU needed). */
+int granite4_host_fp8_encode(const float* y, size_t n, float scale, uint8_t* codes);
+int granite4_host_kv_codes(const float* x, size_t n, float scale, int qmax, int32_t* codes);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+
+/* The reference's C++ launcher names (prefill_gemm.h:41-105,
+ * forward_gpu_api.h:219-229), forwarding to the C entry points above. */
+namespace granite4 {
+inline int prefill_embed_rows(const int32_t* d_tokens, int start, int rows, const uint16_t* emb,
+                              float mult, uint16_t* out, int H) {
+  return granite4_prefill_embed_rows(d_tokens, start, rows, emb, mult, out, H);
+}
+inline int prefill_rope_split_append(const uint16_t* qkv, const float* c, const float* s,
+                                     int base_pos, int rows, int Hq, int Hk, int d, int stride,
+                                     uint16_t* q_rot, uint16_t* ck, uint16_t* cv,
+                                     const int* d_pt = nullptr) {
+  return granite4_prefill_rope_split_append(qkv, c, s, base_pos, rows, Hq, Hk, d, stride, q_rot,
+                                            ck, cv, d_pt);
+}
+inline int prefill_rope_split_append_int8(const uint16_t* qkv, const float* c, const float* s,
+                                          int base_pos, int rows, int Hq, int Hk, int d,
+                                          int stride, uint16_t* q_rot, int8_t* ck, int8_t* cv,
+                                          float* ks, float* vs, const int* d_pt = nullptr) {
+  return granite4_prefill_rope_split_append_int8(qkv, c, s, base_pos, rows, Hq, Hk, d, stride,
+                                                 q_rot, ck, cv, ks, vs, d_pt);
+}
+inline int prefill_rope_split_append_int4(const uint16_t* qkv, const float* c, const float* s,
+                                          int base_pos, int rows, int Hq, int Hk, int d,
+                                          int stride, uint16_t* q_rot, uint8_t* ck, uint8_t* cv,
+                                          float* ks, float* vs, const int* d_pt = nullptr) {
+  return granite4_prefill_rope_split_append_int4(qkv, c, s, base_pos, rows, Hq, Hk, d, stride,
+                                                 q_rot, ck, cv, ks, vs, d_pt);
+}
+inline int prefill_rope_split_append_k5v4(const uint16_t* qkv, const float* c, const float* s,
+                                          int base_pos, int rows, int Hq, int Hk, int d,
+                                          int stride, uint16_t* q_rot, uint8_t* ck, uint8_t* cv,
+                                          float* ks, float* vs, const int* d_pt = nullptr) {
+  return granite4_prefill_rope_split_append_k5v4(qkv, c, s, base_pos, rows, Hq, Hk, d, stride,
+                                                 q_rot, ck, cv, ks, vs, d_pt);
+}
+inline int prefill_silu_mul(const float* gu, int I, int rows, uint16_t* act) {
+  return granite4_prefill_silu_mul(gu, I, rows, act);
+}
+inline int gpu_multi_rope(const uint16_t* x, const float* c, const float* s,
+                          const GpuMultiRows* d_rows, int rows, int heads, int d, uint16_t* out) {
+  return granite4_multi_rope(x, c, s, d_rows, rows, heads, d, out);
+}
+inline int gpu_multi_rope_append(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                 const float* c, const float* s, const GpuMultiRows* d_rows,
+                                 int rows, int Hq, int Hk, int d, int bits, void* ck, void* cv,
+                                 float* ks, float* vs, int stride, uint16_t* q_rot) {
+  return granite4_multi_rope_append(q, k, v, c, s, d_rows, rows, Hq, Hk, d, bits, ck, cv, ks, vs,
+                                    stride, q_rot);
+}
+inline int gpu_multi_kv_append(const uint16_t* k, const uint16_t* v, int bits, void* ck,
+                               void* cv, float* ks, float* vs, const GpuMultiRows* d_rows,
+                               int rows, int stride, int Hk, int d) {
+  return granite4_multi_kv_append(k, v, bits, ck, cv, ks, vs, d_rows, rows, stride, Hk, d);
+}
+}  // namespace granite4
+#endif /* __cplusplus */
+
+#endif /* GRANITE4_LAYEROPS_H */

@@ -169,9 +169,8 @@ def rope_append(q, k, v, cos_t, sin_t, pos, arena_row, bits, group, stride, Hk, 
     Returns q_rot, cache_k, cache_v, k_scale, v_scale (caches updated in place when given)."""
     rows = k.shape[0]
     Hq = 0 if q is None else q.shape[1] // d
-    kb, vb = KV_ROW_BYTES[bits]
-    if bits == 16:
-        kb, vb = 2 * d, 2 * d
+    kb, vb = {16: (2 * d, 2 * d), 8: (d, d), 4: (d // 2, d // 2),
+              5: (d // 2 + d // 8, d // 2)}[bits]
     if cache_k is None:
         cache_k = np.zeros(Hk * stride * kb, np.uint8)
         cache_v = np.zeros(Hk * stride * vb, np.uint8)

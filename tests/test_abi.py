@@ -1,0 +1,110 @@
+"""CPU checks of the C ABI library: it loads, exports every symbol the header
+declares, validates arguments without touching a GPU, and its host-compiled
+copy of the kernels' scalar arithmetic (FP8 encode, KV codes) matches the
+oracle on exhaustive sweeps."""
+import ctypes
+import re
+
+import numpy as np
+import pytest
+
+import oracle_lib as ol
+from pkg import HEADER, layerops
+
+L = layerops()
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = text.split("#ifdef __cplusplus\n}")[0]  # C declarations only
+    return sorted(set(re.findall(r"\b(granite4_\w+)\s*\(", text)))
+
+
+def test_header_symbols_exported():
+    syms = declared_symbols()
+    assert len(syms) >= 35
+    missing = [s for s in syms if not hasattr(L.lib, s)]
+    assert not missing, missing
+    # every declared symbol also has a ctypes signature in the host module
+    assert not [s for s in syms if s not in L._SIG], [s for s in syms if s not in L._SIG]
+
+
+def test_argument_validation_returns_minus_one():
+    lib = L.lib
+    assert lib.granite4_kernel_rmsnorm(None, None, 1e-5, 1, 4096, None) == -1
+    assert lib.granite4_kernel_rmsnorm(8, 8, 0.0, 1, 4096, 8) == -1      # eps must be > 0
+    assert lib.granite4_kernel_rmsnorm_batched(8, 8, 1e-5, 17, 4096, 8) == -1  # rows > 16
+    assert lib.granite4_add_rmsnorm_fp8(8, 8, 1.0, 8, 1e-5, 4, 4096, 8, 8, 8, None) == -1
+    assert lib.granite4_swiglu_fp8(8, 4, 12801, 8, 8, 8, None) == -1
+    assert lib.granite4_kernel_kv_append_int8_batched(8, 8, 8, 8, 8, 8, 10, 4, 12, 8, 128,
+                                                      None) == -1  # stride < base + rows
+    assert lib.granite4_kernel_kv_append_k5v4_batched(8, 8, 8, 8, 8, 8, 0, 4, 12, 8, 64,
+                                                      None) == -1  # d != 128
+    assert lib.granite4_prefill_rope_split_append_int8(8, 8, 8, 0, 4, 32, 8, 64, 16, 8, 8, 8, 8,
+                                                       8, None) == -1  # d != 128
+    assert lib.granite4_rope_append(8, 4096, 8, 1024, 8, 1024, 8, 8, 100, 4, 32, 8, 128, 0, None,
+                                    None, None, 8, 48, 0, 1, 8, 4096, 8, 8, 8, 8, 16) == -1  # group
+    assert lib.granite4_embed_rows(8, 0, 8, 100, 4096, 1.0, 8) == -1
+    assert lib.granite4_rope_tables_build(1e7, 127, 16, None, None) == -1
+
+
+def test_row_table_host_matches_oracle_and_golden():
+    G = np.load(ol.os.path.join(ol.ROOT, "tests", "golden", "golden.npz"))
+    for s in range(G["pt_blocks"].shape[0]):
+        bt = np.ascontiguousarray(G["pt_blocks"][s], np.int32)
+        n = G["pt_rows"].shape[1]
+        out = np.empty(n, np.int32)
+        assert L.lib.granite4_row_table(bt.ctypes.data, n, 16, out.ctypes.data) == 0
+        np.testing.assert_array_equal(out, G["pt_rows"][s])
+
+
+def _host_fp8(y, scale):
+    y = np.ascontiguousarray(y, np.float32)
+    out = np.empty(y.size, np.uint8)
+    assert L.lib.granite4_host_fp8_encode(y.ctypes.data, y.size, scale, out.ctypes.data) == 0
+    return out
+
+
+ALL_BF16 = np.arange(65536, dtype=np.uint16)
+
+
+@pytest.mark.parametrize("amax", [1.0, 448.0, 3.7, 0.015625, 7.2e-3, 1234.5, 2.5e-29, 6.0e37,
+                                  1e-40, 0.0])
+def test_fp8_fast_encoder_exhaustive_bf16(amax):
+    """Every bf16 value through the kernels' encoder (host build) vs the oracle."""
+    scale = ol.lib.g4o_fp8_scale_for(amax)
+    got = _host_fp8(ol.bf16_to_f32(ALL_BF16), scale)
+    if scale > 0:
+        want = ol.fp8_encode_scaled(ALL_BF16, scale)
+    else:
+        want = np.zeros(65536, np.uint8)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_fp8_fast_encoder_near_midpoints():
+    """Values straddling every e4m3 midpoint for awkward scales (the fma decision)."""
+    grid = np.array([ol.lib.g4o_fp8_decode(c) for c in range(0x7F)])
+    mids = (grid[:-1] + grid[1:]) / 2
+    rs = np.random.default_rng(5)
+    for scale in [np.float32(1.0), np.float32(3.0 / 448), np.float32(0.1), np.float32(rs.uniform()),
+                  np.float32(1e-20), np.float32(7.77e5)]:
+        t = np.concatenate([mids, grid])
+        y = (t * np.float64(scale)).astype(np.float32)
+        ys = np.concatenate([y, np.nextafter(y, np.float32(np.inf)),
+                             np.nextafter(y, np.float32(-np.inf))])
+        ys = np.concatenate([ys, -ys])
+        got = _host_fp8(ys, float(scale))
+        want = np.array([ol.lib.g4o_fp8_encode(float(v) / float(scale)) for v in ys], np.uint8)
+        np.testing.assert_array_equal(got, want)
+
+
+def test_kv_codes_host_match_oracle():
+    x = ol.bf16_to_f32(ALL_BF16[np.isfinite(ol.bf16_to_f32(ALL_BF16))])
+    for qmax in (127, 7, 15):
+        for s in (np.float32(0.03), np.float32(1.0) / np.float32(qmax), np.float32(0.0),
+                  np.float32(2.5)):
+            out = np.empty(x.size, np.int32)
+            assert L.lib.granite4_host_kv_codes(x.ctypes.data, x.size, float(s), qmax,
+                                                out.ctypes.data) == 0
+            want = np.array([ol.lib.g4o_kv_code(float(v), float(s), qmax) for v in x], np.int32)
+            np.testing.assert_array_equal(out, want)
