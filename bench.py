@@ -1,0 +1,464 @@
+"""Benchmark of the Granite 4.2 8B non-GEMM layer ops on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+
+Headline (`value`): achieved HBM GB/s of one prefill step at T = 512 tokens
+embedding gather + fused residual-add/RMSNorm with FP8
+output + SwiGLU with FP8 output + RoPE with the int8 paged-KV write, i.e.
+ideal (algorithmic) bytes of the step / measured time of the step. Inputs are
+resident in HBM; 8 distinct input sets rotate so the 256 MB Infinity Cache
+does not serve repeated iterations.
+
+Also reported (extra keys): each op's µs, GB/s and fraction of the 8 TB/s
+peak at T = 1, 8, 512 and 8192; the µs of a 40-layer batch-1 decode step
+(161 launches replayed as one HIP graph); the bandwidth-stress sequence
+(config 5); and the CPU baseline (the oracle, one core, on a bounded sample).
+
+Timing: HIP events recorded on the stream the kernels are launched on (torch's
+current stream, handed to the library with granite4_set_stream), bracketing
+K back-to-back steps after W warmup steps, with torch.cuda.synchronize() on
+both sides.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+H, I, HQ, HK, D = 4096, 12800, 32, 8, 128
+VOCAB = 100352
+PEAK_GBS = 8000.0  # MI355X HBM3E
+
+# Algorithmic bytes per token (BASELINE.md section 3 / the survey's 8(d)).
+B_EMBED = 4 * H + 4
+B_NORM_FP8 = 7 * H
+B_NORM_BF16 = 8 * H
+B_SWIGLU_FP8 = 5 * I
+B_SWIGLU_BF16 = 6 * I
+B_ROPE_COMMON = (HQ + 2 * HK) * D * 2 + 2 * 64 * 4 + HQ * D * 2 + 4  # qkv R, cos/sin R, q_rot W, pt
+B_ROPE = {16: B_ROPE_COMMON + 2 * HK * D * 2,
+          8: B_ROPE_COMMON + 2 * HK * D + 2 * HK * 4,
+          "k5v4g32": B_ROPE_COMMON + HK * (80 + 64) + 2 * HK * 4 * 4}
+
+
+def per_launch_extra(op):
+    return {"norm_fp8": 2 * H + 4, "norm_bf16": 2 * H, "swiglu_fp8": 4}.get(op, 0)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--quick", action="store_true", help="headline + decode only")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (the non-GEMM layer ops are "
+              "token-parallel; see DESIGN.md for how they would shard). Run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from pkg import layerops
+    L = layerops()
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.init()
+    stream = torch.cuda.current_stream()
+    L.use_stream(stream)
+    dev = "cuda"
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x6A4)
+
+    def randn(shape, std=1.0, mean=0.0):
+        t = torch.empty(shape, dtype=torch.float32, device=dev).normal_(mean, std, generator=gen)
+        return t.to(torch.bfloat16)
+
+    def timed(fn, steps, warmup, sets, replays=3):
+        """ms per fn() call: `steps` calls over rotating input sets captured in
+        one HIP graph, replayed `replays` times between two events on the
+        launch stream (no host launch cost inside the timed region)."""
+        for i in range(warmup):
+            fn(sets[i % len(sets)])
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        cap = torch.cuda.Stream()
+        cap.wait_stream(stream)
+        with torch.cuda.stream(cap):
+            L.use_stream(cap)
+            with torch.cuda.graph(g, stream=cap):
+                for i in range(steps):
+                    fn(sets[i % len(sets)])
+        L.use_stream(stream)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(replays):
+            g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        del g
+        return e0.elapsed_time(e1) / (steps * replays)  # ms
+
+    cos_t, sin_t = L.rope_tables(1e7, D, 65536)
+    emb = randn((VOCAB, H), std=0.02)
+    gamma = randn((H,), std=0.1, mean=1.0)
+    work = L.fp8_workspace()
+
+    def prefill_sets(T, nsets, bits, group, pos0):
+        sets = []
+        pages = (T + 15) // 16
+        for s in range(nsets):
+            res = randn((T, H))
+            ch = torch.randperm(H, generator=gen, device=dev)[: H // 100]
+            res[:, ch] = (res[:, ch].float() * 20).to(torch.bfloat16)
+            st = {
+                "tok": torch.randint(0, VOCAB, (T,), generator=gen, device=dev, dtype=torch.int32),
+                "emb_out": torch.empty((T, H), dtype=torch.bfloat16, device=dev),
+                "res": res, "branch": randn((T, H)),
+                "res_out": torch.empty((T, H), dtype=torch.bfloat16, device=dev),
+                "codes_h": torch.empty((T, H), dtype=torch.uint8, device=dev),
+                "scale": torch.empty(1, dtype=torch.float32, device=dev),
+                "gu": randn((T, 2 * I)),
+                "codes_i": torch.empty((T, I), dtype=torch.uint8, device=dev),
+                "qkv": randn((T, (HQ + 2 * HK) * D)),
+                "q_rot": torch.empty((T, HQ * D), dtype=torch.bfloat16, device=dev),
+                "arena": L.KvArena(bits, HK, (pos0 % 16) + pages * 16 + 16, group=group),
+                "pos0": pos0,
+            }
+            # fresh contiguous pages of the pool, page table by position
+            stride = st["arena"].stride
+            pt = torch.full((pos0 + T,), -1, dtype=torch.int32)
+            pt[pos0:] = torch.arange(T, dtype=torch.int32) + (pos0 % 16)
+            st["pt"] = pt.to(dev)
+            assert int(pt[-1]) < stride
+            sets.append(st)
+        return sets
+
+    def op_embed(s):
+        T = s["res"].shape[0]
+        L.call("granite4_embed_rows", s["tok"], T, emb, VOCAB, H, 1.0, s["emb_out"])
+
+    def op_norm_fp8(s):
+        T = s["res"].shape[0]
+        L.call("granite4_add_rmsnorm_fp8", s["res"], s["branch"], 1.0, gamma, 1e-5, T, H,
+               s["res_out"], s["codes_h"], s["scale"], work)
+
+    def op_swiglu_fp8(s):
+        T = s["gu"].shape[0]
+        L.call("granite4_swiglu_fp8", s["gu"], T, I, s["codes_i"], s["scale"], work, None)
+
+    def op_rope(s):
+        qkv = s["qkv"]
+        L.rope_append(s["arena"], qkv[:, :HQ * D], qkv[:, HQ * D:(HQ + HK) * D],
+                      qkv[:, (HQ + HK) * D:], cos_t, sin_t, base_pos=s["pos0"], d_pt=s["pt"],
+                      k_round_bf16=False, q_rot=s["q_rot"])
+
+    def op_step(s):
+        op_embed(s)
+        op_norm_fp8(s)
+        op_swiglu_fp8(s)
+        op_rope(s)
+
+    def measure_ops(T, nsets, bits, group, pos0, rope_key, steps, warmup):
+        sets = prefill_sets(T, nsets, bits, group, pos0)
+        out = {}
+        for name, fn, b in (("embed", op_embed, B_EMBED * T),
+                            ("add_rmsnorm_fp8", op_norm_fp8, B_NORM_FP8 * T + per_launch_extra("norm_fp8")),
+                            ("swiglu_fp8", op_swiglu_fp8, B_SWIGLU_FP8 * T + per_launch_extra("swiglu_fp8")),
+                            (f"rope_append_{rope_key}", op_rope, B_ROPE[rope_key] * T)):
+            ms = timed(fn, steps, warmup, sets)
+            gbs = b / (ms * 1e-3) / 1e9
+            out[name] = {"us": round(ms * 1e3, 3), "bytes": int(b), "GBps": round(gbs, 1),
+                         "frac_peak": round(gbs / PEAK_GBS, 4)}
+        step_bytes = sum(v["bytes"] for v in out.values())
+        ms = timed(op_step, steps, warmup, sets)
+        out["step"] = {"us": round(ms * 1e3, 3), "bytes": int(step_bytes),
+                       "GBps": round(step_bytes / (ms * 1e-3) / 1e9, 1)}
+        del sets
+        torch.cuda.empty_cache()
+        return out
+
+    result_extra = {}
+
+    # ---------------------------------------------------------------- headline: T = 512
+    log("config 3: prefill T=512 (embed + add_rmsnorm_fp8 + swiglu_fp8 + rope_int8)")
+    c3 = measure_ops(512, 8, 8, 128, 0, 8, args.steps, args.warmup)
+    log(json.dumps(c3))
+    result_extra["prefill_T512"] = c3
+
+    # ---------------------------------------------------------------- decode T = 1, 40 layers
+    log("config 1: 40-layer batch-1 decode step as one HIP graph")
+    decode = bench_decode(torch, L, randn, cos_t, sin_t, emb, gamma, stream, args)
+    log(json.dumps(decode))
+    result_extra["decode_T1"] = decode
+
+    if not args.quick:
+        log("config 2: T=8 sessions")
+        result_extra["decode_T8"] = bench_multi8(torch, L, randn, cos_t, sin_t, gamma, work, gen,
+                                                 stream, timed, args)
+        log(json.dumps(result_extra["decode_T8"]))
+        log("config 4: prefill T=8192, RoPE at 57344.., K5V4 group 32")
+        result_extra["prefill_T8192"] = measure_ops(8192, 2, 5, 32, 57344, "k5v4g32",
+                                                    max(5, args.steps // 2), 2)
+        log(json.dumps(result_extra["prefill_T8192"]))
+        log("config 5: bandwidth stress, 40 layers x T=32768, bf16")
+        result_extra["stress_T32768"] = bench_stress(torch, L, randn, cos_t, sin_t, gamma, stream)
+        log(json.dumps(result_extra["stress_T32768"]))
+
+    # ---------------------------------------------------------------- CPU baseline
+    cpu = None if args.no_cpu else cpu_baseline()
+    if cpu is not None:
+        log(json.dumps(cpu))
+
+    dom = c3["swiglu_fp8"]
+    line = {
+        "metric": "achieved HBM GB/s (% of peak) for fused layer ops at T=1 and T=512; "
+                  "µs/decode step",
+        "value": c3["step"]["GBps"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(c3["step"]["us"] / 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded torch RNG; N(0,1) hidden with 1% x20 outlier channels)",
+        "config": {"workload": "prefill T=512, one layer: embed + add_rmsnorm_fp8 + swiglu_fp8 "
+                               "+ rope_append int8 paged KV",
+                   "T": 512, "H": H, "I": I, "Hq": HQ, "Hk": HK, "head_dim": D,
+                   "kv": "int8 per (head,token)", "page": 16},
+        "roofline": {"bound": "hbm", "kernel": "swiglu_fp8 (amax + encode launches)",
+                     "achieved": dom["GBps"], "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dom["GBps"] / PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "decode_us_per_step": decode["graph_us_per_step"],
+        "detail": result_extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def bench_decode(torch, L, randn, cos_t, sin_t, emb, gamma, stream, args, layers=40):
+    """161 launches: embed, then per layer add_rmsnorm (attention residual),
+    rope + bf16 KV append at *d_pos, add_rmsnorm (FFN residual), SwiGLU."""
+    dev = "cuda"
+    stride = 8192
+    pos = torch.tensor([4321], dtype=torch.int32, device=dev)
+    toks = torch.randint(0, VOCAB, (8192,), dtype=torch.int32, device=dev)
+    pt = torch.randperm(stride, device=dev).to(torch.int32)
+    res = torch.empty((1, H), dtype=torch.bfloat16, device=dev)
+    normed = torch.empty_like(res)
+    act = torch.empty((1, I), dtype=torch.bfloat16, device=dev)
+    q_rot = torch.empty((1, HQ * D), dtype=torch.bfloat16, device=dev)
+    per = []
+    for _ in range(layers):
+        per.append({"b_attn": randn((1, H)), "b_ffn": randn((1, H)), "gu": randn((1, 2 * I)),
+                    "q": randn((1, HQ * D)), "k": randn((1, HK * D)), "v": randn((1, HK * D)),
+                    "arena": L.KvArena(16, HK, stride)})
+
+    def step():
+        L.call("granite4_embed_at_pos", toks, pos, emb, VOCAB, H, 1.0, res)
+        for p in per:
+            a = p["arena"]
+            L.call("granite4_add_rmsnorm", res, p["b_attn"], 1.0, gamma, 1e-5, 1, H, res, normed)
+            L.call("granite4_rope_append_at_pos", p["q"], p["k"], p["v"], cos_t, sin_t, 65536,
+                   pos, pt, HQ, HK, D, 16, 128, q_rot, a.k, a.v, a.k_scale, a.v_scale, stride)
+            L.call("granite4_add_rmsnorm", res, p["b_ffn"], 1.0, gamma, 1e-5, 1, H, res, normed)
+            L.call("granite4_swiglu", p["gu"], 1, I, act)
+
+    # eager timing (launch-bound: includes host launch cost)
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n_eager = 10
+    for _ in range(n_eager):
+        step()
+    torch.cuda.synchronize()
+    eager_us = (time.perf_counter() - t0) / n_eager * 1e6
+
+    # graph capture on a side stream, replay on it
+    g = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        L.use_stream(cap)
+        step()  # warm the side stream
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=cap):
+            step()
+    L.use_stream(stream)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    reps = 50
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    graph_us = e0.elapsed_time(e1) / reps * 1e3
+    ideal = B_EMBED + layers * (2 * B_NORM_BF16 + B_SWIGLU_BF16 + B_ROPE[16])
+    return {"layers": layers, "launches": 1 + 4 * layers, "graph_us_per_step": round(graph_us, 2),
+            "eager_us_per_step": round(eager_us, 2), "ideal_bytes": ideal,
+            "ideal_us_at_peak": round(ideal / PEAK_GBS / 1e3, 3)}
+
+
+def bench_multi8(torch, L, randn, cos_t, sin_t, gamma, work, gen, stream, timed, args):
+    """Config 2: 8 sessions at random positions in [0, 65536), own page tables,
+    FP8 norm / SwiGLU outputs, int8 KV; per-layer op times."""
+    dev = "cuda"
+    n = 8
+    pool_pages = 8 * 4096 + 64
+    stride = pool_pages * 16
+    rs = np.random.default_rng(2)
+    pos = rs.integers(0, 65536, n).astype(np.int32)
+    perm = torch.randperm(pool_pages, generator=gen, device=dev).to(torch.int32)
+    # session i owns pages perm[i*4096:(i+1)*4096]; its position p -> row
+    pts = []
+    for i in range(n):
+        pages = perm[i * 4096:(i + 1) * 4096].to(torch.int64)
+        rows = (pages[:, None] * 16 + torch.arange(16, device=dev)[None, :]).reshape(-1)
+        pts.append(rows.to(torch.int32).contiguous())
+    M = L.multi_rows_struct()
+    m = M()
+    m.n = n
+    for i in range(n):
+        m.pos[i] = int(pos[i])
+        m.pt[i] = pts[i].data_ptr()
+    d_m = torch.from_numpy(np.frombuffer(bytes(m), np.uint8).copy()).to(dev)
+    arena = L.KvArena(8, HK, stride)
+    sets = []
+    for _ in range(8):
+        sets.append({"res": randn((n, H)), "branch": randn((n, H)), "gu": randn((n, 2 * I)),
+                     "q": randn((n, HQ * D)), "k": randn((n, HK * D)), "v": randn((n, HK * D)),
+                     "res_out": torch.empty((n, H), dtype=torch.bfloat16, device=dev),
+                     "codes_h": torch.empty((n, H), dtype=torch.uint8, device=dev),
+                     "codes_i": torch.empty((n, I), dtype=torch.uint8, device=dev),
+                     "q_rot": torch.empty((n, HQ * D), dtype=torch.bfloat16, device=dev),
+                     "scale": torch.empty(1, dtype=torch.float32, device=dev)})
+
+    def norm(s):
+        L.call("granite4_add_rmsnorm_fp8", s["res"], s["branch"], 1.0, gamma, 1e-5, n, H,
+               s["res_out"], s["codes_h"], s["scale"], work)
+
+    def swiglu(s):
+        L.call("granite4_swiglu_fp8", s["gu"], n, I, s["codes_i"], s["scale"], work, None)
+
+    def rope(s):
+        L.call("granite4_multi_rope_append", s["q"], s["k"], s["v"], cos_t, sin_t, d_m, n, HQ, HK,
+               D, 8, arena.k, arena.v, arena.k_scale, arena.v_scale, stride, s["q_rot"])
+
+    out = {}
+    for name, fn in (("add_rmsnorm_fp8", norm), ("swiglu_fp8", swiglu),
+                     ("multi_rope_append_int8", rope)):
+        out[name + "_us"] = round(timed(fn, 200, 20, sets) * 1e3, 3)
+    out["layer_us"] = round(2 * out["add_rmsnorm_fp8_us"] + out["swiglu_fp8_us"] +
+                            out["multi_rope_append_int8_us"], 3)
+    return out
+
+
+def bench_stress(torch, L, randn, cos_t, sin_t, gamma, stream, layers=40, T=32768):
+    dev = "cuda"
+    res = randn((T, H))
+    branch = randn((T, H))
+    normed = torch.empty_like(res)
+    gu = randn((T, 2 * I))
+    act = torch.empty((T, I), dtype=torch.bfloat16, device=dev)
+    qkv = randn((T, (HQ + 2 * HK) * D))
+    q_rot = torch.empty((T, HQ * D), dtype=torch.bfloat16, device=dev)
+    arena = L.KvArena(16, HK, T)
+    pt = torch.arange(T, dtype=torch.int32, device=dev)
+
+    def layer():
+        L.call("granite4_add_rmsnorm", res, branch, 1.0, gamma, 1e-5, T, H, res, normed)
+        L.rope_append(arena, qkv[:, :HQ * D], qkv[:, HQ * D:(HQ + HK) * D], qkv[:, (HQ + HK) * D:],
+                      cos_t, sin_t, base_pos=0, d_pt=pt, q_rot=q_rot)
+        L.call("granite4_add_rmsnorm", res, branch, 1.0, gamma, 1e-5, T, H, res, normed)
+        L.call("granite4_swiglu", gu, T, I, act)
+
+    layer()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(layers):
+        layer()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    per_layer = (2 * B_NORM_BF16 + B_SWIGLU_BF16 + B_ROPE[16]) * T
+    total = per_layer * layers
+    return {"layers": layers, "T": T, "ms": round(ms, 3), "bytes": total,
+            "GBps": round(total / (ms * 1e-3) / 1e9, 1),
+            "frac_peak": round(total / (ms * 1e-3) / 1e9 / PEAK_GBS, 4)}
+
+
+def cpu_baseline(budget_s=12.0):
+    """The oracle (scalar C, one core) on a bounded sample of the headline
+    workload: the T=512 step's four ops over `rows` tokens, repeated for about
+    budget_s seconds; GB/s in the same ideal-byte units."""
+    import oracle_lib as ol
+    rows = 16
+    rs = 0x5EED
+    emb = ol.normal_bf16(rs, 0.0, 0.02, 4096 * H).reshape(4096, H)
+    tok = (ol.u32(rs + 1, rows) % 4096).astype(np.int32)
+    res = ol.normal_bf16(rs + 2, 0.0, 1.0, rows * H).reshape(rows, H)
+    br = ol.normal_bf16(rs + 3, 0.0, 1.0, rows * H).reshape(rows, H)
+    w = ol.normal_bf16(rs + 4, 1.0, 0.1, H)
+    gu = ol.normal_bf16(rs + 5, 0.0, 1.0, rows * 2 * I).reshape(rows, 2 * I)
+    qkv = ol.normal_bf16(rs + 6, 0.0, 1.0, rows * 48 * D).reshape(rows, 48 * D)
+    c, s = ol.rope_tables(1e7, D, 1024)
+    stride = 1024
+    pos = np.arange(rows)
+
+    def step():
+        ol.embed_rows(tok, emb, 1.0)
+        ro, no = ol.add_rmsnorm(res, br, 1.0, w, 1e-5)
+        ol.fp8_quantize(no)
+        ol.fp8_quantize(ol.swiglu(gu))
+        ol.rope_append(qkv[:, :HQ * D], qkv[:, HQ * D:40 * D], qkv[:, 40 * D:], c, s, pos, pos, 8,
+                       128, stride, HK)
+
+    step()
+    n = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s:
+        step()
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    step_bytes = rows * (B_EMBED + B_NORM_FP8 + B_SWIGLU_FP8 + B_ROPE[8])
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(step_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": 1,
+            "kind": "port", "cpu": model, "ms_per_token": round(dt / rows * 1e3, 4),
+            "sample": f"the T=512 step's four ops (embed, add_rmsnorm+FP8 quantise, SwiGLU+FP8 "
+                      f"quantise, RoPE+int8 KV) on {rows} tokens, repeated {n}x over "
+                      f"{budget_s:.0f}s; scalar C oracle, one thread"}
+
+
+if __name__ == "__main__":
+    main()

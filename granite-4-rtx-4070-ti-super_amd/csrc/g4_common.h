@@ -15,6 +15,9 @@ constexpr int kMaxVerifyRows = 16;     // model_config.h:56
 constexpr int kMaxHeadDim = 256;       // model_config.h:52
 constexpr int kCUs = 256;              // MI355X compute units
 constexpr int kPersistBlocks = kCUs * 8;  // grid cap for grid-stride kernels
+// Grid cap of the FP8 amax passes: one f32 partial maximum per workgroup, so
+// the workspace holds kMaxPartials floats (GRANITE4_FP8_WORK_BYTES).
+constexpr int kMaxPartials = 1024;
 
 // The calling thread's launch stream (default: the per-thread stream, the
 // reference's --default-stream per-thread build).
@@ -41,6 +44,48 @@ __device__ __forceinline__ void st8(uint16_t* p, const V8& v) {
 __device__ __forceinline__ float v8_get(const V8& v, int e) {
   return (e & 1) ? __builtin_bit_cast(float, v.w[e >> 1] & 0xffff0000u)
                  : __builtin_bit_cast(float, v.w[e >> 1] << 16);
+}
+
+// Maximum of n per-workgroup partials (pass 2 of the FP8 ops), returned to
+// every thread of the workgroup. Plain loads: the partials were written by
+// the previous launch on the same stream.
+__device__ __forceinline__ float reduce_partials(const float* part, int n) {
+  __shared__ float s_red[4];
+  float m = 0.0f;
+  for (int i = threadIdx.x; i < n; i += 256) m = fmaxf(m, part[i]);
+  m = fmaxf(m, __shfl_xor(m, 1));
+  m = fmaxf(m, __shfl_xor(m, 2));
+  m = fmaxf(m, __shfl_xor(m, 4));
+  m = fmaxf(m, __shfl_xor(m, 8));
+  m = fmaxf(m, __shfl_xor(m, 16));
+  m = fmaxf(m, __shfl_xor(m, 32));
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+  __syncthreads();
+  return m;
+}
+
+// Workgroup maximum written to part[blockIdx.x] (pass 1 of the FP8 ops).
+__device__ __forceinline__ void write_partial(float* part, float m) {
+  __shared__ float s_red[4];
+  m = fmaxf(m, __shfl_xor(m, 1));
+  m = fmaxf(m, __shfl_xor(m, 2));
+  m = fmaxf(m, __shfl_xor(m, 4));
+  m = fmaxf(m, __shfl_xor(m, 8));
+  m = fmaxf(m, __shfl_xor(m, 16));
+  m = fmaxf(m, __shfl_xor(m, 32));
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) part[blockIdx.x] = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+}
+
+// q = n / d for n < 2^31 via a double reciprocal and one correction step.
+__device__ __forceinline__ int div_fast(int n, int d, double inv_d) {
+  int q = static_cast<int>(static_cast<double>(n) * inv_d);
+  const int r = n - q * d;
+  q += (r >= d) - (r < 0);
+  return q;
 }
 
 }  // namespace g4

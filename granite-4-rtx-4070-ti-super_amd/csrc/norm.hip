@@ -18,13 +18,14 @@
 //
 // FP8 output (granite4_add_rmsnorm_fp8): the per-tensor scale depends on the
 // maximum over the whole [rows][cols] tensor, so two launches run back to
-// back: pass 1 writes res' and folds each workgroup's max |y| into work[0]
-// with one atomicMax on the f32 bit pattern (non-negative floats order as
-// unsigned integers); pass 2 re-reads res' (2 B / element, usually still in
-// the 256 MB Infinity Cache), recomputes r and y exactly as pass 1 did, and
-// writes the codes. The last workgroup of pass 2 (atomic counter in work[1])
-// zeroes the workspace for the next call.
+// back. Pass 1 writes res' and one partial max |y| per workgroup into the
+// workspace (plain stores to distinct addresses: no same-address atomics,
+// which serialise across the 8 XCDs); its grid is capped at kMaxPartials
+// workgroups that loop over row groups. Pass 2 reduces the partials, re-reads
+// res' (2 B / element, usually still in the 256 MB Infinity Cache),
+// recomputes r and y exactly as pass 1 did, and writes the codes.
 #include "g4_common.h"
+#include "g4_hw.h"
 #include "g4_math.h"
 #include "g4_wave.h"
 #include "granite4_layerops.h"
@@ -47,41 +48,16 @@ struct NormArgs {
   uint16_t* normed;   // kOutBf16
   uint8_t* codes;     // kOutFp8
   float* scale_out;   // kOutFp8
-  uint32_t* work;     // kOutAmax / kOutFp8: [0] amax bits, [1] done counter
+  float* partials;    // kOutAmax writes [gridDim.x]; kOutFp8 reads [n_partials]
+  int n_partials;
 };
-
-__device__ __forceinline__ void fp8_finish(const NormArgs& a, float s) {
-  if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = s;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    __threadfence();
-    const uint32_t prev = atomicAdd(&a.work[1], 1u);
-    if (prev == gridDim.x - 1) {
-      atomicExch(&a.work[0], 0u);
-      atomicExch(&a.work[1], 0u);
-    }
-  }
-}
-
-__device__ __forceinline__ void block_amax(const NormArgs& a, float m) {
-  __shared__ float s_max[kBlock / 64];
-  m = wave_max(m);
-  if ((threadIdx.x & 63) == 0) s_max[threadIdx.x >> 6] = m;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float b = s_max[0];
-    for (int i = 1; i < kBlock / 64; ++i) b = fmaxf(b, s_max[i]);
-    if (b > 0.0f) atomicMax(&a.work[0], __builtin_bit_cast(uint32_t, b));
-  }
-}
 
 struct Fp8Scale {
   float s, inv;
   bool fast;
 };
 
-__device__ __forceinline__ Fp8Scale fp8_scale_from_work(const uint32_t* work) {
-  const float amax = __builtin_bit_cast(float, __atomic_load_n(work, __ATOMIC_RELAXED));
+__device__ __forceinline__ Fp8Scale fp8_scale_of(float amax) {
   Fp8Scale f;
   f.s = fp8_scale_for(amax);
   f.fast = fp8_fast_scale(f.s);
@@ -89,12 +65,13 @@ __device__ __forceinline__ Fp8Scale fp8_scale_from_work(const uint32_t* work) {
   return f;
 }
 
+// One row group (4 / WPR rows) of the workgroup; MODE kOutAmax folds into *m.
 template <int VPL, int WPR, int MODE>
-__global__ __launch_bounds__(kBlock) void norm_kernel(NormArgs a) {
+__device__ __forceinline__ void norm_rows(const NormArgs& a, int rg, const Fp8Scale& f, float* m_acc) {
   constexpr int RPB = 4 / WPR;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * RPB + wave / WPR;
+  const int row = rg * RPB + wave / WPR;
   const int part = wave % WPR;
   const bool live = row < a.rows;
   const int nvec = a.cols >> 3;
@@ -123,7 +100,7 @@ __global__ __launch_bounds__(kBlock) void norm_kernel(NormArgs a) {
       for (int e = 0; e < 4; ++e) {
         const float lo = lo_bf16(xv[j].w[e]) + a.mult * lo_bf16(bv[j].w[e]);
         const float hi = hi_bf16(xv[j].w[e]) + a.mult * hi_bf16(bv[j].w[e]);
-        xv[j].w[e] = pack_bf16(lo, hi);
+        xv[j].w[e] = pack_bf16_hw(lo, hi);
       }
       if (ok[j] && a.res_out != nullptr) {
         const int vi = (j * WPR + part) * 64 + lane;
@@ -146,6 +123,7 @@ __global__ __launch_bounds__(kBlock) void norm_kernel(NormArgs a) {
     ss = s_part[w0];
 #pragma unroll
     for (int k = 1; k < WPR; ++k) ss += s_part[w0 + k];
+    __syncthreads();  // s_part is reused by the next row group
   }
   const float r = 1.0f / sqrtf(static_cast<float>(ss / a.cols) + a.eps);
 
@@ -156,8 +134,8 @@ __global__ __launch_bounds__(kBlock) void norm_kernel(NormArgs a) {
       V8 y;
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        y.w[e] = pack_bf16(lo_bf16(xv[j].w[e]) * r * lo_bf16(wv[j].w[e]),
-                           hi_bf16(xv[j].w[e]) * r * hi_bf16(wv[j].w[e]));
+        y.w[e] = pack_bf16_hw(lo_bf16(xv[j].w[e]) * r * lo_bf16(wv[j].w[e]),
+                              hi_bf16(xv[j].w[e]) * r * hi_bf16(wv[j].w[e]));
       const int vi = (j * WPR + part) * 64 + lane;
       st8(a.normed + base + 8 * vi, y);
     }
@@ -169,41 +147,51 @@ __global__ __launch_bounds__(kBlock) void norm_kernel(NormArgs a) {
     for (int j = 0; j < VPL; ++j) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const uint32_t yl = f32_to_bf16(lo_bf16(xv[j].w[e]) * r * lo_bf16(wv[j].w[e]));
-        const uint32_t yh = f32_to_bf16(hi_bf16(xv[j].w[e]) * r * hi_bf16(wv[j].w[e]));
-        m = fmaxf(m, bf16_to_f32(yl & 0x7fffu));
-        m = fmaxf(m, bf16_to_f32(yh & 0x7fffu));
+        const uint32_t y = pack_bf16_hw(lo_bf16(xv[j].w[e]) * r * lo_bf16(wv[j].w[e]),
+                                        hi_bf16(xv[j].w[e]) * r * hi_bf16(wv[j].w[e]));
+        m = fmaxf(m, lo_bf16(y & 0x7fff7fffu));
+        m = fmaxf(m, hi_bf16(y & 0x7fff7fffu));
       }
     }
-    block_amax(a, m);
+    *m_acc = fmaxf(*m_acc, m);
     return;
   }
   // kOutFp8
-  const Fp8Scale f = fp8_scale_from_work(a.work);
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     if (!ok[j]) continue;
     uint32_t c[2] = {0u, 0u};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float yl = bf16_to_f32(f32_to_bf16(lo_bf16(xv[j].w[e]) * r * lo_bf16(wv[j].w[e])));
-      const float yh = bf16_to_f32(f32_to_bf16(hi_bf16(xv[j].w[e]) * r * hi_bf16(wv[j].w[e])));
-      const uint32_t pair = fp8_encode_scaled(yl, f.s, f.inv, f.fast) |
-                            (fp8_encode_scaled(yh, f.s, f.inv, f.fast) << 8);
+      const uint32_t y = pack_bf16_hw(lo_bf16(xv[j].w[e]) * r * lo_bf16(wv[j].w[e]),
+                                      hi_bf16(xv[j].w[e]) * r * hi_bf16(wv[j].w[e]));
+      const uint32_t pair = fp8x2_encode_scaled(lo_bf16(y), hi_bf16(y), f.s, f.inv, f.fast);
       c[e >> 1] |= pair << (16 * (e & 1));
     }
     const int vi = (j * WPR + part) * 64 + lane;
     *reinterpret_cast<uint2*>(a.codes + base + 8 * vi) = make_uint2(c[0], c[1]);
   }
-  fp8_finish(a, f.s);
+}
+
+template <int VPL, int WPR, int MODE>
+__global__ __launch_bounds__(kBlock) void norm_kernel(NormArgs a) {
+  constexpr int RPB = 4 / WPR;
+  const int nrg = (a.rows + RPB - 1) / RPB;
+  Fp8Scale f{0.0f, 0.0f, false};
+  if (MODE == kOutFp8) {
+    f = fp8_scale_of(reduce_partials(a.partials, a.n_partials));
+    if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = f.s;
+  }
+  float m = 0.0f;
+  for (int rg = blockIdx.x; rg < nrg; rg += gridDim.x) norm_rows<VPL, WPR, MODE>(a, rg, f, &m);
+  if (MODE == kOutAmax) write_partial(a.partials, m);
 }
 
 // Any-shape fallback: one workgroup per row, element loops, two passes over
 // the row (the second re-reads it from cache). Same arithmetic and reduction
 // order as above at the wave level.
 template <int MODE>
-__global__ __launch_bounds__(kBlock) void norm_generic_kernel(NormArgs a) {
-  const int row = blockIdx.x;
+__device__ void norm_generic_row(const NormArgs& a, int row, const Fp8Scale& f, float* m_acc) {
   const size_t base = static_cast<size_t>(row) * static_cast<size_t>(a.cols);
   auto load_x = [&](int c) {
     const float x = bf16_to_f32(a.x[base + c]);
@@ -221,6 +209,7 @@ __global__ __launch_bounds__(kBlock) void norm_generic_kernel(NormArgs a) {
   if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = ss;
   __syncthreads();
   ss = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
+  __syncthreads();
   const float r = 1.0f / sqrtf(static_cast<float>(ss / a.cols) + a.eps);
   // The same thread reads back what it wrote above, so res_out aliasing res
   // needs no extra barrier: recompute from the inputs when res' was not stored.
@@ -237,15 +226,25 @@ __global__ __launch_bounds__(kBlock) void norm_generic_kernel(NormArgs a) {
     float m = 0.0f;
     for (int c = threadIdx.x; c < a.cols; c += kBlock)
       m = fmaxf(m, bf16_to_f32(f32_to_bf16(x_again(c) * r * bf16_to_f32(a.w[c])) & 0x7fffu));
-    block_amax(a, m);
+    *m_acc = fmaxf(*m_acc, m);
     return;
   }
-  const Fp8Scale f = fp8_scale_from_work(a.work);
   for (int c = threadIdx.x; c < a.cols; c += kBlock) {
     const float y = bf16_to_f32(f32_to_bf16(x_again(c) * r * bf16_to_f32(a.w[c])));
     a.codes[base + c] = static_cast<uint8_t>(fp8_encode_scaled(y, f.s, f.inv, f.fast));
   }
-  fp8_finish(a, f.s);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kBlock) void norm_generic_kernel(NormArgs a) {
+  Fp8Scale f{0.0f, 0.0f, false};
+  if (MODE == kOutFp8) {
+    f = fp8_scale_of(reduce_partials(a.partials, a.n_partials));
+    if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = f.s;
+  }
+  float m = 0.0f;
+  for (int row = blockIdx.x; row < a.rows; row += gridDim.x) norm_generic_row<MODE>(a, row, f, &m);
+  if (MODE == kOutAmax) write_partial(a.partials, m);
 }
 
 // Waves per row: more waves per row when there are too few rows to fill the
@@ -259,26 +258,36 @@ int pick_wpr(int rows) {
   return rows <= 2048 ? 4 : 1;
 }
 
+// Grid of a norm launch: one workgroup per row group, capped at kMaxPartials
+// for the FP8 passes (their workgroups loop over row groups).
+unsigned norm_grid(int MODE, int row_groups) {
+  if (MODE == kOutBf16) return static_cast<unsigned>(row_groups);
+  return static_cast<unsigned>(row_groups < kMaxPartials ? row_groups : kMaxPartials);
+}
+
 template <int MODE>
-int launch_norm(const NormArgs& a, const char* what) {
+int launch_norm(NormArgs& a, const char* what) {
   const int nvec = a.cols / 8;
   const bool vec = (a.cols % 8) == 0;
   const int wpr = pick_wpr(a.rows);
   const hipStream_t st = stream();
   if (vec && wpr == 4 && nvec <= 4 * 64 * 4) {
-    const unsigned grid = static_cast<unsigned>(a.rows);
+    const unsigned grid = norm_grid(MODE, a.rows);
+    if (MODE == kOutAmax) a.n_partials = static_cast<int>(grid);
     if (nvec <= 256) hipLaunchKernelGGL((norm_kernel<1, 4, MODE>), grid, kBlock, 0, st, a);
     else if (nvec <= 512) hipLaunchKernelGGL((norm_kernel<2, 4, MODE>), grid, kBlock, 0, st, a);
     else hipLaunchKernelGGL((norm_kernel<4, 4, MODE>), grid, kBlock, 0, st, a);
   } else if (vec && nvec <= 8 * 64) {
-    const unsigned grid = static_cast<unsigned>((a.rows + 3) / 4);
+    const unsigned grid = norm_grid(MODE, (a.rows + 3) / 4);
+    if (MODE == kOutAmax) a.n_partials = static_cast<int>(grid);
     if (nvec <= 64) hipLaunchKernelGGL((norm_kernel<1, 1, MODE>), grid, kBlock, 0, st, a);
     else if (nvec <= 128) hipLaunchKernelGGL((norm_kernel<2, 1, MODE>), grid, kBlock, 0, st, a);
     else if (nvec <= 256) hipLaunchKernelGGL((norm_kernel<4, 1, MODE>), grid, kBlock, 0, st, a);
     else hipLaunchKernelGGL((norm_kernel<8, 1, MODE>), grid, kBlock, 0, st, a);
   } else {
-    hipLaunchKernelGGL((norm_generic_kernel<MODE>), static_cast<unsigned>(a.rows), kBlock, 0, st,
-                       a);
+    const unsigned grid = norm_grid(MODE, a.rows);
+    if (MODE == kOutAmax) a.n_partials = static_cast<int>(grid);
+    hipLaunchKernelGGL((norm_generic_kernel<MODE>), grid, kBlock, 0, st, a);
   }
   return launch_status(what);
 }
@@ -296,7 +305,7 @@ int rmsnorm_ref_api(const uint16_t* d_x, const uint16_t* d_w, float eps, int row
     std::fprintf(stderr, "granite4: %s: invalid arguments\n", what);
     return -1;
   }
-  NormArgs a{d_x, nullptr, 1.0f, d_w, eps, rows, cols, nullptr, d_out, nullptr, nullptr, nullptr};
+  NormArgs a{d_x, nullptr, 1.0f, d_w, eps, rows, cols, nullptr, d_out, nullptr, nullptr, nullptr, 0};
   return launch_norm<kOutBf16>(a, what);
 }
 
@@ -327,7 +336,7 @@ int granite4_add_rmsnorm(const uint16_t* d_res, const uint16_t* d_branch, float 
     return -1;
   }
   NormArgs a{d_res, d_branch, resid_mult, d_w, eps, rows, cols,
-             d_branch != nullptr ? d_res_out : nullptr, d_normed, nullptr, nullptr, nullptr};
+             d_branch != nullptr ? d_res_out : nullptr, d_normed, nullptr, nullptr, nullptr, 0};
   return launch_norm<kOutBf16>(a, "granite4_add_rmsnorm");
 }
 
@@ -340,10 +349,9 @@ int granite4_add_rmsnorm_fp8(const uint16_t* d_res, const uint16_t* d_branch, fl
     std::fprintf(stderr, "granite4: granite4_add_rmsnorm_fp8: invalid arguments\n");
     return -1;
   }
-  uint32_t* work = static_cast<uint32_t*>(d_work);
   uint16_t* res_out = d_branch != nullptr ? d_res_out : nullptr;
   NormArgs p1{d_res, d_branch, resid_mult, d_w, eps, rows, cols,
-              res_out, nullptr, nullptr, nullptr, work};
+              res_out, nullptr, nullptr, nullptr, static_cast<float*>(d_work), 0};
   if (launch_norm<kOutAmax>(p1, "granite4_add_rmsnorm_fp8 (amax)") != 0) return -1;
   // Pass 2 reads the stored residual when there is one (it may alias d_res).
   NormArgs p2 = p1;

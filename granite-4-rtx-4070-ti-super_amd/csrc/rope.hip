@@ -19,6 +19,7 @@
 // bytes + 1 plane byte (bit j of plane byte l is bit 4 of dim 8l + j), scales
 // by the group's first lane.
 #include "g4_common.h"
+#include "g4_hw.h"
 #include "g4_math.h"
 #include "g4_wave.h"
 #include "granite4_layerops.h"
@@ -125,7 +126,7 @@ __device__ __forceinline__ void rotate8(const V8& x, const float* cs, const floa
 __device__ __forceinline__ V8 to_bf16x8(const float* f) {
   V8 v;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) v.w[e] = pack_bf16(f[2 * e], f[2 * e + 1]);
+  for (int e = 0; e < 4; ++e) v.w[e] = pack_bf16_hw(f[2 * e], f[2 * e + 1]);
   return v;
 }
 
@@ -375,7 +376,7 @@ __global__ __launch_bounds__(kBlock) void embed_kernel(const int32_t* tokens, in
     if (valid) {
       v = ld8(emb + src + j);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v.w[e] = pack_bf16(mult * lo_bf16(v.w[e]), mult * hi_bf16(v.w[e]));
+      for (int e = 0; e < 4; ++e) v.w[e] = pack_bf16_hw(mult * lo_bf16(v.w[e]), mult * hi_bf16(v.w[e]));
     }
     st8(out + dst + j, v);
   } else {

@@ -13,9 +13,11 @@
 // read + 2 B (bf16) or 1 B (FP8) written per element.
 //
 // FP8 output uses the same two-launch scheme as the add+RMSNorm kernel
-// (norm.hip): pass 1 folds max |act| into work[0], pass 2 recomputes act and
-// writes the codes; the last workgroup of pass 2 zeroes the workspace.
+// (norm.hip): pass 1 writes one partial max |act| per workgroup (grid capped
+// at kMaxPartials), pass 2 reduces the partials, recomputes act and writes
+// the codes.
 #include "g4_common.h"
+#include "g4_hw.h"
 #include "g4_math.h"
 #include "g4_wave.h"
 #include "granite4_layerops.h"
@@ -31,7 +33,9 @@ struct SwArgs {
   uint16_t* act;     // bf16 output (kOutBf16) or optional copy (kOutAmax)
   uint8_t* codes;    // kOutFp8
   float* scale_out;  // kOutFp8
-  uint32_t* work;
+  float* partials;   // kOutAmax writes [gridDim.x]; kOutFp8 reads [n_partials]
+  int n_partials;
+  double inv_nv;     // 1 / (I / 8)
 };
 
 __device__ __forceinline__ float silu_mul(float g, float u) {
@@ -40,15 +44,16 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g * sig * u;
 }
 
+// Vector v (8 elements) of the [rows][I / 8] output: act offset 8 v, gate
+// offset 8 v + r I (the row stride of gu is 2I), up offset one I further.
 template <bool F32IN>
-__device__ __forceinline__ void load_gu(const SwArgs& a, long long v, int nv, float* g,
-                                        float* u, long long* out_off) {
-  const long long r = v / nv;
-  const long long c = v - r * nv;
-  const long long row = r * 2LL * a.I;
-  *out_off = r * a.I + 8 * c;
+__device__ __forceinline__ void load_gu(const SwArgs& a, int v, int nv, float* g, float* u,
+                                        long long* out_off) {
+  const int r = div_fast(v, nv, a.inv_nv);
+  *out_off = 8LL * v;
+  const long long gofs = 8LL * v + static_cast<long long>(r) * a.I;
   if (F32IN) {
-    const float* p = static_cast<const float*>(a.gu) + row + 8 * c;
+    const float* p = static_cast<const float*>(a.gu) + gofs;
     const float4 g0 = *reinterpret_cast<const float4*>(p);
     const float4 g1 = *reinterpret_cast<const float4*>(p + 4);
     const float4 u0 = *reinterpret_cast<const float4*>(p + a.I);
@@ -58,7 +63,7 @@ __device__ __forceinline__ void load_gu(const SwArgs& a, long long v, int nv, fl
     u[0] = u0.x; u[1] = u0.y; u[2] = u0.z; u[3] = u0.w;
     u[4] = u1.x; u[5] = u1.y; u[6] = u1.z; u[7] = u1.w;
   } else {
-    const uint16_t* p = static_cast<const uint16_t*>(a.gu) + row + 8 * c;
+    const uint16_t* p = static_cast<const uint16_t*>(a.gu) + gofs;
     const V8 gv = ld8(p);
     const V8 uv = ld8(p + a.I);
 #pragma unroll
@@ -72,20 +77,19 @@ __device__ __forceinline__ void load_gu(const SwArgs& a, long long v, int nv, fl
 template <int MODE, bool F32IN>
 __global__ __launch_bounds__(kBlock) void swiglu_kernel(SwArgs a) {
   const int nv = a.I >> 3;
-  const long long total = static_cast<long long>(a.rows) * nv;
-  const long long step = static_cast<long long>(gridDim.x) * kBlock;
+  const int total = a.rows * nv;
+  const int step = gridDim.x * kBlock;
   float s = 0.0f, inv = 0.0f;
   bool fast = false;
   if (MODE == kOutFp8) {
-    const float amax = __builtin_bit_cast(float, __atomic_load_n(a.work, __ATOMIC_RELAXED));
-    s = fp8_scale_for(amax);
+    s = fp8_scale_for(reduce_partials(a.partials, a.n_partials));
     fast = fp8_fast_scale(s);
     inv = fast ? 1.0f / s : 0.0f;
+    if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = s;
   }
   float m = 0.0f;
-  for (long long v0 = static_cast<long long>(blockIdx.x) * kBlock + threadIdx.x; v0 < total;
-       v0 += 2 * step) {
-    const long long v1 = v0 + step;
+  for (int v0 = blockIdx.x * kBlock + threadIdx.x; v0 < total; v0 += 2 * step) {
+    const int v1 = v0 + step;
     float g[2][8], u[2][8];
     long long off[2];
     load_gu<F32IN>(a, v0, nv, g[0], u[0], &off[0]);
@@ -97,50 +101,27 @@ __global__ __launch_bounds__(kBlock) void swiglu_kernel(SwArgs a) {
       uint32_t w[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        w[e] = pack_bf16(silu_mul(g[k][2 * e], u[k][2 * e]),
-                         silu_mul(g[k][2 * e + 1], u[k][2 * e + 1]));
+        w[e] = pack_bf16_hw(silu_mul(g[k][2 * e], u[k][2 * e]),
+                            silu_mul(g[k][2 * e + 1], u[k][2 * e + 1]));
       if (MODE == kOutBf16 || (MODE == kOutAmax && a.act != nullptr))
         st8(a.act + off[k], V8{{w[0], w[1], w[2], w[3]}});
       if (MODE == kOutAmax) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          m = fmaxf(m, fmaxf(bf16_to_f32(w[e] & 0x7fffu), bf16_to_f32((w[e] >> 16) & 0x7fffu)));
+          m = fmaxf(m, fmaxf(lo_bf16(w[e] & 0x7fff7fffu), hi_bf16(w[e] & 0x7fff7fffu)));
       }
       if (MODE == kOutFp8) {
         uint32_t c[2] = {0u, 0u};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const uint32_t pair = fp8_encode_scaled(lo_bf16(w[e]), s, inv, fast) |
-                                (fp8_encode_scaled(hi_bf16(w[e]), s, inv, fast) << 8);
+          const uint32_t pair = fp8x2_encode_scaled(lo_bf16(w[e]), hi_bf16(w[e]), s, inv, fast);
           c[e >> 1] |= pair << (16 * (e & 1));
         }
         *reinterpret_cast<uint2*>(a.codes + off[k]) = make_uint2(c[0], c[1]);
       }
     }
   }
-  if (MODE == kOutAmax) {
-    __shared__ float s_max[kBlock / 64];
-    m = wave_max(m);
-    if ((threadIdx.x & 63) == 0) s_max[threadIdx.x >> 6] = m;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      float b = s_max[0];
-      for (int i = 1; i < kBlock / 64; ++i) b = fmaxf(b, s_max[i]);
-      if (b > 0.0f) atomicMax(&a.work[0], __builtin_bit_cast(uint32_t, b));
-    }
-  }
-  if (MODE == kOutFp8) {
-    if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = s;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      __threadfence();
-      const uint32_t prev = atomicAdd(&a.work[1], 1u);
-      if (prev == gridDim.x - 1) {
-        atomicExch(&a.work[0], 0u);
-        atomicExch(&a.work[1], 0u);
-      }
-    }
-  }
+  if (MODE == kOutAmax) write_partial(a.partials, m);
 }
 
 // Element-wise fallback for I not a multiple of 8 (bf16 / f32 in, bf16 out).
@@ -164,13 +145,25 @@ __global__ __launch_bounds__(kBlock) void swiglu_scalar_kernel(SwArgs a) {
   }
 }
 
-unsigned grid_for(long long vectors) {
+unsigned grid_for(long long vectors, int cap) {
   const long long want = (vectors + 2LL * kBlock - 1) / (2LL * kBlock);
-  return static_cast<unsigned>(want < kPersistBlocks ? (want > 0 ? want : 1) : kPersistBlocks);
+  return static_cast<unsigned>(want < cap ? (want > 0 ? want : 1) : cap);
 }
 
+// Vector indices are 32-bit: rows * I / 8 plus one grid stride must fit.
 bool sw_args_ok(const void* gu, int rows, int I) {
-  return gu != nullptr && rows > 0 && I > 0 && static_cast<long long>(rows) * 2 * I < (1LL << 40);
+  return gu != nullptr && rows > 0 && I > 0 &&
+         static_cast<long long>(rows) * (I / 8) + 2LL * kPersistBlocks * kBlock < INT_MAX &&
+         static_cast<long long>(rows) * I < INT_MAX;
+}
+
+SwArgs sw_args(const void* gu, int rows, int I) {
+  SwArgs a{};
+  a.gu = gu;
+  a.rows = rows;
+  a.I = I;
+  a.inv_nv = I >= 8 ? 1.0 / static_cast<double>(I / 8) : 0.0;
+  return a;
 }
 
 }  // namespace
@@ -185,10 +178,12 @@ int granite4_swiglu(const uint16_t* d_gu, int rows, int I, uint16_t* d_act) {
     std::fprintf(stderr, "granite4: granite4_swiglu: invalid arguments\n");
     return -1;
   }
-  SwArgs a{d_gu, rows, I, d_act, nullptr, nullptr, nullptr};
+  SwArgs a = sw_args(d_gu, rows, I);
+  a.act = d_act;
   if (I % 8 == 0)
     hipLaunchKernelGGL((swiglu_kernel<kOutBf16, false>),
-                       grid_for(static_cast<long long>(rows) * (I / 8)), kBlock, 0, stream(), a);
+                       grid_for(static_cast<long long>(rows) * (I / 8), kPersistBlocks), kBlock, 0,
+                       stream(), a);
   else
     hipLaunchKernelGGL((swiglu_scalar_kernel<false>), kPersistBlocks, kBlock, 0, stream(), a);
   return launch_status("granite4_swiglu");
@@ -199,10 +194,12 @@ int granite4_prefill_silu_mul(const float* gu, int I, int rows, uint16_t* act) {
     std::fprintf(stderr, "granite4: granite4_prefill_silu_mul: invalid arguments\n");
     return -1;
   }
-  SwArgs a{gu, rows, I, act, nullptr, nullptr, nullptr};
+  SwArgs a = sw_args(gu, rows, I);
+  a.act = act;
   if (I % 8 == 0)
     hipLaunchKernelGGL((swiglu_kernel<kOutBf16, true>),
-                       grid_for(static_cast<long long>(rows) * (I / 8)), kBlock, 0, stream(), a);
+                       grid_for(static_cast<long long>(rows) * (I / 8), kPersistBlocks), kBlock, 0,
+                       stream(), a);
   else
     hipLaunchKernelGGL((swiglu_scalar_kernel<true>), kPersistBlocks, kBlock, 0, stream(), a);
   return launch_status("granite4_prefill_silu_mul");
@@ -215,12 +212,17 @@ int granite4_swiglu_fp8(const uint16_t* d_gu, int rows, int I, uint8_t* d_codes,
     std::fprintf(stderr, "granite4: granite4_swiglu_fp8: invalid arguments (I %% 8 == 0)\n");
     return -1;
   }
-  uint32_t* work = static_cast<uint32_t*>(d_work);
-  const unsigned grid = grid_for(static_cast<long long>(rows) * (I / 8));
-  SwArgs p1{d_gu, rows, I, d_act, nullptr, nullptr, work};
+  const unsigned grid = grid_for(static_cast<long long>(rows) * (I / 8), kMaxPartials);
+  SwArgs p1 = sw_args(d_gu, rows, I);
+  p1.act = d_act;
+  p1.partials = static_cast<float*>(d_work);
   hipLaunchKernelGGL((swiglu_kernel<kOutAmax, false>), grid, kBlock, 0, stream(), p1);
   if (launch_status("granite4_swiglu_fp8 (amax)") != 0) return -1;
-  SwArgs p2{d_gu, rows, I, nullptr, d_codes, d_scale, work};
+  SwArgs p2 = sw_args(d_gu, rows, I);
+  p2.codes = d_codes;
+  p2.scale_out = d_scale;
+  p2.partials = static_cast<float*>(d_work);
+  p2.n_partials = static_cast<int>(grid);
   hipLaunchKernelGGL((swiglu_kernel<kOutFp8, false>), grid, kBlock, 0, stream(), p2);
   return launch_status("granite4_swiglu_fp8 (encode)");
 }

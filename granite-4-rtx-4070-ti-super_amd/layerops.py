@@ -20,7 +20,7 @@ import torch  # noqa: F401  (loads the HIP runtime first, so the library binds t
 PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG, "lib", "libgranite4_layerops.so")
 
-FP8_WORK_BYTES = 256
+FP8_WORK_BYTES = 4096
 MAX_VERIFY_ROWS = 16
 
 
@@ -77,6 +77,8 @@ _SIG = {
     "granite4_row_table": [P, I, I, P],
     "granite4_host_fp8_encode": [P, _c.c_size_t, F, P],
     "granite4_host_kv_codes": [P, _c.c_size_t, F, I, P],
+    "granite4_selftest_bf16": [P],
+    "granite4_selftest_fp8": [F, P],
 }
 for _name, _args in _SIG.items():
     _fn = getattr(_lib, _name)

@@ -226,10 +226,10 @@ int granite4_add_rmsnorm(const uint16_t* d_res, const uint16_t* d_branch, float 
  * code = RNE_e4m3(normed / scale) (the reference's weight quantiser
  * gpu_pack.cc:44-51, 296-308 applied to the bf16 normed tensor). Two launches
  * (amax, then encode). d_work: caller-owned device workspace of at least
- * GRANITE4_FP8_WORK_BYTES, zero-filled once before first use; every call
- * leaves it zeroed again. Calls that share one workspace must be ordered on
- * one stream. */
-#define GRANITE4_FP8_WORK_BYTES 256
+ * GRANITE4_FP8_WORK_BYTES that holds the first launch's per-workgroup partial
+ * maxima for the second; no initialisation is needed. Calls that share one
+ * workspace must be ordered on one stream. */
+#define GRANITE4_FP8_WORK_BYTES 4096
 int granite4_add_rmsnorm_fp8(const uint16_t* d_res, const uint16_t* d_branch, float resid_mult,
                              const uint16_t* d_w, float eps, int rows, int cols,
                              uint16_t* d_res_out, uint8_t* d_codes, float* d_scale,
@@ -286,6 +286,15 @@ int granite4_row_table(const int32_t* block_table, int n, int page, int32_t* out
  * inline code the kernels use, on the CPU (no GPU needed). */
 int granite4_host_fp8_encode(const float* y, size_t n, float scale, uint8_t* codes);
 int granite4_host_kv_codes(const float* x, size_t n, float scale, int qmax, int32_t* codes);
+
+/* Device self-tests of the hardware conversions the kernels use, against the
+ * library's exact software arithmetic (the pattern of the reference's
+ * granite4_fp8_decode_all probe, kernels_phase2.cu:844). d_result: two
+ * zero-initialised device uint64 (mismatch count, first mismatching input
+ * bits). _bf16 sweeps every non-NaN f32 through v_cvt_pk_bf16_f32; _fp8 every
+ * f32 y in [0, 470 * scale] (and -y) through the FP8 pair encoder. */
+int granite4_selftest_bf16(unsigned long long* d_result);
+int granite4_selftest_fp8(float scale, unsigned long long* d_result);
 
 #ifdef __cplusplus
 }  /* extern "C" */

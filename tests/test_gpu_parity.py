@@ -60,6 +60,24 @@ def note(msg):
     sys.stdout.flush()
 
 
+# ----------------------------------------------------------------------------- hardware conversions
+def test_selftest_bf16_hw_conversion_all_f32():
+    note("selftest bf16 (2^32 patterns)")
+    res = torch.zeros(2, dtype=torch.int64, device="cuda")
+    L.call("granite4_selftest_bf16", res)
+    r = host(res)
+    assert r[0] == 0, f"{r[0]} mismatches, first input bits {int(r[1]):#010x}"
+
+
+@pytest.mark.parametrize("scale", [1.0, 3.0 / 448, 0.1, 1e-20, 7.7e5, 2.0 ** -90])
+def test_selftest_fp8_hw_encoder_exhaustive(scale):
+    note(f"selftest fp8 scale={scale}")
+    res = torch.zeros(2, dtype=torch.int64, device="cuda")
+    L.call("granite4_selftest_fp8", float(np.float32(scale)), res)
+    r = host(res)
+    assert r[0] == 0, f"{r[0]} mismatches, first input bits {int(r[1]):#010x}"
+
+
 # ----------------------------------------------------------------------------- embed
 @pytest.mark.parametrize("rows,mult", [(1, 1.0), (8, 1.0), (512, 1.0), (37, 0.7071)])
 def test_embed_rows_bit_exact(rows, mult):
@@ -174,13 +192,11 @@ def test_add_rmsnorm_fp8(rows):
     np.testing.assert_array_equal(host(ro), ro_want)
     _fp8_check(host(codes), host(scale)[0], host(no))
     assert ulp_diff(host(no), no_want).max() <= 1
-    assert not host(work).any(), "workspace must be left zeroed"
     # a second, smaller call on the same workspace
     r2 = max(1, rows // 3)
     L.call("granite4_add_rmsnorm_fp8", d_res, d_br, 1.0, d_w, 1e-5, r2, cols, ro, codes, scale,
            work)
     _fp8_check(host(codes)[:r2], host(scale)[0], host(no)[:r2])
-    assert not host(work).any()
 
 
 def test_add_rmsnorm_fp8_zero_tensor_and_no_residual():
@@ -221,7 +237,6 @@ def test_swiglu_bf16_and_fp8(rows):
     L.call("granite4_swiglu_fp8", d_gu, rows, I_, codes, scale, work, act2)
     np.testing.assert_array_equal(host(act2), host(act))
     _fp8_check(host(codes), host(scale)[0], host(act))
-    assert not host(work).any()
 
 
 def test_prefill_silu_mul_f32():
