@@ -61,6 +61,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline + decode only")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", choices=["t512", "t8192", "decode", "t8", "stress"],
+                    help="run one configuration and print its detail (profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the non-GEMM layer ops are "
@@ -133,6 +135,7 @@ def main():
                 "scale": torch.empty(1, dtype=torch.float32, device=dev),
                 "gu": randn((T, 2 * I)),
                 "codes_i": torch.empty((T, I), dtype=torch.uint8, device=dev),
+                "act": torch.empty((T, I), dtype=torch.bfloat16, device=dev),
                 "qkv": randn((T, (HQ + 2 * HK) * D)),
                 "q_rot": torch.empty((T, HQ * D), dtype=torch.bfloat16, device=dev),
                 "arena": L.KvArena(bits, HK, (pos0 % 16) + pages * 16 + 16, group=group),
@@ -158,7 +161,7 @@ def main():
 
     def op_swiglu_fp8(s):
         T = s["gu"].shape[0]
-        L.call("granite4_swiglu_fp8", s["gu"], T, I, s["codes_i"], s["scale"], work, None)
+        L.call("granite4_swiglu_fp8", s["gu"], T, I, s["codes_i"], s["scale"], work, s["act"])
 
     def op_rope(s):
         qkv = s["qkv"]
@@ -192,6 +195,20 @@ def main():
         return out
 
     result_extra = {}
+
+    if args.only:
+        if args.only == "t512":
+            r = measure_ops(512, 8, 8, 128, 0, 8, args.steps, args.warmup)
+        elif args.only == "t8192":
+            r = measure_ops(8192, 2, 5, 32, 57344, "k5v4g32", args.steps, args.warmup)
+        elif args.only == "decode":
+            r = bench_decode(torch, L, randn, cos_t, sin_t, emb, gamma, stream, args)
+        elif args.only == "t8":
+            r = bench_multi8(torch, L, randn, cos_t, sin_t, gamma, work, gen, stream, timed, args)
+        else:
+            r = bench_stress(torch, L, randn, cos_t, sin_t, gamma, stream)
+        print(json.dumps({"only": args.only, "detail": r}), flush=True)
+        return
 
     # ---------------------------------------------------------------- headline: T = 512
     log("config 3: prefill T=512 (embed + add_rmsnorm_fp8 + swiglu_fp8 + rope_int8)")

@@ -6,6 +6,7 @@
 #include "granite4_layerops.h"
 
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -19,6 +20,7 @@ thread_local hipStream_t t_stream = hipStreamPerThread;
 }
 
 hipStream_t stream() { return t_stream; }
+
 
 int launch_status(const char* what) {
   const hipError_t e = hipGetLastError();
@@ -128,6 +130,10 @@ int granite4_rope_tables_free(float* d_cos, float* d_sin) {
   const bool ok = (d_cos == nullptr || hipFree(d_cos) == hipSuccess) &&
                   (d_sin == nullptr || hipFree(d_sin) == hipSuccess);
   return ok ? 0 : -1;
+}
+
+size_t granite4_fp8_work_bytes(int rows) {
+  return 4u * (static_cast<size_t>(kMaxPartials) + static_cast<size_t>(rows > 0 ? rows : 0));
 }
 
 int granite4_row_table(const int32_t* block_table, int n, int page, int32_t* out) {

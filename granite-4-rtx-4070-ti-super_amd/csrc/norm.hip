@@ -32,6 +32,8 @@
 
 #include <cstdlib>
 
+static_assert(g4::kMaxPartials == GRANITE4_FP8_MAX_PARTIALS, "workspace layout");
+
 namespace g4 {
 namespace {
 
@@ -50,6 +52,8 @@ struct NormArgs {
   float* scale_out;   // kOutFp8
   float* partials;    // kOutAmax writes [gridDim.x]; kOutFp8 reads [n_partials]
   int n_partials;
+  float* row_r;       // kOutAmax writes each row's 1 / rms, the encode pass reads it
+  double inv_nvec;    // 1 / (cols / 8)
 };
 
 struct Fp8Scale {
@@ -87,8 +91,10 @@ __device__ __forceinline__ void norm_rows(const NormArgs& a, int rg, const Fp8Sc
     bv[j] = V8{{0u, 0u, 0u, 0u}};
     wv[j] = V8{{0u, 0u, 0u, 0u}};
     if (ok[j]) {
-      xv[j] = ld8(a.x + base + 8 * vi);
-      if (a.branch != nullptr) bv[j] = ld8(a.branch + base + 8 * vi);
+      // Pass 2 of the FP8 op re-reads res' that pass 1 just wrote: cached
+      // loads, so the Infinity Cache can serve it; every other input streams.
+      xv[j] = ld8_nt(a.x + base + 8 * vi);
+      if (a.branch != nullptr) bv[j] = ld8_nt(a.branch + base + 8 * vi);
       wv[j] = ld8(a.w + 8 * vi);
     }
   }
@@ -126,6 +132,7 @@ __device__ __forceinline__ void norm_rows(const NormArgs& a, int rg, const Fp8Sc
     __syncthreads();  // s_part is reused by the next row group
   }
   const float r = 1.0f / sqrtf(static_cast<float>(ss / a.cols) + a.eps);
+  if (MODE == kOutAmax && live && part == 0 && lane == 0) a.row_r[row] = r;
 
   if (MODE == kOutBf16) {
 #pragma unroll
@@ -137,7 +144,7 @@ __device__ __forceinline__ void norm_rows(const NormArgs& a, int rg, const Fp8Sc
         y.w[e] = pack_bf16_hw(lo_bf16(xv[j].w[e]) * r * lo_bf16(wv[j].w[e]),
                               hi_bf16(xv[j].w[e]) * r * hi_bf16(wv[j].w[e]));
       const int vi = (j * WPR + part) * 64 + lane;
-      st8(a.normed + base + 8 * vi, y);
+      st8_nt(a.normed + base + 8 * vi, y);
     }
     return;
   }
@@ -169,7 +176,7 @@ __device__ __forceinline__ void norm_rows(const NormArgs& a, int rg, const Fp8Sc
       c[e >> 1] |= pair << (16 * (e & 1));
     }
     const int vi = (j * WPR + part) * 64 + lane;
-    *reinterpret_cast<uint2*>(a.codes + base + 8 * vi) = make_uint2(c[0], c[1]);
+    st_u32x2_nt(a.codes + base + 8 * vi, c[0], c[1]);
   }
 }
 
@@ -185,6 +192,56 @@ __global__ __launch_bounds__(kBlock) void norm_kernel(NormArgs a) {
   float m = 0.0f;
   for (int rg = blockIdx.x; rg < nrg; rg += gridDim.x) norm_rows<VPL, WPR, MODE>(a, rg, f, &m);
   if (MODE == kOutAmax) write_partial(a.partials, m);
+}
+
+// FP8 pass 2 of the vector path: element-wise over [rows][cols / 8] vectors.
+// Each row's 1 / rms comes from pass 1 (row_r), so y = bf16((x * r) * w) is
+// recomputed bit-identically without a row reduction, and the pass streams
+// at full occupancy. x is re-read with cached loads: pass 1 wrote it just
+// before (it is usually still in the Infinity Cache).
+__global__ __launch_bounds__(kBlock) void norm_encode_kernel(NormArgs a) {
+  const int nvec = a.cols >> 3;
+  const int total = a.rows * nvec;
+  const int step = gridDim.x * kBlock;
+  const Fp8Scale f = fp8_scale_of(reduce_partials(a.partials, a.n_partials));
+  if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = f.s;
+  constexpr int U = 4;  // vectors in flight per lane
+  for (int v0 = blockIdx.x * kBlock + threadIdx.x; v0 < total; v0 += U * step) {
+    V8 x[U], w[U];
+    float r[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int v = v0 + k * step;
+      if (v >= total) break;
+      const int row = div_fast(v, nvec, a.inv_nvec);
+      const int c = v - row * nvec;
+      const size_t off = 8ull * static_cast<unsigned>(v);
+      x[k] = ld8(a.x + off);
+      if (a.branch != nullptr) {
+        const V8 b = ld8_nt(a.branch + off);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          x[k].w[e] = pack_bf16_hw(lo_bf16(x[k].w[e]) + a.mult * lo_bf16(b.w[e]),
+                                   hi_bf16(x[k].w[e]) + a.mult * hi_bf16(b.w[e]));
+      }
+      w[k] = ld8(a.w + 8 * c);
+      r[k] = a.row_r[row];
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int v = v0 + k * step;
+      if (v >= total) break;
+      uint32_t cw[2] = {0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t y = pack_bf16_hw(lo_bf16(x[k].w[e]) * r[k] * lo_bf16(w[k].w[e]),
+                                        hi_bf16(x[k].w[e]) * r[k] * hi_bf16(w[k].w[e]));
+        cw[e >> 1] |= fp8x2_encode_scaled(lo_bf16(y), hi_bf16(y), f.s, f.inv, f.fast)
+                      << (16 * (e & 1));
+      }
+      st_u32x2_nt(a.codes + 8ull * static_cast<unsigned>(v), cw[0], cw[1]);
+    }
+  }
 }
 
 // Any-shape fallback: one workgroup per row, element loops, two passes over
@@ -265,19 +322,31 @@ unsigned norm_grid(int MODE, int row_groups) {
   return static_cast<unsigned>(row_groups < kMaxPartials ? row_groups : kMaxPartials);
 }
 
+// Whether the row-vector kernels (and the element-wise FP8 encode pass) take
+// this shape; otherwise the any-shape fallback runs.
+bool norm_vector_path(int rows, int cols) {
+  return cols % 8 == 0 && cols / 8 <= 8 * 64 && static_cast<long long>(rows) * cols < INT_MAX;
+}
+
 template <int MODE>
 int launch_norm(NormArgs& a, const char* what) {
   const int nvec = a.cols / 8;
-  const bool vec = (a.cols % 8) == 0;
+  const bool vec = norm_vector_path(a.rows, a.cols);
   const int wpr = pick_wpr(a.rows);
   const hipStream_t st = stream();
-  if (vec && wpr == 4 && nvec <= 4 * 64 * 4) {
+  if (MODE == kOutFp8 && vec) {
+    a.inv_nvec = 1.0 / nvec;
+    const long long vectors = static_cast<long long>(a.rows) * nvec;
+    const long long want = (vectors + 4LL * kBlock - 1) / (4LL * kBlock);
+    const unsigned grid = static_cast<unsigned>(want < kPersistBlocks ? want : kPersistBlocks);
+    hipLaunchKernelGGL(norm_encode_kernel, grid, kBlock, 0, st, a);
+  } else if (vec && wpr == 4 && nvec <= 4 * 64 * 4) {
     const unsigned grid = norm_grid(MODE, a.rows);
     if (MODE == kOutAmax) a.n_partials = static_cast<int>(grid);
     if (nvec <= 256) hipLaunchKernelGGL((norm_kernel<1, 4, MODE>), grid, kBlock, 0, st, a);
     else if (nvec <= 512) hipLaunchKernelGGL((norm_kernel<2, 4, MODE>), grid, kBlock, 0, st, a);
     else hipLaunchKernelGGL((norm_kernel<4, 4, MODE>), grid, kBlock, 0, st, a);
-  } else if (vec && nvec <= 8 * 64) {
+  } else if (vec) {
     const unsigned grid = norm_grid(MODE, (a.rows + 3) / 4);
     if (MODE == kOutAmax) a.n_partials = static_cast<int>(grid);
     if (nvec <= 64) hipLaunchKernelGGL((norm_kernel<1, 1, MODE>), grid, kBlock, 0, st, a);
@@ -305,7 +374,7 @@ int rmsnorm_ref_api(const uint16_t* d_x, const uint16_t* d_w, float eps, int row
     std::fprintf(stderr, "granite4: %s: invalid arguments\n", what);
     return -1;
   }
-  NormArgs a{d_x, nullptr, 1.0f, d_w, eps, rows, cols, nullptr, d_out, nullptr, nullptr, nullptr, 0};
+  NormArgs a{d_x, nullptr, 1.0f, d_w, eps, rows, cols, nullptr, d_out, nullptr, nullptr, nullptr, 0, nullptr, 0.0};
   return launch_norm<kOutBf16>(a, what);
 }
 
@@ -336,7 +405,8 @@ int granite4_add_rmsnorm(const uint16_t* d_res, const uint16_t* d_branch, float 
     return -1;
   }
   NormArgs a{d_res, d_branch, resid_mult, d_w, eps, rows, cols,
-             d_branch != nullptr ? d_res_out : nullptr, d_normed, nullptr, nullptr, nullptr, 0};
+             d_branch != nullptr ? d_res_out : nullptr, d_normed, nullptr, nullptr, nullptr, 0, nullptr,
+             0.0};
   return launch_norm<kOutBf16>(a, "granite4_add_rmsnorm");
 }
 
@@ -351,7 +421,8 @@ int granite4_add_rmsnorm_fp8(const uint16_t* d_res, const uint16_t* d_branch, fl
   }
   uint16_t* res_out = d_branch != nullptr ? d_res_out : nullptr;
   NormArgs p1{d_res, d_branch, resid_mult, d_w, eps, rows, cols,
-              res_out, nullptr, nullptr, nullptr, static_cast<float*>(d_work), 0};
+              res_out, nullptr, nullptr, nullptr, static_cast<float*>(d_work), 0,
+              static_cast<float*>(d_work) + kMaxPartials, 0.0};
   if (launch_norm<kOutAmax>(p1, "granite4_add_rmsnorm_fp8 (amax)") != 0) return -1;
   // Pass 2 reads the stored residual when there is one (it may alias d_res).
   NormArgs p2 = p1;

@@ -188,7 +188,7 @@ __global__ __launch_bounds__(kBlock) void rope_append_kernel(RopeArgs a) {
     const int h = is_q ? u : u - a.Hq;
     const uint16_t* src = is_q ? a.q + r * a.q_stride + h * 128LL
                                : a.k + r * a.k_stride + h * 128LL;
-    const V8 x = ld8(src + 8 * lane16);
+    const V8 x = ld8_nt(src + 8 * lane16);
     const float* cp = a.cos_t + static_cast<long long>(rp) * 64 + 8 * (lane16 & 7);
     const float* sp = a.sin_t + static_cast<long long>(rp) * 64 + 8 * (lane16 & 7);
     float cs[8], sn[8];
@@ -200,7 +200,7 @@ __global__ __launch_bounds__(kBlock) void rope_append_kernel(RopeArgs a) {
     rotate8(x, cs, sn, first_half, rot);
     const V8 rb = to_bf16x8(rot);
     if (is_q) {
-      st8(a.q_rot + r * a.q_rot_stride + h * 128LL + 8 * lane16, rb);
+      st8_nt(a.q_rot + r * a.q_rot_stride + h * 128LL + 8 * lane16, rb);
       return;
     }
     if (a.k_rot != nullptr) st8(a.k_rot + (static_cast<long long>(r) * a.Hk + h) * 128 + 8 * lane16, rb);
@@ -225,7 +225,7 @@ __global__ __launch_bounds__(kBlock) void rope_append_kernel(RopeArgs a) {
   const bool is_k = u < a.Hq + a.Hk;
   const int h = is_k ? u - a.Hq : u - a.Hq - a.Hk;
   const uint16_t* src = is_k ? a.k + r * a.k_stride + h * 128LL : a.v + r * a.v_stride + h * 128LL;
-  const V8 x = ld8(src + 8 * lane16);
+  const V8 x = ld8_nt(src + 8 * lane16);
   const long long slot = static_cast<long long>(h) * a.stride + row;
   if (BITS == 16) {
     st8(static_cast<uint16_t*>(is_k ? a.cache_k : a.cache_v) + slot * 128 + 8 * lane16, x);
@@ -374,11 +374,11 @@ __global__ __launch_bounds__(kBlock) void embed_kernel(const int32_t* tokens, in
     if (j >= H) return;
     V8 v{{0u, 0u, 0u, 0u}};
     if (valid) {
-      v = ld8(emb + src + j);
+      v = ld8_nt(emb + src + j);
 #pragma unroll
       for (int e = 0; e < 4; ++e) v.w[e] = pack_bf16_hw(mult * lo_bf16(v.w[e]), mult * hi_bf16(v.w[e]));
     }
-    st8(out + dst + j, v);
+    st8_nt(out + dst + j, v);
   } else {
     const int j = blockIdx.x * kBlock + threadIdx.x;
     if (j >= H) return;

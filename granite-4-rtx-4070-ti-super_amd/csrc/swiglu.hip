@@ -36,6 +36,7 @@ struct SwArgs {
   float* partials;   // kOutAmax writes [gridDim.x]; kOutFp8 reads [n_partials]
   int n_partials;
   double inv_nv;     // 1 / (I / 8)
+  const uint16_t* act_in;  // kOutFp8: encode this stored bf16 act instead of recomputing
 };
 
 __device__ __forceinline__ float silu_mul(float g, float u) {
@@ -46,7 +47,7 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 
 // Vector v (8 elements) of the [rows][I / 8] output: act offset 8 v, gate
 // offset 8 v + r I (the row stride of gu is 2I), up offset one I further.
-template <bool F32IN>
+template <bool F32IN, bool NT>
 __device__ __forceinline__ void load_gu(const SwArgs& a, int v, int nv, float* g, float* u,
                                         long long* out_off) {
   const int r = div_fast(v, nv, a.inv_nv);
@@ -54,18 +55,18 @@ __device__ __forceinline__ void load_gu(const SwArgs& a, int v, int nv, float* g
   const long long gofs = 8LL * v + static_cast<long long>(r) * a.I;
   if (F32IN) {
     const float* p = static_cast<const float*>(a.gu) + gofs;
-    const float4 g0 = *reinterpret_cast<const float4*>(p);
-    const float4 g1 = *reinterpret_cast<const float4*>(p + 4);
-    const float4 u0 = *reinterpret_cast<const float4*>(p + a.I);
-    const float4 u1 = *reinterpret_cast<const float4*>(p + a.I + 4);
+    const float4 g0 = ld_f4_nt(p);
+    const float4 g1 = ld_f4_nt(p + 4);
+    const float4 u0 = ld_f4_nt(p + a.I);
+    const float4 u1 = ld_f4_nt(p + a.I + 4);
     g[0] = g0.x; g[1] = g0.y; g[2] = g0.z; g[3] = g0.w;
     g[4] = g1.x; g[5] = g1.y; g[6] = g1.z; g[7] = g1.w;
     u[0] = u0.x; u[1] = u0.y; u[2] = u0.z; u[3] = u0.w;
     u[4] = u1.x; u[5] = u1.y; u[6] = u1.z; u[7] = u1.w;
   } else {
     const uint16_t* p = static_cast<const uint16_t*>(a.gu) + gofs;
-    const V8 gv = ld8(p);
-    const V8 uv = ld8(p + a.I);
+    const V8 gv = ld8_t<NT>(p);
+    const V8 uv = ld8_t<NT>(p + a.I);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       g[e] = v8_get(gv, e);
@@ -88,23 +89,23 @@ __global__ __launch_bounds__(kBlock) void swiglu_kernel(SwArgs a) {
     if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = s;
   }
   float m = 0.0f;
-  for (int v0 = blockIdx.x * kBlock + threadIdx.x; v0 < total; v0 += 2 * step) {
-    const int v1 = v0 + step;
-    float g[2][8], u[2][8];
-    long long off[2];
-    load_gu<F32IN>(a, v0, nv, g[0], u[0], &off[0]);
-    const bool has1 = v1 < total;
-    if (has1) load_gu<F32IN>(a, v1, nv, g[1], u[1], &off[1]);
+  constexpr int U = 4;  // vectors (of gate and of up) in flight per lane
+  for (int v0 = blockIdx.x * kBlock + threadIdx.x; v0 < total; v0 += U * step) {
+    float g[U][8], u[U][8];
+    long long off[U];
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      if (k == 1 && !has1) break;
+    for (int k = 0; k < U; ++k)
+      if (v0 + k * step < total) load_gu<F32IN, true>(a, v0 + k * step, nv, g[k], u[k], &off[k]);
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      if (v0 + k * step >= total) break;
       uint32_t w[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         w[e] = pack_bf16_hw(silu_mul(g[k][2 * e], u[k][2 * e]),
                             silu_mul(g[k][2 * e + 1], u[k][2 * e + 1]));
       if (MODE == kOutBf16 || (MODE == kOutAmax && a.act != nullptr))
-        st8(a.act + off[k], V8{{w[0], w[1], w[2], w[3]}});
+        st8_nt(a.act + off[k], V8{{w[0], w[1], w[2], w[3]}});
       if (MODE == kOutAmax) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
@@ -117,11 +118,39 @@ __global__ __launch_bounds__(kBlock) void swiglu_kernel(SwArgs a) {
           const uint32_t pair = fp8x2_encode_scaled(lo_bf16(w[e]), hi_bf16(w[e]), s, inv, fast);
           c[e >> 1] |= pair << (16 * (e & 1));
         }
-        *reinterpret_cast<uint2*>(a.codes + off[k]) = make_uint2(c[0], c[1]);
+        st_u32x2_nt(a.codes + off[k], c[0], c[1]);
       }
     }
   }
   if (MODE == kOutAmax) write_partial(a.partials, m);
+}
+
+// FP8 encode of a stored bf16 [rows][I] tensor under the per-tensor scale
+// from the pass-1 partials (8 elements per lane per step, two steps in flight).
+__global__ __launch_bounds__(kBlock) void encode_bf16_kernel(SwArgs a) {
+  constexpr int U = 4;  // vectors in flight per lane
+  const int total = a.rows * (a.I >> 3);
+  const int step = gridDim.x * kBlock;
+  const float s = fp8_scale_for(reduce_partials(a.partials, a.n_partials));
+  const bool fast = fp8_fast_scale(s);
+  const float inv = fast ? 1.0f / s : 0.0f;
+  if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = s;
+  for (int v0 = blockIdx.x * kBlock + threadIdx.x; v0 < total; v0 += U * step) {
+    V8 x[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k)
+      if (v0 + k * step < total) x[k] = ld8_nt(a.act_in + 8LL * (v0 + k * step));
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      if (v0 + k * step >= total) break;
+      uint32_t c[2] = {0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        c[e >> 1] |= fp8x2_encode_scaled(lo_bf16(x[k].w[e]), hi_bf16(x[k].w[e]), s, inv, fast)
+                     << (16 * (e & 1));
+      st_u32x2_nt(a.codes + 8LL * (v0 + k * step), c[0], c[1]);
+    }
+  }
 }
 
 // Element-wise fallback for I not a multiple of 8 (bf16 / f32 in, bf16 out).
@@ -146,14 +175,14 @@ __global__ __launch_bounds__(kBlock) void swiglu_scalar_kernel(SwArgs a) {
 }
 
 unsigned grid_for(long long vectors, int cap) {
-  const long long want = (vectors + 2LL * kBlock - 1) / (2LL * kBlock);
+  const long long want = (vectors + 4LL * kBlock - 1) / (4LL * kBlock);
   return static_cast<unsigned>(want < cap ? (want > 0 ? want : 1) : cap);
 }
 
 // Vector indices are 32-bit: rows * I / 8 plus one grid stride must fit.
 bool sw_args_ok(const void* gu, int rows, int I) {
   return gu != nullptr && rows > 0 && I > 0 &&
-         static_cast<long long>(rows) * (I / 8) + 2LL * kPersistBlocks * kBlock < INT_MAX &&
+         static_cast<long long>(rows) * (I / 8) + 4LL * kPersistBlocks * kBlock < INT_MAX &&
          static_cast<long long>(rows) * I < INT_MAX;
 }
 
@@ -223,7 +252,15 @@ int granite4_swiglu_fp8(const uint16_t* d_gu, int rows, int I, uint8_t* d_codes,
   p2.scale_out = d_scale;
   p2.partials = static_cast<float*>(d_work);
   p2.n_partials = static_cast<int>(grid);
-  hipLaunchKernelGGL((swiglu_kernel<kOutFp8, false>), grid, kBlock, 0, stream(), p2);
+  if (d_act != nullptr) {
+    // Pass 1 stored the bf16 act: pass 2 only encodes it (2 B read instead
+    // of re-reading 4 B of gate|up and re-evaluating the SiLU).
+    p2.act_in = d_act;
+    hipLaunchKernelGGL(encode_bf16_kernel, grid_for(static_cast<long long>(rows) * (I / 8), kPersistBlocks),
+                       kBlock, 0, stream(), p2);
+  } else {
+    hipLaunchKernelGGL((swiglu_kernel<kOutFp8, false>), grid, kBlock, 0, stream(), p2);
+  }
   return launch_status("granite4_swiglu_fp8 (encode)");
 }
 

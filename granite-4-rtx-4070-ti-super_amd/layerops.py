@@ -20,7 +20,7 @@ import torch  # noqa: F401  (loads the HIP runtime first, so the library binds t
 PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG, "lib", "libgranite4_layerops.so")
 
-FP8_WORK_BYTES = 4096
+FP8_MAX_PARTIALS = 1024
 MAX_VERIFY_ROWS = 16
 
 
@@ -75,15 +75,17 @@ _SIG = {
                              P, P, P, P, I],
     "granite4_rope_append_at_pos": [P, P, P, P, P, I, P, P, I, I, I, I, I, P, P, P, P, P, I],
     "granite4_row_table": [P, I, I, P],
+    "granite4_fp8_work_bytes": [I],
     "granite4_host_fp8_encode": [P, _c.c_size_t, F, P],
     "granite4_host_kv_codes": [P, _c.c_size_t, F, I, P],
     "granite4_selftest_bf16": [P],
+    "granite4_bw_probe": [P, P, _c.c_size_t, I, I],
     "granite4_selftest_fp8": [F, P],
 }
 for _name, _args in _SIG.items():
     _fn = getattr(_lib, _name)
     _fn.argtypes = _args
-    _fn.restype = P if _name == "granite4_get_stream" else I
+    _fn.restype = {"granite4_get_stream": P, "granite4_fp8_work_bytes": _c.c_size_t}.get(_name, I)
 
 lib = _lib
 
@@ -148,8 +150,13 @@ def add_rmsnorm(res, branch, w, eps, resid_mult=1.0, res_out=None, normed=None):
     return res_out, normed
 
 
-def fp8_workspace(device="cuda"):
-    return torch.zeros(FP8_WORK_BYTES, dtype=torch.uint8, device=device)
+def fp8_work_bytes(rows):
+    return 4 * (FP8_MAX_PARTIALS + rows)
+
+
+def fp8_workspace(rows=65536, device="cuda"):
+    """Workspace for the FP8 ops on tensors of up to `rows` rows."""
+    return torch.zeros(fp8_work_bytes(rows), dtype=torch.uint8, device=device)
 
 
 def add_rmsnorm_fp8(res, branch, w, eps, work, resid_mult=1.0, res_out=None, codes=None,

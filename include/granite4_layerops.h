@@ -226,10 +226,13 @@ int granite4_add_rmsnorm(const uint16_t* d_res, const uint16_t* d_branch, float 
  * code = RNE_e4m3(normed / scale) (the reference's weight quantiser
  * gpu_pack.cc:44-51, 296-308 applied to the bf16 normed tensor). Two launches
  * (amax, then encode). d_work: caller-owned device workspace of at least
- * GRANITE4_FP8_WORK_BYTES that holds the first launch's per-workgroup partial
- * maxima for the second; no initialisation is needed. Calls that share one
- * workspace must be ordered on one stream. */
-#define GRANITE4_FP8_WORK_BYTES 4096
+ * GRANITE4_FP8_WORK_BYTES(rows) bytes (= granite4_fp8_work_bytes(rows)): the
+ * first launch's per-workgroup partial maxima and per-row 1 / rms for the
+ * second. No initialisation is needed. Calls that share one workspace must be
+ * ordered on one stream. */
+#define GRANITE4_FP8_MAX_PARTIALS 1024
+#define GRANITE4_FP8_WORK_BYTES(rows) (4 * (GRANITE4_FP8_MAX_PARTIALS + (rows)))
+size_t granite4_fp8_work_bytes(int rows);
 int granite4_add_rmsnorm_fp8(const uint16_t* d_res, const uint16_t* d_branch, float resid_mult,
                              const uint16_t* d_w, float eps, int rows, int cols,
                              uint16_t* d_res_out, uint8_t* d_codes, float* d_scale,
@@ -241,7 +244,10 @@ int granite4_add_rmsnorm_fp8(const uint16_t* d_res, const uint16_t* d_branch, fl
 int granite4_swiglu(const uint16_t* d_gu, int rows, int I, uint16_t* d_act);
 
 /* SwiGLU with FP8 requantisation of act (per-tensor scale, as
- * granite4_add_rmsnorm_fp8). d_act (may be NULL) also receives the bf16 act. */
+ * granite4_add_rmsnorm_fp8; d_work needs GRANITE4_FP8_WORK_BYTES(0)). d_act
+ * may be NULL; when given it receives the bf16 act, and the encode launch
+ * reads it back (2 B / element) instead of re-reading gate|up (4 B) and
+ * re-evaluating the SiLU. */
 int granite4_swiglu_fp8(const uint16_t* d_gu, int rows, int I, uint8_t* d_codes,
                         float* d_scale, void* d_work, uint16_t* d_act);
 
@@ -286,6 +292,13 @@ int granite4_row_table(const int32_t* block_table, int n, int page, int32_t* out
  * inline code the kernels use, on the CPU (no GPU needed). */
 int granite4_host_fp8_encode(const float* y, size_t n, float scale, uint8_t* codes);
 int granite4_host_kv_codes(const float* x, size_t n, float scale, int qmax, int32_t* codes);
+
+/* Streaming bandwidth probe (kernels_bench.cu:36-53 pattern): mode 1 copies
+ * `bytes` (multiple of 16) from src to dst, mode 0 only reads src (dst: a
+ * 4-byte sink); modes 2 / 3 are the read / copy with non-temporal accesses,
+ * 4 a copy with one vector per lane per iteration, 5 a non-temporal copy with
+ * eight; `blocks` 256-thread workgroups in a grid-stride loop. */
+int granite4_bw_probe(const void* src, void* dst, size_t bytes, int mode, int blocks);
 
 /* Device self-tests of the hardware conversions the kernels use, against the
  * library's exact software arithmetic (the pattern of the reference's

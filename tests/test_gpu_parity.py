@@ -204,7 +204,7 @@ def test_add_rmsnorm_fp8_zero_tensor_and_no_residual():
     rows, cols = 4, 4096
     z = np.zeros((rows, cols), np.uint16)
     w = ol.normal_bf16(0xB4, 1.0, 0.1, cols)
-    work = L.fp8_workspace()
+    work = L.fp8_workspace(rows)
     codes = torch.full((rows, cols), 0x55, dtype=torch.uint8, device="cuda")
     scale = torch.full((1,), 7.0, dtype=torch.float32, device="cuda")
     L.call("granite4_add_rmsnorm_fp8", dev(z), None, 1.0, dev(w), 1e-5, rows, cols, None, codes,
@@ -237,6 +237,12 @@ def test_swiglu_bf16_and_fp8(rows):
     L.call("granite4_swiglu_fp8", d_gu, rows, I_, codes, scale, work, act2)
     np.testing.assert_array_equal(host(act2), host(act))
     _fp8_check(host(codes), host(scale)[0], host(act))
+    # without the act buffer the encode launch recomputes the SiLU: same codes
+    codes2 = torch.empty_like(codes)
+    scale2 = torch.empty_like(scale)
+    L.call("granite4_swiglu_fp8", d_gu, rows, I_, codes2, scale2, work, None)
+    np.testing.assert_array_equal(host(codes2), host(codes))
+    assert host(scale2)[0] == host(scale)[0]
 
 
 def test_prefill_silu_mul_f32():
