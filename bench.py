@@ -46,6 +46,15 @@ B_ROPE = {16: B_ROPE_COMMON + 2 * HK * D * 2,
           "k5v4g32": B_ROPE_COMMON + HK * (80 + 64) + 2 * HK * 4 * 4}
 
 
+# HBM bytes per swiglu_fp8 call at T=512 (both launches), measured with two
+# rocprofv3 --pmc runs of `bench.py --only t512` (FETCH_SIZE, then WRITE_SIZE,
+# KiB per dispatch): fetch (12827.0 + 12984.5) KiB x 2.0 + write (25.0 +
+# 6400.0) KiB x 1.0. The factors are what the same counters read for the
+# known-size copy probe (`bench.py --only probe`): FETCH_SIZE half the bytes,
+# WRITE_SIZE all of them.
+SWIGLU_FP8_T512_TRAFFIC = int((12827.0 + 12984.5) * 2.0 * 1024 + (25.0 + 6400.0) * 1024)
+
+
 def per_launch_extra(op):
     return {"norm_fp8": 2 * H + 4, "norm_bf16": 2 * H, "swiglu_fp8": 4}.get(op, 0)
 
@@ -61,8 +70,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline + decode only")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["t512", "t8192", "decode", "t8", "stress"],
+    ap.add_argument("--only", choices=["t512", "t8192", "decode", "t8", "stress", "tN", "probe"],
                     help="run one configuration and print its detail (profiling runs)")
+    ap.add_argument("--T", type=int, default=1024, help="token count for --only tN")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the non-GEMM layer ops are "
@@ -135,7 +145,6 @@ def main():
                 "scale": torch.empty(1, dtype=torch.float32, device=dev),
                 "gu": randn((T, 2 * I)),
                 "codes_i": torch.empty((T, I), dtype=torch.uint8, device=dev),
-                "act": torch.empty((T, I), dtype=torch.bfloat16, device=dev),
                 "qkv": randn((T, (HQ + 2 * HK) * D)),
                 "q_rot": torch.empty((T, HQ * D), dtype=torch.bfloat16, device=dev),
                 "arena": L.KvArena(bits, HK, (pos0 % 16) + pages * 16 + 16, group=group),
@@ -161,7 +170,7 @@ def main():
 
     def op_swiglu_fp8(s):
         T = s["gu"].shape[0]
-        L.call("granite4_swiglu_fp8", s["gu"], T, I, s["codes_i"], s["scale"], work, s["act"])
+        L.call("granite4_swiglu_fp8", s["gu"], T, I, s["codes_i"], s["scale"], work, None)
 
     def op_rope(s):
         qkv = s["qkv"]
@@ -201,6 +210,11 @@ def main():
             r = measure_ops(512, 8, 8, 128, 0, 8, args.steps, args.warmup)
         elif args.only == "t8192":
             r = measure_ops(8192, 2, 5, 32, 57344, "k5v4g32", args.steps, args.warmup)
+        elif args.only == "probe":
+            r = bench_probe(torch, L, stream, timed)
+        elif args.only == "tN":
+            r = measure_ops(args.T, max(2, min(8, 4096 // args.T)), 8, 128, 0, 8, args.steps,
+                            args.warmup)
         elif args.only == "decode":
             r = bench_decode(torch, L, randn, cos_t, sin_t, emb, gamma, stream, args)
         elif args.only == "t8":
@@ -235,6 +249,10 @@ def main():
         result_extra["stress_T32768"] = bench_stress(torch, L, randn, cos_t, sin_t, gamma, stream)
         log(json.dumps(result_extra["stress_T32768"]))
 
+    log("bandwidth probe (achievable read / copy rate on this device)")
+    result_extra["probe"] = bench_probe(torch, L, stream, timed)
+    log(json.dumps(result_extra["probe"]))
+
     # ---------------------------------------------------------------- CPU baseline
     cpu = None if args.no_cpu else cpu_baseline()
     if cpu is not None:
@@ -261,8 +279,10 @@ def main():
                    "kv": "int8 per (head,token)", "page": 16},
         "roofline": {"bound": "hbm", "kernel": "swiglu_fp8 (amax + encode launches)",
                      "achieved": dom["GBps"], "peak": PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dom["GBps"] / PEAK_GBS, 4), "traffic": None},
+                     "frac": round(dom["GBps"] / PEAK_GBS, 4),
+                     "traffic": SWIGLU_FP8_T512_TRAFFIC},
         "cpu_baseline": cpu,
+        "measured_probe_GBps": result_extra["probe"],
         "decode_us_per_step": decode["graph_us_per_step"],
         "detail": result_extra,
     }
@@ -389,6 +409,27 @@ def bench_multi8(torch, L, randn, cos_t, sin_t, gamma, work, gen, stream, timed,
         out[name + "_us"] = round(timed(fn, 200, 20, sets) * 1e3, 3)
     out["layer_us"] = round(2 * out["add_rmsnorm_fp8_us"] + out["swiglu_fp8_us"] +
                             out["multi_rope_append_int8_us"], 3)
+    return out
+
+
+def bench_probe(torch, L, stream, timed):
+    """Streaming read / copy probe (the reference's kernels_bench.cu pattern):
+    the achievable HBM rate here, and known-size kernels for calibrating the
+    FETCH_SIZE / WRITE_SIZE counters. 32 MB and 512 MB buffers, 4 rotating sets."""
+    out = {}
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    for mb in (32, 512):
+        nb = mb << 20
+        sets = [(torch.ones(nb, dtype=torch.uint8, device="cuda"),
+                 torch.empty(nb, dtype=torch.uint8, device="cuda")) for _ in range(4)]
+        for mode, name, mult in ((2, "read_nt", 1), (3, "copy_nt", 2), (0, "read", 1),
+                                 (1, "copy", 2)):
+            ms = timed(lambda st, m=mode: L.call("granite4_bw_probe", st[0],
+                                                  sink if m in (0, 2) else st[1], nb, m, 2048),
+                       8, 2, sets)
+            out[f"{name}_{mb}MB_GBps"] = round(mult * nb / (ms * 1e-3) / 1e9, 1)
+        del sets
+        torch.cuda.empty_cache()
     return out
 
 

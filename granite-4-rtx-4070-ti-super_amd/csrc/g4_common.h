@@ -15,9 +15,12 @@ constexpr int kMaxVerifyRows = 16;     // model_config.h:56
 constexpr int kMaxHeadDim = 256;       // model_config.h:52
 constexpr int kCUs = 256;              // MI355X compute units
 constexpr int kPersistBlocks = kCUs * 8;  // grid cap for grid-stride kernels
-// Grid cap of the FP8 amax passes: one f32 partial maximum per workgroup, so
-// the FP8 workspace starts with kMaxPartials floats.
+// FP8 workspace layout (f32 words): kMaxPartials per-workgroup partial
+// maxima (the grid cap of the amax passes), then one f32 per row (the norm's
+// 1 / rms handed from pass 1 to the encode pass).
 constexpr int kMaxPartials = 1024;
+__host__ __device__ inline float* work_partials(void* w) { return static_cast<float*>(w); }
+__host__ __device__ inline float* work_row_r(void* w) { return work_partials(w) + kMaxPartials; }
 
 // The calling thread's launch stream (default: the per-thread stream, the
 // reference's --default-stream per-thread build).

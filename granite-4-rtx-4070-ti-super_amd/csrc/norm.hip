@@ -421,8 +421,8 @@ int granite4_add_rmsnorm_fp8(const uint16_t* d_res, const uint16_t* d_branch, fl
   }
   uint16_t* res_out = d_branch != nullptr ? d_res_out : nullptr;
   NormArgs p1{d_res, d_branch, resid_mult, d_w, eps, rows, cols,
-              res_out, nullptr, nullptr, nullptr, static_cast<float*>(d_work), 0,
-              static_cast<float*>(d_work) + kMaxPartials, 0.0};
+              res_out, nullptr, nullptr, nullptr, work_partials(d_work), 0,
+              work_row_r(d_work), 0.0};
   if (launch_norm<kOutAmax>(p1, "granite4_add_rmsnorm_fp8 (amax)") != 0) return -1;
   // Pass 2 reads the stored residual when there is one (it may alias d_res).
   NormArgs p2 = p1;

@@ -244,13 +244,13 @@ int granite4_swiglu_fp8(const uint16_t* d_gu, int rows, int I, uint8_t* d_codes,
   const unsigned grid = grid_for(static_cast<long long>(rows) * (I / 8), kMaxPartials);
   SwArgs p1 = sw_args(d_gu, rows, I);
   p1.act = d_act;
-  p1.partials = static_cast<float*>(d_work);
+  p1.partials = work_partials(d_work);
   hipLaunchKernelGGL((swiglu_kernel<kOutAmax, false>), grid, kBlock, 0, stream(), p1);
   if (launch_status("granite4_swiglu_fp8 (amax)") != 0) return -1;
   SwArgs p2 = sw_args(d_gu, rows, I);
   p2.codes = d_codes;
   p2.scale_out = d_scale;
-  p2.partials = static_cast<float*>(d_work);
+  p2.partials = work_partials(d_work);
   p2.n_partials = static_cast<int>(grid);
   if (d_act != nullptr) {
     // Pass 1 stored the bf16 act: pass 2 only encodes it (2 B read instead

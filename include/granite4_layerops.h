@@ -309,6 +309,7 @@ int granite4_bw_probe(const void* src, void* dst, size_t bytes, int mode, int bl
 int granite4_selftest_bf16(unsigned long long* d_result);
 int granite4_selftest_fp8(float scale, unsigned long long* d_result);
 
+
 #ifdef __cplusplus
 }  /* extern "C" */
 

@@ -170,7 +170,7 @@ def _fp8_check(codes, scale, normed_bf16):
     np.testing.assert_array_equal(codes, want_codes)
 
 
-@pytest.mark.parametrize("rows", [1, 8, 512, 3000])
+@pytest.mark.parametrize("rows", [1, 8, 512, 2048, 3000])
 def test_add_rmsnorm_fp8(rows):
     note(f"add_rmsnorm_fp8 rows={rows}")
     cols = 4096
@@ -218,7 +218,7 @@ def test_add_rmsnorm_fp8_zero_tensor_and_no_residual():
 
 
 # ----------------------------------------------------------------------------- swiglu
-@pytest.mark.parametrize("rows", [1, 8, 64])
+@pytest.mark.parametrize("rows", [1, 8, 64, 2048, 2700])
 def test_swiglu_bf16_and_fp8(rows):
     note(f"swiglu rows={rows}")
     I_ = 12800
