@@ -56,22 +56,11 @@ struct NormArgs {
   double inv_nvec;    // 1 / (cols / 8)
 };
 
-struct Fp8Scale {
-  float s, inv;
-  bool fast;
-};
-
-__device__ __forceinline__ Fp8Scale fp8_scale_of(float amax) {
-  Fp8Scale f;
-  f.s = fp8_scale_for(amax);
-  f.fast = fp8_fast_scale(f.s);
-  f.inv = f.fast ? 1.0f / f.s : 0.0f;
-  return f;
-}
+__device__ __forceinline__ Fp8Enc fp8_scale_of(float amax) { return fp8_enc_of(fp8_scale_for(amax)); }
 
 // One row group (4 / WPR rows) of the workgroup; MODE kOutAmax folds into *m.
 template <int VPL, int WPR, int MODE>
-__device__ __forceinline__ void norm_rows(const NormArgs& a, int rg, const Fp8Scale& f, float* m_acc) {
+__device__ __forceinline__ void norm_rows(const NormArgs& a, int rg, const Fp8Enc& f, float* m_acc) {
   constexpr int RPB = 4 / WPR;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -184,7 +173,7 @@ template <int VPL, int WPR, int MODE>
 __global__ __launch_bounds__(kBlock) void norm_kernel(NormArgs a) {
   constexpr int RPB = 4 / WPR;
   const int nrg = (a.rows + RPB - 1) / RPB;
-  Fp8Scale f{0.0f, 0.0f, false};
+  Fp8Enc f = fp8_enc_of(0.0f);
   if (MODE == kOutFp8) {
     f = fp8_scale_of(reduce_partials(a.partials, a.n_partials));
     if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = f.s;
@@ -199,56 +188,60 @@ __global__ __launch_bounds__(kBlock) void norm_kernel(NormArgs a) {
 // recomputed bit-identically without a row reduction, and the pass streams
 // at full occupancy. x is re-read with cached loads: pass 1 wrote it just
 // before (it is usually still in the Infinity Cache).
-__global__ __launch_bounds__(kBlock) void norm_encode_kernel(NormArgs a) {
+template <bool FAST>
+__device__ __forceinline__ void norm_encode_sweep(const NormArgs& a, const Fp8Enc& f) {
   const int nvec = a.cols >> 3;
   const int total = a.rows * nvec;
   const int step = gridDim.x * kBlock;
-  const Fp8Scale f = fp8_scale_of(reduce_partials(a.partials, a.n_partials));
-  if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = f.s;
   constexpr int U = 4;  // vectors in flight per lane
   for (int v0 = blockIdx.x * kBlock + threadIdx.x; v0 < total; v0 += U * step) {
-    V8 x[U], w[U];
+    V8 x[U], w[U], b[U];
     float r[U];
+    // All loads first, unconditionally (indices past the end clamped to the
+    // last vector, whose codes are then not stored), so they overlap.
 #pragma unroll
     for (int k = 0; k < U; ++k) {
-      const int v = v0 + k * step;
-      if (v >= total) break;
+      const int v = min(v0 + k * step, total - 1);
       const int row = div_fast(v, nvec, a.inv_nvec);
-      const int c = v - row * nvec;
       const size_t off = 8ull * static_cast<unsigned>(v);
       x[k] = ld8(a.x + off);
-      if (a.branch != nullptr) {
-        const V8 b = ld8_nt(a.branch + off);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          x[k].w[e] = pack_bf16_hw(lo_bf16(x[k].w[e]) + a.mult * lo_bf16(b.w[e]),
-                                   hi_bf16(x[k].w[e]) + a.mult * hi_bf16(b.w[e]));
-      }
-      w[k] = ld8(a.w + 8 * c);
+      if (a.branch != nullptr) b[k] = ld8_nt(a.branch + off);
+      w[k] = ld8(a.w + 8 * (v - row * nvec));
       r[k] = a.row_r[row];
     }
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       const int v = v0 + k * step;
       if (v >= total) break;
-      uint32_t cw[2] = {0u, 0u};
+      if (a.branch != nullptr) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t y = pack_bf16_hw(lo_bf16(x[k].w[e]) * r[k] * lo_bf16(w[k].w[e]),
-                                        hi_bf16(x[k].w[e]) * r[k] * hi_bf16(w[k].w[e]));
-        cw[e >> 1] |= fp8x2_encode_scaled(lo_bf16(y), hi_bf16(y), f.s, f.inv, f.fast)
-                      << (16 * (e & 1));
+        for (int e = 0; e < 4; ++e)
+          x[k].w[e] = pack_bf16_hw(lo_bf16(x[k].w[e]) + a.mult * lo_bf16(b[k].w[e]),
+                                   hi_bf16(x[k].w[e]) + a.mult * hi_bf16(b[k].w[e]));
       }
-      st_u32x2_nt(a.codes + 8ull * static_cast<unsigned>(v), cw[0], cw[1]);
+      uint32_t y[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        y[e] = pack_bf16_hw(lo_bf16(x[k].w[e]) * r[k] * lo_bf16(w[k].w[e]),
+                            hi_bf16(x[k].w[e]) * r[k] * hi_bf16(w[k].w[e]));
+      const uint2 c = fp8x8_encode_bf16<FAST>(y, f);
+      st_u32x2_nt(a.codes + 8ull * static_cast<unsigned>(v), c.x, c.y);
     }
   }
+}
+
+__global__ __launch_bounds__(kBlock) void norm_encode_kernel(NormArgs a) {
+  const Fp8Enc f = fp8_scale_of(reduce_partials(a.partials, a.n_partials));
+  if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = f.s;
+  if (f.fast) norm_encode_sweep<true>(a, f);
+  else norm_encode_sweep<false>(a, f);
 }
 
 // Any-shape fallback: one workgroup per row, element loops, two passes over
 // the row (the second re-reads it from cache). Same arithmetic and reduction
 // order as above at the wave level.
 template <int MODE>
-__device__ void norm_generic_row(const NormArgs& a, int row, const Fp8Scale& f, float* m_acc) {
+__device__ void norm_generic_row(const NormArgs& a, int row, const Fp8Enc& f, float* m_acc) {
   const size_t base = static_cast<size_t>(row) * static_cast<size_t>(a.cols);
   auto load_x = [&](int c) {
     const float x = bf16_to_f32(a.x[base + c]);
@@ -294,7 +287,7 @@ __device__ void norm_generic_row(const NormArgs& a, int row, const Fp8Scale& f, 
 
 template <int MODE>
 __global__ __launch_bounds__(kBlock) void norm_generic_kernel(NormArgs a) {
-  Fp8Scale f{0.0f, 0.0f, false};
+  Fp8Enc f = fp8_enc_of(0.0f);
   if (MODE == kOutFp8) {
     f = fp8_scale_of(reduce_partials(a.partials, a.n_partials));
     if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = f.s;
@@ -304,15 +297,16 @@ __global__ __launch_bounds__(kBlock) void norm_generic_kernel(NormArgs a) {
   if (MODE == kOutAmax) write_partial(a.partials, m);
 }
 
-// Waves per row: more waves per row when there are too few rows to fill the
-// 1024 SIMDs. G4_NORM_WPR=1|4 overrides (benchmark sweeps).
-int pick_wpr(int rows) {
+// Waves per row. Four waves per 4096-wide row (2 vectors per lane, 54-62
+// VGPRs, full occupancy) measured faster than one wave per row (8 vectors per
+// lane, 142-152 VGPRs, 3 waves per SIMD) at every size: T=8192 FP8 70 vs 76 µs,
+// T=32768 bf16 stress 5.62 vs 5.52 TB/s. G4_NORM_WPR=1|4 overrides (sweeps).
+int pick_wpr(int /*rows*/) {
   static const int forced = [] {
     const char* e = std::getenv("G4_NORM_WPR");
     return e ? std::atoi(e) : 0;
   }();
-  if (forced == 1 || forced == 4) return forced;
-  return rows <= 2048 ? 4 : 1;
+  return forced == 1 ? 1 : 4;
 }
 
 // Grid of a norm launch: one workgroup per row group, capped at kMaxPartials

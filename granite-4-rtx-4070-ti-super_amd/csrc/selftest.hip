@@ -31,17 +31,28 @@ __global__ __launch_bounds__(kBlock) void bf16_selftest_kernel(unsigned long lon
 }
 
 // Every non-negative f32 y with y / s <= 470, and its negation: the hardware
-// pair encoder vs the exact software encoder.
+// pair encoder and the octet encoder (y and -y of four consecutive patterns
+// per octet) vs the exact software encoder.
 __global__ __launch_bounds__(kBlock) void fp8_selftest_kernel(float s, uint32_t limit,
                                                               unsigned long long* result) {
   const float inv = 1.0f / s;
+  const Fp8Enc enc = fp8_enc_of(s);
   const uint32_t stride = gridDim.x * kBlock;
-  for (uint32_t bits = blockIdx.x * kBlock + threadIdx.x; bits < limit; bits += stride) {
-    const float y = __builtin_bit_cast(float, bits);
-    const uint32_t hw = fp8x2_encode(y, -y, s, inv);
-    const uint32_t c = fp8_encode_fast(y, s, inv);
-    const uint32_t sw = c | ((c | 0x80u) << 8);
-    if (hw != sw) record(result, bits);
+  for (uint32_t base = 4u * (blockIdx.x * kBlock + threadIdx.x); base < limit; base += 4u * stride) {
+    float y[8];
+    uint32_t sw[2] = {0u, 0u};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t bits = base + k < limit ? base + k : limit - 1u;
+      y[2 * k] = __builtin_bit_cast(float, bits);
+      y[2 * k + 1] = -y[2 * k];
+      const uint32_t c = fp8_encode_fast(y[2 * k], s, inv);
+      const uint32_t pair = c | ((c | 0x80u) << 8);
+      sw[k >> 1] |= pair << (16 * (k & 1));
+      if (fp8x2_encode(y[2 * k], y[2 * k + 1], s, inv) != pair) record(result, bits);
+    }
+    const uint2 hw = fp8x8_encode<true>(y, enc);
+    if (hw.x != sw[0] || hw.y != sw[1]) record(result, base);
   }
 }
 

@@ -45,112 +45,137 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g * sig * u;
 }
 
+// Raw gate and up vectors of one 8-element output vector, as loaded: bf16
+// (one 16-byte load each) or f32 (two 16-byte loads each).
+template <bool F32IN>
+struct GuRaw {
+  V8 g, u;
+};
+template <>
+struct GuRaw<true> {
+  float4 g0, g1, u0, u1;
+};
+
 // Vector v (8 elements) of the [rows][I / 8] output: act offset 8 v, gate
 // offset 8 v + r I (the row stride of gu is 2I), up offset one I further.
-template <bool F32IN, bool NT>
-__device__ __forceinline__ void load_gu(const SwArgs& a, int v, int nv, float* g, float* u,
-                                        long long* out_off) {
+// Loads only: the caller issues all of a step's loads before unpacking any,
+// so they are in flight together.
+template <bool F32IN>
+__device__ __forceinline__ GuRaw<F32IN> load_gu(const SwArgs& a, int v, int nv) {
   const int r = div_fast(v, nv, a.inv_nv);
-  *out_off = 8LL * v;
   const long long gofs = 8LL * v + static_cast<long long>(r) * a.I;
-  if (F32IN) {
+  GuRaw<F32IN> x;
+  if constexpr (F32IN) {
     const float* p = static_cast<const float*>(a.gu) + gofs;
-    const float4 g0 = ld_f4_nt(p);
-    const float4 g1 = ld_f4_nt(p + 4);
-    const float4 u0 = ld_f4_nt(p + a.I);
-    const float4 u1 = ld_f4_nt(p + a.I + 4);
-    g[0] = g0.x; g[1] = g0.y; g[2] = g0.z; g[3] = g0.w;
-    g[4] = g1.x; g[5] = g1.y; g[6] = g1.z; g[7] = g1.w;
-    u[0] = u0.x; u[1] = u0.y; u[2] = u0.z; u[3] = u0.w;
-    u[4] = u1.x; u[5] = u1.y; u[6] = u1.z; u[7] = u1.w;
+    x.g0 = ld_f4_nt(p);
+    x.g1 = ld_f4_nt(p + 4);
+    x.u0 = ld_f4_nt(p + a.I);
+    x.u1 = ld_f4_nt(p + a.I + 4);
   } else {
     const uint16_t* p = static_cast<const uint16_t*>(a.gu) + gofs;
-    const V8 gv = ld8_t<NT>(p);
-    const V8 uv = ld8_t<NT>(p + a.I);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      g[e] = v8_get(gv, e);
-      u[e] = v8_get(uv, e);
-    }
+    x.g = ld8_nt(p);
+    x.u = ld8_nt(p + a.I);
   }
+  return x;
 }
 
-template <int MODE, bool F32IN>
-__global__ __launch_bounds__(kBlock) void swiglu_kernel(SwArgs a) {
+// act of element e (0..7), bf16-rounded, as a packed pair word for e even.
+template <bool F32IN>
+__device__ __forceinline__ uint32_t act_pair(const GuRaw<F32IN>& x, int p) {
+  float g0, g1, u0, u1;
+  if constexpr (F32IN) {
+    const float4& gq = p < 2 ? x.g0 : x.g1;
+    const float4& uq = p < 2 ? x.u0 : x.u1;
+    const bool hi = p & 1;
+    g0 = hi ? gq.z : gq.x;
+    g1 = hi ? gq.w : gq.y;
+    u0 = hi ? uq.z : uq.x;
+    u1 = hi ? uq.w : uq.y;
+  } else {
+    g0 = lo_bf16(x.g.w[p]);
+    g1 = hi_bf16(x.g.w[p]);
+    u0 = lo_bf16(x.u.w[p]);
+    u1 = hi_bf16(x.u.w[p]);
+  }
+  return pack_bf16_hw(silu_mul(g0, u0), silu_mul(g1, u1));
+}
+
+// One grid-stride sweep; FAST selects the FP8 encode form (kOutFp8 only).
+// Each step loads U vectors per lane unconditionally (indices past the end
+// are clamped to the last vector, whose result is then not stored).
+template <int MODE, bool F32IN, bool FAST>
+__device__ __forceinline__ float swiglu_sweep(const SwArgs& a, const Fp8Enc& f) {
   const int nv = a.I >> 3;
   const int total = a.rows * nv;
   const int step = gridDim.x * kBlock;
-  float s = 0.0f, inv = 0.0f;
-  bool fast = false;
-  if (MODE == kOutFp8) {
-    s = fp8_scale_for(reduce_partials(a.partials, a.n_partials));
-    fast = fp8_fast_scale(s);
-    inv = fast ? 1.0f / s : 0.0f;
-    if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = s;
-  }
   float m = 0.0f;
-  constexpr int U = 4;  // vectors (of gate and of up) in flight per lane
+  constexpr int U = 2;  // vectors (of gate and of up) in flight per lane
   for (int v0 = blockIdx.x * kBlock + threadIdx.x; v0 < total; v0 += U * step) {
-    float g[U][8], u[U][8];
-    long long off[U];
+    GuRaw<F32IN> x[U];
 #pragma unroll
-    for (int k = 0; k < U; ++k)
-      if (v0 + k * step < total) load_gu<F32IN, true>(a, v0 + k * step, nv, g[k], u[k], &off[k]);
+    for (int k = 0; k < U; ++k) x[k] = load_gu<F32IN>(a, min(v0 + k * step, total - 1), nv);
 #pragma unroll
     for (int k = 0; k < U; ++k) {
-      if (v0 + k * step >= total) break;
+      const int v = v0 + k * step;
+      if (v >= total) break;
+      const long long off = 8LL * v;
       uint32_t w[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        w[e] = pack_bf16_hw(silu_mul(g[k][2 * e], u[k][2 * e]),
-                            silu_mul(g[k][2 * e + 1], u[k][2 * e + 1]));
+      for (int e = 0; e < 4; ++e) w[e] = act_pair<F32IN>(x[k], e);
       if (MODE == kOutBf16 || (MODE == kOutAmax && a.act != nullptr))
-        st8_nt(a.act + off[k], V8{{w[0], w[1], w[2], w[3]}});
+        st8_nt(a.act + off, V8{{w[0], w[1], w[2], w[3]}});
       if (MODE == kOutAmax) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           m = fmaxf(m, fmaxf(lo_bf16(w[e] & 0x7fff7fffu), hi_bf16(w[e] & 0x7fff7fffu)));
       }
       if (MODE == kOutFp8) {
-        uint32_t c[2] = {0u, 0u};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t pair = fp8x2_encode_scaled(lo_bf16(w[e]), hi_bf16(w[e]), s, inv, fast);
-          c[e >> 1] |= pair << (16 * (e & 1));
-        }
-        st_u32x2_nt(a.codes + off[k], c[0], c[1]);
+        const uint2 c = fp8x8_encode_bf16<FAST>(w, f);
+        st_u32x2_nt(a.codes + off, c.x, c.y);
       }
     }
   }
+  return m;
+}
+
+template <int MODE, bool F32IN>
+__global__ __launch_bounds__(kBlock) void swiglu_kernel(SwArgs a) {
+  if (MODE == kOutFp8) {
+    const Fp8Enc f = fp8_enc_of(fp8_scale_for(reduce_partials(a.partials, a.n_partials)));
+    if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = f.s;
+    if (f.fast) swiglu_sweep<MODE, F32IN, true>(a, f);
+    else swiglu_sweep<MODE, F32IN, false>(a, f);
+    return;
+  }
+  const float m = swiglu_sweep<MODE, F32IN, true>(a, fp8_enc_of(0.0f));
   if (MODE == kOutAmax) write_partial(a.partials, m);
 }
 
 // FP8 encode of a stored bf16 [rows][I] tensor under the per-tensor scale
 // from the pass-1 partials (8 elements per lane per step, two steps in flight).
-__global__ __launch_bounds__(kBlock) void encode_bf16_kernel(SwArgs a) {
+template <bool FAST>
+__device__ __forceinline__ void encode_bf16_sweep(const SwArgs& a, const Fp8Enc& f) {
   constexpr int U = 4;  // vectors in flight per lane
   const int total = a.rows * (a.I >> 3);
   const int step = gridDim.x * kBlock;
-  const float s = fp8_scale_for(reduce_partials(a.partials, a.n_partials));
-  const bool fast = fp8_fast_scale(s);
-  const float inv = fast ? 1.0f / s : 0.0f;
-  if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = s;
   for (int v0 = blockIdx.x * kBlock + threadIdx.x; v0 < total; v0 += U * step) {
     V8 x[U];
 #pragma unroll
-    for (int k = 0; k < U; ++k)
-      if (v0 + k * step < total) x[k] = ld8_nt(a.act_in + 8LL * (v0 + k * step));
+    for (int k = 0; k < U; ++k) x[k] = ld8_nt(a.act_in + 8LL * min(v0 + k * step, total - 1));
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       if (v0 + k * step >= total) break;
-      uint32_t c[2] = {0u, 0u};
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        c[e >> 1] |= fp8x2_encode_scaled(lo_bf16(x[k].w[e]), hi_bf16(x[k].w[e]), s, inv, fast)
-                     << (16 * (e & 1));
-      st_u32x2_nt(a.codes + 8LL * (v0 + k * step), c[0], c[1]);
+      const uint2 c = fp8x8_encode_bf16<FAST>(x[k].w, f);
+      st_u32x2_nt(a.codes + 8LL * (v0 + k * step), c.x, c.y);
     }
   }
+}
+
+__global__ __launch_bounds__(kBlock) void encode_bf16_kernel(SwArgs a) {
+  const Fp8Enc f = fp8_enc_of(fp8_scale_for(reduce_partials(a.partials, a.n_partials)));
+  if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = f.s;
+  if (f.fast) encode_bf16_sweep<true>(a, f);
+  else encode_bf16_sweep<false>(a, f);
 }
 
 // Element-wise fallback for I not a multiple of 8 (bf16 / f32 in, bf16 out).
@@ -259,7 +284,11 @@ int granite4_swiglu_fp8(const uint16_t* d_gu, int rows, int I, uint8_t* d_codes,
     hipLaunchKernelGGL(encode_bf16_kernel, grid_for(static_cast<long long>(rows) * (I / 8), kPersistBlocks),
                        kBlock, 0, stream(), p2);
   } else {
-    hipLaunchKernelGGL((swiglu_kernel<kOutFp8, false>), grid, kBlock, 0, stream(), p2);
+    // Pass 2 reads only the partials' count from the grid, not its size:
+    // it runs at full occupancy.
+    hipLaunchKernelGGL((swiglu_kernel<kOutFp8, false>),
+                       grid_for(static_cast<long long>(rows) * (I / 8), kPersistBlocks), kBlock, 0,
+                       stream(), p2);
   }
   return launch_status("granite4_swiglu_fp8 (encode)");
 }

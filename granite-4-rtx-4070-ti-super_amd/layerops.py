@@ -18,7 +18,8 @@ import os
 import torch  # noqa: F401  (loads the HIP runtime first, so the library binds to it)
 
 PKG = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(PKG, "lib", "libgranite4_layerops.so")
+# G4_LAYEROPS_LIB selects another build of the same library (A/B measurements).
+LIB_PATH = os.environ.get("G4_LAYEROPS_LIB") or os.path.join(PKG, "lib", "libgranite4_layerops.so")
 
 FP8_MAX_PARTIALS = 1024
 MAX_VERIFY_ROWS = 16

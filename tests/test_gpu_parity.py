@@ -69,7 +69,7 @@ def test_selftest_bf16_hw_conversion_all_f32():
     assert r[0] == 0, f"{r[0]} mismatches, first input bits {int(r[1]):#010x}"
 
 
-@pytest.mark.parametrize("scale", [1.0, 3.0 / 448, 0.1, 1e-20, 7.7e5, 2.0 ** -90])
+@pytest.mark.parametrize("scale", [1.0, 3.0 / 448, 4.0 / 448, 7.0 / 448, 0.1, 1e-20, 7.7e5, 2.0 ** -90])
 def test_selftest_fp8_hw_encoder_exhaustive(scale):
     note(f"selftest fp8 scale={scale}")
     res = torch.zeros(2, dtype=torch.int64, device="cuda")
