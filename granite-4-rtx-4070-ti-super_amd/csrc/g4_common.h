@@ -7,6 +7,7 @@
 #include <climits>
 #include <cstdint>
 #include <cstdio>
+#include <type_traits>
 
 namespace g4 {
 
@@ -116,6 +117,48 @@ __device__ __forceinline__ int div_fast(int n, int d, double inv_d) {
   const int r = n - q * d;
   q += (r >= d) - (r < 0);
   return q;
+}
+
+// Grid-stride sweep over items [0, total), U items per lane per step (a
+// grid stride apart), all of a step's loads issued before any is used.
+// sweep_begin issues the first step's loads, so a kernel can start them
+// before other work with a long latency (the FP8 encode passes reduce the
+// amax partials meanwhile); sweep_run processes that step and the rest.
+// load(i) returns item i's raw registers; body(i, raw) computes and stores.
+// Loads are unconditional: indices past the end are clamped to total - 1 (a
+// re-read of one cached vector) and body runs only for indices < total.
+// Requires total >= 1.
+template <int U, class Raw>
+struct Sweep {
+  int v0, total, step;
+  Raw x[U];
+};
+
+template <int U, class Load>
+__device__ __forceinline__ auto sweep_begin(int total, Load load) {
+  Sweep<U, decltype(load(0))> s;
+  s.v0 = blockIdx.x * kBlock + threadIdx.x;
+  s.total = total;
+  s.step = gridDim.x * kBlock;
+#pragma unroll
+  for (int k = 0; k < U; ++k) s.x[k] = load(min(s.v0 + k * s.step, total - 1));
+  return s;
+}
+
+template <int U, class Raw, class Load, class Body>
+__device__ __forceinline__ void sweep_run(Sweep<U, Raw>& s, Load load, Body body) {
+  while (s.v0 < s.total) {
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int v = s.v0 + k * s.step;
+      if (v >= s.total) break;
+      body(v, s.x[k]);
+    }
+    s.v0 += U * s.step;
+    if (s.v0 >= s.total) break;
+#pragma unroll
+    for (int k = 0; k < U; ++k) s.x[k] = load(min(s.v0 + k * s.step, s.total - 1));
+  }
 }
 
 }  // namespace g4

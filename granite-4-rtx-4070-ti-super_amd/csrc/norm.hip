@@ -80,8 +80,8 @@ __device__ __forceinline__ void norm_rows(const NormArgs& a, int rg, const Fp8En
     bv[j] = V8{{0u, 0u, 0u, 0u}};
     wv[j] = V8{{0u, 0u, 0u, 0u}};
     if (ok[j]) {
-      // Pass 2 of the FP8 op re-reads res' that pass 1 just wrote: cached
-      // loads, so the Infinity Cache can serve it; every other input streams.
+      // x and branch stream; res' goes out through the caches, where the FP8
+      // op's encode pass re-reads it.
       xv[j] = ld8_nt(a.x + base + 8 * vi);
       if (a.branch != nullptr) bv[j] = ld8_nt(a.branch + base + 8 * vi);
       wv[j] = ld8(a.w + 8 * vi);
@@ -188,53 +188,49 @@ __global__ __launch_bounds__(kBlock) void norm_kernel(NormArgs a) {
 // recomputed bit-identically without a row reduction, and the pass streams
 // at full occupancy. x is re-read with cached loads: pass 1 wrote it just
 // before (it is usually still in the Infinity Cache).
-template <bool FAST>
-__device__ __forceinline__ void norm_encode_sweep(const NormArgs& a, const Fp8Enc& f) {
+struct NormEncRaw {
+  V8 x, b, w;
+  float r;
+};
+
+__global__ __launch_bounds__(kBlock) void norm_encode_kernel(NormArgs a) {
   const int nvec = a.cols >> 3;
-  const int total = a.rows * nvec;
-  const int step = gridDim.x * kBlock;
-  constexpr int U = 4;  // vectors in flight per lane
-  for (int v0 = blockIdx.x * kBlock + threadIdx.x; v0 < total; v0 += U * step) {
-    V8 x[U], w[U], b[U];
-    float r[U];
-    // All loads first, unconditionally (indices past the end clamped to the
-    // last vector, whose codes are then not stored), so they overlap.
+  const auto load = [&](int v) {
+    NormEncRaw t;
+    const int row = div_fast(v, nvec, a.inv_nvec);
+    const size_t off = 8ull * static_cast<unsigned>(v);
+    t.x = ld8(a.x + off);
+    if (a.branch != nullptr) t.b = ld8_nt(a.branch + off);
+    t.w = ld8(a.w + 8 * (v - row * nvec));
+    t.r = a.row_r[row];
+    return t;
+  };
+  auto sw = sweep_begin<4>(a.rows * nvec, load);
+  // The partials' reduction overlaps the first loads.
+  const Fp8Enc f = fp8_scale_of(reduce_partials(a.partials, a.n_partials));
+  if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = f.s;
+  const auto body = [&](auto fast_tag) {
+    return [&, fast_tag](int v, const NormEncRaw& t) {
+      uint32_t x[4];
 #pragma unroll
-    for (int k = 0; k < U; ++k) {
-      const int v = min(v0 + k * step, total - 1);
-      const int row = div_fast(v, nvec, a.inv_nvec);
-      const size_t off = 8ull * static_cast<unsigned>(v);
-      x[k] = ld8(a.x + off);
-      if (a.branch != nullptr) b[k] = ld8_nt(a.branch + off);
-      w[k] = ld8(a.w + 8 * (v - row * nvec));
-      r[k] = a.row_r[row];
-    }
-#pragma unroll
-    for (int k = 0; k < U; ++k) {
-      const int v = v0 + k * step;
-      if (v >= total) break;
+      for (int e = 0; e < 4; ++e) x[e] = t.x.w[e];
       if (a.branch != nullptr) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          x[k].w[e] = pack_bf16_hw(lo_bf16(x[k].w[e]) + a.mult * lo_bf16(b[k].w[e]),
-                                   hi_bf16(x[k].w[e]) + a.mult * hi_bf16(b[k].w[e]));
+          x[e] = pack_bf16_hw(lo_bf16(x[e]) + a.mult * lo_bf16(t.b.w[e]),
+                              hi_bf16(x[e]) + a.mult * hi_bf16(t.b.w[e]));
       }
       uint32_t y[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        y[e] = pack_bf16_hw(lo_bf16(x[k].w[e]) * r[k] * lo_bf16(w[k].w[e]),
-                            hi_bf16(x[k].w[e]) * r[k] * hi_bf16(w[k].w[e]));
-      const uint2 c = fp8x8_encode_bf16<FAST>(y, f);
+        y[e] = pack_bf16_hw(lo_bf16(x[e]) * t.r * lo_bf16(t.w.w[e]),
+                            hi_bf16(x[e]) * t.r * hi_bf16(t.w.w[e]));
+      const uint2 c = fp8x8_encode_bf16<decltype(fast_tag)::value>(y, f);
       st_u32x2_nt(a.codes + 8ull * static_cast<unsigned>(v), c.x, c.y);
-    }
-  }
-}
-
-__global__ __launch_bounds__(kBlock) void norm_encode_kernel(NormArgs a) {
-  const Fp8Enc f = fp8_scale_of(reduce_partials(a.partials, a.n_partials));
-  if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = f.s;
-  if (f.fast) norm_encode_sweep<true>(a, f);
-  else norm_encode_sweep<false>(a, f);
+    };
+  };
+  if (f.fast) sweep_run(sw, load, body(std::true_type{}));
+  else sweep_run(sw, load, body(std::false_type{}));
 }
 
 // Any-shape fallback: one workgroup per row, element loops, two passes over

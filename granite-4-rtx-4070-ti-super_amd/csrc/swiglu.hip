@@ -60,7 +60,7 @@ struct GuRaw<true> {
 // offset 8 v + r I (the row stride of gu is 2I), up offset one I further.
 // Loads only: the caller issues all of a step's loads before unpacking any,
 // so they are in flight together.
-template <bool F32IN>
+template <bool F32IN, bool NT>
 __device__ __forceinline__ GuRaw<F32IN> load_gu(const SwArgs& a, int v, int nv) {
   const int r = div_fast(v, nv, a.inv_nv);
   const long long gofs = 8LL * v + static_cast<long long>(r) * a.I;
@@ -73,8 +73,8 @@ __device__ __forceinline__ GuRaw<F32IN> load_gu(const SwArgs& a, int v, int nv) 
     x.u1 = ld_f4_nt(p + a.I + 4);
   } else {
     const uint16_t* p = static_cast<const uint16_t*>(a.gu) + gofs;
-    x.g = ld8_nt(p);
-    x.u = ld8_nt(p + a.I);
+    x.g = ld8_t<NT>(p);
+    x.u = ld8_t<NT>(p + a.I);
   }
   return x;
 }
@@ -100,82 +100,70 @@ __device__ __forceinline__ uint32_t act_pair(const GuRaw<F32IN>& x, int p) {
   return pack_bf16_hw(silu_mul(g0, u0), silu_mul(g1, u1));
 }
 
-// One grid-stride sweep; FAST selects the FP8 encode form (kOutFp8 only).
-// Each step loads U vectors per lane unconditionally (indices past the end
-// are clamped to the last vector, whose result is then not stored).
-template <int MODE, bool F32IN, bool FAST>
-__device__ __forceinline__ float swiglu_sweep(const SwArgs& a, const Fp8Enc& f) {
-  const int nv = a.I >> 3;
-  const int total = a.rows * nv;
-  const int step = gridDim.x * kBlock;
+// Vectors (of gate and of up) in flight per lane.
+constexpr int kSwU = 2;
+
+// The rest of the grid-stride sweep begun by the kernel; FAST selects the
+// FP8 encode form (kOutFp8 only). Returns the lane's max |act| (kOutAmax).
+template <int MODE, bool F32IN, bool FAST, class S, class Load>
+__device__ __forceinline__ float swiglu_run(const SwArgs& a, const Fp8Enc& f, S& sw, Load load) {
   float m = 0.0f;
-  constexpr int U = 2;  // vectors (of gate and of up) in flight per lane
-  for (int v0 = blockIdx.x * kBlock + threadIdx.x; v0 < total; v0 += U * step) {
-    GuRaw<F32IN> x[U];
+  sweep_run(sw, load, [&](int v, const GuRaw<F32IN>& x) {
+    const long long off = 8LL * v;
+    uint32_t w[4];
 #pragma unroll
-    for (int k = 0; k < U; ++k) x[k] = load_gu<F32IN>(a, min(v0 + k * step, total - 1), nv);
+    for (int e = 0; e < 4; ++e) w[e] = act_pair<F32IN>(x, e);
+    if (MODE == kOutBf16 || (MODE == kOutAmax && a.act != nullptr))
+      st8_nt(a.act + off, V8{{w[0], w[1], w[2], w[3]}});
+    if (MODE == kOutAmax) {
 #pragma unroll
-    for (int k = 0; k < U; ++k) {
-      const int v = v0 + k * step;
-      if (v >= total) break;
-      const long long off = 8LL * v;
-      uint32_t w[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) w[e] = act_pair<F32IN>(x[k], e);
-      if (MODE == kOutBf16 || (MODE == kOutAmax && a.act != nullptr))
-        st8_nt(a.act + off, V8{{w[0], w[1], w[2], w[3]}});
-      if (MODE == kOutAmax) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          m = fmaxf(m, fmaxf(lo_bf16(w[e] & 0x7fff7fffu), hi_bf16(w[e] & 0x7fff7fffu)));
-      }
-      if (MODE == kOutFp8) {
-        const uint2 c = fp8x8_encode_bf16<FAST>(w, f);
-        st_u32x2_nt(a.codes + off, c.x, c.y);
-      }
+      for (int e = 0; e < 4; ++e)
+        m = fmaxf(m, fmaxf(lo_bf16(w[e] & 0x7fff7fffu), hi_bf16(w[e] & 0x7fff7fffu)));
     }
-  }
+    if (MODE == kOutFp8) {
+      const uint2 c = fp8x8_encode_bf16<FAST>(w, f);
+      st_u32x2_nt(a.codes + off, c.x, c.y);
+    }
+  });
   return m;
 }
 
 template <int MODE, bool F32IN>
 __global__ __launch_bounds__(kBlock) void swiglu_kernel(SwArgs a) {
+  const int nv = a.I >> 3;
+  // The FP8 amax pass loads through the caches (the encode pass re-reads
+  // the same gate|up right after it, and part of it is still cached: measured
+  // faster in total); single-pass and final passes stream.
+  constexpr bool kNt = MODE != kOutAmax;
+  const auto load = [&](int v) { return load_gu<F32IN, kNt>(a, v, nv); };
+  auto sw = sweep_begin<kSwU>(a.rows * nv, load);
   if (MODE == kOutFp8) {
+    // The partials' reduction overlaps the first loads.
     const Fp8Enc f = fp8_enc_of(fp8_scale_for(reduce_partials(a.partials, a.n_partials)));
     if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = f.s;
-    if (f.fast) swiglu_sweep<MODE, F32IN, true>(a, f);
-    else swiglu_sweep<MODE, F32IN, false>(a, f);
+    if (f.fast) swiglu_run<MODE, F32IN, true>(a, f, sw, load);
+    else swiglu_run<MODE, F32IN, false>(a, f, sw, load);
     return;
   }
-  const float m = swiglu_sweep<MODE, F32IN, true>(a, fp8_enc_of(0.0f));
+  const float m = swiglu_run<MODE, F32IN, true>(a, fp8_enc_of(0.0f), sw, load);
   if (MODE == kOutAmax) write_partial(a.partials, m);
 }
 
 // FP8 encode of a stored bf16 [rows][I] tensor under the per-tensor scale
-// from the pass-1 partials (8 elements per lane per step, two steps in flight).
-template <bool FAST>
-__device__ __forceinline__ void encode_bf16_sweep(const SwArgs& a, const Fp8Enc& f) {
-  constexpr int U = 4;  // vectors in flight per lane
-  const int total = a.rows * (a.I >> 3);
-  const int step = gridDim.x * kBlock;
-  for (int v0 = blockIdx.x * kBlock + threadIdx.x; v0 < total; v0 += U * step) {
-    V8 x[U];
-#pragma unroll
-    for (int k = 0; k < U; ++k) x[k] = ld8_nt(a.act_in + 8LL * min(v0 + k * step, total - 1));
-#pragma unroll
-    for (int k = 0; k < U; ++k) {
-      if (v0 + k * step >= total) break;
-      const uint2 c = fp8x8_encode_bf16<FAST>(x[k].w, f);
-      st_u32x2_nt(a.codes + 8LL * (v0 + k * step), c.x, c.y);
-    }
-  }
-}
-
+// from the pass-1 partials (8 elements per lane per step, four steps in flight).
 __global__ __launch_bounds__(kBlock) void encode_bf16_kernel(SwArgs a) {
+  const auto load = [&](int v) { return ld8_nt(a.act_in + 8LL * v); };
+  auto sw = sweep_begin<4>(a.rows * (a.I >> 3), load);
   const Fp8Enc f = fp8_enc_of(fp8_scale_for(reduce_partials(a.partials, a.n_partials)));
   if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = f.s;
-  if (f.fast) encode_bf16_sweep<true>(a, f);
-  else encode_bf16_sweep<false>(a, f);
+  const auto body = [&](auto fast_tag) {
+    return [&, fast_tag](int v, const V8& x) {
+      const uint2 c = fp8x8_encode_bf16<decltype(fast_tag)::value>(x.w, f);
+      st_u32x2_nt(a.codes + 8LL * v, c.x, c.y);
+    };
+  };
+  if (f.fast) sweep_run(sw, load, body(std::true_type{}));
+  else sweep_run(sw, load, body(std::false_type{}));
 }
 
 // Element-wise fallback for I not a multiple of 8 (bf16 / f32 in, bf16 out).
