@@ -5,9 +5,13 @@
 #include "g4_math.h"
 #include "granite4_layerops.h"
 
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <map>
+#include <mutex>
+#include <utility>
 #include <vector>
 
 namespace g4 {
@@ -29,6 +33,35 @@ int launch_status(const char* what) {
     return -1;
   }
   return 0;
+}
+
+namespace {
+std::atomic<int> g_fp8_mode{[] {
+  const char* e = std::getenv("G4_FP8_SINGLE_LAUNCH");
+  return e != nullptr && e[0] == '0' ? 1 : 0;
+}()};
+}  // namespace
+
+int fp8_launch_mode() { return g_fp8_mode.load(std::memory_order_relaxed); }
+
+int resident_blocks(const void* kernel, int threads) {
+  static std::mutex mu;
+  static std::map<std::pair<int, const void*>, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_pair(dev, kernel);
+  const auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  const int n = cus > 0 && per_cu > 0 ? cus * per_cu : 0;
+  cache[key] = n;
+  return n;
 }
 
 namespace {
@@ -132,8 +165,13 @@ int granite4_rope_tables_free(float* d_cos, float* d_sin) {
   return ok ? 0 : -1;
 }
 
+int granite4_set_fp8_launch_mode(int mode) {
+  if (mode != 0 && mode != 1) return -1;
+  return g_fp8_mode.exchange(mode);
+}
+
 size_t granite4_fp8_work_bytes(int rows) {
-  return 4u * (static_cast<size_t>(kMaxPartials) + static_cast<size_t>(rows > 0 ? rows : 0));
+  return kWorkRowOff + 4u * static_cast<size_t>(rows > 0 ? rows : 0);
 }
 
 int granite4_row_table(const int32_t* block_table, int n, int page, int32_t* out) {

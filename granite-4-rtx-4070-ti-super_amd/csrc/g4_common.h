@@ -16,12 +16,28 @@ constexpr int kMaxVerifyRows = 16;     // model_config.h:56
 constexpr int kMaxHeadDim = 256;       // model_config.h:52
 constexpr int kCUs = 256;              // MI355X compute units
 constexpr int kPersistBlocks = kCUs * 8;  // grid cap for grid-stride kernels
-// FP8 workspace layout (f32 words): kMaxPartials per-workgroup partial
-// maxima (the grid cap of the amax passes), then one f32 per row (the norm's
-// 1 / rms handed from pass 1 to the encode pass).
+// FP8 workspace layout (bytes):
+//   [0, 4096)          f32 partial maxima of the two-launch form's amax pass
+//                      (its grid is capped at kMaxPartials)
+//   [4096, 12288)      u64 tagged slots of the single-launch form's grid
+//                      maximum (one per workgroup, at most kMaxPartials)
+//   [12288, 12544)     u32 generation word of those slots (+ padding)
+//   [12544, ...)       f32 per row: the norm's 1 / rms from pass 1 to pass 2
+// The slots and the generation word must start zero-filled.
 constexpr int kMaxPartials = 1024;
+constexpr size_t kWorkSlotsOff = 4096;
+constexpr size_t kWorkGenOff = kWorkSlotsOff + 8 * kMaxPartials;
+constexpr size_t kWorkRowOff = kWorkGenOff + 256;
 __host__ __device__ inline float* work_partials(void* w) { return static_cast<float*>(w); }
-__host__ __device__ inline float* work_row_r(void* w) { return work_partials(w) + kMaxPartials; }
+__host__ __device__ inline unsigned long long* work_slots(void* w) {
+  return reinterpret_cast<unsigned long long*>(static_cast<char*>(w) + kWorkSlotsOff);
+}
+__host__ __device__ inline unsigned* work_gen(void* w) {
+  return reinterpret_cast<unsigned*>(static_cast<char*>(w) + kWorkGenOff);
+}
+__host__ __device__ inline float* work_row_r(void* w) {
+  return reinterpret_cast<float*>(static_cast<char*>(w) + kWorkRowOff);
+}
 
 // The calling thread's launch stream (default: the per-thread stream, the
 // reference's --default-stream per-thread build).
@@ -30,6 +46,16 @@ hipStream_t stream();
 // Reports a failed launch (or a sticky device error) like the reference's
 // G4_CUDA_CHECK: message on stderr, -1 to the caller.
 int launch_status(const char* what);
+
+// How many workgroups of `threads` threads of `kernel` the current device
+// holds at once (occupancy per CU x CUs); 0 if the query fails. The
+// single-launch FP8 forms launch at most this many, so that every workgroup
+// is resident for the grid synchronisation. Cached per (device, kernel).
+int resident_blocks(const void* kernel, int threads);
+
+// Process-wide FP8 launch mode (granite4_set_fp8_launch_mode): 0 = single
+// launch where the tensor fits, 1 = always two launches.
+int fp8_launch_mode();
 
 inline bool fits_int(long long v) { return v >= 0 && v <= INT_MAX; }
 

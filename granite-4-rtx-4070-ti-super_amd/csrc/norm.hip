@@ -33,6 +33,7 @@
 #include <cstdlib>
 
 static_assert(g4::kMaxPartials == GRANITE4_FP8_MAX_PARTIALS, "workspace layout");
+static_assert(GRANITE4_FP8_WORK_BYTES(0) == g4::kWorkRowOff, "workspace layout");
 
 namespace g4 {
 namespace {

@@ -19,8 +19,11 @@
 #include "g4_common.h"
 #include "g4_hw.h"
 #include "g4_math.h"
+#include "g4_sync.h"
 #include "g4_wave.h"
 #include "granite4_layerops.h"
+
+#include <type_traits>
 
 namespace g4 {
 namespace {
@@ -166,6 +169,69 @@ __global__ __launch_bounds__(kBlock) void encode_bf16_kernel(SwArgs a) {
   else sweep_run(sw, load, body(std::false_type{}));
 }
 
+// Single-launch FP8 form: one workgroup of kFusedThreads per CU (at most
+// the resident count), each lane holding up to kFusedVpt vectors of act in
+// VGPRs; the workgroups agree on max |act| with one grid synchronisation and
+// encode what they hold. HBM traffic is the algorithmic 4 B read + 1 B
+// written per element (+2 B with the optional bf16 act), against 9 B for
+// the two-launch form, and one launch instead of two.
+constexpr int kFusedThreads = 1024;
+constexpr int kFusedVpt = 4;
+
+__global__ __launch_bounds__(kFusedThreads) void swiglu_fp8_fused_kernel(SwArgs a, GridSync gs) {
+  const unsigned tag = grid_sync_tag(gs);
+  const int nv = a.I >> 3;
+  const int total = a.rows * nv;
+  const int step = gridDim.x * kFusedThreads;
+  const int v0 = blockIdx.x * kFusedThreads + threadIdx.x;
+  GuRaw<false> x[kFusedVpt];
+#pragma unroll
+  for (int k = 0; k < kFusedVpt; ++k) x[k] = load_gu<false, true>(a, min(v0 + k * step, total - 1), nv);
+  uint32_t w[kFusedVpt][4];
+  float m = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kFusedVpt; ++k) {
+    const int v = v0 + k * step;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) w[k][e] = act_pair<false>(x[k], e);
+    if (v < total) {
+      if (a.act != nullptr) st8_nt(a.act + 8LL * v, V8{{w[k][0], w[k][1], w[k][2], w[k][3]}});
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        m = fmaxf(m, fmaxf(lo_bf16(w[k][e] & 0x7fff7fffu), hi_bf16(w[k][e] & 0x7fff7fffu)));
+    }
+  }
+  const Fp8Enc f = fp8_enc_of(fp8_scale_for(grid_max(m, gs, tag)));
+  if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = f.s;
+  const auto encode = [&](auto fast_tag) {
+#pragma unroll
+    for (int k = 0; k < kFusedVpt; ++k) {
+      const int v = v0 + k * step;
+      if (v >= total) break;
+      const uint2 c = fp8x8_encode_bf16<decltype(fast_tag)::value>(w[k], f);
+      st_u32x2_nt(a.codes + 8LL * v, c.x, c.y);
+    }
+  };
+  if (f.fast) encode(std::true_type{});
+  else encode(std::false_type{});
+}
+
+// Grid of the single-launch form for `vectors` 8-element vectors, or 0 when
+// the tensor does not fit the resident grid's registers.
+unsigned fused_grid(long long vectors) {
+  if (fp8_launch_mode() != 0) return 0;
+  const int resident = resident_blocks(reinterpret_cast<const void*>(swiglu_fp8_fused_kernel),
+                                       kFusedThreads);
+  const int cap = resident < kMaxPartials ? resident : kMaxPartials;
+  const long long per_block = static_cast<long long>(kFusedThreads) * kFusedVpt;
+  const long long need = (vectors + per_block - 1) / per_block;
+  if (cap <= 0 || need > cap) return 0;
+  // As many workgroups as CUs (up to the resident count) spread the loads.
+  const long long lanes = (vectors + kFusedThreads - 1) / kFusedThreads;
+  const long long want = lanes < kCUs ? lanes : kCUs;
+  return static_cast<unsigned>(want > need ? (want < cap ? want : cap) : need);
+}
+
 // Element-wise fallback for I not a multiple of 8 (bf16 / f32 in, bf16 out).
 template <bool F32IN>
 __global__ __launch_bounds__(kBlock) void swiglu_scalar_kernel(SwArgs a) {
@@ -254,7 +320,18 @@ int granite4_swiglu_fp8(const uint16_t* d_gu, int rows, int I, uint8_t* d_codes,
     std::fprintf(stderr, "granite4: granite4_swiglu_fp8: invalid arguments (I %% 8 == 0)\n");
     return -1;
   }
-  const unsigned grid = grid_for(static_cast<long long>(rows) * (I / 8), kMaxPartials);
+  const long long vectors = static_cast<long long>(rows) * (I / 8);
+  const unsigned fgrid = fused_grid(vectors);
+  if (fgrid != 0) {
+    SwArgs f = sw_args(d_gu, rows, I);
+    f.act = d_act;
+    f.codes = d_codes;
+    f.scale_out = d_scale;
+    const GridSync gs{work_slots(d_work), work_gen(d_work)};
+    hipLaunchKernelGGL(swiglu_fp8_fused_kernel, fgrid, kFusedThreads, 0, stream(), f, gs);
+    return launch_status("granite4_swiglu_fp8");
+  }
+  const unsigned grid = grid_for(vectors, kMaxPartials);
   SwArgs p1 = sw_args(d_gu, rows, I);
   p1.act = d_act;
   p1.partials = work_partials(d_work);

@@ -77,6 +77,7 @@ _SIG = {
     "granite4_rope_append_at_pos": [P, P, P, P, P, I, P, P, I, I, I, I, I, P, P, P, P, P, I],
     "granite4_row_table": [P, I, I, P],
     "granite4_fp8_work_bytes": [I],
+    "granite4_set_fp8_launch_mode": [I],
     "granite4_host_fp8_encode": [P, _c.c_size_t, F, P],
     "granite4_host_kv_codes": [P, _c.c_size_t, F, I, P],
     "granite4_selftest_bf16": [P],
@@ -117,6 +118,15 @@ def use_stream(stream=None):
     _lib.granite4_set_stream(stream.cuda_stream)
 
 
+def set_fp8_launch_mode(mode):
+    """granite4_set_fp8_launch_mode: 0 = single launch where it fits, 1 = two
+    launches. Returns the previous mode."""
+    prev = _lib.granite4_set_fp8_launch_mode(mode)
+    if prev < 0:
+        raise ValueError(f"FP8 launch mode {mode}")
+    return prev
+
+
 def device_arch():
     buf = _c.create_string_buffer(64)
     if _lib.granite4_device_arch(buf, 64) != 0:
@@ -152,11 +162,13 @@ def add_rmsnorm(res, branch, w, eps, resid_mult=1.0, res_out=None, normed=None):
 
 
 def fp8_work_bytes(rows):
-    return 4 * (FP8_MAX_PARTIALS + rows)
+    """GRANITE4_FP8_WORK_BYTES(rows): partials, grid-sync slots, per-row 1/rms."""
+    return 12544 + 4 * rows
 
 
 def fp8_workspace(rows=65536, device="cuda"):
-    """Workspace for the FP8 ops on tensors of up to `rows` rows."""
+    """Workspace for the FP8 ops on tensors of up to `rows` rows (zero-filled,
+    as the single-launch forms' synchronisation slots require)."""
     return torch.zeros(fp8_work_bytes(rows), dtype=torch.uint8, device=device)
 
 

@@ -224,15 +224,25 @@ int granite4_add_rmsnorm(const uint16_t* d_res, const uint16_t* d_branch, float 
 /* As granite4_add_rmsnorm, with the normed output as FP8 e4m3 codes under one
  * per-tensor scale: scale = float(amax / 448) over all |normed| (bf16 values),
  * code = RNE_e4m3(normed / scale) (the reference's weight quantiser
- * gpu_pack.cc:44-51, 296-308 applied to the bf16 normed tensor). Two launches
+ * gpu_pack.cc:44-51, 296-308 applied to the bf16 normed tensor). One launch
+ * when the tensor fits in the registers of one resident grid (its workgroups
+ * meet once to agree on the maximum), otherwise two launches
  * (amax, then encode). d_work: caller-owned device workspace of at least
  * GRANITE4_FP8_WORK_BYTES(rows) bytes (= granite4_fp8_work_bytes(rows)): the
- * first launch's per-workgroup partial maxima and per-row 1 / rms for the
- * second. No initialisation is needed. Calls that share one workspace must be
- * ordered on one stream. */
+ * two-launch form's per-workgroup partial maxima and per-row 1 / rms, and
+ * the single-launch form's synchronisation slots. Zero-fill it once after
+ * allocating it; the ops keep it valid from then on. Calls that share one
+ * workspace must be ordered on one stream. */
 #define GRANITE4_FP8_MAX_PARTIALS 1024
-#define GRANITE4_FP8_WORK_BYTES(rows) (4 * (GRANITE4_FP8_MAX_PARTIALS + (rows)))
+#define GRANITE4_FP8_WORK_BYTES(rows) (12544 + 4 * (rows))
 size_t granite4_fp8_work_bytes(int rows);
+/* FP8 launch form for granite4_add_rmsnorm_fp8 / granite4_swiglu_fp8, process
+ * wide: 0 (default) = one launch when the tensor fits the registers of one
+ * resident grid, else two; 1 = always two launches (also selected at load by
+ * the environment variable G4_FP8_SINGLE_LAUNCH=0). Both forms give identical
+ * codes and scales. Returns the previous mode, -1 for another value. No
+ * reference counterpart (a tuning switch). */
+int granite4_set_fp8_launch_mode(int mode);
 int granite4_add_rmsnorm_fp8(const uint16_t* d_res, const uint16_t* d_branch, float resid_mult,
                              const uint16_t* d_w, float eps, int rows, int cols,
                              uint16_t* d_res_out, uint8_t* d_codes, float* d_scale,

@@ -218,7 +218,9 @@ def test_add_rmsnorm_fp8_zero_tensor_and_no_residual():
 
 
 # ----------------------------------------------------------------------------- swiglu
-@pytest.mark.parametrize("rows", [1, 8, 64, 2048, 2700])
+# 655 rows of I = 12800 are the largest the single-launch form holds on 256
+# CUs (1024 lanes x 4 vectors each); 656 and up take two launches.
+@pytest.mark.parametrize("rows", [1, 8, 64, 655, 656, 2048, 2700])
 def test_swiglu_bf16_and_fp8(rows):
     note(f"swiglu rows={rows}")
     I_ = 12800
@@ -243,6 +245,60 @@ def test_swiglu_bf16_and_fp8(rows):
     L.call("granite4_swiglu_fp8", d_gu, rows, I_, codes2, scale2, work, None)
     np.testing.assert_array_equal(host(codes2), host(codes))
     assert host(scale2)[0] == host(scale)[0]
+    # the two-launch form gives the same codes and scale
+    prev = L.set_fp8_launch_mode(1)
+    try:
+        codes3 = torch.empty_like(codes)
+        scale3 = torch.empty_like(scale)
+        L.call("granite4_swiglu_fp8", d_gu, rows, I_, codes3, scale3, work, None)
+    finally:
+        L.set_fp8_launch_mode(prev)
+    np.testing.assert_array_equal(host(codes3), host(codes))
+    assert host(scale3)[0] == host(scale)[0]
+
+
+def test_swiglu_fp8_single_launch_repeated_and_graph_replay():
+    """Back-to-back single-launch calls on one workspace (the synchronisation
+    slots are reused through the generation word), then a captured graph
+    replayed several times with new inputs written between replays: every
+    result equals an eager call on the same inputs."""
+    note("swiglu_fp8 repeated + graph")
+    rows, I_ = 96, 12800
+    work = L.fp8_workspace()
+    gus = [dev(ol.normal_bf16(0xC7 + i, 0.0, 1.0 + i, rows * 2 * I_).reshape(rows, 2 * I_))
+           for i in range(4)]
+    codes = torch.empty((rows, I_), dtype=torch.uint8, device="cuda")
+    scale = torch.empty(1, dtype=torch.float32, device="cuda")
+    want = []
+    for g in gus:
+        L.call("granite4_swiglu_fp8", g, rows, I_, codes, scale, work, None)
+        want.append((host(codes).copy(), host(scale)[0]))
+        act = torch.empty((rows, I_), dtype=torch.int16, device="cuda")
+        L.call("granite4_swiglu", g, rows, I_, act)
+        _fp8_check(want[-1][0], want[-1][1], host(act))
+    # repeated calls alternate inputs of different scales on one workspace
+    for i in (1, 0, 3, 2):
+        L.call("granite4_swiglu_fp8", gus[i], rows, I_, codes, scale, work, None)
+        np.testing.assert_array_equal(host(codes), want[i][0])
+        assert host(scale)[0] == want[i][1]
+    src = torch.empty_like(gus[0])
+    src.copy_(gus[0])
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    L.use_stream(s)
+    try:
+        with torch.cuda.graph(g, stream=s):
+            L.call("granite4_swiglu_fp8", src, rows, I_, codes, scale, work, None)
+    finally:
+        L.call("granite4_set_stream", None)  # back to the per-thread default stream
+    for i in (2, 1, 3, 0, 2):
+        src.copy_(gus[i])
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(host(codes), want[i][0])
+        assert host(scale)[0] == want[i][1]
 
 
 def test_prefill_silu_mul_f32():
