@@ -46,13 +46,13 @@ B_ROPE = {16: B_ROPE_COMMON + 2 * HK * D * 2,
           "k5v4g32": B_ROPE_COMMON + HK * (80 + 64) + 2 * HK * 4 * 4}
 
 
-# HBM bytes per swiglu_fp8 call at T=512 (both launches), measured with two
-# rocprofv3 --pmc runs of `bench.py --only t512` (FETCH_SIZE, then WRITE_SIZE,
-# KiB per dispatch): fetch (12819.0 + 12877.0) KiB x 2.0 + write (25.0 +
-# 6400.0) KiB x 1.0. The factors are what the same counters read for the
-# known-size copy probe (`bench.py --only probe`): FETCH_SIZE half the bytes,
-# WRITE_SIZE all of them.
-SWIGLU_FP8_T512_TRAFFIC = int((12819.0 + 12877.0) * 2.0 * 1024 + (25.0 + 6400.0) * 1024)
+# HBM bytes per swiglu_fp8 call at T=512 (one launch, swiglu_fp8_fused_kernel),
+# measured with two rocprofv3 --pmc runs of `bench.py --only t512` (FETCH_SIZE,
+# then WRITE_SIZE, KiB per dispatch): fetch 12996.0 KiB x 2.0 + write 6432.1
+# KiB x 1.0. The factors are what the same counters read for the known-size
+# copy probe (`bench.py --only probe`): FETCH_SIZE half the bytes, WRITE_SIZE
+# all of them.
+SWIGLU_FP8_T512_TRAFFIC = int(12996.0 * 2.0 * 1024 + 6432.1 * 1024)
 
 
 def per_launch_extra(op):
@@ -277,7 +277,7 @@ def main():
                                "+ rope_append int8 paged KV",
                    "T": 512, "H": H, "I": I, "Hq": HQ, "Hk": HK, "head_dim": D,
                    "kv": "int8 per (head,token)", "page": 16},
-        "roofline": {"bound": "hbm", "kernel": "swiglu_fp8 (amax + encode launches)",
+        "roofline": {"bound": "hbm", "kernel": "swiglu_fp8 (single launch: swiglu_fp8_fused_kernel)",
                      "achieved": dom["GBps"], "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom["GBps"] / PEAK_GBS, 4),
                      "traffic": SWIGLU_FP8_T512_TRAFFIC},

@@ -27,10 +27,12 @@
 #include "g4_common.h"
 #include "g4_hw.h"
 #include "g4_math.h"
+#include "g4_sync.h"
 #include "g4_wave.h"
 #include "granite4_layerops.h"
 
 #include <cstdlib>
+#include <type_traits>
 
 static_assert(g4::kMaxPartials == GRANITE4_FP8_MAX_PARTIALS, "workspace layout");
 static_assert(GRANITE4_FP8_WORK_BYTES(0) == g4::kWorkRowOff, "workspace layout");
@@ -59,9 +61,22 @@ struct NormArgs {
 
 __device__ __forceinline__ Fp8Enc fp8_scale_of(float amax) { return fp8_enc_of(fp8_scale_for(amax)); }
 
-// One row group (4 / WPR rows) of the workgroup; MODE kOutAmax folds into *m.
-template <int VPL, int WPR, int MODE>
-__device__ __forceinline__ void norm_rows(const NormArgs& a, int rg, const Fp8Enc& f, float* m_acc) {
+// The lane's share of one row of a row group (4 / WPR rows per 256-thread
+// workgroup): res' (x + mult * branch, bf16; stored when res_out is given),
+// the gamma vectors, and the row's r = 1 / rms. Every thread of the
+// workgroup must call it (it synchronises when WPR > 1).
+template <int VPL, int WPR>
+struct NormRow {
+  V8 xv[VPL], wv[VPL];
+  bool ok[VPL];
+  size_t base;
+  int row, part, lane;
+  bool live;
+  float r;
+};
+
+template <int VPL, int WPR>
+__device__ __forceinline__ void norm_row_front(const NormArgs& a, int rg, NormRow<VPL, WPR>& t) {
   constexpr int RPB = 4 / WPR;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -71,8 +86,10 @@ __device__ __forceinline__ void norm_rows(const NormArgs& a, int rg, const Fp8En
   const int nvec = a.cols >> 3;
   const size_t base = live ? static_cast<size_t>(row) * static_cast<size_t>(a.cols) : 0;
 
-  V8 xv[VPL], bv[VPL], wv[VPL];
-  bool ok[VPL];
+  V8 (&xv)[VPL] = t.xv;
+  V8 (&wv)[VPL] = t.wv;
+  bool (&ok)[VPL] = t.ok;
+  V8 bv[VPL];
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     const int vi = (j * WPR + part) * 64 + lane;
@@ -121,7 +138,26 @@ __device__ __forceinline__ void norm_rows(const NormArgs& a, int rg, const Fp8En
     for (int k = 1; k < WPR; ++k) ss += s_part[w0 + k];
     __syncthreads();  // s_part is reused by the next row group
   }
-  const float r = 1.0f / sqrtf(static_cast<float>(ss / a.cols) + a.eps);
+  t.base = base;
+  t.row = row;
+  t.part = part;
+  t.lane = lane;
+  t.live = live;
+  t.r = 1.0f / sqrtf(static_cast<float>(ss / a.cols) + a.eps);
+}
+
+// One row group of the workgroup; MODE kOutAmax folds into *m.
+template <int VPL, int WPR, int MODE>
+__device__ __forceinline__ void norm_rows(const NormArgs& a, int rg, const Fp8Enc& f, float* m_acc) {
+  NormRow<VPL, WPR> t;
+  norm_row_front<VPL, WPR>(a, rg, t);
+  const V8 (&xv)[VPL] = t.xv;
+  const V8 (&wv)[VPL] = t.wv;
+  const bool (&ok)[VPL] = t.ok;
+  const size_t base = t.base;
+  const int row = t.row, part = t.part, lane = t.lane;
+  const bool live = t.live;
+  const float r = t.r;
   if (MODE == kOutAmax && live && part == 0 && lane == 0) a.row_r[row] = r;
 
   if (MODE == kOutBf16) {
@@ -294,6 +330,64 @@ __global__ __launch_bounds__(kBlock) void norm_generic_kernel(NormArgs a) {
   if (MODE == kOutAmax) write_partial(a.partials, m);
 }
 
+// Single-launch FP8 form for tensors that fit one resident grid: each
+// 256-thread workgroup (four waves per row, as the two-launch form's first
+// pass, so y and the amax are bit-identical to it) holds up to kNormHold rows'
+// y = bf16(res' * r * w) in VGPRs, the workgroups agree on max |y| with one
+// grid synchronisation, and each encodes what it holds. HBM traffic: x (+
+// branch) read once, res' and codes written once, against a second read of
+// res' in the two-launch form, and one launch instead of two.
+constexpr int kNormHold = 4;
+
+template <int VPL>
+__global__ __launch_bounds__(kBlock) void norm_fp8_fused_kernel(NormArgs a, GridSync gs) {
+  const unsigned tag = grid_sync_tag(gs);
+  V8 y[kNormHold][VPL];
+  bool ok[kNormHold][VPL];
+  size_t base[kNormHold];
+  int part = 0, lane = 0;
+  float m = 0.0f;
+#pragma unroll
+  for (int h = 0; h < kNormHold; ++h) {
+    const int rg = blockIdx.x + h * gridDim.x;  // uniform over the workgroup
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) ok[h][j] = false;
+    base[h] = 0;
+    if (rg >= a.rows) continue;
+    NormRow<VPL, 4> t;
+    norm_row_front<VPL, 4>(a, rg, t);
+    part = t.part;
+    lane = t.lane;
+    base[h] = t.base;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      ok[h][j] = t.ok[j];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        y[h][j].w[e] = pack_bf16_hw(lo_bf16(t.xv[j].w[e]) * t.r * lo_bf16(t.wv[j].w[e]),
+                                    hi_bf16(t.xv[j].w[e]) * t.r * hi_bf16(t.wv[j].w[e]));
+        m = fmaxf(m, lo_bf16(y[h][j].w[e] & 0x7fff7fffu));
+        m = fmaxf(m, hi_bf16(y[h][j].w[e] & 0x7fff7fffu));
+      }
+    }
+  }
+  const Fp8Enc f = fp8_scale_of(grid_max(m, gs, tag));
+  if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = f.s;
+  const auto encode = [&](auto fast_tag) {
+#pragma unroll
+    for (int h = 0; h < kNormHold; ++h)
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) {
+        if (!ok[h][j]) continue;
+        const uint2 c = fp8x8_encode_bf16<decltype(fast_tag)::value>(y[h][j].w, f);
+        const int vi = (j * 4 + part) * 64 + lane;
+        st_u32x2_nt(a.codes + base[h] + 8 * vi, c.x, c.y);
+      }
+  };
+  if (f.fast) encode(std::true_type{});
+  else encode(std::false_type{});
+}
+
 // Waves per row. Four waves per 4096-wide row (2 vectors per lane, 54-62
 // VGPRs, full occupancy) measured faster than one wave per row (8 vectors per
 // lane, 142-152 VGPRs, 3 waves per SIMD) at every size: T=8192 FP8 70 vs 76 µs,
@@ -350,6 +444,33 @@ int launch_norm(NormArgs& a, const char* what) {
     hipLaunchKernelGGL((norm_generic_kernel<MODE>), grid, kBlock, 0, st, a);
   }
   return launch_status(what);
+}
+
+// Launches the single-launch FP8 form when the shape takes the four-waves-
+// per-row vector path (as the two-launch form would) and the rows fit the
+// resident grid; returns false (nothing launched) otherwise.
+bool launch_norm_fp8_fused(const uint16_t* x, const uint16_t* branch, float mult, const uint16_t* w,
+                           float eps, int rows, int cols, uint16_t* res_out, uint8_t* codes,
+                           float* scale, void* work) {
+  const int nvec = cols / 8;
+  if (fp8_launch_mode() != 0 || !norm_vector_path(rows, cols) || pick_wpr(rows) != 4 ||
+      nvec > 4 * 64 * 4)
+    return false;
+  const void* kern = nvec <= 256   ? reinterpret_cast<const void*>(norm_fp8_fused_kernel<1>)
+                     : nvec <= 512 ? reinterpret_cast<const void*>(norm_fp8_fused_kernel<2>)
+                                   : reinterpret_cast<const void*>(norm_fp8_fused_kernel<4>);
+  const int resident = resident_blocks(kern, kBlock);
+  const int cap = resident < kMaxPartials ? resident : kMaxPartials;
+  if (cap <= 0 || rows > static_cast<long long>(cap) * kNormHold) return false;
+  const unsigned grid = static_cast<unsigned>(rows < cap ? rows : cap);
+  NormArgs a{x, branch, mult, w, eps, rows, cols, res_out, nullptr, codes, scale, nullptr, 0,
+             nullptr, 0.0};
+  const GridSync gs{work_slots(work), work_gen(work)};
+  const hipStream_t st = stream();
+  if (nvec <= 256) hipLaunchKernelGGL(norm_fp8_fused_kernel<1>, grid, kBlock, 0, st, a, gs);
+  else if (nvec <= 512) hipLaunchKernelGGL(norm_fp8_fused_kernel<2>, grid, kBlock, 0, st, a, gs);
+  else hipLaunchKernelGGL(norm_fp8_fused_kernel<4>, grid, kBlock, 0, st, a, gs);
+  return true;
 }
 
 bool norm_args_ok(const void* x, const void* w, float eps, int rows, int cols) {
@@ -411,6 +532,9 @@ int granite4_add_rmsnorm_fp8(const uint16_t* d_res, const uint16_t* d_branch, fl
     return -1;
   }
   uint16_t* res_out = d_branch != nullptr ? d_res_out : nullptr;
+  if (launch_norm_fp8_fused(d_res, d_branch, resid_mult, d_w, eps, rows, cols, res_out, d_codes,
+                            d_scale, d_work))
+    return launch_status("granite4_add_rmsnorm_fp8");
   NormArgs p1{d_res, d_branch, resid_mult, d_w, eps, rows, cols,
               res_out, nullptr, nullptr, nullptr, work_partials(d_work), 0,
               work_row_r(d_work), 0.0};

@@ -169,13 +169,13 @@ __global__ __launch_bounds__(kBlock) void encode_bf16_kernel(SwArgs a) {
   else sweep_run(sw, load, body(std::false_type{}));
 }
 
-// Single-launch FP8 form: one workgroup of kFusedThreads per CU (at most
-// the resident count), each lane holding up to kFusedVpt vectors of act in
+// Single-launch FP8 form: up to kMaxPartials workgroups (at most the
+// resident count), each lane holding up to kFusedVpt vectors of act in
 // VGPRs; the workgroups agree on max |act| with one grid synchronisation and
 // encode what they hold. HBM traffic is the algorithmic 4 B read + 1 B
 // written per element (+2 B with the optional bf16 act), against 9 B for
 // the two-launch form, and one launch instead of two.
-constexpr int kFusedThreads = 1024;
+constexpr int kFusedThreads = kBlock;
 constexpr int kFusedVpt = 4;
 
 __global__ __launch_bounds__(kFusedThreads) void swiglu_fp8_fused_kernel(SwArgs a, GridSync gs) {
@@ -217,7 +217,10 @@ __global__ __launch_bounds__(kFusedThreads) void swiglu_fp8_fused_kernel(SwArgs 
 }
 
 // Grid of the single-launch form for `vectors` 8-element vectors, or 0 when
-// the tensor does not fit the resident grid's registers.
+// the tensor does not fit the resident grid's registers. One vector per lane
+// where the grid allows (up to kMaxPartials workgroups, the slot count):
+// measured against 1024-thread workgroups on one per CU, T=512 14.0 vs
+// 14.8 us and T=8 5.9 vs 7.4 us.
 unsigned fused_grid(long long vectors) {
   if (fp8_launch_mode() != 0) return 0;
   const int resident = resident_blocks(reinterpret_cast<const void*>(swiglu_fp8_fused_kernel),
@@ -226,10 +229,8 @@ unsigned fused_grid(long long vectors) {
   const long long per_block = static_cast<long long>(kFusedThreads) * kFusedVpt;
   const long long need = (vectors + per_block - 1) / per_block;
   if (cap <= 0 || need > cap) return 0;
-  // As many workgroups as CUs (up to the resident count) spread the loads.
   const long long lanes = (vectors + kFusedThreads - 1) / kFusedThreads;
-  const long long want = lanes < kCUs ? lanes : kCUs;
-  return static_cast<unsigned>(want > need ? (want < cap ? want : cap) : need);
+  return static_cast<unsigned>(lanes < cap ? lanes : cap);
 }
 
 // Element-wise fallback for I not a multiple of 8 (bf16 / f32 in, bf16 out).

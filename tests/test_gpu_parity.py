@@ -170,7 +170,9 @@ def _fp8_check(codes, scale, normed_bf16):
     np.testing.assert_array_equal(codes, want_codes)
 
 
-@pytest.mark.parametrize("rows", [1, 8, 512, 2048, 3000])
+# Up to 4096 rows of 4096 take the single-launch form on 256 CUs (1024
+# workgroups x 4 held rows); 4097 takes two launches.
+@pytest.mark.parametrize("rows", [1, 8, 512, 2048, 3000, 4096, 4097])
 def test_add_rmsnorm_fp8(rows):
     note(f"add_rmsnorm_fp8 rows={rows}")
     cols = 4096
@@ -192,11 +194,62 @@ def test_add_rmsnorm_fp8(rows):
     np.testing.assert_array_equal(host(ro), ro_want)
     _fp8_check(host(codes), host(scale)[0], host(no))
     assert ulp_diff(host(no), no_want).max() <= 1
+    # the two-launch form: same residual, codes and scale
+    prev = L.set_fp8_launch_mode(1)
+    try:
+        ro3 = torch.empty_like(d_res)
+        codes3 = torch.empty_like(codes)
+        scale3 = torch.empty_like(scale)
+        L.call("granite4_add_rmsnorm_fp8", d_res, d_br, 1.0, d_w, 1e-5, rows, cols, ro3, codes3,
+               scale3, work)
+    finally:
+        L.set_fp8_launch_mode(prev)
+    np.testing.assert_array_equal(host(ro3), ro_want)
+    np.testing.assert_array_equal(host(codes3), host(codes))
+    assert host(scale3)[0] == host(scale)[0]
     # a second, smaller call on the same workspace
     r2 = max(1, rows // 3)
     L.call("granite4_add_rmsnorm_fp8", d_res, d_br, 1.0, d_w, 1e-5, r2, cols, ro, codes, scale,
            work)
     _fp8_check(host(codes)[:r2], host(scale)[0], host(no)[:r2])
+
+
+def test_add_rmsnorm_fp8_graph_replay():
+    """A captured single-launch add+RMSNorm->FP8 replayed with new inputs
+    between replays (the synchronisation slots advance through the
+    workspace's generation word): every replay equals an eager call."""
+    note("add_rmsnorm_fp8 graph")
+    rows, cols = 200, 4096
+    w = dev(ol.normal_bf16(0xB6, 1.0, 0.1, cols))
+    work = L.fp8_workspace(rows)
+    xs = [dev(_hidden(rows, cols, 0xB7 + i)) for i in range(3)]
+    br = dev(ol.normal_bf16(0xBA, 0.0, 0.5, rows * cols).reshape(rows, cols))
+    ro = torch.empty_like(xs[0])
+    codes = torch.empty((rows, cols), dtype=torch.uint8, device="cuda")
+    scale = torch.empty(1, dtype=torch.float32, device="cuda")
+    want = []
+    for x in xs:
+        L.call("granite4_add_rmsnorm_fp8", x, br, 0.5, w, 1e-5, rows, cols, ro, codes, scale, work)
+        want.append((host(ro).copy(), host(codes).copy(), host(scale)[0]))
+    src = torch.empty_like(xs[0])
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    L.use_stream(s)
+    try:
+        with torch.cuda.graph(g, stream=s):
+            L.call("granite4_add_rmsnorm_fp8", src, br, 0.5, w, 1e-5, rows, cols, ro, codes, scale,
+                   work)
+    finally:
+        L.call("granite4_set_stream", None)
+    for i in (1, 2, 0, 1):
+        src.copy_(xs[i])
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(host(ro), want[i][0])
+        np.testing.assert_array_equal(host(codes), want[i][1])
+        assert host(scale)[0] == want[i][2]
 
 
 def test_add_rmsnorm_fp8_zero_tensor_and_no_residual():
@@ -218,8 +271,8 @@ def test_add_rmsnorm_fp8_zero_tensor_and_no_residual():
 
 
 # ----------------------------------------------------------------------------- swiglu
-# 655 rows of I = 12800 are the largest the single-launch form holds on 256
-# CUs (1024 lanes x 4 vectors each); 656 and up take two launches.
+# 655 rows of I = 12800 are the largest the single-launch form holds (1024
+# workgroups x 256 lanes x 4 vectors); 656 and up take two launches.
 @pytest.mark.parametrize("rows", [1, 8, 64, 655, 656, 2048, 2700])
 def test_swiglu_bf16_and_fp8(rows):
     note(f"swiglu rows={rows}")
