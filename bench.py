@@ -70,7 +70,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline + decode only")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["t512", "t8192", "decode", "t8", "stress", "tN", "probe"],
+    ap.add_argument("--only", choices=["t512", "t8192", "decode", "t8", "stress", "tN", "probe",
+                                       "attn"],
                     help="run one configuration and print its detail (profiling runs)")
     ap.add_argument("--T", type=int, default=1024, help="token count for --only tN")
     args = ap.parse_args()
@@ -219,6 +220,8 @@ def main():
             r = bench_decode(torch, L, randn, cos_t, sin_t, emb, gamma, stream, args)
         elif args.only == "t8":
             r = bench_multi8(torch, L, randn, cos_t, sin_t, gamma, work, gen, stream, timed, args)
+        elif args.only == "attn":
+            r = bench_attn(torch, L, randn, gen, timed, args)
         else:
             r = bench_stress(torch, L, randn, cos_t, sin_t, gamma, stream)
         print(json.dumps({"only": args.only, "detail": r}), flush=True)
@@ -248,6 +251,10 @@ def main():
         log("config 5: bandwidth stress, 40 layers x T=32768, bf16")
         result_extra["stress_T32768"] = bench_stress(torch, L, randn, cos_t, sin_t, gamma, stream)
         log(json.dumps(result_extra["stress_T32768"]))
+
+        log("split-KV decode attention over the paged pool (next row: the KV consumer)")
+        result_extra["attn_decode"] = bench_attn(torch, L, randn, gen, timed, args)
+        log(json.dumps(result_extra["attn_decode"]))
 
     log("bandwidth probe (achievable read / copy rate on this device)")
     result_extra["probe"] = bench_probe(torch, L, stream, timed)
@@ -409,6 +416,82 @@ def bench_multi8(torch, L, randn, cos_t, sin_t, gamma, work, gen, stream, timed,
         out[name + "_us"] = round(timed(fn, 200, 20, sets) * 1e3, 3)
     out["layer_us"] = round(2 * out["add_rmsnorm_fp8_us"] + out["swiglu_fp8_us"] +
                             out["multi_rope_append_int8_us"], 3)
+    return out
+
+
+def kv_bytes_per_position(bits, group):
+    """K row + V row + f32 scales of one KV head at one position."""
+    kb, vb = {16: (256, 256), 8: (128, 128), 4: (64, 64), 5: (80, 64)}[bits]
+    return kb + vb + (0 if bits == 16 else 2 * 4 * (D // group))
+
+
+def bench_attn(torch, L, randn, gen, timed, args):
+    """Split-KV decode attention (granite4_attn_paged) over one layer's paged
+    pool: batch-1 decode at 8K and 32K context (bf16, int8, K5V4 group 32) and
+    8 sessions at positions U[0, 65536) with their own page tables (int8).
+    Algorithmic bytes: the KV rows and scales every query row attends to, plus
+    q, out and the page-table entries. Input sets rotate past the 256 MB
+    Infinity Cache (each layer's KV is cold in a real step)."""
+    dev = "cuda"
+    cases = [("T1_ctx8192_bf16", 1, 8192, 16, 128), ("T1_ctx8192_int8", 1, 8192, 8, 128),
+             ("T1_ctx8192_k5v4g32", 1, 8192, 5, 32), ("T1_ctx32768_int8", 1, 32768, 8, 128),
+             ("T8_sessions_ctx65536_int8", 8, 65536, 8, 128)]
+    out = {}
+    for name, rows, ctx, bits, group in cases:
+        stride = ctx
+        pages = stride // 16
+        kb, vb = {16: (256, 256), 8: (128, 128), 4: (64, 64), 5: (80, 64)}[bits]
+        multi = rows > 1
+        if multi:
+            pos = torch.randint(0, ctx, (rows,), generator=gen, device=dev, dtype=torch.int32)
+        else:
+            pos = torch.tensor([ctx - 1], dtype=torch.int32, device=dev)
+        lens = (pos.cpu().long() + 1)
+        set_bytes = HK * stride * (kb + vb)
+        nsets = max(2, min(8, -(-640 * 2 ** 20 // set_bytes)))
+        sets = []
+        for _ in range(nsets):
+            st = {}
+            if bits == 16:
+                st["k"] = randn((HK * stride * D,), std=0.5)
+                st["v"] = randn((HK * stride * D,))
+                st["ks"] = st["vs"] = None
+            else:
+                st["k"] = torch.randint(0, 256, (HK * stride * kb,), generator=gen, device=dev,
+                                        dtype=torch.uint8)
+                st["v"] = torch.randint(0, 256, (HK * stride * vb,), generator=gen, device=dev,
+                                        dtype=torch.uint8)
+                ng = D // group
+                st["ks"] = torch.rand((HK * stride * ng,), generator=gen, device=dev) * 0.005
+                st["vs"] = torch.rand((HK * stride * ng,), generator=gen, device=dev) * 0.1
+            st["q"] = randn((rows, HQ * D))
+            tables = [(torch.randperm(pages, generator=gen, device=dev).to(torch.int32)[:, None] * 16 +
+                       torch.arange(16, device=dev, dtype=torch.int32)).reshape(-1)
+                      for _ in range(rows if multi else 1)]
+            st["tables"] = tables
+            st["pt"] = None if multi else tables[0]
+            st["row_pos"] = pos if multi else None
+            st["row_pt"] = (torch.tensor([t.data_ptr() for t in tables], dtype=torch.int64,
+                                         device=dev) if multi else None)
+            sets.append(st)
+        d_pos = None if multi else pos
+        scratch = torch.empty(L.call_size("granite4_attn_split_scratch_bytes", HQ, rows, stride),
+                              dtype=torch.uint8, device=dev)
+        o = torch.empty((rows, HQ * D), dtype=torch.bfloat16, device=dev)
+
+        def fn(s):
+            L.call("granite4_attn_paged", s["q"], rows, HQ, HK, D, 1.0 / 128, s["k"], s["v"],
+                   s["ks"], s["vs"], bits, group, stride, 0, d_pos, s["pt"], s["row_pos"],
+                   s["row_pt"], 0, 0, scratch, o)
+
+        ms = timed(fn, 20, 3, sets)
+        kv = int(sum(int(n) for n in lens)) * HK * kv_bytes_per_position(bits, group)
+        b = kv + 2 * rows * HQ * D * 2 + int(sum(int(n) for n in lens)) * 4
+        gbs = b / (ms * 1e-3) / 1e9
+        out[name] = {"us": round(ms * 1e3, 3), "bytes": b, "GBps": round(gbs, 1),
+                     "frac_peak": round(gbs / PEAK_GBS, 4), "sets": nsets}
+        del sets, scratch
+        torch.cuda.empty_cache()
     return out
 
 

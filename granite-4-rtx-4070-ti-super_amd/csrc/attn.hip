@@ -1,0 +1,621 @@
+// attn.hip - split-KV decode attention over the paged KV pool, gfx950.
+//
+// The reference's attn_split (attention_split.cu:1083-1255; its default
+// tensor-core kernel :791-1047 and attn_combine_kernel :1049-1074): causal
+// GQA for up to 16 query rows, head dim 128, Hq = 4 Hk, reading the pool
+// written by the append kernels (bf16, int8, int4, or K5 K + int4 V, with
+// per-row or per-group f32 scales) through a position -> arena-row table.
+//
+// Work split: positions are cut into 64-position tiles and the tiles into
+// splits of tps tiles (tps = ceil(tiles / 256) of the longest sequence, as
+// the reference). One 64-lane wave owns one (KV head, split, group of up to
+// four query rows of one sequence): the 16 MFMA rows are 4 query rows x the
+// KV head's 4 query heads. Per tile:
+//
+//   S^T = K Q^T   v_mfma_f32_16x16x32_bf16, A = K rows straight from global
+//                 memory (codes converted to exact bf16 integers), B = Q^T
+//                 held in VGPRs. Lane l ends up owning query column l % 16
+//                 and keys 16 mb + 4 (l / 16) + i - a whole query row per
+//                 lane, so the online softmax needs no transpose: the row
+//                 maximum is an in-register max plus two cross-lane steps.
+//   O^T += V^T P^T  A = V^T read from a row-major LDS copy of the tile with
+//                 ds_read_b64_tr_b16 (each 16-lane group receives 4 keys x 1
+//                 dim per lane), B = P^T packed from the lane's own
+//                 probabilities. The MFMA's contraction index runs over the
+//                 tile's keys in the order the S^T lanes hold them (4 g + i,
+//                 then 16 + 4 g + i), the same for both operands.
+//
+// Numerics (the reference's tensor-core path): logit = bf16(scale * dot) with
+// dot = q . k (bf16 K) or q . codes * k_scale (quantised K; per group, then
+// summed, for group scales); p = exp(logit - m) in f32 against the split's
+// running maximum m, l sums the unrounded p, and the value product uses
+// bf16(p * v_scale) (or bf16(p)) against the V codes (values). The combine
+// kernel rescales the splits' (m, l, o) and writes bf16(sum o w / sum l w).
+// The MFMA accumulates in f32 in its own order; the tests hold the result to
+// the oracle's sequential f32 evaluation within stated bf16 tolerances.
+#include "g4_common.h"
+#include "g4_hw.h"
+#include "g4_math.h"
+#include "granite4_layerops.h"
+
+#include <climits>
+#include <cmath>
+
+namespace g4 {
+namespace {
+
+constexpr int kTile = 64;
+constexpr int kHd = 128;         // head dim
+constexpr int kGq = 4;           // query heads per KV head
+constexpr int kRowsPerWave = 4;  // query rows per wave (x 4 heads = 16 MFMA rows)
+constexpr int kAttnMaxSplits = 256;
+constexpr int kAttnWaves = 4;  // splits per workgroup, merged before the combine
+constexpr int kVPitch = kHd + 16;  // LDS V row pitch (bf16): 288 B, rows 8 banks apart
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+
+struct AttnArgs {
+  const uint16_t* q;   // [rows][Hq][128]
+  const uint8_t* k;    // [Hk][stride][K row bytes]
+  const uint8_t* v;    // [Hk][stride][V row bytes]
+  const float* ksc;    // [Hk][stride][ngrp] (quantised)
+  const float* vsc;
+  float scale;
+  int Hq, stride, rows, tps, splits, window, kv_base;
+  int nblk;  // split blocks (ceil(splits / kAttnWaves)): partials per (row, head)
+  const int* d_pos;
+  const int* d_pt;
+  const int* row_pos;
+  const int* const* row_pt;
+  float2* part_ml;  // [rows][Hq][nblk]
+  float* part_o;    // [rows][Hq][nblk][128]
+  uint16_t* out;    // [rows][Hq][128]
+};
+
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+
+// Four bf16 of a row-major LDS tile, transposed across each 16-lane group
+// (ds_read_b64_tr_b16): lane i of a group receives element i % 4 of the
+// 8-byte vectors addressed by lanes i / 4, 4 + i / 4, 8 + i / 4, 12 + i / 4.
+__device__ __forceinline__ u32x2_t lds_read_tr(const uint16_t* p) {
+  return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(p)));
+}
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  const u32x4_t u = {a, b, c, d};
+  return __builtin_bit_cast(bf16x8_t, u);
+}
+
+// Exact bf16 pair of two small integers (|x| <= 127).
+__device__ __forceinline__ uint32_t int_pair_bf16(int a, int b) {
+  return pack_bf16_hw(static_cast<float>(a), static_cast<float>(b));
+}
+
+// Row bytes of the K / V caches per format.
+__host__ __device__ constexpr int k_row_bytes(int bits) {
+  return bits == 16 ? 2 * kHd : bits == 8 ? kHd : bits == 4 ? kHd / 2 : kHd / 2 + kHd / 8;
+}
+__host__ __device__ constexpr int v_row_bytes(int bits) {
+  return bits == 16 ? 2 * kHd : bits == 8 ? kHd : kHd / 2;
+}
+
+// Eight K elements (dims c .. c + 7, c a multiple of 8) of one cached row as
+// bf16: the value (bf16 cache) or the integer code.
+template <int BITS>
+__device__ __forceinline__ bf16x8_t load_k8(const uint8_t* row, int c) {
+  if constexpr (BITS == 16) {
+    const u32x4_t u = *reinterpret_cast<const u32x4_t*>(row + 2 * c);
+    return __builtin_bit_cast(bf16x8_t, u);
+  } else if constexpr (BITS == 8) {
+    const u32x2_t u = *reinterpret_cast<const u32x2_t*>(row + c);
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t x = e < 2 ? u.x : u.y;
+      const int sh = 16 * (e & 1);
+      w[e] = int_pair_bf16(static_cast<int8_t>(x >> sh), static_cast<int8_t>(x >> (sh + 8)));
+    }
+    return as_bf16x8(w[0], w[1], w[2], w[3]);
+  } else {
+    const uint32_t x = *reinterpret_cast<const uint32_t*>(row + c / 2);
+    uint32_t hib = 0;
+    if constexpr (BITS == 5) hib = row[kHd / 2 + c / 8];
+    constexpr int off = BITS == 5 ? 16 : 8;
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      int lo = static_cast<int>((x >> (8 * e)) & 0xFu);
+      int hi = static_cast<int>((x >> (8 * e + 4)) & 0xFu);
+      if constexpr (BITS == 5) {
+        lo |= static_cast<int>((hib >> (2 * e)) & 1u) << 4;
+        hi |= static_cast<int>((hib >> (2 * e + 1)) & 1u) << 4;
+      }
+      w[e] = int_pair_bf16(lo - off, hi - off);
+    }
+    return as_bf16x8(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// Stages the tile's V rows (keys 0..63 of the tile, arena rows from lane
+// `key`'s prow) into LDS as bf16 values / integer codes; invalid keys as 0.
+template <int BITS>
+__device__ __forceinline__ void stage_v(const AttnArgs& a, const uint8_t* vbase, int prow,
+                                        uint16_t* vl) {
+  const int lane = threadIdx.x & 63;  // lane within this wave (each wave stages its own tile)
+  if constexpr (BITS == 16) {
+    // 16 chunks of 16 B per row: 4 keys per step.
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int key = 4 * i + (lane >> 4), c = lane & 15;
+      const int pr = __shfl(prow, key);
+      u32x4_t u = {0u, 0u, 0u, 0u};
+      if (pr >= 0) u = *reinterpret_cast<const u32x4_t*>(vbase + static_cast<size_t>(pr) * 256 + 16 * c);
+      *reinterpret_cast<u32x4_t*>(vl + key * kVPitch + 8 * c) = u;
+    }
+  } else if constexpr (BITS == 8) {
+    // 8 chunks of 16 codes per row: 8 keys per step.
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int key = 8 * i + (lane >> 3), c = lane & 7;
+      const int pr = __shfl(prow, key);
+      u32x4_t u = {0u, 0u, 0u, 0u};
+      if (pr >= 0) u = *reinterpret_cast<const u32x4_t*>(vbase + static_cast<size_t>(pr) * 128 + 16 * c);
+      uint32_t w[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t x = u[e >> 1];
+        const int sh = 16 * (e & 1);
+        w[e] = int_pair_bf16(static_cast<int8_t>(x >> sh), static_cast<int8_t>(x >> (sh + 8)));
+      }
+      uint16_t* dst = vl + key * kVPitch + 16 * c;
+      *reinterpret_cast<u32x4_t*>(dst) = u32x4_t{w[0], w[1], w[2], w[3]};
+      *reinterpret_cast<u32x4_t*>(dst + 8) = u32x4_t{w[4], w[5], w[6], w[7]};
+    }
+  } else {
+    // int4 V (also under K5): 4 chunks of 32 codes per row: 16 keys per step.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = 16 * i + (lane >> 2), c = lane & 3;
+      const int pr = __shfl(prow, key);
+      u32x4_t u = {0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};  // code 8 = value 0
+      if (pr >= 0) u = *reinterpret_cast<const u32x4_t*>(vbase + static_cast<size_t>(pr) * 64 + 16 * c);
+      uint32_t w[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t x = u[e >> 2];
+        const int b = 8 * (e & 3);
+        w[e] = int_pair_bf16(static_cast<int>((x >> b) & 0xFu) - 8,
+                             static_cast<int>((x >> (b + 4)) & 0xFu) - 8);
+      }
+      uint16_t* dst = vl + key * kVPitch + 32 * c;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        *reinterpret_cast<u32x4_t*>(dst + 8 * e) = u32x4_t{w[4 * e], w[4 * e + 1], w[4 * e + 2], w[4 * e + 3]};
+    }
+  }
+  (void)a;
+}
+
+// Completes this wave's LDS writes before other lanes of the wave read them
+// (each wave owns its LDS tile, so no workgroup barrier is needed).
+__device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+template <int BITS, int GROUP>
+__global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a) {
+  constexpr bool kQuant = BITS != 16;
+  constexpr int kNgrp = kQuant ? kHd / GROUP : 1;
+  constexpr int kKb = k_row_bytes(BITS), kVb = v_row_bytes(BITS);
+  // Per wave: its V tile (reused for the end-of-block merge) and scales.
+  __shared__ __align__(16) uint16_t vl_all[kAttnWaves][kTile * kVPitch];
+  __shared__ float ksc_all[kAttnWaves][kTile * kNgrp], vsc_all[kAttnWaves][kTile * kNgrp];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint16_t* vl = vl_all[wave];
+  float* ksc_l = ksc_all[wave];
+  float* vsc_l = vsc_all[wave];
+  const int g = lane >> 4;   // lane group: keys 4 g + i of each 16-key block
+  const int n = lane & 15;   // query column: row n / 4, head n % 4
+  const int hkv = blockIdx.x, split = blockIdx.y * kAttnWaves + wave;
+  const int per = a.row_pos != nullptr ? 1 : kRowsPerWave;
+  const int r0 = blockIdx.z * per;
+  const int nr = min(per, a.rows - r0);
+  const int base = a.row_pos != nullptr ? 0 : (a.d_pos != nullptr ? *a.d_pos : a.kv_base);
+  // Causal length, clamped to the arena (a position read from device memory
+  // never sends the page-table reads past the arena's positions).
+  auto row_len = [&](int rr) {
+    const int len = a.row_pos != nullptr ? a.row_pos[r0 + rr] + 1 : base + r0 + rr + 1;
+    return min(max(len, 0), a.stride);
+  };
+  auto row_lo = [&](int rr) { return a.window > 0 ? max(0, row_len(rr) - a.window) : 0; };
+  int kv_max = 0, lo_min = INT_MAX;
+  for (int rr = 0; rr < nr; ++rr) {
+    kv_max = max(kv_max, row_len(rr));
+    lo_min = min(lo_min, row_lo(rr));
+  }
+  const int span = a.tps * kTile;
+  const int blk_begin = blockIdx.y * kAttnWaves * span;
+  if (blk_begin >= kv_max || blk_begin + kAttnWaves * span <= lo_min) return;  // whole block idle
+  const int t_begin = split * span;
+  const int t_end_max = min(kv_max, t_begin + span);
+  const bool active = split < a.splits && t_begin < kv_max && t_end_max > lo_min;
+  const int t_first = max(t_begin, (lo_min / kTile) * kTile);
+  const int* pt = a.row_pt != nullptr ? a.row_pt[r0] : a.d_pt;
+
+  // This lane's query column.
+  const int rr = n >> 2, hq = hkv * kGq + (n & 3);
+  const bool live = rr < nr;
+  const int my_len = live ? row_len(rr) : 0;
+  const int my_lo = live ? row_lo(rr) : 0;
+  bf16x8_t qb[4];
+  {
+    const uint16_t* qp = a.q + (static_cast<size_t>(r0 + (live ? rr : 0)) * a.Hq + hq) * kHd;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      u32x4_t u = {0u, 0u, 0u, 0u};
+      if (live && active) u = *reinterpret_cast<const u32x4_t*>(qp + 32 * s + 8 * g);
+      qb[s] = __builtin_bit_cast(bf16x8_t, u);
+    }
+  }
+
+  const uint8_t* kbase = a.k + static_cast<size_t>(hkv) * a.stride * kKb;
+  const uint8_t* vbase = a.v + static_cast<size_t>(hkv) * a.stride * kVb;
+  const float* kscb = kQuant ? a.ksc + static_cast<size_t>(hkv) * a.stride * kNgrp : nullptr;
+  const float* vscb = kQuant ? a.vsc + static_cast<size_t>(hkv) * a.stride * kNgrp : nullptr;
+
+  f32x4_t o[8];
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) o[nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  float m = -INFINITY, l = 0.0f;
+
+  for (int t0 = active ? t_first : t_end_max; t0 < t_end_max; t0 += kTile) {
+    // Arena row of key t0 + lane (-1: past the split's end or outside the arena).
+    int prow = -1;
+    if (t0 + lane < t_end_max) {
+      const int p = t0 + lane;
+      const int r = pt != nullptr ? pt[p] : p;
+      prow = (r >= 0 && r < a.stride) ? r : -1;
+    }
+    // V tile -> LDS (bf16 values / codes), scales -> LDS.
+    stage_v<BITS>(a, vbase, prow, vl);
+    if constexpr (kQuant) {
+#pragma unroll
+      for (int gi = 0; gi < kNgrp; ++gi) {
+        ksc_l[lane * kNgrp + gi] = prow >= 0 ? kscb[static_cast<size_t>(prow) * kNgrp + gi] : 0.0f;
+        vsc_l[lane * kNgrp + gi] = prow >= 0 ? vscb[static_cast<size_t>(prow) * kNgrp + gi] : 0.0f;
+      }
+    }
+    const unsigned long long kvalid = __ballot(prow >= 0);
+    wave_lds_sync();  // V tile and scales in LDS
+    // S^T = K Q^T per 16-key block mb: lane l holds keys 16 mb + 4 g + i.
+    float sv[4][4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      const int kr = __shfl(prow, 16 * mb + n);  // key 16 mb + n (the A row of lane l)
+      const uint8_t* krow = kbase + static_cast<size_t>(kr >= 0 ? kr : 0) * kKb;
+      bf16x8_t ka[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) ka[s] = load_k8<BITS>(krow, 32 * s + 8 * g);
+      f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      if constexpr (!kQuant || GROUP == kHd) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s], qb[s], acc, 0, 0, 0);
+        if constexpr (kQuant) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[i] = acc[i] * ksc_l[(16 * mb + 4 * g + i) * kNgrp];
+        }
+      } else {
+        constexpr int kSteps = GROUP / 32;
+#pragma unroll
+        for (int gi = 0; gi < kNgrp; ++gi) {
+          f32x4_t part = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int s = gi * kSteps; s < (gi + 1) * kSteps; ++s)
+            part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s], qb[s], part, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[i] += part[i] * ksc_l[(16 * mb + 4 * g + i) * kNgrp + gi];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int p = t0 + 16 * mb + 4 * g + i;
+        const bool ok = live && p < my_len && p >= my_lo && ((kvalid >> (16 * mb + 4 * g + i)) & 1ull);
+        sv[mb][i] = ok ? bf16_to_f32(f32_to_bf16(a.scale * acc[i])) : -INFINITY;
+      }
+    }
+    // Online softmax of this lane's query row over the tile.
+    float mx = m;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sv[mb][i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float alpha = mx == -INFINITY ? 1.0f : __expf(m - mx);
+    m = mx;
+    l *= alpha;
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) o[nb] *= alpha;
+    float e[4][4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        e[mb][i] = m == -INFINITY ? 0.0f : __expf(sv[mb][i] - m);
+        l += e[mb][i];
+      }
+    // O^T += V^T P^T, two 32-key steps: contraction slot j -> key 32 s + 4 g + j
+    // (j < 4) or 32 s + 16 + 4 g + j - 4.
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      bf16x8_t pb[kNgrp];
+#pragma unroll
+      for (int gi = 0; gi < kNgrp; ++gi) {
+        float pv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int mb = 2 * s + (j >> 2), i = j & 3;
+          const float sc = kQuant ? vsc_l[(16 * mb + 4 * g + i) * kNgrp + gi] : 1.0f;
+          pv[j] = e[mb][i] * sc;
+        }
+        pb[gi] = as_bf16x8(pack_bf16_hw(pv[0], pv[1]), pack_bf16_hw(pv[2], pv[3]),
+                           pack_bf16_hw(pv[4], pv[5]), pack_bf16_hw(pv[6], pv[7]));
+      }
+      const int kk = n >> 2, dd = 4 * (n & 3);
+      const uint16_t* r1 = vl + (32 * s + 4 * g + kk) * kVPitch + dd;
+      const uint16_t* r2 = r1 + 16 * kVPitch;
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) {
+        const u32x2_t lo = lds_read_tr(r1 + 16 * nb);
+        const u32x2_t hi = lds_read_tr(r2 + 16 * nb);
+        const bf16x8_t va = as_bf16x8(lo.x, lo.y, hi.x, hi.y);
+        const int gi = kQuant ? (16 * nb) / GROUP : 0;
+        o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[gi], o[nb], 0, 0, 0);
+      }
+    }
+    wave_lds_sync();  // this tile's LDS reads are done before the next tile's writes
+  }
+  // l: sum over the four lanes of this query column.
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+
+  // Merge the block's kAttnWaves splits (the combine's formula over these
+  // splits): per query column, M = max m_w, w_w = exp(m_w - M), then one
+  // partial (M, sum l_w w_w, sum o_w w_w) per (row, head, block).
+  __syncthreads();  // every wave's last tile reads are done: vl_all is free
+  float* mo = reinterpret_cast<float*>(&vl_all[0][0]);  // [wave][16 cols][128 dims]
+  float* mml = mo + kAttnWaves * 16 * kHd;              // [wave][16 cols][2]
+  static_assert(sizeof(vl_all) >= sizeof(float) * kAttnWaves * 16 * (kHd + 2), "merge area");
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb)
+    *reinterpret_cast<f32x4_t*>(mo + (wave * 16 + n) * kHd + 16 * nb + 4 * g) = o[nb];
+  if (g == 0) {
+    const bool has = active && live && t_begin < my_len && t_end_max > my_lo;
+    mml[(wave * 16 + n) * 2] = has ? m : -INFINITY;
+    mml[(wave * 16 + n) * 2 + 1] = has ? l : 0.0f;
+  }
+  __syncthreads();
+  {
+    const int col = threadIdx.x >> 4, dc = threadIdx.x & 15;  // 16 columns x 8 dims each
+    const int crr = col >> 2, chq = hkv * kGq + (col & 3);
+    if (crr >= nr) return;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, mml[(w * 16 + col) * 2]);
+    if (M == -INFINITY) return;  // no key of this row in the block
+    float L = 0.0f, acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) {
+      const float mw = mml[(w * 16 + col) * 2];
+      const float wt = mw == -INFINITY ? 0.0f : expf(mw - M);
+      L += mml[(w * 16 + col) * 2 + 1] * wt;
+      const float* ow = mo + (w * 16 + col) * kHd + 8 * dc;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += ow[e] * wt;
+    }
+    const size_t slot = (static_cast<size_t>(r0 + crr) * a.Hq + chq) * a.nblk + blockIdx.y;
+    if (dc == 0) a.part_ml[slot] = make_float2(M, L);
+    float* po = a.part_o + slot * kHd + 8 * dc;
+    *reinterpret_cast<f32x4_t*>(po) = f32x4_t{acc[0], acc[1], acc[2], acc[3]};
+    *reinterpret_cast<f32x4_t*>(po + 4) = f32x4_t{acc[4], acc[5], acc[6], acc[7]};
+  }
+}
+
+// One workgroup per (head, row) rescales and sums the row's split-block partials:
+// the splits' maxima and weights w_s = exp(m_s - M) in parallel (weights
+// kept in LDS), then each half of the workgroup sums every other split's
+// o_s w_s for all 128 dims, four splits in flight per lane.
+constexpr int kCombineThreads = 256;
+
+__device__ __forceinline__ float block_reduce(float v, bool is_max, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float u = __shfl_xor(v, o);
+    v = is_max ? fmaxf(v, u) : v + u;
+  }
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int i = 1; i < kCombineThreads / 64; ++i) r = is_max ? fmaxf(r, red[i]) : r + red[i];
+  return r;
+}
+
+__global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(AttnArgs a) {
+  __shared__ float s_w[kAttnMaxSplits];
+  __shared__ float s_red[kCombineThreads / 64];
+  __shared__ float s_half[kHd];
+  const int h = blockIdx.x, row = blockIdx.y;
+  const int len = a.row_pos != nullptr ? a.row_pos[row] + 1
+                                       : (a.d_pos != nullptr ? *a.d_pos : a.kv_base) + row + 1;
+  const int span = kAttnWaves * a.tps * kTile;  // positions per split block
+  const int used = min((min(max(len, 0), a.stride) + span - 1) / span, a.nblk);
+  const int s0 = a.window > 0 ? max(0, len - a.window) / span : 0;
+  const size_t base = (static_cast<size_t>(row) * a.Hq + h) * a.nblk;
+  const int t = threadIdx.x;
+  float mx = -INFINITY;
+  for (int s = s0 + t; s < used; s += kCombineThreads) mx = fmaxf(mx, a.part_ml[base + s].x);
+  const float M = block_reduce(mx, true, s_red);
+  float ls = 0.0f;
+  for (int s = s0 + t; s < used; s += kCombineThreads) {
+    const float2 ml = a.part_ml[base + s];
+    const float w = expf(ml.x - M);
+    s_w[s - s0] = w;
+    ls += ml.y * w;
+  }
+  const float L = block_reduce(ls, false, s_red);  // its barriers also publish s_w
+  const int d = t & (kHd - 1), half = t >> 7;
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  int s = s0 + half;
+  for (; s + 6 < used; s += 8) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      acc[k] += a.part_o[(base + s + 2 * k) * kHd + d] * s_w[s + 2 * k - s0];
+  }
+  for (; s < used; s += 2) acc[0] += a.part_o[(base + s) * kHd + d] * s_w[s - s0];
+  float v = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  if (half == 1) s_half[d] = v;
+  __syncthreads();
+  if (half == 0)
+    a.out[(static_cast<size_t>(row) * a.Hq + h) * kHd + d] =
+        static_cast<uint16_t>(f32_to_bf16((v + s_half[d]) / L));
+}
+
+}  // namespace
+}  // namespace g4
+
+namespace g4 {
+namespace {
+
+// Tiles per split and split count for sequences up to max_len positions
+// (attention_split.cu:61-76, 1154-1157): at most 256 splits.
+int attn_tps(int max_len) {
+  const int tiles = (max_len + kTile - 1) / kTile;
+  return (tiles + kAttnMaxSplits - 1) / kAttnMaxSplits;
+}
+int attn_splits(int max_len) {
+  const int tiles = (max_len + kTile - 1) / kTile;
+  const int tps = attn_tps(max_len);
+  return (tiles + tps - 1) / tps;
+}
+
+template <int BITS>
+void launch_attn_bits(const AttnArgs& a, int group, dim3 grid, hipStream_t st) {
+  if constexpr (BITS == 16) {
+    (void)group;
+    hipLaunchKernelGGL((attn_split_kernel<16, kHd>), grid, kAttnWaves * 64, 0, st, a);
+  } else {
+    if (group == kHd) hipLaunchKernelGGL((attn_split_kernel<BITS, kHd>), grid, kAttnWaves * 64, 0, st, a);
+    else if (group == 64) hipLaunchKernelGGL((attn_split_kernel<BITS, 64>), grid, kAttnWaves * 64, 0, st, a);
+    else hipLaunchKernelGGL((attn_split_kernel<BITS, 32>), grid, kAttnWaves * 64, 0, st, a);
+  }
+}
+
+}  // namespace
+}  // namespace g4
+
+using namespace g4;
+
+extern "C" {
+
+size_t granite4_attn_split_scratch_bytes(int Hq, int rows, int stride) {
+  if (Hq <= 0 || rows <= 0 || stride <= 0) return 0;
+  const size_t nblk = (attn_splits(stride) + kAttnWaves - 1) / kAttnWaves;
+  const size_t slots = static_cast<size_t>(rows) * Hq * nblk;
+  return slots * (sizeof(float2) + kHd * sizeof(float));
+}
+
+int granite4_attn_paged(const uint16_t* q, int rows, int Hq, int Hk, int d, float scale,
+                        const void* cache_k, const void* cache_v, const float* k_scale,
+                        const float* v_scale, int bits, int group, int stride, int kv_base,
+                        const int* d_pos, const int* d_pt, const int* row_pos,
+                        const int* const* row_pt, int max_len, int window, void* scratch,
+                        uint16_t* out) {
+  const int ml = max_len > 0 ? max_len : stride;
+  const bool quant = bits != 16;
+  if (q == nullptr || scratch == nullptr || out == nullptr || cache_k == nullptr ||
+      cache_v == nullptr || !std::isfinite(scale) || d != kHd || Hk <= 0 || Hq != kGq * Hk ||
+      rows <= 0 || rows > kMaxVerifyRows || stride <= 0 || ml > stride || window < 0 ||
+      (d_pos == nullptr && row_pos == nullptr && kv_base + rows > ml) || kv_base < 0 ||
+      ((row_pos == nullptr) != (row_pt == nullptr)) ||
+      (bits != 16 && bits != 8 && bits != 4 && bits != 5) ||
+      (quant && (k_scale == nullptr || v_scale == nullptr ||
+                 (group != 32 && group != 64 && group != kHd)))) {
+    std::fprintf(stderr, "granite4: granite4_attn_paged: invalid arguments\n");
+    return -1;
+  }
+  AttnArgs a{};
+  a.q = q;
+  a.k = static_cast<const uint8_t*>(cache_k);
+  a.v = static_cast<const uint8_t*>(cache_v);
+  a.ksc = k_scale;
+  a.vsc = v_scale;
+  a.scale = scale;
+  a.Hq = Hq;
+  a.stride = stride;
+  a.rows = rows;
+  a.tps = attn_tps(ml);
+  a.splits = attn_splits(ml);
+  a.window = window;
+  a.kv_base = kv_base;
+  a.d_pos = d_pos;
+  a.d_pt = d_pt;
+  a.row_pos = row_pos;
+  a.row_pt = row_pt;
+  a.nblk = (a.splits + kAttnWaves - 1) / kAttnWaves;
+  a.part_ml = static_cast<float2*>(scratch);
+  a.part_o = reinterpret_cast<float*>(a.part_ml + static_cast<size_t>(rows) * Hq * a.nblk);
+  a.out = out;
+  // Multi-sequence rows (row_pos) take one wave each; rows of one sequence
+  // share a wave in groups of four (their keys are read once per group).
+  const int nz = row_pos != nullptr ? rows : (rows + kRowsPerWave - 1) / kRowsPerWave;
+  const dim3 grid(Hk, a.nblk, nz);
+  const hipStream_t st = stream();
+  switch (bits) {
+    case 16: launch_attn_bits<16>(a, group, grid, st); break;
+    case 8: launch_attn_bits<8>(a, group, grid, st); break;
+    case 4: launch_attn_bits<4>(a, group, grid, st); break;
+    default: launch_attn_bits<5>(a, group, grid, st); break;
+  }
+  if (launch_status("granite4_attn_paged (split)") != 0) return -1;
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(Hq, rows), kCombineThreads, 0, st, a);
+  return launch_status("granite4_attn_paged (combine)");
+}
+
+int granite4_attn_split(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cache_v,
+                        float scale, int Hq, int Hk, int d, int kv_base, const int* d_pos,
+                        int rows, int stride, void* scratch, uint16_t* out,
+                        const int8_t* cache_k8, const int8_t* cache_v8,
+                        const float* cache_k_scale, const float* cache_v_scale, int int8,
+                        const uint8_t* cache_k4, const uint8_t* cache_v4, int int4,
+                        const int* d_pt, int max_len, const int* row_pos,
+                        const int* const* row_pt, const int* row_grp, int ngroups,
+                        const int* row_tbase, const int* row_tail, int kv_hint, int k5,
+                        int window) {
+  (void)kv_hint;  // a launch-size hint only; every split still exits at once past the rows
+  if ((row_grp != nullptr && (row_pos == nullptr || ngroups <= 0 || ngroups > rows)) ||
+      (int8 && int4) || (k5 && !int4)) {
+    std::fprintf(stderr, "granite4: granite4_attn_split: invalid arguments\n");
+    return -1;
+  }
+  if (row_tbase != nullptr || row_tail != nullptr) {
+    std::fprintf(stderr, "granite4: granite4_attn_split: draft-tree rows are not supported\n");
+    return -1;
+  }
+  // row_grp groups rows of one sequence so they share K/V tiles; results are
+  // identical without it (attention_gpu.h), so rows run one per wave here.
+  const int bits = int8 ? 8 : (int4 ? (k5 ? 5 : 4) : 16);
+  const void* ck = int8 ? static_cast<const void*>(cache_k8)
+                        : (int4 ? static_cast<const void*>(cache_k4) : cache_k);
+  const void* cv = int8 ? static_cast<const void*>(cache_v8)
+                        : (int4 ? static_cast<const void*>(cache_v4) : cache_v);
+  return granite4_attn_paged(q, rows, Hq, Hk, d, scale, ck, cv, cache_k_scale, cache_v_scale,
+                             bits, kHd, stride, kv_base, d_pos, d_pt, row_pos, row_pt, max_len,
+                             window, scratch, out);
+}
+
+}  // extern "C"

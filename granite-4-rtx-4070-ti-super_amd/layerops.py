@@ -78,6 +78,10 @@ _SIG = {
     "granite4_row_table": [P, I, I, P],
     "granite4_fp8_work_bytes": [I],
     "granite4_set_fp8_launch_mode": [I],
+    "granite4_attn_split_scratch_bytes": [I, I, I],
+    "granite4_attn_split": [P, P, P, F, I, I, I, I, P, I, I, P, P, P, P, P, P, I, P, P, I, P, I,
+                            P, P, P, I, P, P, I, I, I],
+    "granite4_attn_paged": [P, I, I, I, I, F, P, P, P, P, I, I, I, I, P, P, P, P, I, I, P, P],
     "granite4_host_fp8_encode": [P, _c.c_size_t, F, P],
     "granite4_host_kv_codes": [P, _c.c_size_t, F, I, P],
     "granite4_selftest_bf16": [P],
@@ -87,7 +91,8 @@ _SIG = {
 for _name, _args in _SIG.items():
     _fn = getattr(_lib, _name)
     _fn.argtypes = _args
-    _fn.restype = {"granite4_get_stream": P, "granite4_fp8_work_bytes": _c.c_size_t}.get(_name, I)
+    _fn.restype = {"granite4_get_stream": P, "granite4_fp8_work_bytes": _c.c_size_t,
+                   "granite4_attn_split_scratch_bytes": _c.c_size_t}.get(_name, I)
 
 lib = _lib
 
@@ -109,6 +114,11 @@ def call(name, *args):
     """Calls a C entry point by name; tensors are passed as device pointers."""
     conv = [(_ptr(a) if (a is None or isinstance(a, torch.Tensor)) else a) for a in args]
     _check(getattr(_lib, name)(*conv), name)
+
+
+def call_size(name, *args):
+    """Calls a C entry point that returns a size (not a status)."""
+    return getattr(_lib, name)(*args)
 
 
 def use_stream(stream=None):

@@ -320,6 +320,51 @@ int granite4_selftest_bf16(unsigned long long* d_result);
 int granite4_selftest_fp8(float scale, unsigned long long* d_result);
 
 
+/* ---------------------------------------------------------------------------
+ * Split-KV decode attention over the paged KV pool (attention_split.cu,
+ * attention_gpu.h:14-60).
+ * ------------------------------------------------------------------------- */
+
+/* Scratch bytes for `rows` query rows at cache stride `stride`
+ * (attention_gpu.h:17 attn_split_scratch_bytes; the split layout follows
+ * stride, or max_len when a call passes one). */
+size_t granite4_attn_split_scratch_bytes(int Hq, int rows, int stride);
+
+/* The reference's attn_split (attention_gpu.h:53-60, bools as int). Causal
+ * GQA for rows (1..16) query rows q [rows][Hq * d]: row r sits at position
+ * p + r (p = *d_pos when d_pos is non-NULL, else kv_base; or row_pos[r] for
+ * multi-sequence rows with their own tables row_pt[r]) and attends to
+ * positions [0, p + r] (the last `window` of them when window > 0), read
+ * through d_pt (position -> arena row; NULL = contiguous). Caches are
+ * [Hk][stride][row bytes]: bf16 (cache_k / cache_v), int8 (cache_k8 /
+ * cache_v8 with per-row scales, int8 = 1), int4 (cache_k4 / cache_v4,
+ * int4 = 1) or K5 K + int4 V (k5 = 1). d = 128 and Hq = 4 Hk only; out is
+ * [rows][Hq * d]. row_grp / ngroups (rows of one sequence sharing tiles) and
+ * kv_hint only shape the reference's launch: results are identical without
+ * them. Draft-tree rows (row_tbase / row_tail) are not supported: -1.
+ * Arena rows outside [0, stride) are skipped (their keys are masked). */
+int granite4_attn_split(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cache_v,
+                        float scale, int Hq, int Hk, int d, int kv_base, const int* d_pos,
+                        int rows, int stride, void* scratch, uint16_t* out,
+                        const int8_t* cache_k8, const int8_t* cache_v8,
+                        const float* cache_k_scale, const float* cache_v_scale, int int8,
+                        const uint8_t* cache_k4, const uint8_t* cache_v4, int int4,
+                        const int* d_pt, int max_len, const int* row_pos,
+                        const int* const* row_pt, const int* row_grp, int ngroups,
+                        const int* row_tbase, const int* row_tail, int kv_hint, int k5,
+                        int window);
+
+/* The same attention for any pool format of this library, including the
+ * group scales of granite4_rope_append: bits 16 / 8 / 4 / 5 (K5 K + int4 V),
+ * group 32 / 64 / 128 (scales [Hk][stride][128 / group]; ignored for bf16).
+ * New entry point (the reference's attention reads per-row scales only). */
+int granite4_attn_paged(const uint16_t* q, int rows, int Hq, int Hk, int d, float scale,
+                        const void* cache_k, const void* cache_v, const float* k_scale,
+                        const float* v_scale, int bits, int group, int stride, int kv_base,
+                        const int* d_pos, const int* d_pt, const int* row_pos,
+                        const int* const* row_pt, int max_len, int window, void* scratch,
+                        uint16_t* out);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 
@@ -376,6 +421,27 @@ inline int gpu_multi_kv_append(const uint16_t* k, const uint16_t* v, int bits, v
                                void* cv, float* ks, float* vs, const GpuMultiRows* d_rows,
                                int rows, int stride, int Hk, int d) {
   return granite4_multi_kv_append(k, v, bits, ck, cv, ks, vs, d_rows, rows, stride, Hk, d);
+}
+
+// attention_gpu.h:17, 53-60 (bool flags, default arguments).
+inline size_t attn_split_scratch_bytes(int Hq, int rows, int stride) {
+  return granite4_attn_split_scratch_bytes(Hq, rows, stride);
+}
+inline int attn_split(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cache_v,
+                      float scale, int Hq, int Hk, int d, int kv_base, const int* d_pos, int rows,
+                      int stride, void* scratch, uint16_t* out, const int8_t* cache_k8 = nullptr,
+                      const int8_t* cache_v8 = nullptr, const float* cache_k_scale = nullptr,
+                      const float* cache_v_scale = nullptr, bool int8 = false,
+                      const uint8_t* cache_k4 = nullptr, const uint8_t* cache_v4 = nullptr,
+                      bool int4 = false, const int* d_pt = nullptr, int max_len = 0,
+                      const int* row_pos = nullptr, const int* const* row_pt = nullptr,
+                      const int* row_grp = nullptr, int ngroups = 0,
+                      const int* row_tbase = nullptr, const int* row_tail = nullptr,
+                      int kv_hint = 0, bool k5 = false, int window = 0) {
+  return granite4_attn_split(q, cache_k, cache_v, scale, Hq, Hk, d, kv_base, d_pos, rows, stride,
+                             scratch, out, cache_k8, cache_v8, cache_k_scale, cache_v_scale, int8,
+                             cache_k4, cache_v4, int4, d_pt, max_len, row_pos, row_pt, row_grp,
+                             ngroups, row_tbase, row_tail, kv_hint, k5, window);
 }
 }  // namespace granite4
 #endif /* __cplusplus */

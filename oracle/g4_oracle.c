@@ -13,6 +13,7 @@
 #include "g4_oracle.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 /* ------------------------------------------------------------------------ */
@@ -403,4 +404,119 @@ void g4o_rope_append(const uint16_t* q, long q_stride, const uint16_t* k, long k
 /* row(p) = block_table[p / page] * page + p % page (kv_pool.cc:285-297). */
 void g4o_row_table(const int32_t* block_table, int n, int page, int32_t* out) {
   for (int p = 0; p < n; ++p) out[p] = block_table[p / page] * page + p % page;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Split-KV decode attention (attention_split.cu:791-1074).                  */
+
+/* Value of element i of a cached row: bf16 value, or the integer code (the
+ * stored byte / nibble / 5-bit value minus its offset). */
+static float kv_elem(const uint8_t* row, int bits, int is_k, int d, int i) {
+  switch (bits) {
+    case 16: return g4o_bf16_to_f32(((const uint16_t*)row)[i]);
+    case 8: return (float)(int8_t)row[i];
+    case 4: return (float)((int)((row[i / 2] >> (4 * (i & 1))) & 0xFu) - 8);
+    case 5:
+      if (!is_k) return (float)((int)((row[i / 2] >> (4 * (i & 1))) & 0xFu) - 8);
+      return (float)((int)(((row[i / 2] >> (4 * (i & 1))) & 0xFu) |
+                           (((row[d / 2 + i / 8] >> (i & 7)) & 1u) << 4)) - 16);
+    default: return 0.0f;
+  }
+}
+
+void g4o_attn_split(const uint16_t* q, int rows, int Hq, int Hk, int d, float scale,
+                    const void* cache_k, const void* cache_v, const float* k_scale,
+                    const float* v_scale, int bits, int group, int stride, const int* pos,
+                    const int* const* pt, int window, int tps, uint16_t* out) {
+  const int G = Hq / Hk, ngrp = d / group, tile = 64, span = tps * tile;
+  const int kb = kv_row_bytes(bits, d, 1), vb = kv_row_bytes(bits, d, 0);
+  const int quant = bits != 16;
+  float qf[1024], oacc[1024], acc[1024], logit[64], pbf[64 * 32];
+  float *ms = NULL, *ls = NULL, *os = NULL;
+  for (int r = 0; r < rows; ++r) {
+    const int len = pos[r] + 1;
+    const int lo = window > 0 ? (len - window > 0 ? len - window : 0) : 0;
+    const int nsplit = (len + span - 1) / span;
+    ms = (float*)realloc(ms, sizeof(float) * nsplit);
+    ls = (float*)realloc(ls, sizeof(float) * nsplit);
+    os = (float*)realloc(os, sizeof(float) * (size_t)nsplit * d);
+    for (int h = 0; h < Hq; ++h) {
+      const int hk = h / G;
+      for (int i = 0; i < d; ++i) qf[i] = g4o_bf16_to_f32(q[((size_t)r * Hq + h) * d + i]);
+      int used0 = -1, used1 = -1;
+      for (int sp = 0; sp < nsplit; ++sp) {
+        const int t_begin = sp * span;
+        const int t_end = len < t_begin + span ? len : t_begin + span;
+        if (t_end <= lo) continue; /* the whole split is below the window */
+        if (used0 < 0) used0 = sp;
+        used1 = sp;
+        const int t_first = t_begin > (lo / tile) * tile ? t_begin : (lo / tile) * tile;
+        float m = -INFINITY, l = 0.0f;
+        for (int i = 0; i < d; ++i) oacc[i] = 0.0f;
+        for (int t0 = t_first; t0 < t_end; t0 += tile) {
+          float mx = m;
+          for (int j = 0; j < tile; ++j) {
+            const int p = t0 + j;
+            if (p >= t_end || p < lo) {
+              logit[j] = -INFINITY;
+              continue;
+            }
+            const int arow = pt != NULL && pt[r] != NULL ? pt[r][p] : p;
+            const uint8_t* krow = (const uint8_t*)cache_k + ((size_t)hk * stride + arow) * kb;
+            float dot = 0.0f;
+            if (!quant) {
+              for (int i = 0; i < d; ++i) dot += qf[i] * kv_elem(krow, bits, 1, d, i);
+            } else {
+              const float* ks = k_scale + ((size_t)hk * stride + arow) * ngrp;
+              for (int g = 0; g < ngrp; ++g) {
+                float part = 0.0f;
+                for (int i = g * group; i < (g + 1) * group; ++i) part += qf[i] * kv_elem(krow, bits, 1, d, i);
+                dot += part * ks[g];
+              }
+            }
+            logit[j] = g4o_bf16_to_f32(g4o_f32_to_bf16(scale * dot));
+            if (logit[j] > mx) mx = logit[j];
+          }
+          const float alpha = mx == -INFINITY ? 1.0f : expf(m - mx);
+          l *= alpha;
+          m = mx;
+          for (int i = 0; i < d; ++i) oacc[i] *= alpha;
+          for (int j = 0; j < tile; ++j) {
+            const float e = m == -INFINITY || logit[j] == -INFINITY ? 0.0f : expf(logit[j] - m);
+            l += e;
+            const int p = t0 + j;
+            const int valid = logit[j] != -INFINITY;
+            const int arow = valid ? (pt != NULL && pt[r] != NULL ? pt[r][p] : p) : 0;
+            for (int g = 0; g < ngrp; ++g) {
+              const float sv = quant && valid ? v_scale[((size_t)hk * stride + arow) * ngrp + g] : 1.0f;
+              pbf[j * ngrp + g] = g4o_bf16_to_f32(g4o_f32_to_bf16(e * sv));
+            }
+          }
+          for (int j = 0; j < tile; ++j) {
+            if (logit[j] == -INFINITY) continue;
+            const int p = t0 + j;
+            const int arow = pt != NULL && pt[r] != NULL ? pt[r][p] : p;
+            const uint8_t* vrow = (const uint8_t*)cache_v + ((size_t)hk * stride + arow) * vb;
+            for (int i = 0; i < d; ++i) oacc[i] += pbf[j * ngrp + i / group] * kv_elem(vrow, bits, 0, d, i);
+          }
+        }
+        ms[sp] = m;
+        ls[sp] = l;
+        memcpy(os + (size_t)sp * d, oacc, sizeof(float) * d);
+      }
+      float M = -INFINITY;
+      for (int sp = used0; sp <= used1; ++sp) M = ms[sp] > M ? ms[sp] : M;
+      float L = 0.0f;
+      for (int i = 0; i < d; ++i) acc[i] = 0.0f;
+      for (int sp = used0; sp <= used1; ++sp) {
+        const float w = expf(ms[sp] - M);
+        L += ls[sp] * w;
+        for (int i = 0; i < d; ++i) acc[i] += os[(size_t)sp * d + i] * w;
+      }
+      for (int i = 0; i < d; ++i) out[((size_t)r * Hq + h) * d + i] = g4o_f32_to_bf16(acc[i] / L);
+    }
+  }
+  free(ms);
+  free(ls);
+  free(os);
 }

@@ -87,6 +87,28 @@ void g4o_rope_append(const uint16_t* q, long q_stride, const uint16_t* k, long k
                      long q_rot_stride, void* cache_k, void* cache_v, float* k_scale,
                      float* v_scale, int stride);
 
+/* Split-KV decode attention over the paged pool (attention_split.cu: the
+ * tensor-core kernel :791-1047 and attn_combine_kernel :1049-1074, launched
+ * by attn_split :1083-1255). Row r (query q[r][Hq][d], Hq = 4 Hk, query head h
+ * reads KV head h / 4) sits at position pos[r] and attends to positions
+ * [lo, pos[r]], lo = max(0, pos[r] + 1 - window) when window > 0 else 0,
+ * found at arena row pt[r][position] (pt[r] NULL: row = position). Cache
+ * formats as g4o_rope_append's. Positions are cut into 64-position tiles and
+ * the tiles into splits of tps tiles; each split keeps its own online
+ * softmax, and the splits are combined, as the kernels do:
+ *   logit  = bf16(scale * dot), dot = q . k (bf16 K) or sum over scale groups
+ *            of (q . codes) * k_scale (quantised K; one group = the
+ *            reference's per-row scale)
+ *   p      = exp(logit - m) (f32, m = the split's running maximum), summed
+ *            unrounded into l; the value product uses bf16(p * v_scale)
+ *            (quantised V) or bf16(p) (bf16 V) against the code / value
+ *   out    = bf16(sum_s o_s w_s / sum_s l_s w_s), w_s = exp(m_s - max_s m_s).
+ * Sums run in f32 in key / dim order. */
+void g4o_attn_split(const uint16_t* q, int rows, int Hq, int Hk, int d, float scale,
+                    const void* cache_k, const void* cache_v, const float* k_scale,
+                    const float* v_scale, int bits, int group, int stride, const int* pos,
+                    const int* const* pt, int window, int tps, uint16_t* out);
+
 /* Paged pool: position -> arena row (kv_pool.cc:285-297). */
 void g4o_row_table(const int32_t* block_table, int n, int page, int32_t* out);
 

@@ -115,4 +115,13 @@ int ref_paged_row_tables(int seqs, int tokens, int* blocks, int* rows) {
   return npages;
 }
 
+// kernel_math.h:312-331: the reference's host GQA decode attention on a
+// contiguous bf16 cache k, v [Hk][kv_len][d]; out [Hq][d].
+void ref_gqa_attention_bf16(const std::uint16_t* q, const std::uint16_t* k, const std::uint16_t* v,
+                            float scale, int Hq, int Hk, int d, int kv_len, std::uint16_t* out) {
+  std::vector<std::uint16_t> o;
+  gqa_attention_bf16(q, k, v, scale, Hq, Hk, d, kv_len, &o);
+  std::memcpy(out, o.data(), o.size() * sizeof(std::uint16_t));
+}
+
 }  // extern "C"

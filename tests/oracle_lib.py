@@ -58,6 +58,9 @@ def _load():
                                    _c.c_int, _c.c_int, _c.c_int, _c.c_int, u16p, _c.c_long,
                                    vp, vp, f32p, f32p, _c.c_int]),
         "g4o_row_table": (None, [i32p, _c.c_int, _c.c_int, i32p]),
+        "g4o_attn_split": (None, [u16p, _c.c_int, _c.c_int, _c.c_int, _c.c_int, _c.c_float, vp,
+                                  vp, f32p, f32p, _c.c_int, _c.c_int, _c.c_int, i32p,
+                                  _c.POINTER(i32p), _c.c_int, _c.c_int, u16p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -195,6 +198,41 @@ def row_table(block_table, n, page=16):
     return out
 
 
+ATTN_TILE = 64
+ATTN_MAX_SPLITS = 256
+
+
+def attn_tiles_per_split(max_len):
+    """Tiles per split of the split-KV attention (attention_split.cu:61-76):
+    at most 256 splits of the longest sequence, 64-position tiles."""
+    tiles = (max_len + ATTN_TILE - 1) // ATTN_TILE
+    return (tiles + ATTN_MAX_SPLITS - 1) // ATTN_MAX_SPLITS
+
+
+def attn_split(q, cache_k, cache_v, k_scale, v_scale, bits, group, stride, pos, pts=None,
+               window=0, scale=1.0 / 128, Hk=8, d=128, tps=None, max_len=None):
+    """Oracle split-KV attention. q: uint16 [rows][Hq*d]; pos: per-row positions;
+    pts: None or a list of per-row int32 position -> arena-row tables.
+    Returns uint16 [rows][Hq*d]."""
+    q = np.ascontiguousarray(q, np.uint16)
+    rows, Hq = q.shape[0], q.shape[1] // d
+    pos = np.ascontiguousarray(pos, np.int32)
+    if tps is None:
+        tps = attn_tiles_per_split(max_len if max_len else stride)
+    out = np.empty((rows, Hq * d), np.uint16)
+    keep = None
+    arr = None
+    if pts is not None:
+        keep = [np.ascontiguousarray(t, np.int32) for t in pts]
+        arr = (i32p * rows)(*[_p(t, i32p) for t in keep])
+    ks = None if k_scale is None else np.ascontiguousarray(k_scale, np.float32)
+    vs = None if v_scale is None else np.ascontiguousarray(v_scale, np.float32)
+    lib.g4o_attn_split(_p(q, u16p), rows, Hq, Hk, d, scale, cache_k.ctypes.data,
+                       cache_v.ctypes.data, _p(ks, f32p), _p(vs, f32p), bits, group, stride,
+                       _p(pos, i32p), arr, window, tps, _p(out, u16p))
+    return out
+
+
 _REF = []
 
 
@@ -211,5 +249,7 @@ def ref_lib():
     r.ref_fp8_encode.argtypes = [_c.c_double]
     r.ref_rmsnorm_bf16.argtypes = [u16p, u16p, _c.c_float, _c.c_int, _c.c_int, u16p]
     r.ref_rope_tables.argtypes = [_c.c_double, _c.c_int, _c.c_int, f32p, f32p]
+    r.ref_gqa_attention_bf16.argtypes = [u16p, u16p, u16p, _c.c_float, _c.c_int, _c.c_int,
+                                         _c.c_int, _c.c_int, u16p]
     _REF.append(r)
     return r
