@@ -74,6 +74,7 @@ def main():
                                        "attn"],
                     help="run one configuration and print its detail (profiling runs)")
     ap.add_argument("--T", type=int, default=1024, help="token count for --only tN")
+    ap.add_argument("--attn-case", default=None, help="run only this bench_attn case")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the non-GEMM layer ops are "
@@ -438,6 +439,8 @@ def bench_attn(torch, L, randn, gen, timed, args):
              ("T8_sessions_ctx65536_int8", 8, 65536, 8, 128)]
     out = {}
     for name, rows, ctx, bits, group in cases:
+        if getattr(args, "attn_case", None) and name != args.attn_case:
+            continue
         stride = ctx
         pages = stride // 16
         kb, vb = {16: (256, 256), 8: (128, 128), 4: (64, 64), 5: (80, 64)}[bits]

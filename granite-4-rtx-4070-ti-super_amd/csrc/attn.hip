@@ -103,36 +103,50 @@ __host__ __device__ constexpr int v_row_bytes(int bits) {
   return bits == 16 ? 2 * kHd : bits == 8 ? kHd : kHd / 2;
 }
 
-// Eight K elements (dims c .. c + 7, c a multiple of 8) of one cached row as
-// bf16: the value (bf16 cache) or the integer code.
+// Raw bytes of eight K elements (dims c .. c + 7, c a multiple of 8) of one
+// cached row: bf16 16 B, int8 8 B, int4 4 B, K5 4 nibble bytes + the high-bit
+// plane byte. Loading and converting are separate so that a tile's K and V
+// loads are all in flight before any of them is used.
 template <int BITS>
-__device__ __forceinline__ bf16x8_t load_k8(const uint8_t* row, int c) {
+__device__ __forceinline__ u32x4_t load_k_raw(const uint8_t* row, int c) {
+  u32x4_t r = {0u, 0u, 0u, 0u};
   if constexpr (BITS == 16) {
-    const u32x4_t u = *reinterpret_cast<const u32x4_t*>(row + 2 * c);
-    return __builtin_bit_cast(bf16x8_t, u);
+    r = *reinterpret_cast<const u32x4_t*>(row + 2 * c);
   } else if constexpr (BITS == 8) {
     const u32x2_t u = *reinterpret_cast<const u32x2_t*>(row + c);
+    r.x = u.x;
+    r.y = u.y;
+  } else {
+    r.x = *reinterpret_cast<const uint32_t*>(row + c / 2);
+    if constexpr (BITS == 5) r.y = row[kHd / 2 + c / 8];
+  }
+  return r;
+}
+
+// The eight K elements as bf16: the value (bf16 cache) or the integer code.
+template <int BITS>
+__device__ __forceinline__ bf16x8_t k_raw_bf16(const u32x4_t& r) {
+  if constexpr (BITS == 16) {
+    return __builtin_bit_cast(bf16x8_t, r);
+  } else if constexpr (BITS == 8) {
     uint32_t w[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const uint32_t x = e < 2 ? u.x : u.y;
+      const uint32_t x = e < 2 ? r.x : r.y;
       const int sh = 16 * (e & 1);
       w[e] = int_pair_bf16(static_cast<int8_t>(x >> sh), static_cast<int8_t>(x >> (sh + 8)));
     }
     return as_bf16x8(w[0], w[1], w[2], w[3]);
   } else {
-    const uint32_t x = *reinterpret_cast<const uint32_t*>(row + c / 2);
-    uint32_t hib = 0;
-    if constexpr (BITS == 5) hib = row[kHd / 2 + c / 8];
     constexpr int off = BITS == 5 ? 16 : 8;
     uint32_t w[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      int lo = static_cast<int>((x >> (8 * e)) & 0xFu);
-      int hi = static_cast<int>((x >> (8 * e + 4)) & 0xFu);
+      int lo = static_cast<int>((r.x >> (8 * e)) & 0xFu);
+      int hi = static_cast<int>((r.x >> (8 * e + 4)) & 0xFu);
       if constexpr (BITS == 5) {
-        lo |= static_cast<int>((hib >> (2 * e)) & 1u) << 4;
-        hi |= static_cast<int>((hib >> (2 * e + 1)) & 1u) << 4;
+        lo |= static_cast<int>((r.y >> (2 * e)) & 1u) << 4;
+        hi |= static_cast<int>((r.y >> (2 * e + 1)) & 1u) << 4;
       }
       w[e] = int_pair_bf16(lo - off, hi - off);
     }
@@ -140,30 +154,43 @@ __device__ __forceinline__ bf16x8_t load_k8(const uint8_t* row, int c) {
   }
 }
 
-// Stages the tile's V rows (keys 0..63 of the tile, arena rows from lane
-// `key`'s prow) into LDS as bf16 values / integer codes; invalid keys as 0.
+// V staging: each step moves one 16-byte chunk per lane of the tile's rows
+// (bf16: 4 keys x 16 chunks per step, 16 steps; int8: 8 keys x 8 chunks, 8
+// steps; int4: 16 keys x 4 chunks, 4 steps) from the pool into a row-major
+// LDS tile, as bf16 values / integer codes; keys without an arena row read 0.
 template <int BITS>
-__device__ __forceinline__ void stage_v(const AttnArgs& a, const uint8_t* vbase, int prow,
-                                        uint16_t* vl) {
-  const int lane = threadIdx.x & 63;  // lane within this wave (each wave stages its own tile)
-  if constexpr (BITS == 16) {
-    // 16 chunks of 16 B per row: 4 keys per step.
+struct VStage {
+  static constexpr int kSteps = BITS == 16 ? 16 : BITS == 8 ? 8 : 4;
+  static constexpr int kChunks = 64 / (kTile / kSteps);  // chunks per row
+  static constexpr int kRowB = BITS == 16 ? 256 : BITS == 8 ? 128 : 64;
+};
+
+template <int BITS>
+__device__ __forceinline__ void v_load(const uint8_t* vbase, int prow,
+                                       u32x4_t (&raw)[VStage<BITS>::kSteps]) {
+  using VS = VStage<BITS>;
+  const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int key = 4 * i + (lane >> 4), c = lane & 15;
-      const int pr = __shfl(prow, key);
-      u32x4_t u = {0u, 0u, 0u, 0u};
-      if (pr >= 0) u = *reinterpret_cast<const u32x4_t*>(vbase + static_cast<size_t>(pr) * 256 + 16 * c);
+  for (int i = 0; i < VS::kSteps; ++i) {
+    const int key = i * (64 / VS::kChunks) + lane / VS::kChunks, c = lane % VS::kChunks;
+    const int pr = __shfl(prow, key);
+    const uint32_t z = BITS == 16 || BITS == 8 ? 0u : 0x88888888u;  // int4 code 8 = value 0
+    raw[i] = u32x4_t{z, z, z, z};
+    if (pr >= 0) raw[i] = *reinterpret_cast<const u32x4_t*>(vbase + static_cast<size_t>(pr) * VS::kRowB + 16 * c);
+  }
+}
+
+template <int BITS>
+__device__ __forceinline__ void v_store(const u32x4_t (&raw)[VStage<BITS>::kSteps], uint16_t* vl) {
+  using VS = VStage<BITS>;
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < VS::kSteps; ++i) {
+    const int key = i * (64 / VS::kChunks) + lane / VS::kChunks, c = lane % VS::kChunks;
+    const u32x4_t u = raw[i];
+    if constexpr (BITS == 16) {
       *reinterpret_cast<u32x4_t*>(vl + key * kVPitch + 8 * c) = u;
-    }
-  } else if constexpr (BITS == 8) {
-    // 8 chunks of 16 codes per row: 8 keys per step.
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int key = 8 * i + (lane >> 3), c = lane & 7;
-      const int pr = __shfl(prow, key);
-      u32x4_t u = {0u, 0u, 0u, 0u};
-      if (pr >= 0) u = *reinterpret_cast<const u32x4_t*>(vbase + static_cast<size_t>(pr) * 128 + 16 * c);
+    } else if constexpr (BITS == 8) {
       uint32_t w[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -174,15 +201,7 @@ __device__ __forceinline__ void stage_v(const AttnArgs& a, const uint8_t* vbase,
       uint16_t* dst = vl + key * kVPitch + 16 * c;
       *reinterpret_cast<u32x4_t*>(dst) = u32x4_t{w[0], w[1], w[2], w[3]};
       *reinterpret_cast<u32x4_t*>(dst + 8) = u32x4_t{w[4], w[5], w[6], w[7]};
-    }
-  } else {
-    // int4 V (also under K5): 4 chunks of 32 codes per row: 16 keys per step.
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = 16 * i + (lane >> 2), c = lane & 3;
-      const int pr = __shfl(prow, key);
-      u32x4_t u = {0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};  // code 8 = value 0
-      if (pr >= 0) u = *reinterpret_cast<const u32x4_t*>(vbase + static_cast<size_t>(pr) * 64 + 16 * c);
+    } else {
       uint32_t w[16];
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
@@ -197,7 +216,6 @@ __device__ __forceinline__ void stage_v(const AttnArgs& a, const uint8_t* vbase,
         *reinterpret_cast<u32x4_t*>(dst + 8 * e) = u32x4_t{w[4 * e], w[4 * e + 1], w[4 * e + 2], w[4 * e + 3]};
     }
   }
-  (void)a;
 }
 
 // Completes this wave's LDS writes before other lanes of the wave read them
@@ -271,21 +289,44 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
   for (int nb = 0; nb < 8; ++nb) o[nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   float m = -INFINITY, l = 0.0f;
 
+  // Page-table entry of position p (-1 past the split's end; arena rows
+  // outside [0, stride) are skipped like the append kernels skip them).
+  auto arena_row_of = [&](int p) {
+    if (p >= t_end_max) return -1;
+    const int r = pt != nullptr ? pt[p] : p;
+    return (r >= 0 && r < a.stride) ? r : -1;
+  };
+  int prow_next = active ? arena_row_of(t_first + lane) : -1;
   for (int t0 = active ? t_first : t_end_max; t0 < t_end_max; t0 += kTile) {
-    // Arena row of key t0 + lane (-1: past the split's end or outside the arena).
-    int prow = -1;
-    if (t0 + lane < t_end_max) {
-      const int p = t0 + lane;
-      const int r = pt != nullptr ? pt[p] : p;
-      prow = (r >= 0 && r < a.stride) ? r : -1;
+    // Arena row of key t0 + lane; the next tile's entry is fetched a tile ahead.
+    const int prow = prow_next;
+    prow_next = arena_row_of(t0 + kTile + lane);
+    // Every K and V load of the tile first (one memory round trip), then V
+    // and the scales to LDS.
+    u32x4_t vraw[VStage<BITS>::kSteps];
+    v_load<BITS>(vbase, prow, vraw);
+    u32x4_t kraw[4][4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      const int kr = __shfl(prow, 16 * mb + n);  // key 16 mb + n: the A row of this lane
+      const uint8_t* krow = kbase + static_cast<size_t>(kr >= 0 ? kr : 0) * kKb;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kraw[mb][s] = load_k_raw<BITS>(krow, 32 * s + 8 * g);
     }
-    // V tile -> LDS (bf16 values / codes), scales -> LDS.
-    stage_v<BITS>(a, vbase, prow, vl);
+    float ksr[kNgrp], vsr[kNgrp];
     if constexpr (kQuant) {
 #pragma unroll
       for (int gi = 0; gi < kNgrp; ++gi) {
-        ksc_l[lane * kNgrp + gi] = prow >= 0 ? kscb[static_cast<size_t>(prow) * kNgrp + gi] : 0.0f;
-        vsc_l[lane * kNgrp + gi] = prow >= 0 ? vscb[static_cast<size_t>(prow) * kNgrp + gi] : 0.0f;
+        ksr[gi] = prow >= 0 ? kscb[static_cast<size_t>(prow) * kNgrp + gi] : 0.0f;
+        vsr[gi] = prow >= 0 ? vscb[static_cast<size_t>(prow) * kNgrp + gi] : 0.0f;
+      }
+    }
+    v_store<BITS>(vraw, vl);
+    if constexpr (kQuant) {
+#pragma unroll
+      for (int gi = 0; gi < kNgrp; ++gi) {
+        ksc_l[lane * kNgrp + gi] = ksr[gi];
+        vsc_l[lane * kNgrp + gi] = vsr[gi];
       }
     }
     const unsigned long long kvalid = __ballot(prow >= 0);
@@ -294,11 +335,9 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
     float sv[4][4];
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) {
-      const int kr = __shfl(prow, 16 * mb + n);  // key 16 mb + n (the A row of lane l)
-      const uint8_t* krow = kbase + static_cast<size_t>(kr >= 0 ? kr : 0) * kKb;
       bf16x8_t ka[4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) ka[s] = load_k8<BITS>(krow, 32 * s + 8 * g);
+      for (int s = 0; s < 4; ++s) ka[s] = k_raw_bf16<BITS>(kraw[mb][s]);
       f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
       if constexpr (!kQuant || GROUP == kHd) {
 #pragma unroll
@@ -424,10 +463,11 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
   }
 }
 
-// One workgroup per (head, row) rescales and sums the row's split-block partials:
-// the splits' maxima and weights w_s = exp(m_s - M) in parallel (weights
-// kept in LDS), then each half of the workgroup sums every other split's
-// o_s w_s for all 128 dims, four splits in flight per lane.
+// One workgroup per (head, row) rescales and sums the row's split-block
+// partials: every (m, l) and partial output is loaded at once (a lane per
+// block for (m, l); each half of the workgroup holds every other block's o
+// for all 128 dims), then M = max m, w = exp(m - M), L = sum l w and
+// out = bf16(sum o w / L).
 constexpr int kCombineThreads = 256;
 
 __device__ __forceinline__ float block_reduce(float v, bool is_max, float* red) {
@@ -446,7 +486,8 @@ __device__ __forceinline__ float block_reduce(float v, bool is_max, float* red) 
 }
 
 __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(AttnArgs a) {
-  __shared__ float s_w[kAttnMaxSplits];
+  constexpr int kPer = kAttnMaxSplits / kAttnWaves / 2;  // blocks summed per lane (max)
+  __shared__ float s_w[kAttnMaxSplits / kAttnWaves];
   __shared__ float s_red[kCombineThreads / 64];
   __shared__ float s_half[kHd];
   const int h = blockIdx.x, row = blockIdx.y;
@@ -457,32 +498,28 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(AttnArgs 
   const int s0 = a.window > 0 ? max(0, len - a.window) / span : 0;
   const size_t base = (static_cast<size_t>(row) * a.Hq + h) * a.nblk;
   const int t = threadIdx.x;
-  float mx = -INFINITY;
-  for (int s = s0 + t; s < used; s += kCombineThreads) mx = fmaxf(mx, a.part_ml[base + s].x);
-  const float M = block_reduce(mx, true, s_red);
-  float ls = 0.0f;
-  for (int s = s0 + t; s < used; s += kCombineThreads) {
-    const float2 ml = a.part_ml[base + s];
-    const float w = expf(ml.x - M);
-    s_w[s - s0] = w;
-    ls += ml.y * w;
-  }
-  const float L = block_reduce(ls, false, s_red);  // its barriers also publish s_w
   const int d = t & (kHd - 1), half = t >> 7;
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  int s = s0 + half;
-  for (; s + 6 < used; s += 8) {
+  // One round of loads: this lane's (m, l) and its half's partial outputs.
+  const float2 ml = s0 + t < used ? a.part_ml[base + s0 + t] : make_float2(-INFINITY, 0.0f);
+  float ov[kPer];
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-      acc[k] += a.part_o[(base + s + 2 * k) * kHd + d] * s_w[s + 2 * k - s0];
+  for (int j = 0; j < kPer; ++j) {
+    const int sb = s0 + half + 2 * j;
+    ov[j] = sb < used ? a.part_o[(base + sb) * kHd + d] : 0.0f;
   }
-  for (; s < used; s += 2) acc[0] += a.part_o[(base + s) * kHd + d] * s_w[s - s0];
-  float v = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-  if (half == 1) s_half[d] = v;
+  const float M = block_reduce(ml.x, true, s_red);
+  const float w = s0 + t < used ? expf(ml.x - M) : 0.0f;
+  if (s0 + t < used) s_w[t] = w;
+  const float L = block_reduce(ml.y * w, false, s_red);  // its barriers also publish s_w
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j)
+    if (s0 + half + 2 * j < used) acc += ov[j] * s_w[half + 2 * j];
+  if (half == 1) s_half[d] = acc;
   __syncthreads();
   if (half == 0)
     a.out[(static_cast<size_t>(row) * a.Hq + h) * kHd + d] =
-        static_cast<uint16_t>(f32_to_bf16((v + s_half[d]) / L));
+        static_cast<uint16_t>(f32_to_bf16((acc + s_half[d]) / L));
 }
 
 }  // namespace
