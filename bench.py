@@ -495,6 +495,40 @@ def bench_attn(torch, L, randn, gen, timed, args):
                      "frac_peak": round(gbs / PEAK_GBS, 4), "sets": nsets}
         del sets, scratch
         torch.cuda.empty_cache()
+    # Causal prefill attention over the pool: T = 512 from position 0 (int8, config
+    # 3's shape) and T = 8192 at positions 57344.. (K5V4 group 32, config 4's shape).
+    # MFMA-bound: the figure is TFLOP/s of the QK^T and PV products over the
+    # causal (lower-triangular) key ranges.
+    for name, T, pos0, bits, group in (("prefill_T512_int8", 512, 0, 8, 128),
+                                       ("prefill_T8192_at57344_k5v4g32", 8192, 57344, 5, 32)):
+        if getattr(args, "attn_case", None) and name != args.attn_case:
+            continue
+        stride = pos0 + T
+        kb, vb = {16: (256, 256), 8: (128, 128), 4: (64, 64), 5: (80, 64)}[bits]
+        ng = D // group
+        st = {"k": torch.randint(0, 256, (HK * stride * kb,), generator=gen, device=dev,
+                                 dtype=torch.uint8),
+              "v": torch.randint(0, 256, (HK * stride * vb,), generator=gen, device=dev,
+                                 dtype=torch.uint8),
+              "ks": torch.rand((HK * stride * ng,), generator=gen, device=dev) * 0.005,
+              "vs": torch.rand((HK * stride * ng,), generator=gen, device=dev) * 0.1,
+              "q": randn((T, HQ * D)),
+              "pt": (torch.randperm(stride // 16, generator=gen, device=dev).to(torch.int32)[:, None] * 16 +
+                     torch.arange(16, device=dev, dtype=torch.int32)).reshape(-1)}
+        o = torch.empty((T, HQ * D), dtype=torch.bfloat16, device=dev)
+
+        def fnp(s):
+            L.call("granite4_prefill_attn", s["q"], T, HQ, HK, D, 1.0 / 128, s["k"], s["v"], s["ks"],
+                   s["vs"], bits, group, stride, pos0, s["pt"], 0, o)
+
+        steps = 20 if T <= 512 else 3
+        ms = timed(fnp, steps, 1, [st])
+        keys = sum(pos0 + r + 1 for r in range(T))
+        flops = 4.0 * HQ * D * keys
+        out[name] = {"us": round(ms * 1e3, 3), "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 2),
+                     "frac_bf16_peak": round(flops / (ms * 1e-3) / 2.5e15, 4)}
+        del st
+        torch.cuda.empty_cache()
     return out
 
 

@@ -522,6 +522,269 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(AttnArgs 
         static_cast<uint16_t>(f32_to_bf16((acc + s_half[d]) / L));
 }
 
+// ---------------------------------------------------------------------------
+// Causal prefill attention over the pool (prefill_gemm.cu:626-1188,
+// prefill_attention :1392-1474): query rows at positions base + r, each
+// attending to [lo, base + r] in one pass of 64-position tiles.
+//
+// One workgroup = one KV head x 16 consecutive positions: its 4 waves each
+// own 4 positions x the 4 query heads (16 MFMA columns, the decode wave's
+// layout), and share every K / V tile, which the 256 lanes stage into LDS
+// once (codes converted to exact bf16 integers, scales alongside). Per tile
+// each wave runs S^T = K Q^T with A read from the K tile, the causal / window
+// mask, the online softmax, and O^T += V^T P^T as the decode kernel does; the
+// output is bf16(o * (1 / l)) (prefill_gemm.cu:930-940).
+// ---------------------------------------------------------------------------
+constexpr int kKPitch = kHd + 8;  // K tile pitch (bf16): 272 B, 16 rows on distinct banks
+constexpr int kPrefillPos = 16;   // positions per workgroup (4 per wave)
+
+struct PrefillArgs {
+  const uint16_t* q;  // [rows][Hq][128]
+  const uint8_t* k;
+  const uint8_t* v;
+  const float* ksc;
+  const float* vsc;
+  float scale;
+  int Hq, stride, rows, base, window;
+  const int* d_pt;
+  uint16_t* out;      // [rows][Hq][128]
+};
+
+// Stages K (converted) and V of keys [j0, j0 + 64) for all 4 waves: thread t
+// moves chunk t (and t + 256, ...) of the tile, chunk = 16 bytes of one row's
+// codes; keys past kv_end or without an arena row store zeros.
+template <int BITS, int GROUP>
+__device__ __forceinline__ void prefill_stage(const PrefillArgs& a, const uint8_t* kbase,
+                                              const uint8_t* vbase, const float* kscb,
+                                              const float* vscb, int j0, int kv_end,
+                                              uint16_t* ks, uint16_t* vs, float* ksc_l,
+                                              float* vsc_l, unsigned* s_valid) {
+  constexpr bool kQuant = BITS != 16;
+  constexpr int kNgrp = kQuant ? kHd / GROUP : 1;
+  constexpr int kKb = k_row_bytes(BITS);
+  const int t = threadIdx.x;
+  auto arena_row = [&](int key) {
+    const int p = j0 + key;
+    if (p >= kv_end) return -1;
+    const int r = a.d_pt != nullptr ? a.d_pt[p] : p;
+    return (r >= 0 && r < a.stride) ? r : -1;
+  };
+  // K: elements per 16-byte chunk = 8 (bf16), 16 (int8), 32 (int4 / K5 nibbles).
+  constexpr int kKElems = BITS == 16 ? 8 : BITS == 8 ? 16 : 32;
+  constexpr int kKChunks = kTile * kHd / kKElems;
+#pragma unroll
+  for (int it = 0; it < (kKChunks + kAttnWaves * 64 - 1) / (kAttnWaves * 64); ++it) {
+    const int idx = t + it * kAttnWaves * 64;
+    if (idx >= kKChunks) break;
+    const int key = idx / (kHd / kKElems), c = (idx % (kHd / kKElems)) * kKElems;  // first dim
+    const int pr = arena_row(key);
+    uint16_t* dst = ks + key * kKPitch + c;
+    const uint8_t* row = kbase + static_cast<size_t>(pr >= 0 ? pr : 0) * kKb;
+    if constexpr (BITS == 16) {
+      u32x4_t u = {0u, 0u, 0u, 0u};
+      if (pr >= 0) u = *reinterpret_cast<const u32x4_t*>(row + 2 * c);
+      *reinterpret_cast<u32x4_t*>(dst) = u;
+    } else {
+#pragma unroll
+      for (int h = 0; h < kKElems / 8; ++h) {
+        bf16x8_t kv = __builtin_bit_cast(bf16x8_t, u32x4_t{0u, 0u, 0u, 0u});
+        if (pr >= 0) kv = k_raw_bf16<BITS>(load_k_raw<BITS>(row, c + 8 * h));
+        *reinterpret_cast<bf16x8_t*>(dst + 8 * h) = kv;
+      }
+    }
+    if (c == 0 && kQuant) {
+#pragma unroll
+      for (int gi = 0; gi < kNgrp; ++gi) {
+        ksc_l[key * kNgrp + gi] = pr >= 0 ? kscb[static_cast<size_t>(pr) * kNgrp + gi] : 0.0f;
+        vsc_l[key * kNgrp + gi] = pr >= 0 ? vscb[static_cast<size_t>(pr) * kNgrp + gi] : 0.0f;
+      }
+    }
+    if (c == 0) s_valid[key] = pr >= 0 ? 1u : 0u;
+  }
+  // V: the decode staging's chunking (16-byte chunks of the row), over 256 lanes.
+  using VS = VStage<BITS>;
+  constexpr int kVRowChunks = VS::kChunks;
+  constexpr int kVChunks = kTile * kVRowChunks;
+#pragma unroll
+  for (int it = 0; it < (kVChunks + kAttnWaves * 64 - 1) / (kAttnWaves * 64); ++it) {
+    const int idx = t + it * kAttnWaves * 64;
+    if (idx >= kVChunks) break;
+    const int key = idx / kVRowChunks, c = idx % kVRowChunks;
+    const int pr = arena_row(key);
+    const uint32_t z = BITS == 16 || BITS == 8 ? 0u : 0x88888888u;
+    u32x4_t u = {z, z, z, z};
+    if (pr >= 0) u = *reinterpret_cast<const u32x4_t*>(vbase + static_cast<size_t>(pr) * VS::kRowB + 16 * c);
+    if constexpr (BITS == 16) {
+      *reinterpret_cast<u32x4_t*>(vs + key * kVPitch + 8 * c) = u;
+    } else if constexpr (BITS == 8) {
+      uint32_t w[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t x = u[e >> 1];
+        const int sh = 16 * (e & 1);
+        w[e] = int_pair_bf16(static_cast<int8_t>(x >> sh), static_cast<int8_t>(x >> (sh + 8)));
+      }
+      uint16_t* dst = vs + key * kVPitch + 16 * c;
+      *reinterpret_cast<u32x4_t*>(dst) = u32x4_t{w[0], w[1], w[2], w[3]};
+      *reinterpret_cast<u32x4_t*>(dst + 8) = u32x4_t{w[4], w[5], w[6], w[7]};
+    } else {
+      uint32_t w[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t x = u[e >> 2];
+        const int b = 8 * (e & 3);
+        w[e] = int_pair_bf16(static_cast<int>((x >> b) & 0xFu) - 8,
+                             static_cast<int>((x >> (b + 4)) & 0xFu) - 8);
+      }
+      uint16_t* dst = vs + key * kVPitch + 32 * c;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        *reinterpret_cast<u32x4_t*>(dst + 8 * e) = u32x4_t{w[4 * e], w[4 * e + 1], w[4 * e + 2], w[4 * e + 3]};
+    }
+  }
+}
+
+template <int BITS, int GROUP>
+__global__ __launch_bounds__(kAttnWaves * 64) void attn_prefill_kernel(PrefillArgs a) {
+  constexpr bool kQuant = BITS != 16;
+  constexpr int kNgrp = kQuant ? kHd / GROUP : 1;
+  constexpr int kKb = k_row_bytes(BITS), kVb = v_row_bytes(BITS);
+  __shared__ __align__(16) uint16_t ks[kTile * kKPitch];
+  __shared__ __align__(16) uint16_t vs[kTile * kVPitch];
+  __shared__ float ksc_l[kTile * kNgrp], vsc_l[kTile * kNgrp];
+  __shared__ unsigned s_valid[kTile];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane >> 4, n = lane & 15;
+  const int hkv = blockIdx.y;
+  const int p0 = blockIdx.x * kPrefillPos;
+  const int r = p0 + 4 * wave + (n >> 2);  // this lane's query row
+  const int hq = hkv * kGq + (n & 3);
+  const bool live = r < a.rows;
+  const int my_pos = a.base + r;
+  const int my_lo = a.window > 0 ? max(0, my_pos + 1 - a.window) : 0;
+  const int last = min(p0 + kPrefillPos, a.rows) - 1;
+  const int kv_end = min(a.base + last + 1, a.stride);
+  const int j_first = a.window > 0 ? (max(0, a.base + p0 + 1 - a.window) / kTile) * kTile : 0;
+
+  bf16x8_t qb[4];
+  {
+    const uint16_t* qp = a.q + (static_cast<size_t>(live ? r : 0) * a.Hq + hq) * kHd;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      u32x4_t u = {0u, 0u, 0u, 0u};
+      if (live) u = *reinterpret_cast<const u32x4_t*>(qp + 32 * s + 8 * g);
+      qb[s] = __builtin_bit_cast(bf16x8_t, u);
+    }
+  }
+  const uint8_t* kbase = a.k + static_cast<size_t>(hkv) * a.stride * kKb;
+  const uint8_t* vbase = a.v + static_cast<size_t>(hkv) * a.stride * kVb;
+  const float* kscb = kQuant ? a.ksc + static_cast<size_t>(hkv) * a.stride * kNgrp : nullptr;
+  const float* vscb = kQuant ? a.vsc + static_cast<size_t>(hkv) * a.stride * kNgrp : nullptr;
+
+  f32x4_t o[8];
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) o[nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  float m = -INFINITY, l = 0.0f;
+
+  for (int j0 = j_first; j0 < kv_end; j0 += kTile) {
+    __syncthreads();  // the previous tile's readers are done
+    prefill_stage<BITS, GROUP>(a, kbase, vbase, kscb, vscb, j0, kv_end, ks, vs, ksc_l, vsc_l,
+                               s_valid);
+    __syncthreads();
+    float sv[4][4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      bf16x8_t ka[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        ka[s] = *reinterpret_cast<const bf16x8_t*>(ks + (16 * mb + n) * kKPitch + 32 * s + 8 * g);
+      f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      if constexpr (!kQuant || GROUP == kHd) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s], qb[s], acc, 0, 0, 0);
+        if constexpr (kQuant) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[i] = acc[i] * ksc_l[(16 * mb + 4 * g + i) * kNgrp];
+        }
+      } else {
+        constexpr int kSteps = GROUP / 32;
+#pragma unroll
+        for (int gi = 0; gi < kNgrp; ++gi) {
+          f32x4_t part = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int s = gi * kSteps; s < (gi + 1) * kSteps; ++s)
+            part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s], qb[s], part, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[i] += part[i] * ksc_l[(16 * mb + 4 * g + i) * kNgrp + gi];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = 16 * mb + 4 * g + i, j = j0 + key;
+        const bool ok = live && j <= my_pos && j >= my_lo && s_valid[key] != 0u;
+        sv[mb][i] = ok ? bf16_to_f32(f32_to_bf16(a.scale * acc[i])) : -INFINITY;
+      }
+    }
+    float mx = m;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sv[mb][i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float alpha = mx == -INFINITY ? 1.0f : __expf(m - mx);
+    m = mx;
+    l *= alpha;
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) o[nb] *= alpha;
+    float e[4][4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        e[mb][i] = m == -INFINITY ? 0.0f : __expf(sv[mb][i] - m);
+        l += e[mb][i];
+      }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      bf16x8_t pb[kNgrp];
+#pragma unroll
+      for (int gi = 0; gi < kNgrp; ++gi) {
+        float pv[8];
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          const int mb = 2 * s + (jj >> 2), i = jj & 3;
+          const float sc = kQuant ? vsc_l[(16 * mb + 4 * g + i) * kNgrp + gi] : 1.0f;
+          pv[jj] = e[mb][i] * sc;
+        }
+        pb[gi] = as_bf16x8(pack_bf16_hw(pv[0], pv[1]), pack_bf16_hw(pv[2], pv[3]),
+                           pack_bf16_hw(pv[4], pv[5]), pack_bf16_hw(pv[6], pv[7]));
+      }
+      const int kk = n >> 2, dd = 4 * (n & 3);
+      const uint16_t* r1 = vs + (32 * s + 4 * g + kk) * kVPitch + dd;
+      const uint16_t* r2 = r1 + 16 * kVPitch;
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) {
+        const u32x2_t lo2 = lds_read_tr(r1 + 16 * nb);
+        const u32x2_t hi2 = lds_read_tr(r2 + 16 * nb);
+        const bf16x8_t va = as_bf16x8(lo2.x, lo2.y, hi2.x, hi2.y);
+        const int gi = kQuant ? (16 * nb) / GROUP : 0;
+        o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[gi], o[nb], 0, 0, 0);
+      }
+    }
+  }
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+  if (!live) return;
+  const float inv = 1.0f / l;
+  uint16_t* dst = a.out + (static_cast<size_t>(r) * a.Hq + hq) * kHd + 4 * g;
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb)
+    *reinterpret_cast<u32x2_t*>(dst + 16 * nb) =
+        u32x2_t{pack_bf16_hw(o[nb][0] * inv, o[nb][1] * inv), pack_bf16_hw(o[nb][2] * inv, o[nb][3] * inv)};
+}
+
 }  // namespace
 }  // namespace g4
 
@@ -552,12 +815,83 @@ void launch_attn_bits(const AttnArgs& a, int group, dim3 grid, hipStream_t st) {
   }
 }
 
+template <int BITS>
+void launch_prefill_bits(const PrefillArgs& a, int group, dim3 grid, hipStream_t st) {
+  if constexpr (BITS == 16) {
+    (void)group;
+    hipLaunchKernelGGL((attn_prefill_kernel<16, kHd>), grid, kAttnWaves * 64, 0, st, a);
+  } else {
+    if (group == kHd) hipLaunchKernelGGL((attn_prefill_kernel<BITS, kHd>), grid, kAttnWaves * 64, 0, st, a);
+    else if (group == 64) hipLaunchKernelGGL((attn_prefill_kernel<BITS, 64>), grid, kAttnWaves * 64, 0, st, a);
+    else hipLaunchKernelGGL((attn_prefill_kernel<BITS, 32>), grid, kAttnWaves * 64, 0, st, a);
+  }
+}
+
 }  // namespace
 }  // namespace g4
 
 using namespace g4;
 
 extern "C" {
+
+int granite4_prefill_attn(const uint16_t* q_rot, int rows, int Hq, int Hk, int d, float scale,
+                          const void* cache_k, const void* cache_v, const float* k_scale,
+                          const float* v_scale, int bits, int group, int stride, int base_pos,
+                          const int* d_pt, int window, uint16_t* out) {
+  const bool quant = bits != 16;
+  if (q_rot == nullptr || out == nullptr || cache_k == nullptr || cache_v == nullptr ||
+      !std::isfinite(scale) || d != kHd || Hk <= 0 || Hq != kGq * Hk || rows <= 0 ||
+      base_pos < 0 || stride < base_pos + rows || window < 0 ||
+      (bits != 16 && bits != 8 && bits != 4 && bits != 5) ||
+      (quant && (k_scale == nullptr || v_scale == nullptr ||
+                 (group != 32 && group != 64 && group != kHd)))) {
+    std::fprintf(stderr, "granite4: granite4_prefill_attn: invalid arguments\n");
+    return -1;
+  }
+  PrefillArgs a{};
+  a.q = q_rot;
+  a.k = static_cast<const uint8_t*>(cache_k);
+  a.v = static_cast<const uint8_t*>(cache_v);
+  a.ksc = k_scale;
+  a.vsc = v_scale;
+  a.scale = scale;
+  a.Hq = Hq;
+  a.stride = stride;
+  a.rows = rows;
+  a.base = base_pos;
+  a.window = window;
+  a.d_pt = d_pt;
+  a.out = out;
+  const dim3 grid((rows + kPrefillPos - 1) / kPrefillPos, Hk);
+  const hipStream_t st = stream();
+  switch (bits) {
+    case 16: launch_prefill_bits<16>(a, group, grid, st); break;
+    case 8: launch_prefill_bits<8>(a, group, grid, st); break;
+    case 4: launch_prefill_bits<4>(a, group, grid, st); break;
+    default: launch_prefill_bits<5>(a, group, grid, st); break;
+  }
+  return launch_status("granite4_prefill_attn");
+}
+
+int granite4_prefill_attention(const uint16_t* q_rot, const uint16_t* cache_k,
+                               const uint16_t* cache_v, float scale, int Hq, int Hk, int d,
+                               int base_pos, int rows, int stride, uint16_t* out,
+                               const int8_t* cache_k8, const int8_t* cache_v8,
+                               const float* k_scale, const float* v_scale, int int8,
+                               const uint8_t* cache_k4, const uint8_t* cache_v4, int int4,
+                               const int* d_pt, int k5, int window) {
+  if ((int8 && int4) || (k5 && !int4)) {
+    std::fprintf(stderr, "granite4: granite4_prefill_attention: invalid arguments\n");
+    return -1;
+  }
+  const int bits = int8 ? 8 : (int4 ? (k5 ? 5 : 4) : 16);
+  const void* ck = int8 ? static_cast<const void*>(cache_k8)
+                        : (int4 ? static_cast<const void*>(cache_k4) : cache_k);
+  const void* cv = int8 ? static_cast<const void*>(cache_v8)
+                        : (int4 ? static_cast<const void*>(cache_v4) : cache_v);
+  return granite4_prefill_attn(q_rot, rows, Hq, Hk, d, scale, ck, cv, k_scale, v_scale, bits, kHd,
+                               stride, base_pos, d_pt, window, out);
+}
 
 size_t granite4_attn_split_scratch_bytes(int Hq, int rows, int stride) {
   if (Hq <= 0 || rows <= 0 || stride <= 0) return 0;

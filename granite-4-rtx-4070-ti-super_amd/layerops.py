@@ -82,6 +82,9 @@ _SIG = {
     "granite4_attn_split": [P, P, P, F, I, I, I, I, P, I, I, P, P, P, P, P, P, I, P, P, I, P, I,
                             P, P, P, I, P, P, I, I, I],
     "granite4_attn_paged": [P, I, I, I, I, F, P, P, P, P, I, I, I, I, P, P, P, P, I, I, P, P],
+    "granite4_prefill_attn": [P, I, I, I, I, F, P, P, P, P, I, I, I, I, P, I, P],
+    "granite4_prefill_attention": [P, P, P, F, I, I, I, I, I, I, P, P, P, P, P, I, P, P, I, P, I,
+                                   I],
     "granite4_host_fp8_encode": [P, _c.c_size_t, F, P],
     "granite4_host_kv_codes": [P, _c.c_size_t, F, I, P],
     "granite4_selftest_bf16": [P],

@@ -354,6 +354,26 @@ int granite4_attn_split(const uint16_t* q, const uint16_t* cache_k, const uint16
                         const int* row_tbase, const int* row_tail, int kv_hint, int k5,
                         int window);
 
+/* Causal prefill attention over the pool (prefill_gemm.h:87-101
+ * prefill_attention; bools as int): query rows q_rot [rows][Hq * d] at
+ * positions [base_pos, base_pos + rows) attend to positions [0, position]
+ * (the last `window` when window > 0) through d_pt (NULL: contiguous);
+ * out [rows][Hq * d]. d = 128, Hq = 4 Hk only; stride >= base_pos + rows. */
+int granite4_prefill_attention(const uint16_t* q_rot, const uint16_t* cache_k,
+                               const uint16_t* cache_v, float scale, int Hq, int Hk, int d,
+                               int base_pos, int rows, int stride, uint16_t* out,
+                               const int8_t* cache_k8, const int8_t* cache_v8,
+                               const float* k_scale, const float* v_scale, int int8,
+                               const uint8_t* cache_k4, const uint8_t* cache_v4, int int4,
+                               const int* d_pt, int k5, int window);
+
+/* granite4_prefill_attention for every pool format of this library (bits 16
+ * / 8 / 4 / 5, group 32 / 64 / 128 scales). New entry point. */
+int granite4_prefill_attn(const uint16_t* q_rot, int rows, int Hq, int Hk, int d, float scale,
+                          const void* cache_k, const void* cache_v, const float* k_scale,
+                          const float* v_scale, int bits, int group, int stride, int base_pos,
+                          const int* d_pt, int window, uint16_t* out);
+
 /* The same attention for any pool format of this library, including the
  * group scales of granite4_rope_append: bits 16 / 8 / 4 / 5 (K5 K + int4 V),
  * group 32 / 64 / 128 (scales [Hk][stride][128 / group]; ignored for bf16).
@@ -423,6 +443,18 @@ inline int gpu_multi_kv_append(const uint16_t* k, const uint16_t* v, int bits, v
   return granite4_multi_kv_append(k, v, bits, ck, cv, ks, vs, d_rows, rows, stride, Hk, d);
 }
 
+// prefill_gemm.h:94-101 (bool flags, default arguments).
+inline int prefill_attention(const uint16_t* q_rot, const uint16_t* cache_k,
+                             const uint16_t* cache_v, float scale, int Hq, int Hk, int d,
+                             int base_pos, int rows, int stride, uint16_t* out,
+                             const int8_t* cache_k8, const int8_t* cache_v8, const float* k_scale,
+                             const float* v_scale, bool int8, const uint8_t* cache_k4,
+                             const uint8_t* cache_v4, bool int4, const int* d_pt = nullptr,
+                             bool k5 = false, int window = 0) {
+  return granite4_prefill_attention(q_rot, cache_k, cache_v, scale, Hq, Hk, d, base_pos, rows,
+                                    stride, out, cache_k8, cache_v8, k_scale, v_scale, int8,
+                                    cache_k4, cache_v4, int4, d_pt, k5, window);
+}
 // attention_gpu.h:17, 53-60 (bool flags, default arguments).
 inline size_t attn_split_scratch_bytes(int Hq, int rows, int stride) {
   return granite4_attn_split_scratch_bytes(Hq, rows, stride);

@@ -520,3 +520,84 @@ void g4o_attn_split(const uint16_t* q, int rows, int Hq, int Hk, int d, float sc
   free(ls);
   free(os);
 }
+
+/* One head's online softmax over the 64-position tiles [t_first, t_end) of
+ * positions, keys masked outside [lo, len): the state the split and prefill
+ * kernels keep (attention_split.cu:873-1020, prefill_gemm.cu:878-928). */
+static void attn_tiles(const float* qf, int hk, float scale, const void* cache_k,
+                       const void* cache_v, const float* k_scale, const float* v_scale, int bits,
+                       int group, int d, int stride, const int* pt, int t_first, int t_end, int lo,
+                       float* m_out, float* l_out, float* oacc) {
+  const int ngrp = d / group, tile = 64, quant = bits != 16;
+  const int kb = kv_row_bytes(bits, d, 1), vb = kv_row_bytes(bits, d, 0);
+  float logit[64], pbf[64 * 32];
+  float m = -INFINITY, l = 0.0f;
+  for (int i = 0; i < d; ++i) oacc[i] = 0.0f;
+  for (int t0 = t_first; t0 < t_end; t0 += tile) {
+    float mx = m;
+    for (int j = 0; j < tile; ++j) {
+      const int p = t0 + j;
+      if (p >= t_end || p < lo) {
+        logit[j] = -INFINITY;
+        continue;
+      }
+      const int arow = pt != NULL ? pt[p] : p;
+      const uint8_t* krow = (const uint8_t*)cache_k + ((size_t)hk * stride + arow) * kb;
+      float dot = 0.0f;
+      if (!quant) {
+        for (int i = 0; i < d; ++i) dot += qf[i] * kv_elem(krow, bits, 1, d, i);
+      } else {
+        const float* ks = k_scale + ((size_t)hk * stride + arow) * ngrp;
+        for (int g = 0; g < ngrp; ++g) {
+          float part = 0.0f;
+          for (int i = g * group; i < (g + 1) * group; ++i) part += qf[i] * kv_elem(krow, bits, 1, d, i);
+          dot += part * ks[g];
+        }
+      }
+      logit[j] = g4o_bf16_to_f32(g4o_f32_to_bf16(scale * dot));
+      if (logit[j] > mx) mx = logit[j];
+    }
+    const float alpha = mx == -INFINITY ? 1.0f : expf(m - mx);
+    l *= alpha;
+    m = mx;
+    for (int i = 0; i < d; ++i) oacc[i] *= alpha;
+    for (int j = 0; j < tile; ++j) {
+      const float e = m == -INFINITY || logit[j] == -INFINITY ? 0.0f : expf(logit[j] - m);
+      l += e;
+      const int valid = logit[j] != -INFINITY;
+      const int arow = valid ? (pt != NULL ? pt[t0 + j] : t0 + j) : 0;
+      for (int g = 0; g < ngrp; ++g) {
+        const float sv = quant && valid ? v_scale[((size_t)hk * stride + arow) * ngrp + g] : 1.0f;
+        pbf[j * ngrp + g] = g4o_bf16_to_f32(g4o_f32_to_bf16(e * sv));
+      }
+    }
+    for (int j = 0; j < tile; ++j) {
+      if (logit[j] == -INFINITY) continue;
+      const int arow = pt != NULL ? pt[t0 + j] : t0 + j;
+      const uint8_t* vrow = (const uint8_t*)cache_v + ((size_t)hk * stride + arow) * vb;
+      for (int i = 0; i < d; ++i) oacc[i] += pbf[j * ngrp + i / group] * kv_elem(vrow, bits, 0, d, i);
+    }
+  }
+  *m_out = m;
+  *l_out = l;
+}
+
+void g4o_prefill_attn(const uint16_t* q, int rows, int Hq, int Hk, int d, float scale,
+                      const void* cache_k, const void* cache_v, const float* k_scale,
+                      const float* v_scale, int bits, int group, int stride, int base_pos,
+                      const int* pt, int window, uint16_t* out) {
+  const int G = Hq / Hk;
+  float qf[1024], oacc[1024];
+  for (int r = 0; r < rows; ++r) {
+    const int len = base_pos + r + 1;
+    const int lo = window > 0 ? (len - window > 0 ? len - window : 0) : 0;
+    for (int h = 0; h < Hq; ++h) {
+      for (int i = 0; i < d; ++i) qf[i] = g4o_bf16_to_f32(q[((size_t)r * Hq + h) * d + i]);
+      float m, l;
+      attn_tiles(qf, h / G, scale, cache_k, cache_v, k_scale, v_scale, bits, group, d, stride, pt,
+                 (lo / 64) * 64, len, lo, &m, &l, oacc);
+      const float inv = 1.0f / l;
+      for (int i = 0; i < d; ++i) out[((size_t)r * Hq + h) * d + i] = g4o_f32_to_bf16(oacc[i] * inv);
+    }
+  }
+}

@@ -109,6 +109,19 @@ void g4o_attn_split(const uint16_t* q, int rows, int Hq, int Hk, int d, float sc
                     const float* v_scale, int bits, int group, int stride, const int* pos,
                     const int* const* pt, int window, int tps, uint16_t* out);
 
+/* Causal prefill attention over the paged pool (prefill_gemm.cu:626-1188,
+ * prefill_attention :1392-1474; the quantised-cache form keeps the codes and
+ * applies the scales to the logits and probabilities, :942-1188). Query rows
+ * q [rows][Hq][d] sit at positions base_pos + r and attend to positions
+ * [lo, base_pos + r] (lo as g4o_attn_split's window rule) through pt (NULL:
+ * row = position), in one pass of 64-position tiles from position 0: the
+ * same logits, online softmax and bf16(p * v_scale) value product as
+ * g4o_attn_split, and out = bf16(o * (1 / l)). */
+void g4o_prefill_attn(const uint16_t* q, int rows, int Hq, int Hk, int d, float scale,
+                      const void* cache_k, const void* cache_v, const float* k_scale,
+                      const float* v_scale, int bits, int group, int stride, int base_pos,
+                      const int* pt, int window, uint16_t* out);
+
 /* Paged pool: position -> arena row (kv_pool.cc:285-297). */
 void g4o_row_table(const int32_t* block_table, int n, int page, int32_t* out);
 

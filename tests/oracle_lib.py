@@ -58,6 +58,9 @@ def _load():
                                    _c.c_int, _c.c_int, _c.c_int, _c.c_int, u16p, _c.c_long,
                                    vp, vp, f32p, f32p, _c.c_int]),
         "g4o_row_table": (None, [i32p, _c.c_int, _c.c_int, i32p]),
+        "g4o_prefill_attn": (None, [u16p, _c.c_int, _c.c_int, _c.c_int, _c.c_int, _c.c_float, vp,
+                                    vp, f32p, f32p, _c.c_int, _c.c_int, _c.c_int, _c.c_int,
+                                    i32p, _c.c_int, u16p]),
         "g4o_attn_split": (None, [u16p, _c.c_int, _c.c_int, _c.c_int, _c.c_int, _c.c_float, vp,
                                   vp, f32p, f32p, _c.c_int, _c.c_int, _c.c_int, i32p,
                                   _c.POINTER(i32p), _c.c_int, _c.c_int, u16p]),
@@ -230,6 +233,22 @@ def attn_split(q, cache_k, cache_v, k_scale, v_scale, bits, group, stride, pos, 
     lib.g4o_attn_split(_p(q, u16p), rows, Hq, Hk, d, scale, cache_k.ctypes.data,
                        cache_v.ctypes.data, _p(ks, f32p), _p(vs, f32p), bits, group, stride,
                        _p(pos, i32p), arr, window, tps, _p(out, u16p))
+    return out
+
+
+def prefill_attn(q, cache_k, cache_v, k_scale, v_scale, bits, group, stride, base_pos, pt=None,
+                 window=0, scale=1.0 / 128, Hk=8, d=128):
+    """Oracle causal prefill attention: rows q [rows][Hq*d] at positions
+    base_pos + r. Returns uint16 [rows][Hq*d]."""
+    q = np.ascontiguousarray(q, np.uint16)
+    rows, Hq = q.shape[0], q.shape[1] // d
+    out = np.empty((rows, Hq * d), np.uint16)
+    ks = None if k_scale is None else np.ascontiguousarray(k_scale, np.float32)
+    vs = None if v_scale is None else np.ascontiguousarray(v_scale, np.float32)
+    ptc = None if pt is None else np.ascontiguousarray(pt, np.int32)
+    lib.g4o_prefill_attn(_p(q, u16p), rows, Hq, Hk, d, scale, cache_k.ctypes.data,
+                         cache_v.ctypes.data, _p(ks, f32p), _p(vs, f32p), bits, group, stride,
+                         base_pos, _p(ptc, i32p), window, _p(out, u16p))
     return out
 
 

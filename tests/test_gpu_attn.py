@@ -208,3 +208,58 @@ def test_attn_reference_entry_point_int8_and_k5():
                int(int8), None if int8 else dk, None if int8 else dv, int(not int8), None, 0,
                None, None, None, 0, None, None, 0, int(bits == 5), 0)
         np.testing.assert_array_equal(host(out).view(np.uint16), want)
+
+
+# ----------------------------------------------------------------- causal prefill attention
+def run_prefill(q, ck, cv, ks, vs, bits, group, stride, base, d_pt=None, window=0, scale=1.0 / 16):
+    rows = q.shape[0]
+    out = torch.empty((rows, HQ * D), dtype=torch.int16, device="cuda")
+    dks = None if ks is None else dev(ks)
+    dvs = None if vs is None else dev(vs)
+    L.call("granite4_prefill_attn", dev(q), rows, HQ, HK, D, scale, dev(ck), dev(cv), dks, dvs, bits,
+           group, stride, base, d_pt, window, out)
+    return host(out).view(np.uint16)
+
+
+@pytest.mark.parametrize("bits", [16, 8, 4, 5])
+def test_prefill_attn_contiguous(bits):
+    note(f"prefill attn bits={bits}")
+    stride, base, rows = 256, 30, 50
+    ck, cv, ks, vs = make_cache(bits, D, stride, 0xE0 + bits)
+    q = ol.normal_bf16(0xE1 + bits, 0.0, 1.0, rows * HQ * D).reshape(rows, HQ * D)
+    got = run_prefill(q, ck, cv, ks, vs, bits, D, stride, base)
+    want = ol.prefill_attn(q, ck, cv, ks, vs, bits, D, stride, base, scale=1.0 / 16, Hk=HK)
+    check(got, want, vmax(cv, vs, bits), f"prefill bits {bits}")
+
+
+@pytest.mark.parametrize("bits,group,window", [(5, 32, 0), (8, 64, 0), (16, 128, 64), (4, 128, 100)])
+def test_prefill_attn_paged(bits, group, window):
+    note(f"prefill attn paged bits={bits} group={group} window={window}")
+    pages = 24
+    stride = 16 * pages
+    base, rows = 200, 150
+    ck, cv, ks, vs = make_cache(bits, group, stride, 0xE2 + bits + group)
+    rng = np.random.default_rng(bits * 7 + group)
+    pt = ol.row_table(rng.permutation(pages).astype(np.int32), stride)
+    q = ol.normal_bf16(0xE3, 0.0, 1.0, rows * HQ * D).reshape(rows, HQ * D)
+    got = run_prefill(q, ck, cv, ks, vs, bits, group, stride, base, d_pt=dev(pt), window=window)
+    want = ol.prefill_attn(q, ck, cv, ks, vs, bits, group, stride, base, pt=pt, window=window,
+                           scale=1.0 / 16, Hk=HK)
+    check(got, want, vmax(cv, vs, bits), f"prefill paged bits {bits} group {group} w {window}")
+
+
+def test_prefill_attn_t512_from_zero_and_reference_entry_point():
+    """T = 512 from position 0 (BASELINE config 3's prefill shape), int8, and
+    the reference-named granite4_prefill_attention on the same inputs."""
+    note("prefill attn T=512")
+    stride, rows = 512, 512
+    ck, cv, ks, vs = make_cache(8, D, stride, 0xE4)
+    q = ol.normal_bf16(0xE5, 0.0, 1.0, rows * HQ * D).reshape(rows, HQ * D)
+    got = run_prefill(q, ck, cv, ks, vs, 8, D, stride, 0, scale=1.0 / 128)
+    want = ol.prefill_attn(q, ck, cv, ks, vs, 8, D, stride, 0, scale=1.0 / 128, Hk=HK)
+    check(got, want, vmax(cv, vs, 8), "prefill T=512 int8")
+    out = torch.empty((rows, HQ * D), dtype=torch.int16, device="cuda")
+    dk, dv = dev(ck), dev(cv)
+    L.call("granite4_prefill_attention", dev(q), None, None, 1.0 / 128, HQ, HK, D, 0, rows, stride,
+           out, dk, dv, dev(ks), dev(vs), 1, None, None, 0, None, 0, 0)
+    np.testing.assert_array_equal(host(out).view(np.uint16), got)

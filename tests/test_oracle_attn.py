@@ -207,3 +207,82 @@ def test_attn_close_to_f64_softmax(kv_len, tps):
     ex = _exact_attention(_f32(q[0]).astype(np.float64), kf, vf, Hk, kv_len, 1.0 / 8)
     err = np.abs(_f32(got[0]).reshape(Hq, D) - ex)
     assert err.max() <= 2.0 ** -6 * np.abs(vf).max(), err.max()
+
+
+# ----------------------------------------------------------------- prefill (causal) attention
+def test_prefill_attn_vs_reference_host_attention_per_row():
+    """Row r of the causal prefill attention is the reference's decode
+    attention over the first base + r + 1 positions (same tolerance as above)."""
+    r = ol.ref_lib()
+    if r is None:
+        pytest.skip("oracle/_ref not built (no /root/reference)")
+    Hq, Hk, base, rows = 8, 2, 90, 40
+    n = base + rows
+    q = _rand_q(0xB1, rows, Hq)
+    k, v = _bf16_cache(0xB2, Hk, n, std=0.5)
+    got = ol.prefill_attn(q, k, v, None, None, 16, D, n, base, scale=1.0 / 16, Hk=Hk)
+    kk = k.view(np.uint16).reshape(Hk, n, D)
+    vv = v.view(np.uint16).reshape(Hk, n, D)
+    vmax = np.abs(_f32(v.view(np.uint16))).max()
+    for row in range(rows):
+        L = base + row + 1
+        kc = np.ascontiguousarray(kk[:, :L]).reshape(-1)
+        vc = np.ascontiguousarray(vv[:, :L]).reshape(-1)
+        want = np.empty(Hq * D, np.uint16)
+        r.ref_gqa_attention_bf16(q[row].ctypes.data_as(ol.u16p), kc.ctypes.data_as(ol.u16p),
+                                 vc.ctypes.data_as(ol.u16p), 1.0 / 16, Hq, Hk, D, L,
+                                 want.ctypes.data_as(ol.u16p))
+        u = _ulps(got[row], want)
+        absd = np.abs(_f32(got[row]) - _f32(want))
+        assert np.all((u <= 2) | (absd <= 2.0 ** -9 * vmax)), (row, u.max())
+
+
+@pytest.mark.parametrize("bits", [16, 8, 5])
+def test_prefill_attn_is_the_single_split_attention(bits):
+    """One pass over every tile is the split attention with one split; the
+    only difference is the final o / l (split combine) against o * (1 / l)
+    (prefill): at most one bf16 step."""
+    Hq, Hk, base, rows = 8, 2, 150, 20
+    n = base + rows
+    rng = np.random.default_rng(bits)
+    kb, vb = ol.KV_ROW_BYTES[bits]
+    if bits == 16:
+        ck, cv = _bf16_cache(0xB3, Hk, n, std=0.5)
+        ks = vs = None
+    else:
+        ck = rng.integers(0, 256, Hk * n * kb, dtype=np.uint8)
+        cv = rng.integers(0, 256, Hk * n * vb, dtype=np.uint8)
+        ks = (rng.random(Hk * n, dtype=np.float32) * 0.01).astype(np.float32)
+        vs = (rng.random(Hk * n, dtype=np.float32) * 0.1).astype(np.float32)
+    q = _rand_q(0xB4, rows, Hq)
+    a = ol.prefill_attn(q, ck, cv, ks, vs, bits, D, n, base, scale=1.0 / 16, Hk=Hk)
+    b = ol.attn_split(q, ck, cv, ks, vs, bits, D, n, [base + r for r in range(rows)],
+                      scale=1.0 / 16, Hk=Hk, tps=1000)
+    assert _ulps(a, b).max() <= 1
+    assert np.mean(a == b) > 0.9
+
+
+def test_prefill_attn_exact_properties():
+    Hq, Hk, n = 8, 2, 130
+    q = _rand_q(0xB5, n, Hq)
+    k, v = _bf16_cache(0xB6, Hk, n)
+    vv = v.view(np.uint16).reshape(Hk, n, D)
+    out = ol.prefill_attn(q, k, v, None, None, 16, D, n, 0, Hk=Hk)
+    for h in range(Hq):  # position 0 sees one key
+        np.testing.assert_array_equal(out[0, h * D:(h + 1) * D], vv[h // 4, 0])
+    out = ol.prefill_attn(q, k, v, None, None, 16, D, n, 0, window=1, Hk=Hk)
+    for r in (0, 63, 64, 129):  # window 1: each row sees its own key
+        for h in range(Hq):
+            np.testing.assert_array_equal(out[r, h * D:(h + 1) * D], vv[h // 4, r])
+    # paged == contiguous
+    stride = 16 * 12
+    rng = np.random.default_rng(3)
+    pt = ol.row_table(rng.permutation(stride // 16).astype(np.int32), n)
+    kp = np.zeros((Hk, stride, D), np.uint16)
+    vp = np.zeros((Hk, stride, D), np.uint16)
+    kp[:, pt] = k.view(np.uint16).reshape(Hk, n, D)
+    vp[:, pt] = vv
+    a = ol.prefill_attn(q, kp.view(np.uint8).reshape(-1), vp.view(np.uint8).reshape(-1), None, None,
+                        16, D, stride, 0, pt=pt, Hk=Hk)
+    b = ol.prefill_attn(q, k, v, None, None, 16, D, n, 0, Hk=Hk)
+    np.testing.assert_array_equal(a, b)
