@@ -536,7 +536,6 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(AttnArgs 
 // output is bf16(o * (1 / l)) (prefill_gemm.cu:930-940).
 // ---------------------------------------------------------------------------
 constexpr int kKPitch = kHd + 8;  // K tile pitch (bf16): 272 B, 16 rows on distinct banks
-constexpr int kPrefillPos = 16;   // positions per workgroup (4 per wave)
 
 struct PrefillArgs {
   const uint16_t* q;  // [rows][Hq][128]
@@ -644,11 +643,15 @@ __device__ __forceinline__ void prefill_stage(const PrefillArgs& a, const uint8_
   }
 }
 
-template <int BITS, int GROUP>
+// CB: column blocks per wave (4 CB positions x 4 heads each); the K and V^T
+// fragments read from LDS serve all CB blocks, and a staged tile serves
+// 16 CB positions.
+template <int BITS, int GROUP, int CB>
 __global__ __launch_bounds__(kAttnWaves * 64) void attn_prefill_kernel(PrefillArgs a) {
   constexpr bool kQuant = BITS != 16;
   constexpr int kNgrp = kQuant ? kHd / GROUP : 1;
   constexpr int kKb = k_row_bytes(BITS), kVb = v_row_bytes(BITS);
+  constexpr int kPos = kAttnWaves * 4 * CB;  // positions per workgroup
   __shared__ __align__(16) uint16_t ks[kTile * kKPitch];
   __shared__ __align__(16) uint16_t vs[kTile * kVPitch];
   __shared__ float ksc_l[kTile * kNgrp], vsc_l[kTile * kNgrp];
@@ -657,24 +660,30 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_prefill_kernel(PrefillAr
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, n = lane & 15;
   const int hkv = blockIdx.y;
-  const int p0 = blockIdx.x * kPrefillPos;
-  const int r = p0 + 4 * wave + (n >> 2);  // this lane's query row
+  const int p0 = blockIdx.x * kPos;
   const int hq = hkv * kGq + (n & 3);
-  const bool live = r < a.rows;
-  const int my_pos = a.base + r;
-  const int my_lo = a.window > 0 ? max(0, my_pos + 1 - a.window) : 0;
-  const int last = min(p0 + kPrefillPos, a.rows) - 1;
+  int r[CB], my_pos[CB], my_lo[CB];
+  bool live[CB];
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb) {
+    r[cb] = p0 + 4 * (CB * wave + cb) + (n >> 2);  // this lane's query row in block cb
+    live[cb] = r[cb] < a.rows;
+    my_pos[cb] = a.base + r[cb];
+    my_lo[cb] = a.window > 0 ? max(0, my_pos[cb] + 1 - a.window) : 0;
+  }
+  const int last = min(p0 + kPos, a.rows) - 1;
   const int kv_end = min(a.base + last + 1, a.stride);
   const int j_first = a.window > 0 ? (max(0, a.base + p0 + 1 - a.window) / kTile) * kTile : 0;
 
-  bf16x8_t qb[4];
-  {
-    const uint16_t* qp = a.q + (static_cast<size_t>(live ? r : 0) * a.Hq + hq) * kHd;
+  bf16x8_t qb[CB][4];
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb) {
+    const uint16_t* qp = a.q + (static_cast<size_t>(live[cb] ? r[cb] : 0) * a.Hq + hq) * kHd;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       u32x4_t u = {0u, 0u, 0u, 0u};
-      if (live) u = *reinterpret_cast<const u32x4_t*>(qp + 32 * s + 8 * g);
-      qb[s] = __builtin_bit_cast(bf16x8_t, u);
+      if (live[cb]) u = *reinterpret_cast<const u32x4_t*>(qp + 32 * s + 8 * g);
+      qb[cb][s] = __builtin_bit_cast(bf16x8_t, u);
     }
   }
   const uint8_t* kbase = a.k + static_cast<size_t>(hkv) * a.stride * kKb;
@@ -682,85 +691,110 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_prefill_kernel(PrefillAr
   const float* kscb = kQuant ? a.ksc + static_cast<size_t>(hkv) * a.stride * kNgrp : nullptr;
   const float* vscb = kQuant ? a.vsc + static_cast<size_t>(hkv) * a.stride * kNgrp : nullptr;
 
-  f32x4_t o[8];
+  f32x4_t o[CB][8];
+  float m[CB], l[CB];
 #pragma unroll
-  for (int nb = 0; nb < 8; ++nb) o[nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  float m = -INFINITY, l = 0.0f;
+  for (int cb = 0; cb < CB; ++cb) {
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) o[cb][nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    m[cb] = -INFINITY;
+    l[cb] = 0.0f;
+  }
 
   for (int j0 = j_first; j0 < kv_end; j0 += kTile) {
     __syncthreads();  // the previous tile's readers are done
     prefill_stage<BITS, GROUP>(a, kbase, vbase, kscb, vscb, j0, kv_end, ks, vs, ksc_l, vsc_l,
                                s_valid);
     __syncthreads();
-    float sv[4][4];
+    float e[CB][4][4];
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) {
       bf16x8_t ka[4];
 #pragma unroll
       for (int s = 0; s < 4; ++s)
         ka[s] = *reinterpret_cast<const bf16x8_t*>(ks + (16 * mb + n) * kKPitch + 32 * s + 8 * g);
-      f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-      if constexpr (!kQuant || GROUP == kHd) {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s], qb[s], acc, 0, 0, 0);
-        if constexpr (kQuant) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[i] = acc[i] * ksc_l[(16 * mb + 4 * g + i) * kNgrp];
-        }
-      } else {
-        constexpr int kSteps = GROUP / 32;
-#pragma unroll
-        for (int gi = 0; gi < kNgrp; ++gi) {
-          f32x4_t part = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-          for (int s = gi * kSteps; s < (gi + 1) * kSteps; ++s)
-            part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s], qb[s], part, 0, 0, 0);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[i] += part[i] * ksc_l[(16 * mb + 4 * g + i) * kNgrp + gi];
-        }
-      }
+      float ksv[4][kNgrp];
+      bool kv_ok[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int key = 16 * mb + 4 * g + i, j = j0 + key;
-        const bool ok = live && j <= my_pos && j >= my_lo && s_valid[key] != 0u;
-        sv[mb][i] = ok ? bf16_to_f32(f32_to_bf16(a.scale * acc[i])) : -INFINITY;
+        const int key = 16 * mb + 4 * g + i;
+        kv_ok[i] = s_valid[key] != 0u;
+#pragma unroll
+        for (int gi = 0; gi < kNgrp; ++gi) ksv[i][gi] = kQuant ? ksc_l[key * kNgrp + gi] : 1.0f;
+      }
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+        f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (!kQuant || GROUP == kHd) {
+#pragma unroll
+          for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s], qb[cb][s], acc, 0, 0, 0);
+          if constexpr (kQuant) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = acc[i] * ksv[i][0];
+          }
+        } else {
+          constexpr int kSteps = GROUP / 32;
+#pragma unroll
+          for (int gi = 0; gi < kNgrp; ++gi) {
+            f32x4_t part = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int s = gi * kSteps; s < (gi + 1) * kSteps; ++s)
+              part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s], qb[cb][s], part, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] += part[i] * ksv[i][gi];
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int j = j0 + 16 * mb + 4 * g + i;
+          const bool ok = live[cb] && j <= my_pos[cb] && j >= my_lo[cb] && kv_ok[i];
+          e[cb][mb][i] = ok ? bf16_to_f32(f32_to_bf16(a.scale * acc[i])) : -INFINITY;
+        }
       }
     }
-    float mx = m;
+    // Online softmax per column block (e holds the logits until here).
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+    for (int cb = 0; cb < CB; ++cb) {
+      float mx = m[cb];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sv[mb][i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float alpha = mx == -INFINITY ? 1.0f : __expf(m - mx);
-    m = mx;
-    l *= alpha;
+      for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) o[nb] *= alpha;
-    float e[4][4];
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, e[cb][mb][i]);
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float alpha = mx == -INFINITY ? 1.0f : __expf(m[cb] - mx);
+      m[cb] = mx;
+      l[cb] *= alpha;
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+      for (int nb = 0; nb < 8; ++nb) o[cb][nb] *= alpha;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        e[mb][i] = m == -INFINITY ? 0.0f : __expf(sv[mb][i] - m);
-        l += e[mb][i];
-      }
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          e[cb][mb][i] = mx == -INFINITY ? 0.0f : __expf(e[cb][mb][i] - mx);
+          l[cb] += e[cb][mb][i];
+        }
+    }
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      bf16x8_t pb[kNgrp];
+      float vsv[8][kNgrp];
 #pragma unroll
-      for (int gi = 0; gi < kNgrp; ++gi) {
-        float pv[8];
+      for (int jj = 0; jj < 8; ++jj) {
+        const int key = 16 * (2 * s + (jj >> 2)) + 4 * g + (jj & 3);
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          const int mb = 2 * s + (jj >> 2), i = jj & 3;
-          const float sc = kQuant ? vsc_l[(16 * mb + 4 * g + i) * kNgrp + gi] : 1.0f;
-          pv[jj] = e[mb][i] * sc;
-        }
-        pb[gi] = as_bf16x8(pack_bf16_hw(pv[0], pv[1]), pack_bf16_hw(pv[2], pv[3]),
-                           pack_bf16_hw(pv[4], pv[5]), pack_bf16_hw(pv[6], pv[7]));
+        for (int gi = 0; gi < kNgrp; ++gi) vsv[jj][gi] = kQuant ? vsc_l[key * kNgrp + gi] : 1.0f;
       }
+      bf16x8_t pb[CB][kNgrp];
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+        for (int gi = 0; gi < kNgrp; ++gi) {
+          float pv[8];
+#pragma unroll
+          for (int jj = 0; jj < 8; ++jj) pv[jj] = e[cb][2 * s + (jj >> 2)][jj & 3] * vsv[jj][gi];
+          pb[cb][gi] = as_bf16x8(pack_bf16_hw(pv[0], pv[1]), pack_bf16_hw(pv[2], pv[3]),
+                                 pack_bf16_hw(pv[4], pv[5]), pack_bf16_hw(pv[6], pv[7]));
+        }
       const int kk = n >> 2, dd = 4 * (n & 3);
       const uint16_t* r1 = vs + (32 * s + 4 * g + kk) * kVPitch + dd;
       const uint16_t* r2 = r1 + 16 * kVPitch;
@@ -770,19 +804,26 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_prefill_kernel(PrefillAr
         const u32x2_t hi2 = lds_read_tr(r2 + 16 * nb);
         const bf16x8_t va = as_bf16x8(lo2.x, lo2.y, hi2.x, hi2.y);
         const int gi = kQuant ? (16 * nb) / GROUP : 0;
-        o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[gi], o[nb], 0, 0, 0);
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+          o[cb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[cb][gi], o[cb][nb], 0, 0, 0);
       }
     }
   }
-  l += __shfl_xor(l, 16);
-  l += __shfl_xor(l, 32);
-  if (!live) return;
-  const float inv = 1.0f / l;
-  uint16_t* dst = a.out + (static_cast<size_t>(r) * a.Hq + hq) * kHd + 4 * g;
 #pragma unroll
-  for (int nb = 0; nb < 8; ++nb)
-    *reinterpret_cast<u32x2_t*>(dst + 16 * nb) =
-        u32x2_t{pack_bf16_hw(o[nb][0] * inv, o[nb][1] * inv), pack_bf16_hw(o[nb][2] * inv, o[nb][3] * inv)};
+  for (int cb = 0; cb < CB; ++cb) {
+    float lt = l[cb];
+    lt += __shfl_xor(lt, 16);
+    lt += __shfl_xor(lt, 32);
+    if (!live[cb]) continue;
+    const float inv = 1.0f / lt;
+    uint16_t* dst = a.out + (static_cast<size_t>(r[cb]) * a.Hq + hq) * kHd + 4 * g;
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb)
+      *reinterpret_cast<u32x2_t*>(dst + 16 * nb) =
+          u32x2_t{pack_bf16_hw(o[cb][nb][0] * inv, o[cb][nb][1] * inv),
+                  pack_bf16_hw(o[cb][nb][2] * inv, o[cb][nb][3] * inv)};
+  }
 }
 
 }  // namespace
@@ -815,15 +856,22 @@ void launch_attn_bits(const AttnArgs& a, int group, dim3 grid, hipStream_t st) {
   }
 }
 
+// Column blocks per wave. Measured (T=512 int8 / T=8192 at 57344 K5V4): CB = 1
+// 33.7 us / 38.2 ms, CB = 2 45.1 us / 49.2 ms, CB = 4 69.0 us / 42.2 ms - the
+// kernel is VALU-bound (softmax, bf16 logit rounding, P packing ~3x the MFMA
+// cycles per tile), so more registers per wave only cost occupancy.
+constexpr int kPrefillCb = 1;
+
 template <int BITS>
 void launch_prefill_bits(const PrefillArgs& a, int group, dim3 grid, hipStream_t st) {
+  constexpr int CB = kPrefillCb;
   if constexpr (BITS == 16) {
     (void)group;
-    hipLaunchKernelGGL((attn_prefill_kernel<16, kHd>), grid, kAttnWaves * 64, 0, st, a);
+    hipLaunchKernelGGL((attn_prefill_kernel<16, kHd, CB>), grid, kAttnWaves * 64, 0, st, a);
   } else {
-    if (group == kHd) hipLaunchKernelGGL((attn_prefill_kernel<BITS, kHd>), grid, kAttnWaves * 64, 0, st, a);
-    else if (group == 64) hipLaunchKernelGGL((attn_prefill_kernel<BITS, 64>), grid, kAttnWaves * 64, 0, st, a);
-    else hipLaunchKernelGGL((attn_prefill_kernel<BITS, 32>), grid, kAttnWaves * 64, 0, st, a);
+    if (group == kHd) hipLaunchKernelGGL((attn_prefill_kernel<BITS, kHd, CB>), grid, kAttnWaves * 64, 0, st, a);
+    else if (group == 64) hipLaunchKernelGGL((attn_prefill_kernel<BITS, 64, CB>), grid, kAttnWaves * 64, 0, st, a);
+    else hipLaunchKernelGGL((attn_prefill_kernel<BITS, 32, CB>), grid, kAttnWaves * 64, 0, st, a);
   }
 }
 
@@ -862,7 +910,8 @@ int granite4_prefill_attn(const uint16_t* q_rot, int rows, int Hq, int Hk, int d
   a.window = window;
   a.d_pt = d_pt;
   a.out = out;
-  const dim3 grid((rows + kPrefillPos - 1) / kPrefillPos, Hk);
+  constexpr int kPos = kAttnWaves * 4 * kPrefillCb;
+  const dim3 grid((rows + kPos - 1) / kPos, Hk);
   const hipStream_t st = stream();
   switch (bits) {
     case 16: launch_prefill_bits<16>(a, group, grid, st); break;
