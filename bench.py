@@ -218,7 +218,9 @@ def main():
             r = measure_ops(args.T, max(2, min(8, 4096 // args.T)), 8, 128, 0, 8, args.steps,
                             args.warmup)
         elif args.only == "decode":
-            r = bench_decode(torch, L, randn, cos_t, sin_t, emb, gamma, stream, args)
+            r = {"decode_T1": bench_decode(torch, L, randn, cos_t, sin_t, emb, gamma, stream, args),
+                 "decode_T1_with_attention": bench_decode(torch, L, randn, cos_t, sin_t, emb, gamma,
+                                                          stream, args, with_attn=True)}
         elif args.only == "t8":
             r = bench_multi8(torch, L, randn, cos_t, sin_t, gamma, work, gen, stream, timed, args)
         elif args.only == "attn":
@@ -241,6 +243,10 @@ def main():
     result_extra["decode_T1"] = decode
 
     if not args.quick:
+        log("config 1 + attention: the decode step with the split-KV attention per layer")
+        result_extra["decode_T1_with_attention"] = bench_decode(torch, L, randn, cos_t, sin_t, emb,
+                                                                gamma, stream, args, with_attn=True)
+        log(json.dumps(result_extra["decode_T1_with_attention"]))
         log("config 2: T=8 sessions")
         result_extra["decode_T8"] = bench_multi8(torch, L, randn, cos_t, sin_t, gamma, work, gen,
                                                  stream, timed, args)
@@ -297,9 +303,12 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-def bench_decode(torch, L, randn, cos_t, sin_t, emb, gamma, stream, args, layers=40):
+def bench_decode(torch, L, randn, cos_t, sin_t, emb, gamma, stream, args, layers=40,
+                 with_attn=False):
     """161 launches: embed, then per layer add_rmsnorm (attention residual),
-    rope + bf16 KV append at *d_pos, add_rmsnorm (FFN residual), SwiGLU."""
+    rope + bf16 KV append at *d_pos, add_rmsnorm (FFN residual), SwiGLU.
+    with_attn adds the split-KV attention of the appended pool (split +
+    combine, 241 launches): the KV read of a 4322-position context."""
     dev = "cuda"
     stride = 8192
     pos = torch.tensor([4321], dtype=torch.int32, device=dev)
@@ -309,6 +318,9 @@ def bench_decode(torch, L, randn, cos_t, sin_t, emb, gamma, stream, args, layers
     normed = torch.empty_like(res)
     act = torch.empty((1, I), dtype=torch.bfloat16, device=dev)
     q_rot = torch.empty((1, HQ * D), dtype=torch.bfloat16, device=dev)
+    attn_out = torch.empty((1, HQ * D), dtype=torch.bfloat16, device=dev)
+    scratch = torch.empty(L.call_size("granite4_attn_split_scratch_bytes", HQ, 1, stride),
+                          dtype=torch.uint8, device=dev)
     per = []
     for _ in range(layers):
         per.append({"b_attn": randn((1, H)), "b_ffn": randn((1, H)), "gu": randn((1, 2 * I)),
@@ -322,6 +334,9 @@ def bench_decode(torch, L, randn, cos_t, sin_t, emb, gamma, stream, args, layers
             L.call("granite4_add_rmsnorm", res, p["b_attn"], 1.0, gamma, 1e-5, 1, H, res, normed)
             L.call("granite4_rope_append_at_pos", p["q"], p["k"], p["v"], cos_t, sin_t, 65536,
                    pos, pt, HQ, HK, D, 16, 128, q_rot, a.k, a.v, a.k_scale, a.v_scale, stride)
+            if with_attn:
+                L.call("granite4_attn_paged", q_rot, 1, HQ, HK, D, 1.0 / 128, a.k, a.v, None, None,
+                       16, 128, stride, 0, pos, pt, None, None, 0, 0, scratch, attn_out)
             L.call("granite4_add_rmsnorm", res, p["b_ffn"], 1.0, gamma, 1e-5, 1, H, res, normed)
             L.call("granite4_swiglu", p["gu"], 1, I, act)
 
@@ -361,7 +376,10 @@ def bench_decode(torch, L, randn, cos_t, sin_t, emb, gamma, stream, args, layers
     torch.cuda.synchronize()
     graph_us = e0.elapsed_time(e1) / reps * 1e3
     ideal = B_EMBED + layers * (2 * B_NORM_BF16 + B_SWIGLU_BF16 + B_ROPE[16])
-    return {"layers": layers, "launches": 1 + 4 * layers, "graph_us_per_step": round(graph_us, 2),
+    if with_attn:
+        ideal += layers * (int(pos.item()) + 1) * HK * kv_bytes_per_position(16, 128)
+    return {"layers": layers, "launches": 1 + (6 if with_attn else 4) * layers,
+            "graph_us_per_step": round(graph_us, 2),
             "eager_us_per_step": round(eager_us, 2), "ideal_bytes": ideal,
             "ideal_us_at_peak": round(ideal / PEAK_GBS / 1e3, 3)}
 
