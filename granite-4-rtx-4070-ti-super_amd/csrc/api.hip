@@ -195,7 +195,9 @@ int granite4_host_fp8_encode(const float* y, size_t n, float scale, uint8_t* cod
 
 int granite4_host_kv_codes(const float* x, size_t n, float scale, int qmax, int32_t* codes) {
   if (x == nullptr || codes == nullptr || qmax <= 0) return -1;
-  for (size_t i = 0; i < n; ++i) codes[i] = kv_code(x[i], scale, qmax);
+  // The reciprocal form the append kernels use (bit-identical to kv_code).
+  const float inv = 1.0f / scale;
+  for (size_t i = 0; i < n; ++i) codes[i] = kv_code_inv(x[i], scale, inv, qmax);
   return 0;
 }
 

@@ -132,6 +132,29 @@ __host__ __device__ __forceinline__ int kv_code(float x, float s, int qmax) {
   return static_cast<int>(c);
 }
 
+// True when kv_code_inv may take the reciprocal form for scale s: the
+// reciprocal and every residual that can decide a code stay normal.
+__host__ __device__ __forceinline__ bool kv_recip_ok(float s) {
+  return s >= 0x1p-96f && s < 0x1p100f;
+}
+
+// kv_code with inv = 1.0f / s (correctly rounded) precomputed: the quotient
+// q0 = x * inv is corrected once with its exact residual r = x - q0 * s
+// (one fma), and RN(q0 + r * inv) is the correctly rounded x / s (Markstein,
+// "Computation of elementary functions on the IBM RISC System/6000", 1990:
+// a correctly rounded reciprocal and a faithful quotient suffice). So the
+// code equals kv_code's bit for bit, with a few VALU operations instead of
+// an IEEE division. Scales outside kv_recip_ok use the division.
+__host__ __device__ __forceinline__ int kv_code_inv(float x, float s, float inv, int qmax) {
+  if (!kv_recip_ok(s)) return kv_code(x, s, qmax);
+  const float q0 = x * inv;
+  // |q0| >= 256 saturates every code (qmax <= 127) and may be inf, whose
+  // residual would be NaN: keep q0 there.
+  const float q = fabsf(q0) < 256.0f ? fmaf(fmaf(-q0, s, x), inv, q0) : q0;
+  const float c = fminf(fmaxf(roundf(q), -static_cast<float>(qmax)), static_cast<float>(qmax));
+  return static_cast<int>(c);
+}
+
 }  // namespace g4
 
 #endif  // G4_MATH_H

@@ -67,7 +67,7 @@ __device__ __forceinline__ Fp8Enc fp8_scale_of(float amax) { return fp8_enc_of(f
 // workgroup must call it (it synchronises when WPR > 1).
 template <int VPL, int WPR>
 struct NormRow {
-  V8 xv[VPL], wv[VPL];
+  V8 xv[VPL], wv[VPL], bv[VPL];
   bool ok[VPL];
   size_t base;
   int row, part, lane;
@@ -75,8 +75,10 @@ struct NormRow {
   float r;
 };
 
+// First half of norm_row_front: the row's indices and its loads (x, branch,
+// gamma).
 template <int VPL, int WPR>
-__device__ __forceinline__ void norm_row_front(const NormArgs& a, int rg, NormRow<VPL, WPR>& t) {
+__device__ __forceinline__ void norm_row_load(const NormArgs& a, int rg, NormRow<VPL, WPR>& t) {
   constexpr int RPB = 4 / WPR;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -85,44 +87,52 @@ __device__ __forceinline__ void norm_row_front(const NormArgs& a, int rg, NormRo
   const bool live = row < a.rows;
   const int nvec = a.cols >> 3;
   const size_t base = live ? static_cast<size_t>(row) * static_cast<size_t>(a.cols) : 0;
-
-  V8 (&xv)[VPL] = t.xv;
-  V8 (&wv)[VPL] = t.wv;
-  bool (&ok)[VPL] = t.ok;
-  V8 bv[VPL];
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     const int vi = (j * WPR + part) * 64 + lane;
-    ok[j] = live && vi < nvec;
-    xv[j] = V8{{0u, 0u, 0u, 0u}};
-    bv[j] = V8{{0u, 0u, 0u, 0u}};
-    wv[j] = V8{{0u, 0u, 0u, 0u}};
-    if (ok[j]) {
+    t.ok[j] = live && vi < nvec;
+    t.xv[j] = V8{{0u, 0u, 0u, 0u}};
+    t.bv[j] = V8{{0u, 0u, 0u, 0u}};
+    t.wv[j] = V8{{0u, 0u, 0u, 0u}};
+    if (t.ok[j]) {
       // x and branch stream; res' goes out through the caches, where the FP8
       // op's encode pass re-reads it.
-      xv[j] = ld8_nt(a.x + base + 8 * vi);
-      if (a.branch != nullptr) bv[j] = ld8_nt(a.branch + base + 8 * vi);
-      wv[j] = ld8(a.w + 8 * vi);
+      t.xv[j] = ld8_nt(a.x + base + 8 * vi);
+      if (a.branch != nullptr) t.bv[j] = ld8_nt(a.branch + base + 8 * vi);
+      t.wv[j] = ld8(a.w + 8 * vi);
     }
   }
+  t.base = base;
+  t.row = row;
+  t.part = part;
+  t.lane = lane;
+  t.live = live;
+}
+
+// Second half: res' = x + mult * branch (bf16; stored when res_out is given)
+// and the row's r = 1 / rms. Every thread of the workgroup must call it (it
+// synchronises when WPR > 1).
+template <int VPL, int WPR>
+__device__ __forceinline__ void norm_row_finish(const NormArgs& a, NormRow<VPL, WPR>& t) {
+  const int wave = threadIdx.x >> 6;
   double ss = 0.0;
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     if (a.branch != nullptr) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float lo = lo_bf16(xv[j].w[e]) + a.mult * lo_bf16(bv[j].w[e]);
-        const float hi = hi_bf16(xv[j].w[e]) + a.mult * hi_bf16(bv[j].w[e]);
-        xv[j].w[e] = pack_bf16_hw(lo, hi);
+        const float lo = lo_bf16(t.xv[j].w[e]) + a.mult * lo_bf16(t.bv[j].w[e]);
+        const float hi = hi_bf16(t.xv[j].w[e]) + a.mult * hi_bf16(t.bv[j].w[e]);
+        t.xv[j].w[e] = pack_bf16_hw(lo, hi);
       }
-      if (ok[j] && a.res_out != nullptr) {
-        const int vi = (j * WPR + part) * 64 + lane;
-        st8(a.res_out + base + 8 * vi, xv[j]);
+      if (t.ok[j] && a.res_out != nullptr) {
+        const int vi = (j * WPR + t.part) * 64 + t.lane;
+        st8(a.res_out + t.base + 8 * vi, t.xv[j]);
       }
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float lo = lo_bf16(xv[j].w[e]), hi = hi_bf16(xv[j].w[e]);
+      const float lo = lo_bf16(t.xv[j].w[e]), hi = hi_bf16(t.xv[j].w[e]);
       ss += static_cast<double>(lo * lo);
       ss += static_cast<double>(hi * hi);
     }
@@ -130,7 +140,7 @@ __device__ __forceinline__ void norm_row_front(const NormArgs& a, int rg, NormRo
   ss = wave_sum(ss);
   if (WPR > 1) {
     __shared__ double s_part[kBlock / 64];
-    if (lane == 0) s_part[wave] = ss;
+    if (t.lane == 0) s_part[wave] = ss;
     __syncthreads();
     const int w0 = (wave / WPR) * WPR;
     ss = s_part[w0];
@@ -138,12 +148,15 @@ __device__ __forceinline__ void norm_row_front(const NormArgs& a, int rg, NormRo
     for (int k = 1; k < WPR; ++k) ss += s_part[w0 + k];
     __syncthreads();  // s_part is reused by the next row group
   }
-  t.base = base;
-  t.row = row;
-  t.part = part;
-  t.lane = lane;
-  t.live = live;
   t.r = 1.0f / sqrtf(static_cast<float>(ss / a.cols) + a.eps);
+}
+
+// The lane's share of one row of a row group (4 / WPR rows per 256-thread
+// workgroup): res', the gamma vectors, and the row's r = 1 / rms.
+template <int VPL, int WPR>
+__device__ __forceinline__ void norm_row_front(const NormArgs& a, int rg, NormRow<VPL, WPR>& t) {
+  norm_row_load<VPL, WPR>(a, rg, t);
+  norm_row_finish<VPL, WPR>(a, t);
 }
 
 // One row group of the workgroup; MODE kOutAmax folds into *m.
@@ -332,61 +345,80 @@ __global__ __launch_bounds__(kBlock) void norm_generic_kernel(NormArgs a) {
 
 // Single-launch FP8 form for tensors that fit one resident grid: each
 // 256-thread workgroup (four waves per row, as the two-launch form's first
-// pass, so y and the amax are bit-identical to it) holds up to kNormHold rows'
-// y = bf16(res' * r * w) in VGPRs, the workgroups agree on max |y| with one
-// grid synchronisation, and each encodes what it holds. HBM traffic: x (+
-// branch) read once, res' and codes written once, against a second read of
-// res' in the two-launch form, and one launch instead of two.
-constexpr int kNormHold = 4;
-
-template <int VPL>
-__global__ __launch_bounds__(kBlock) void norm_fp8_fused_kernel(NormArgs a, GridSync gs) {
+// pass, so y and the amax are bit-identical to it) holds up to HR rows'
+// y = bf16(res' * r * w) in VGPRs and HL more in LDS, the workgroups agree on
+// max |y| with one grid synchronisation, and each encodes what it holds. HBM
+// traffic: x (+ branch) read once, res' and codes written once, against a
+// second read of res' in the two-launch form, and one launch instead of two.
+template <int VPL, int HR, int HL>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(VPL >= 4 ? 1 : 4)))
+void norm_fp8_fused_kernel(NormArgs a, GridSync gs) {
+  __shared__ uint4 s_y[HL > 0 ? HL : 1][VPL][kBlock];
   const unsigned tag = grid_sync_tag(gs);
-  V8 y[kNormHold][VPL];
-  bool ok[kNormHold][VPL];
-  size_t base[kNormHold];
-  int part = 0, lane = 0;
+  V8 y[HR > 0 ? HR : 1][VPL];
   float m = 0.0f;
 #pragma unroll
-  for (int h = 0; h < kNormHold; ++h) {
+  for (int h = 0; h < HR + HL; ++h) {
     const int rg = blockIdx.x + h * gridDim.x;  // uniform over the workgroup
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) ok[h][j] = false;
-    base[h] = 0;
-    if (rg >= a.rows) continue;
+    if (rg >= a.rows) break;
     NormRow<VPL, 4> t;
     norm_row_front<VPL, 4>(a, rg, t);
-    part = t.part;
-    lane = t.lane;
-    base[h] = t.base;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
-      ok[h][j] = t.ok[j];
+      V8 yv;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        y[h][j].w[e] = pack_bf16_hw(lo_bf16(t.xv[j].w[e]) * t.r * lo_bf16(t.wv[j].w[e]),
-                                    hi_bf16(t.xv[j].w[e]) * t.r * hi_bf16(t.wv[j].w[e]));
-        m = fmaxf(m, lo_bf16(y[h][j].w[e] & 0x7fff7fffu));
-        m = fmaxf(m, hi_bf16(y[h][j].w[e] & 0x7fff7fffu));
+        yv.w[e] = pack_bf16_hw(lo_bf16(t.xv[j].w[e]) * t.r * lo_bf16(t.wv[j].w[e]),
+                               hi_bf16(t.xv[j].w[e]) * t.r * hi_bf16(t.wv[j].w[e]));
+        // lanes past the row's end hold zeros (x and w load as 0)
+        m = fmaxf(m, lo_bf16(yv.w[e] & 0x7fff7fffu));
+        m = fmaxf(m, hi_bf16(yv.w[e] & 0x7fff7fffu));
       }
+      if (h < HR) y[h < HR ? h : 0][j] = yv;
+      else s_y[h >= HR ? h - HR : 0][j][threadIdx.x] = make_uint4(yv.w[0], yv.w[1], yv.w[2], yv.w[3]);
     }
   }
   const Fp8Enc f = fp8_scale_of(grid_max(m, gs, tag));
   if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = f.s;
+  const int part = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nvec = a.cols >> 3;
   const auto encode = [&](auto fast_tag) {
 #pragma unroll
-    for (int h = 0; h < kNormHold; ++h)
+    for (int h = 0; h < HR + HL; ++h) {
+      const int rg = blockIdx.x + h * gridDim.x;
+      if (rg >= a.rows) break;
+      const size_t base = static_cast<size_t>(rg) * static_cast<size_t>(a.cols);
 #pragma unroll
       for (int j = 0; j < VPL; ++j) {
-        if (!ok[h][j]) continue;
-        const uint2 c = fp8x8_encode_bf16<decltype(fast_tag)::value>(y[h][j].w, f);
         const int vi = (j * 4 + part) * 64 + lane;
-        st_u32x2_nt(a.codes + base[h] + 8 * vi, c.x, c.y);
+        if (vi >= nvec) continue;
+        V8 yv;
+        if (h < HR) {
+          yv = y[h < HR ? h : 0][j];
+        } else {
+          const uint4 q = s_y[h >= HR ? h - HR : 0][j][threadIdx.x];
+          yv = V8{{q.x, q.y, q.z, q.w}};
+        }
+        const uint2 c = fp8x8_encode_bf16<decltype(fast_tag)::value>(yv.w, f);
+        st_u32x2_nt(a.codes + base + 8 * vi, c.x, c.y);
       }
+    }
   };
   if (f.fast) encode(std::true_type{});
   else encode(std::false_type{});
 }
+
+// Held rows per workgroup of the two single-launch forms: VGPRs only, and
+// VGPRs + LDS for row counts beyond the first's reach.
+#ifndef G4_NORM_DEEP_HR
+#define G4_NORM_DEEP_HR 8
+#endif
+#ifndef G4_NORM_DEEP_HL
+#define G4_NORM_DEEP_HL 4
+#endif
+constexpr int kNormHold = 4;
+constexpr int kNormDeepHR = G4_NORM_DEEP_HR;
+constexpr int kNormDeepHL = G4_NORM_DEEP_HL;
 
 // Waves per row. Four waves per 4096-wide row (2 vectors per lane, 54-62
 // VGPRs, full occupancy) measured faster than one wave per row (8 vectors per
@@ -446,6 +478,23 @@ int launch_norm(NormArgs& a, const char* what) {
   return launch_status(what);
 }
 
+// Launches norm_fp8_fused_kernel<VPL, HR, HL> for the row width when every
+// row fits the resident grid's holds; false (nothing launched) otherwise.
+template <int HR, int HL>
+bool launch_fused_vpl(const NormArgs& a, const GridSync& gs, int nvec) {
+  const auto go = [&](auto kern) {
+    const int resident = resident_blocks(reinterpret_cast<const void*>(kern), kBlock);
+    const int cap = resident < kMaxPartials ? resident : kMaxPartials;
+    if (cap <= 0 || a.rows > static_cast<long long>(cap) * (HR + HL)) return false;
+    const unsigned grid = static_cast<unsigned>(a.rows < cap ? a.rows : cap);
+    hipLaunchKernelGGL(kern, grid, kBlock, 0, stream(), a, gs);
+    return true;
+  };
+  if (nvec <= 256) return go(norm_fp8_fused_kernel<1, HR, HL>);
+  if (nvec <= 512) return go(norm_fp8_fused_kernel<2, HR, HL>);
+  return go(norm_fp8_fused_kernel<4, HR, HL>);
+}
+
 // Launches the single-launch FP8 form when the shape takes the four-waves-
 // per-row vector path (as the two-launch form would) and the rows fit the
 // resident grid; returns false (nothing launched) otherwise.
@@ -456,21 +505,11 @@ bool launch_norm_fp8_fused(const uint16_t* x, const uint16_t* branch, float mult
   if (fp8_launch_mode() != 0 || !norm_vector_path(rows, cols) || pick_wpr(rows) != 4 ||
       nvec > 4 * 64 * 4)
     return false;
-  const void* kern = nvec <= 256   ? reinterpret_cast<const void*>(norm_fp8_fused_kernel<1>)
-                     : nvec <= 512 ? reinterpret_cast<const void*>(norm_fp8_fused_kernel<2>)
-                                   : reinterpret_cast<const void*>(norm_fp8_fused_kernel<4>);
-  const int resident = resident_blocks(kern, kBlock);
-  const int cap = resident < kMaxPartials ? resident : kMaxPartials;
-  if (cap <= 0 || rows > static_cast<long long>(cap) * kNormHold) return false;
-  const unsigned grid = static_cast<unsigned>(rows < cap ? rows : cap);
   NormArgs a{x, branch, mult, w, eps, rows, cols, res_out, nullptr, codes, scale, nullptr, 0,
              nullptr, 0.0};
   const GridSync gs{work_slots(work), work_gen(work)};
-  const hipStream_t st = stream();
-  if (nvec <= 256) hipLaunchKernelGGL(norm_fp8_fused_kernel<1>, grid, kBlock, 0, st, a, gs);
-  else if (nvec <= 512) hipLaunchKernelGGL(norm_fp8_fused_kernel<2>, grid, kBlock, 0, st, a, gs);
-  else hipLaunchKernelGGL(norm_fp8_fused_kernel<4>, grid, kBlock, 0, st, a, gs);
-  return true;
+  return launch_fused_vpl<kNormHold, 0>(a, gs, nvec) ||
+         launch_fused_vpl<kNormDeepHR, kNormDeepHL>(a, gs, nvec);
 }
 
 bool norm_args_ok(const void* x, const void* w, float eps, int rows, int cols) {

@@ -142,9 +142,10 @@ __device__ __forceinline__ void store_quant(const RopeArgs& a, const float* val,
   const float s = am / static_cast<float>(qmax);
   float* scales = is_k ? a.k_scale : a.v_scale;
   if (lane16 % GL == 0) scales[slot * (128 / GROUP) + lane16 / GL] = s;
+  const float inv = 1.0f / s;
   int c[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) c[e] = kv_code(val[e], s, qmax);
+  for (int e = 0; e < 8; ++e) c[e] = kv_code_inv(val[e], s, inv, qmax);
   uint8_t* cache = static_cast<uint8_t*>(is_k ? a.cache_k : a.cache_v);
   if (BITS == 8) {
     uint32_t w0 = 0, w1 = 0;
@@ -174,10 +175,11 @@ __device__ __forceinline__ void store_quant(const RopeArgs& a, const float* val,
 template <int BITS, int GROUP>
 __global__ __launch_bounds__(kBlock) void rope_append_kernel(RopeArgs a) {
   const int lane16 = threadIdx.x & 15;
-  const long long unit = static_cast<long long>(blockIdx.x) * (kBlock / 16) + (threadIdx.x >> 4);
-  if (unit >= static_cast<long long>(a.rows) * a.units_per_row) return;  // whole DPP rows
-  const int r = static_cast<int>(unit / a.units_per_row);
-  const int u = static_cast<int>(unit - static_cast<long long>(r) * a.units_per_row);
+  // rows * units_per_row < 2^31 (checked on the host), so 32-bit indexing.
+  const unsigned unit = blockIdx.x * (kBlock / 16) + (threadIdx.x >> 4);
+  if (unit >= static_cast<unsigned>(a.rows) * static_cast<unsigned>(a.units_per_row)) return;  // whole DPP rows
+  const int r = static_cast<int>(unit / static_cast<unsigned>(a.units_per_row));
+  const int u = static_cast<int>(unit - static_cast<unsigned>(r) * static_cast<unsigned>(a.units_per_row));
   const bool first_half = lane16 < 8;
 
   if (u < a.Hq + a.Hk && (u < a.Hq || a.rotate_k)) {
@@ -322,8 +324,11 @@ int launch_rope_append(RopeArgs a, int bits, int group, const char* what) {
   const long long units = static_cast<long long>(a.rows) * a.units_per_row;
   if (units <= 0) return 0;
   if (a.d == 128 && (bits == 16 || group == 32 || group == 64 || group == 128)) {
+    if (units > INT_MAX) {
+      std::fprintf(stderr, "granite4: %s: %lld (row, head) units exceed 2^31 - 1\n", what, units);
+      return -1;
+    }
     const long long blocks = (units + (kBlock / 16) - 1) / (kBlock / 16);
-    if (blocks > INT_MAX) return -1;
     const unsigned grid = static_cast<unsigned>(blocks);
     switch (bits) {
       case 16: launch_fast_bits<16>(a, 128, grid); break;

@@ -233,6 +233,140 @@ unsigned fused_grid(long long vectors) {
   return static_cast<unsigned>(lanes < cap ? lanes : cap);
 }
 
+// Single-launch FP8 form for tensors beyond the registers' reach: a
+// persistent grid (every workgroup resident, at most kMaxPartials of them)
+// in which each lane holds its first kHoldR vectors of act in VGPRs and the
+// next kHoldL in LDS, and streams the rest once for max |act|. After the
+// grid synchronisation it encodes what it holds, then re-reads and encodes
+// only the streamed rest. HBM traffic per element: 4 B read + 1 B written
+// + 4 B re-read for the streamed fraction only (the two-launch form
+// re-reads everything: 9 B).
+#ifndef G4_SW_HR
+#define G4_SW_HR 18
+#endif
+#ifndef G4_SW_HL
+#define G4_SW_HL 9
+#endif
+#ifndef G4_SW_SU
+#define G4_SW_SU 2
+#endif
+#ifndef G4_SW_HB
+#define G4_SW_HB 4
+#endif
+constexpr int kHoldR = G4_SW_HR;
+constexpr int kHoldL = G4_SW_HL;
+constexpr int kHold = kHoldR + kHoldL;
+constexpr int kHoldBatch = G4_SW_HB;  // held vectors' loads in flight per lane
+constexpr int kStreamU = G4_SW_SU;  // streamed vectors' loads in flight per lane
+
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) void swiglu_fp8_hold_kernel(SwArgs a, GridSync gs) {
+  __shared__ uint4 s_hold[kHoldL > 0 ? kHoldL : 1][kBlock];
+  const unsigned tag = grid_sync_tag(gs);
+  const int nv = a.I >> 3;
+  const int total = a.rows * nv;
+  const int step = gridDim.x * kBlock;
+  const int v0 = blockIdx.x * kBlock + threadIdx.x;
+  float m = 0.0f;
+  // act words of one vector; counts them in the maximum (and stores the
+  // optional bf16 act) when the vector exists.
+  const auto take = [&](const GuRaw<false>& x, int v, uint32_t (&o)[4]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = act_pair<false>(x, e);
+    if (v < total) {
+      if (a.act != nullptr) st8_nt(a.act + 8LL * v, V8{{o[0], o[1], o[2], o[3]}});
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        m = fmaxf(m, fmaxf(lo_bf16(o[e] & 0x7fff7fffu), hi_bf16(o[e] & 0x7fff7fffu)));
+    }
+  };
+  uint32_t w[kHoldR][4];
+#pragma unroll
+  for (int k0 = 0; k0 < kHold; k0 += kHoldBatch) {
+    GuRaw<false> x[kHoldBatch];
+#pragma unroll
+    for (int j = 0; j < kHoldBatch; ++j)
+      if (k0 + j < kHold) x[j] = load_gu<false, true>(a, min(v0 + (k0 + j) * step, total - 1), nv);
+#pragma unroll
+    for (int j = 0; j < kHoldBatch; ++j) {
+      const int k = k0 + j;
+      if (k >= kHold) break;
+      uint32_t o[4];
+      take(x[j], v0 + k * step, o);
+      if (k < kHoldR) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[k < kHoldR ? k : 0][e] = o[e];
+      } else {
+        s_hold[k >= kHoldR ? k - kHoldR : 0][threadIdx.x] = make_uint4(o[0], o[1], o[2], o[3]);
+      }
+    }
+  }
+  // The streamed rest: max only (cached loads: part is still cached when
+  // the second sweep comes back to it).
+  const int vs = v0 + kHold * step;
+  for (int v = vs; v < total; v += kStreamU * step) {
+    GuRaw<false> x[kStreamU];
+#pragma unroll
+    for (int j = 0; j < kStreamU; ++j) x[j] = load_gu<false, false>(a, min(v + j * step, total - 1), nv);
+#pragma unroll
+    for (int j = 0; j < kStreamU; ++j) {
+      uint32_t o[4];
+      take(x[j], v + j * step, o);
+    }
+  }
+  const Fp8Enc f = fp8_enc_of(fp8_scale_for(grid_max(m, gs, tag)));
+  if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = f.s;
+  const auto encode = [&](auto fast_tag) {
+    constexpr bool kFast = decltype(fast_tag)::value;
+#pragma unroll
+    for (int k = 0; k < kHold; ++k) {
+      const int v = v0 + k * step;
+      if (v >= total) break;
+      uint32_t o[4];
+      if (k < kHoldR) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = w[k < kHoldR ? k : 0][e];
+      } else {
+        const uint4 h = s_hold[k >= kHoldR ? k - kHoldR : 0][threadIdx.x];
+        o[0] = h.x;
+        o[1] = h.y;
+        o[2] = h.z;
+        o[3] = h.w;
+      }
+      const uint2 c = fp8x8_encode_bf16<kFast>(o, f);
+      st_u32x2_nt(a.codes + 8LL * v, c.x, c.y);
+    }
+    for (int v = vs; v < total; v += kStreamU * step) {
+      GuRaw<false> x[kStreamU];
+#pragma unroll
+      for (int j = 0; j < kStreamU; ++j) x[j] = load_gu<false, true>(a, min(v + j * step, total - 1), nv);
+#pragma unroll
+      for (int j = 0; j < kStreamU; ++j) {
+        const int vj = v + j * step;
+        if (vj >= total) break;
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = act_pair<false>(x[j], e);
+        const uint2 c = fp8x8_encode_bf16<kFast>(o, f);
+        st_u32x2_nt(a.codes + 8LL * vj, c.x, c.y);
+      }
+    }
+  };
+  if (f.fast) encode(std::true_type{});
+  else encode(std::false_type{});
+}
+
+// Grid of the held single-launch form (every workgroup resident, one
+// partial slot each), or 0 when the device cannot hold a useful grid or the
+// indices would overflow.
+unsigned hold_grid(long long vectors) {
+  if (fp8_launch_mode() != 0) return 0;
+  const int resident = resident_blocks(reinterpret_cast<const void*>(swiglu_fp8_hold_kernel), kBlock);
+  const int grid = resident < kMaxPartials ? resident : kMaxPartials;
+  if (grid < kCUs) return 0;
+  if (vectors + static_cast<long long>(kHold + kStreamU) * grid * kBlock >= INT_MAX) return 0;
+  return static_cast<unsigned>(grid);
+}
+
 // Element-wise fallback for I not a multiple of 8 (bf16 / f32 in, bf16 out).
 template <bool F32IN>
 __global__ __launch_bounds__(kBlock) void swiglu_scalar_kernel(SwArgs a) {
@@ -330,6 +464,16 @@ int granite4_swiglu_fp8(const uint16_t* d_gu, int rows, int I, uint8_t* d_codes,
     f.scale_out = d_scale;
     const GridSync gs{work_slots(d_work), work_gen(d_work)};
     hipLaunchKernelGGL(swiglu_fp8_fused_kernel, fgrid, kFusedThreads, 0, stream(), f, gs);
+    return launch_status("granite4_swiglu_fp8");
+  }
+  const unsigned hgrid = hold_grid(vectors);
+  if (hgrid != 0) {
+    SwArgs h = sw_args(d_gu, rows, I);
+    h.act = d_act;
+    h.codes = d_codes;
+    h.scale_out = d_scale;
+    const GridSync gs{work_slots(d_work), work_gen(d_work)};
+    hipLaunchKernelGGL(swiglu_fp8_hold_kernel, hgrid, kBlock, 0, stream(), h, gs);
     return launch_status("granite4_swiglu_fp8");
   }
   const unsigned grid = grid_for(vectors, kMaxPartials);

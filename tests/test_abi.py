@@ -108,3 +108,28 @@ def test_kv_codes_host_match_oracle():
                                                 out.ctypes.data) == 0
             want = np.array([ol.lib.g4o_kv_code(float(v), float(s), qmax) for v in x], np.int32)
             np.testing.assert_array_equal(out, want)
+
+
+def test_kv_codes_host_half_integer_neighbours():
+    """Operands within 4 ulps of every (k + 1/2) * s boundary, over scales of
+    the form amax / qmax: the reciprocal-and-residual quotient the append
+    kernels use must round exactly as the IEEE division (numpy's f32 divide
+    is that division; a sample is also checked against the oracle)."""
+    rng = np.random.default_rng(11)
+    for qmax in (127, 15, 7):
+        amax = rng.uniform(-30, 30, 64).astype(np.float32)
+        scales = (np.exp2(amax) * rng.uniform(1, 2, 64)).astype(np.float32) / np.float32(qmax)
+        for s in scales:
+            k = np.arange(-qmax - 1, qmax + 1, dtype=np.float32)
+            mid = ((k + np.float32(0.5)) * s).astype(np.float32)
+            bits = mid.view(np.int32)[:, None] + np.arange(-4, 5, dtype=np.int32)[None, :]
+            x = bits.reshape(-1).view(np.float32)
+            out = np.empty(x.size, np.int32)
+            assert L.lib.granite4_host_kv_codes(x.ctypes.data, x.size, float(s), qmax,
+                                                out.ctypes.data) == 0
+            q = x / s
+            t = np.trunc(q)  # half away from zero, with the exact fraction q - t
+            want = np.clip(t + np.sign(q) * (np.abs(q - t) >= 0.5), -qmax, qmax)
+            np.testing.assert_array_equal(out, want.astype(np.int32))
+        for i in range(0, x.size, 37):
+            assert ol.lib.g4o_kv_code(float(x[i]), float(s), qmax) == out[i]

@@ -171,8 +171,9 @@ def _fp8_check(codes, scale, normed_bf16):
 
 
 # Up to 4096 rows of 4096 take the single-launch form on 256 CUs (1024
-# workgroups x 4 held rows); 4097 takes two launches.
-@pytest.mark.parametrize("rows", [1, 8, 512, 2048, 3000, 4096, 4097])
+# workgroups x 4 rows held in VGPRs); up to 12288 the deep single-launch form
+# (x 8 rows in VGPRs + 4 in LDS); 12289 takes two launches.
+@pytest.mark.parametrize("rows", [1, 8, 512, 2048, 3000, 4096, 4097, 8192, 12289])
 def test_add_rmsnorm_fp8(rows):
     note(f"add_rmsnorm_fp8 rows={rows}")
     cols = 4096
@@ -271,9 +272,11 @@ def test_add_rmsnorm_fp8_zero_tensor_and_no_residual():
 
 
 # ----------------------------------------------------------------------------- swiglu
-# 655 rows of I = 12800 are the largest the single-launch form holds (1024
-# workgroups x 256 lanes x 4 vectors); 656 and up take two launches.
-@pytest.mark.parametrize("rows", [1, 8, 64, 655, 656, 2048, 2700])
+# 655 rows of I = 12800 are the largest the register-only single-launch form
+# holds (1024 workgroups x 256 lanes x 4 vectors); 656 and up take the held
+# form, which keeps 21 vectors per lane (12 in VGPRs, 9 in LDS: ~3440 rows
+# on a full grid) and streams the rest twice; 5000 rows stream.
+@pytest.mark.parametrize("rows", [1, 8, 64, 655, 656, 2048, 2700, 5000])
 def test_swiglu_bf16_and_fp8(rows):
     note(f"swiglu rows={rows}")
     I_ = 12800
