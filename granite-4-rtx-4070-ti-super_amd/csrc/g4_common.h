@@ -21,9 +21,10 @@ constexpr int kPersistBlocks = kCUs * 8;  // grid cap for grid-stride kernels
 //                      (its grid is capped at kMaxPartials)
 //   [4096, 12288)      u64 tagged slots of the single-launch form's grid
 //                      maximum (one per workgroup, at most kMaxPartials)
-//   [12288, 12544)     u32 generation word of those slots (+ padding)
+//   [12288, 12544)     u32 generation word of those slots at +0, u64 tagged
+//                      grid maximum at +128 (+ padding)
 //   [12544, ...)       f32 per row: the norm's 1 / rms from pass 1 to pass 2
-// The slots and the generation word must start zero-filled.
+// The slots, the generation word and the grid maximum must start zero-filled.
 constexpr int kMaxPartials = 1024;
 constexpr size_t kWorkSlotsOff = 4096;
 constexpr size_t kWorkGenOff = kWorkSlotsOff + 8 * kMaxPartials;
@@ -34,6 +35,9 @@ __host__ __device__ inline unsigned long long* work_slots(void* w) {
 }
 __host__ __device__ inline unsigned* work_gen(void* w) {
   return reinterpret_cast<unsigned*>(static_cast<char*>(w) + kWorkGenOff);
+}
+__host__ __device__ inline unsigned long long* work_result(void* w) {
+  return reinterpret_cast<unsigned long long*>(static_cast<char*>(w) + kWorkGenOff + 128);
 }
 __host__ __device__ inline float* work_row_r(void* w) {
   return reinterpret_cast<float*>(static_cast<char*>(w) + kWorkRowOff);

@@ -2,26 +2,33 @@
 // FP8 forms (the per-tensor scale needs the maximum over every workgroup's
 // values before any code is written).
 //
-// Protocol: each workgroup publishes its maximum in its own 64-bit slot as
-// (tag << 32 | f32 bits) with one relaxed, device-scope store, then polls
-// every slot (one lane per slot, device-scope relaxed loads) until each holds
-// the current tag. The tag is the workspace's generation word + 1, read at
-// the start of the launch; workgroup 0 stores the new generation once it has
-// seen every slot, which no workgroup can precede: each read the word before
-// publishing. Tags are compared for equality, so the slots only need to
-// start different from the first tag (a zero-filled workspace).
+// Protocol: workgroups 1.. publish their maximum in their own 64-bit slot as
+// (tag << 32 | f32 bits) with one relaxed, device-scope store. Workgroup 0
+// polls every slot (device-scope relaxed loads, all of a thread's slots in
+// flight together) until each holds the current tag, then stores the tagged
+// grid maximum in one result word and the new generation; the other
+// workgroups poll that one word from one thread. The tag is the workspace's
+// generation word + 1, read at the start of the launch; workgroup 0 stores
+// the new generation only once it has seen every slot, and each workgroup
+// read the word before publishing. Tags are compared for equality, so the
+// slots and the result word only need to start different from the first tag
+// (a zero-filled workspace).
 //
-// Costs, measured on MI355X: ~2.6 us per synchronisation with 256
-// workgroups. A release store instead of the relaxed one (the value and the
-// tag share one word, so no ordering is needed) cost ~12.8 us: at device
-// scope it writes back the whole L2. Same-address atomic counters cost
-// ~8 us.
+// Costs, measured on MI355X: ~2 us from the last workgroup's arrival to the
+// maximum reaching every workgroup (two store -> poll hops). Polling every
+// slot from every workgroup (grid^2 loads per round) took ~3 us: the polls
+// crowded out the stores they waited for. A release store instead of the
+// relaxed one (the value and the tag share one word, so no ordering is
+// needed) cost ~12.8 us: at device scope it writes back the whole L2.
+// Same-address atomic counters cost ~8 us.
 //
 // Requirements: every workgroup of the grid resident at once (the host checks
-// the occupancy before choosing this form), and one such launch at a time per
-// workspace. The wait is bounded: a slot that never arrives (which those
-// requirements exclude) ends the wait after kSyncSpinLimit polls, and the
-// returned maximum is NaN, so the op reports a NaN scale rather than hang.
+// the occupancy before choosing this form), at most blockDim.x *
+// kSyncSlotsPerThread workgroups, and one such launch at a time per
+// workspace. The waits are bounded: a slot or result that never arrives
+// (which those requirements exclude) ends the wait after kSyncSpinLimit
+// polls, and the returned maximum is NaN, so the op reports a NaN scale
+// rather than hang.
 #ifndef G4_SYNC_H
 #define G4_SYNC_H
 
@@ -34,9 +41,12 @@ namespace g4 {
 constexpr int kSyncSpinLimit = 1 << 20;
 
 struct GridSync {
-  unsigned long long* slots;  // [gridDim.x] tagged maxima
-  unsigned* gen;              // generation word
+  unsigned long long* slots;   // [gridDim.x] tagged maxima
+  unsigned* gen;               // generation word
+  unsigned long long* result;  // tagged grid maximum (gathered by workgroup 0)
 };
+
+constexpr int kSyncSlotsPerThread = 4;  // kMaxPartials / 256-thread workgroups
 
 // Issued at kernel start (thread 0; the value is used after the compute
 // phase, so the load's latency is hidden).
@@ -47,52 +57,104 @@ __device__ __forceinline__ unsigned grid_sync_tag(const GridSync& gs) {
 
 // Maximum of m over every thread of the grid (non-negative values; NaN
 // inputs are ignored as fmaxf does). tag0: grid_sync_tag's value (read in
-// thread 0 only). Every thread of the workgroup must call it.
+// thread 0 only). Every thread of the workgroup must call it; blockDim.x *
+// kSyncSlotsPerThread must cover gridDim.x.
+//
+// Two levels: workgroups 1.. publish their maximum in their slot; workgroup
+// 0 polls every slot (each thread its <= kSyncSlotsPerThread slots, all
+// loads in flight together), publishes the tagged grid maximum in the result
+// word and the new generation; the others poll that one word from one
+// thread. Polling traffic is ~2 grid loads per round instead of grid^2:
+// measured, all-to-all polling kept ~3 us between the last arrival and the
+// first workgroup seeing the maximum, the polls crowding out the store they
+// wait for.
 __device__ __forceinline__ float grid_max(float m, const GridSync& gs, unsigned tag0) {
   __shared__ float s_red[16];
   __shared__ unsigned s_tag;
-  __shared__ unsigned s_bad;
+  __shared__ float s_out;
   const int wave = threadIdx.x >> 6;
   const int nw = blockDim.x >> 6;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
   if ((threadIdx.x & 63) == 0) s_red[wave] = m;
-  if (threadIdx.x == 0) {
-    s_tag = tag0;
-    s_bad = 0u;
-  }
+  if (threadIdx.x == 0) s_tag = tag0;
   __syncthreads();
   const unsigned tag = s_tag;
-  if (threadIdx.x == 0) {
-    float bm = s_red[0];
-    for (int i = 1; i < nw; ++i) bm = fmaxf(bm, s_red[i]);
-    __hip_atomic_store(&gs.slots[blockIdx.x],
-                       (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(bm),
-                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (blockIdx.x != 0) {
+    if (threadIdx.x == 0) {
+      float bm = s_red[0];
+      for (int i = 1; i < nw; ++i) bm = fmaxf(bm, s_red[i]);
+      __hip_atomic_store(&gs.slots[blockIdx.x],
+                         (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(bm),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      unsigned long long v;
+      int spin = 0;
+      for (;;) {
+        v = __hip_atomic_load(gs.result, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (static_cast<unsigned>(v >> 32) == tag || ++spin >= kSyncSpinLimit) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      s_out = static_cast<unsigned>(v >> 32) == tag ? __uint_as_float(static_cast<unsigned>(v))
+                                                      : __builtin_nanf("");
+    }
+    __syncthreads();
+    return s_out;
   }
-  float mm = 0.0f;
+  // Workgroup 0: gather.
+  float mm = s_red[0];
+  for (int i = 1; i < nw; ++i) mm = fmaxf(mm, s_red[i]);
+  bool need[kSyncSlotsPerThread];
+#pragma unroll
+  for (int k = 0; k < kSyncSlotsPerThread; ++k) {
+    const int j = threadIdx.x + k * blockDim.x;
+    need[k] = j > 0 && j < static_cast<int>(gridDim.x);
+  }
+  int spin = 0;
   bool late = false;
-  for (int j = threadIdx.x; j < static_cast<int>(gridDim.x); j += blockDim.x) {
-    unsigned long long v;
-    int spin = 0;
-    do {
-      v = __hip_atomic_load(&gs.slots[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    } while (static_cast<unsigned>(v >> 32) != tag && ++spin < kSyncSpinLimit);
-    if (static_cast<unsigned>(v >> 32) != tag) late = true;
-    mm = fmaxf(mm, __uint_as_float(static_cast<unsigned>(v)));
+  for (;;) {
+    unsigned long long v[kSyncSlotsPerThread];
+#pragma unroll
+    for (int k = 0; k < kSyncSlotsPerThread; ++k)
+      if (need[k])
+        v[k] = __hip_atomic_load(&gs.slots[threadIdx.x + k * blockDim.x], __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+    bool any = false;
+#pragma unroll
+    for (int k = 0; k < kSyncSlotsPerThread; ++k) {
+      if (!need[k]) continue;
+      if (static_cast<unsigned>(v[k] >> 32) == tag) {
+        mm = fmaxf(mm, __uint_as_float(static_cast<unsigned>(v[k])));
+        need[k] = false;
+      } else {
+        any = true;
+      }
+    }
+    if (!any) break;
+    if (++spin >= kSyncSpinLimit) {
+      late = true;
+      break;
+    }
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) mm = fmaxf(mm, __shfl_xor(mm, o));
   __syncthreads();  // s_red is reused below
-  if ((threadIdx.x & 63) == 0) s_red[wave] = mm;
-  if (late) s_bad = 1u;
+  if ((threadIdx.x & 63) == 0) s_red[wave] = late ? __builtin_nanf("") : mm;
   __syncthreads();
-  float r = s_red[0];
-  for (int i = 1; i < nw; ++i) r = fmaxf(r, s_red[i]);
-  if (s_bad != 0u) r = __builtin_nanf("");
-  if (blockIdx.x == 0 && threadIdx.x == 0)
+  if (threadIdx.x == 0) {
+    float r = s_red[0];
+    bool bad = r != r;
+    for (int i = 1; i < nw; ++i) {
+      bad |= s_red[i] != s_red[i];
+      r = fmaxf(r, s_red[i]);
+    }
+    if (bad) r = __builtin_nanf("");
+    __hip_atomic_store(gs.result, (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(r),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(gs.gen, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return r;
+    s_out = r;
+  }
+  __syncthreads();
+  return s_out;
 }
 
 }  // namespace g4

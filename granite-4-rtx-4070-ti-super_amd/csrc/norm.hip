@@ -36,6 +36,8 @@
 
 static_assert(g4::kMaxPartials == GRANITE4_FP8_MAX_PARTIALS, "workspace layout");
 static_assert(GRANITE4_FP8_WORK_BYTES(0) == g4::kWorkRowOff, "workspace layout");
+static_assert(g4::kMaxPartials <= g4::kBlock * g4::kSyncSlotsPerThread,
+              "grid_max: workgroup 0 polls every slot of the largest grid");
 
 namespace g4 {
 namespace {
@@ -507,7 +509,7 @@ bool launch_norm_fp8_fused(const uint16_t* x, const uint16_t* branch, float mult
     return false;
   NormArgs a{x, branch, mult, w, eps, rows, cols, res_out, nullptr, codes, scale, nullptr, 0,
              nullptr, 0.0};
-  const GridSync gs{work_slots(work), work_gen(work)};
+  const GridSync gs{work_slots(work), work_gen(work), work_result(work)};
   return launch_fused_vpl<kNormHold, 0>(a, gs, nvec) ||
          launch_fused_vpl<kNormDeepHR, kNormDeepHL>(a, gs, nvec);
 }
