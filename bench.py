@@ -48,11 +48,11 @@ B_ROPE = {16: B_ROPE_COMMON + 2 * HK * D * 2,
 
 # HBM bytes per swiglu_fp8 call at T=512 (one launch, swiglu_fp8_fused_kernel),
 # measured with two rocprofv3 --pmc runs of `bench.py --only t512` (FETCH_SIZE,
-# then WRITE_SIZE, KiB per dispatch): fetch 12996.0 KiB x 2.0 + write 6432.1
+# then WRITE_SIZE, KiB per dispatch): fetch 12925.4 KiB x 2.0 + write 6432.1
 # KiB x 1.0. The factors are what the same counters read for the known-size
 # copy probe (`bench.py --only probe`): FETCH_SIZE half the bytes, WRITE_SIZE
 # all of them.
-SWIGLU_FP8_T512_TRAFFIC = int(12996.0 * 2.0 * 1024 + 6432.1 * 1024)
+SWIGLU_FP8_T512_TRAFFIC = int(12925.4 * 2.0 * 1024 + 6432.1 * 1024)
 
 
 def per_launch_extra(op):
