@@ -191,6 +191,12 @@ __device__ __forceinline__ void sweep_run(Sweep<U, Raw>& s, Load load, Body body
   }
 }
 
+// FP8 encode of a stored bf16 [rows][I] tensor (I % 8 == 0) under the scale
+// from n_partials per-workgroup maxima, as the SwiGLU op's second pass
+// (swiglu.hip). False on a launch error.
+bool launch_encode_bf16(const uint16_t* act, int rows, int I, const float* partials, int n_partials,
+                        uint8_t* codes, float* scale_out);
+
 }  // namespace g4
 
 #endif  // G4_COMMON_H

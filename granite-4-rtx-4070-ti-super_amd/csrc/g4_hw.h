@@ -159,6 +159,14 @@ __device__ __forceinline__ uint2 fp8x8_encode_bf16(const uint32_t (&w)[4], const
   return fp8x8_encode<FAST>(y, e);
 }
 
+// silu(g) * u in f32 (hardware exp and reciprocal): the SwiGLU activation
+// of the SwiGLU ops and of the gate|up GEMM epilogue.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  const float e = __expf(-g);
+  const float sig = __builtin_amdgcn_rcpf(1.0f + e);
+  return g * sig * u;
+}
+
 }  // namespace g4
 
 #endif  // G4_HW_H

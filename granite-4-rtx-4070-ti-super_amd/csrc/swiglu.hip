@@ -42,11 +42,6 @@ struct SwArgs {
   const uint16_t* act_in;  // kOutFp8: encode this stored bf16 act instead of recomputing
 };
 
-__device__ __forceinline__ float silu_mul(float g, float u) {
-  const float e = __expf(-g);
-  const float sig = __builtin_amdgcn_rcpf(1.0f + e);
-  return g * sig * u;
-}
 
 // Raw gate and up vectors of one 8-element output vector, as loaded: bf16
 // (one 16-byte load each) or f32 (two 16-byte loads each).
@@ -410,6 +405,23 @@ SwArgs sw_args(const void* gu, int rows, int I) {
 }
 
 }  // namespace
+}  // namespace g4
+
+namespace g4 {
+
+bool launch_encode_bf16(const uint16_t* act, int rows, int I, const float* partials, int n_partials,
+                        uint8_t* codes, float* scale_out) {
+  SwArgs p = sw_args(act, rows, I);
+  p.act_in = act;
+  p.codes = codes;
+  p.scale_out = scale_out;
+  p.partials = const_cast<float*>(partials);
+  p.n_partials = n_partials;
+  hipLaunchKernelGGL(encode_bf16_kernel, grid_for(static_cast<long long>(rows) * (I / 8), kPersistBlocks),
+                     kBlock, 0, stream(), p);
+  return launch_status("granite4 FP8 encode") == 0;
+}
+
 }  // namespace g4
 
 using namespace g4;

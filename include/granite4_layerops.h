@@ -385,6 +385,52 @@ int granite4_attn_paged(const uint16_t* q, int rows, int Hq, int Hk, int d, floa
                         const int* const* row_pt, int max_len, int window, void* scratch,
                         uint16_t* out);
 
+/* ---------------------------------------------------------------------------
+ * FP8 x FP8 GEMM with the layer epilogues fused in (gfx950 matrix cores).
+ *
+ * C[m][n] = a_scale * w_scale(n) * sum_k A[m][k] W[n][k]: A e4m3 codes [M][K]
+ * (row pitch lda bytes, the FP8 output of granite4_add_rmsnorm_fp8 /
+ * granite4_swiglu_fp8 with its per-tensor scale), W e4m3 [N][K] row-major.
+ * The epilogue kinds and the per-segment weight scales are the reference's
+ * GemmOut / GemmEpilogue (prefill_gemm.h:12-28, epi_store
+ * prefill_gemm.cu:69-89); the reference's GEMM takes a bf16 A, this one the
+ * FP8 activations of this library. y = acc * (a_scale * w_scale(n)) in f32.
+ * Needs K % 128 == 0, lda >= K, lda % 16 == 0, 16-byte aligned A and W,
+ * ldc >= N.
+ * ------------------------------------------------------------------------- */
+enum {
+  GRANITE4_GEMM_BF16 = 0,     /* out_bf16[m][n] = bf16(y) */
+  GRANITE4_GEMM_F32 = 1,      /* out_f32[m][n] = y */
+  GRANITE4_GEMM_RESIDUAL = 2  /* out_bf16[m][n] = bf16(residual[m][n] + resid_scale * y) */
+};
+
+typedef struct Granite4GemmEpilogue {
+  float scale0, scale1, scale2; /* w_scale(n): scale0 for n < seg1, scale1 for n < seg2, else scale2 */
+  int seg1, seg2;
+  uint16_t* out_bf16;
+  float* out_f32;
+  const uint16_t* residual;     /* may alias out_bf16 */
+  float resid_scale;
+  int ldc;                      /* output (and residual) row pitch, elements */
+} Granite4GemmEpilogue;
+
+/* Replaces: granite4::prefill_gemm (prefill_gemm.h:37-39) for FP8
+ * activations; `out` is one of GRANITE4_GEMM_*. */
+int granite4_gemm_fp8(int out, const uint8_t* A, int lda, float a_scale, const uint8_t* W, int M,
+                      int N, int K, const Granite4GemmEpilogue* ep);
+
+/* Replaces: the gate|up GEMM with the kF32 epilogue followed by
+ * granite4::prefill_silu_mul (forward_gpu.cu:2837-2839, prefill_gemm.cu:
+ * 1194-1203), fused: W_gu is [2I][K] (gate rows, then up rows), act[m][i] =
+ * bf16(silu(g) * u) with g = acc_gate * (a_scale * gate_scale), u = acc_up *
+ * (a_scale * up_scale); act [M][I] bf16 is always written. With codes != NULL
+ * it is also quantised to FP8 e4m3 under the per-tensor scale amax / 448
+ * (written to d_scale), exactly as granite4_swiglu_fp8 quantises its act.
+ * d_work: the FP8 workspace (GRANITE4_FP8_WORK_BYTES(0) bytes at least). */
+int granite4_gemm_fp8_swiglu(const uint8_t* A, int lda, float a_scale, const uint8_t* W_gu, int M,
+                             int I, int K, float gate_scale, float up_scale, uint16_t* act,
+                             uint8_t* codes, float* d_scale, void* d_work);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 

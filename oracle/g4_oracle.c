@@ -253,6 +253,28 @@ void g4o_silu_mul_f32(const float* gu, int I, int rows, uint16_t* act) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* FP8 x FP8 GEMM (exact products, double accumulation; test_kernels.cu:     */
+/* 1685-1719 pins the reference's GEMM against this form).                  */
+/* ------------------------------------------------------------------------ */
+
+void g4o_gemm_fp8(const uint8_t* A, int lda, float a_scale, const uint8_t* W, int M, int N, int K,
+                  float scale0, float scale1, float scale2, int seg1, int seg2, float* y) {
+  double dec[256];
+  for (int c = 0; c < 256; ++c) dec[c] = g4o_fp8_decode((uint8_t)c);
+  for (int m = 0; m < M; ++m) {
+    const uint8_t* a = A + (size_t)m * (size_t)lda;
+    for (int n = 0; n < N; ++n) {
+      const uint8_t* w = W + (size_t)n * (size_t)K;
+      double acc = 0.0;
+      for (int k = 0; k < K; ++k) acc += dec[a[k]] * dec[w[k]];
+      const float ws = n < seg1 ? scale0 : (n < seg2 ? scale1 : scale2);
+      const float s = a_scale * ws;
+      y[(size_t)m * (size_t)N + n] = (float)((double)s * acc);
+    }
+  }
+}
+
+/* ------------------------------------------------------------------------ */
 /* RoPE (kernel_math.h:191-219): Llama half split; tables built in double.   */
 /* ------------------------------------------------------------------------ */
 

@@ -62,6 +62,18 @@ void g4o_add_rmsnorm(const uint16_t* res, const uint16_t* branch, float mult, co
 void g4o_swiglu_bf16(const uint16_t* gu, int rows, int I, uint16_t* act);
 void g4o_silu_mul_f32(const float* gu, int I, int rows, uint16_t* act);
 
+/* FP8 x FP8 GEMM value before the epilogue's rounding:
+ * y[m][n] = (float)((double)(a_scale * w_scale(n)) * S[m][n]), with
+ * S = sum_k dec(A[m][k]) * dec(W[n][k]) accumulated in double (every product
+ * of two e4m3 values is exact) and w_scale(n) = scale0 / scale1 / scale2 split
+ * at seg1 / seg2 (the reference's GemmEpilogue, prefill_gemm.h:12-28,
+ * epi_scale prefill_gemm.cu:65-67). The reference checks its GEMM the same
+ * way: against the double-accumulated exact product, within 2 bf16 ulp of
+ * the rounded epilogue value (test_kernels.cu:1685-1719). A is [M][lda]
+ * bytes, W [N][K], y [M][N]. */
+void g4o_gemm_fp8(const uint8_t* A, int lda, float a_scale, const uint8_t* W, int M, int N, int K,
+                  float scale0, float scale1, float scale2, int seg1, int seg2, float* y);
+
 /* RoPE (kernel_math.h:191-219, kernels_phase2.cu:138-162). */
 void g4o_rope_tables(double theta, int head_dim, int max_pos, float* cos_t, float* sin_t);
 void g4o_rope_rows(const uint16_t* x, int rows, int heads, int d, const int* pos,

@@ -48,6 +48,8 @@ def _load():
                                    _c.c_int, u16p, u16p]),
         "g4o_swiglu_bf16": (None, [u16p, _c.c_int, _c.c_int, u16p]),
         "g4o_silu_mul_f32": (None, [f32p, _c.c_int, _c.c_int, u16p]),
+        "g4o_gemm_fp8": (None, [u8p, _c.c_int, _c.c_float, u8p, _c.c_int, _c.c_int, _c.c_int,
+                                _c.c_float, _c.c_float, _c.c_float, _c.c_int, _c.c_int, f32p]),
         "g4o_rope_tables": (None, [_c.c_double, _c.c_int, _c.c_int, f32p, f32p]),
         "g4o_rope_rows": (None, [u16p, _c.c_int, _c.c_int, _c.c_int, i32p, f32p, f32p, u16p]),
         "g4o_kv_scale": (_c.c_float, [_c.c_float, _c.c_int]),
@@ -147,6 +149,35 @@ def swiglu(gu):
     act = np.empty((rows, two_i // 2), np.uint16)
     lib.g4o_swiglu_bf16(_p(np.ascontiguousarray(gu), u16p), rows, two_i // 2, _p(act, u16p))
     return act
+
+
+def silu_mul_f32(gu):
+    """act = bf16(silu(g) * u) of f32 gu [rows][2I] (g4o_silu_mul_f32)."""
+    gu = np.ascontiguousarray(gu, np.float32)
+    rows, two_i = gu.shape
+    act = np.empty((rows, two_i // 2), np.uint16)
+    lib.g4o_silu_mul_f32(_p(gu, f32p), two_i // 2, rows, _p(act, u16p))
+    return act
+
+
+def gemm_fp8(A, a_scale, W, scales=(1.0, 1.0, 1.0), segs=None):
+    """y [M][N] f32 (g4o_gemm_fp8): exact products, double accumulation."""
+    A = np.ascontiguousarray(A, np.uint8)
+    W = np.ascontiguousarray(W, np.uint8)
+    M, K = A.shape
+    N = W.shape[0]
+    s1, s2 = segs if segs is not None else (N, N)
+    y = np.empty((M, N), np.float32)
+    lib.g4o_gemm_fp8(_p(A, u8p), K, a_scale, _p(W, u8p), M, N, K, scales[0], scales[1], scales[2],
+                     s1, s2, _p(y, f32p))
+    return y
+
+
+def fp8_codes(seed, shape, std=1.0):
+    """Seeded e4m3 codes of N(0, std) values (finite codes only)."""
+    x = normal_bf16(seed, 0.0, std, int(np.prod(shape)))
+    codes = fp8_encode_scaled(x, 1.0)
+    return codes.reshape(shape)
 
 
 def rope_tables(theta, d, max_pos):

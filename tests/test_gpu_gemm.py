@@ -1,0 +1,184 @@
+"""GPU parity of the FP8 x FP8 GEMM and its fused epilogues
+(granite4_gemm_fp8, granite4_gemm_fp8_swiglu) against the oracle's
+g4o_gemm_fp8 (exact products, double accumulation).
+
+Bar, as the reference's own GEMM test (test_kernels.cu:1685-1719): each bf16
+output within 2 bf16 ulp of the oracle value rounded to bf16, except where
+the sum cancels below the f32 accumulation's reach: there within
+K * 2^-24 * s * sum_k |a_k w_k| (the f32 sum's error bound; the matrix cores
+add in their own order). f32 outputs are held to that bound everywhere. FP8
+codes of the fused SwiGLU are bit-exact against the oracle's quantiser
+applied to the GPU's own bf16 act (the same scale).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as ol
+from pkg import layerops
+
+pytestmark = pytest.mark.gpu
+L = None
+
+
+def setup_module(module):
+    global L
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    L = layerops()
+    torch.cuda.init()
+    L.use_stream()
+
+
+def note(msg):
+    print(msg, flush=True)
+
+
+def dev(a):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return torch.from_numpy(a).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    a = t.cpu().numpy()
+    return a.view(np.uint16) if a.dtype == np.int16 else a
+
+
+def ulp_diff(a, b):
+    ai = a.astype(np.int32)
+    bi = b.astype(np.int32)
+    ai = np.where(ai & 0x8000, 0x8000 - ai, ai)
+    bi = np.where(bi & 0x8000, 0x8000 - bi, bi)
+    return np.abs(ai - bi)
+
+
+def abs_bound(A, W, s):
+    """K * 2^-24 * s * sum_k |a_k w_k| per output (the f32 sum's error bound)."""
+    K = A.shape[1]
+    return ol.gemm_fp8(A & 0x7F, abs(s), W & 0x7F).astype(np.float64) * K * 2.0 ** -24
+
+
+def bf16_ok(got, y_want, bound):
+    """got (bf16 bits) vs the f32 oracle value: 2 ulp of bf16(y) or the sum's bound."""
+    want = np.vectorize(ol.lib.g4o_f32_to_bf16, otypes=[np.uint16])(y_want)
+    d = ulp_diff(got, want)
+    err = np.abs(ol.bf16_to_f32(got).astype(np.float64) - y_want.astype(np.float64))
+    bad = (d > 2) & (err > bound + np.abs(y_want) * 2.0 ** -7)
+    return bad, d
+
+
+def run_gemm(kind, A, a_scale, W, scales=(1.0, 1.0, 1.0), segs=None, residual=None, rs=1.0):
+    M, N = A.shape[0], W.shape[0]
+    dA, dW = dev(A), dev(W)
+    if kind == L.GEMM_F32:
+        out = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    elif residual is not None:
+        out = dev(residual)
+    else:
+        out = torch.empty((M, N), dtype=torch.int16, device="cuda")
+    L.gemm_fp8(dA, a_scale, dW, out_kind=kind, scales=scales, segs=segs, out=out,
+               residual=out if residual is not None else None, resid_scale=rs)
+    return host(out)
+
+
+SHAPES = [(1, 128, 128), (70, 136, 256), (128, 256, 512), (300, 520, 1024), (257, 1024, 4096)]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_gemm_fp8_bf16(M, N, K):
+    note(f"gemm_fp8 bf16 M={M} N={N} K={K}")
+    A = ol.fp8_codes(0x71 + M, (M, K))
+    W = ol.fp8_codes(0x72 + N, (N, K), std=0.5)
+    a_s, w_s = 0.0213, 0.0071
+    got = run_gemm(L.GEMM_BF16, A, a_s, W, scales=(w_s, w_s, w_s))
+    y = ol.gemm_fp8(A, a_s, W, scales=(w_s, w_s, w_s))
+    bad, d = bf16_ok(got, y, abs_bound(A, W, a_s * w_s))
+    note(f"  exact fraction {(d == 0).mean():.4f}, max ulp {d.max()}")
+    assert not bad.any(), (np.argwhere(bad)[:5], d.max())
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES[:4])
+def test_gemm_fp8_f32(M, N, K):
+    note(f"gemm_fp8 f32 M={M} N={N} K={K}")
+    A = ol.fp8_codes(0x73 + M, (M, K))
+    W = ol.fp8_codes(0x74 + N, (N, K), std=0.5)
+    got = run_gemm(L.GEMM_F32, A, 0.5, W, scales=(0.25, 0.25, 0.25))
+    y = ol.gemm_fp8(A, 0.5, W, scales=(0.25, 0.25, 0.25))
+    err = np.abs(got.astype(np.float64) - y)
+    bound = abs_bound(A, W, 0.125) + np.abs(y) * 2.0 ** -23
+    note(f"  exact fraction {(got == y).mean():.4f}")
+    assert np.all(err <= bound), float((err / (bound + 1e-30)).max())
+
+
+def test_gemm_fp8_segment_scales():
+    """q|k|v-style segments: three weight tensors back to back, three scales."""
+    M, K = 96, 512
+    N = 384
+    A = ol.fp8_codes(0x75, (M, K))
+    W = ol.fp8_codes(0x76, (N, K), std=0.5)
+    sc, segs = (0.01, 0.02, 0.04), (128, 256)
+    got = run_gemm(L.GEMM_BF16, A, 0.3, W, scales=sc, segs=segs)
+    y = ol.gemm_fp8(A, 0.3, W, scales=sc, segs=segs)
+    bad, d = bf16_ok(got, y, abs_bound(A, W, 0.3 * 0.04))
+    assert not bad.any()
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 256, 512), (200, 4096, 4096)])
+def test_gemm_fp8_residual_in_place(M, N, K):
+    """The O / down projection: hidden = bf16(hidden + rs * y), in place."""
+    note(f"gemm_fp8 residual M={M} N={N} K={K}")
+    A = ol.fp8_codes(0x77 + M, (M, K))
+    W = ol.fp8_codes(0x78 + N, (N, K), std=0.5)
+    res = ol.normal_bf16(0x79, 0.0, 1.0, M * N).reshape(M, N)
+    rs, a_s, w_s = 0.22, 0.05, 0.003
+    got = run_gemm(L.GEMM_RESIDUAL, A, a_s, W, scales=(w_s, w_s, w_s), residual=res, rs=rs)
+    y = ol.gemm_fp8(A, a_s, W, scales=(w_s, w_s, w_s))
+    want_f32 = (ol.bf16_to_f32(res) + np.float32(rs) * y).astype(np.float32)
+    bad, d = bf16_ok(got, want_f32, abs_bound(A, W, a_s * w_s) * rs)
+    note(f"  exact fraction {(d == 0).mean():.4f}, max ulp {d.max()}")
+    assert not bad.any()
+
+
+@pytest.mark.parametrize("M,I,K", [(1, 64, 128), (100, 328, 512), (257, 1280, 4096)])
+def test_gemm_fp8_swiglu_fused(M, I, K):
+    """gate|up GEMM + SwiGLU (+ FP8) in one GEMM epilogue vs the oracle GEMM
+    followed by the reference's f32 SwiGLU (g4o_silu_mul_f32)."""
+    note(f"gemm_fp8_swiglu M={M} I={I} K={K}")
+    A = ol.fp8_codes(0x7A + M, (M, K))
+    W = ol.fp8_codes(0x7B + I, (2 * I, K), std=0.5)
+    a_s, gs, us = 0.04, 0.006, 0.009
+    dA, dW = dev(A), dev(W)
+    work = L.fp8_workspace(rows=16)
+    act, codes, scale = L.gemm_fp8_swiglu(dA, a_s, dW, gs, us, work,
+                                          act=torch.empty((M, I), dtype=torch.int16, device="cuda"))
+    y = ol.gemm_fp8(A, a_s, W, scales=(gs, us, us), segs=(I, I))
+    want = ol.silu_mul_f32(y)
+    got = host(act)
+    d = ulp_diff(got, want)
+    # where gate or up nearly cancel, bound the act error by the sums' bounds
+    bg = abs_bound(A, W[:I], a_s * gs)
+    bu = abs_bound(A, W[I:], a_s * us)
+    g, u = y[:, :I].astype(np.float64), y[:, I:].astype(np.float64)
+    sig = 1.0 / (1.0 + np.exp(-g))
+    tol = np.abs(sig * u) * bg * 1.2 + np.abs(g * sig) * bu + np.abs(ol.bf16_to_f32(want)) * 2.0 ** -7
+    err = np.abs(ol.bf16_to_f32(got).astype(np.float64) - ol.bf16_to_f32(want))
+    bad = (d > 2) & (err > tol)
+    note(f"  act exact fraction {(d == 0).mean():.4f}, max ulp {d.max()}")
+    assert not bad.any(), (np.argwhere(bad)[:5], d.max())
+    want_codes, want_scale = ol.fp8_quantize(got)
+    assert host(scale)[0] == np.float32(want_scale)
+    np.testing.assert_array_equal(host(codes), want_codes)
+    # act only (no codes)
+    act2 = L.gemm_fp8_swiglu(dA, a_s, dW, gs, us, work, fp8=False,
+                             act=torch.empty((M, I), dtype=torch.int16, device="cuda"))
+    np.testing.assert_array_equal(host(act2), got)
+
+
+def test_gemm_fp8_invalid_arguments():
+    A = torch.zeros((4, 100), dtype=torch.uint8, device="cuda")
+    W = torch.zeros((8, 100), dtype=torch.uint8, device="cuda")
+    with pytest.raises(L.Granite4Error):
+        L.gemm_fp8(A, 1.0, W)  # K % 128 != 0
