@@ -71,7 +71,7 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline + decode only")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=["t512", "t8192", "decode", "t8", "stress", "tN", "probe",
-                                       "attn"],
+                                       "attn", "gemm"],
                     help="run one configuration and print its detail (profiling runs)")
     ap.add_argument("--T", type=int, default=1024, help="token count for --only tN")
     ap.add_argument("--attn-case", default=None, help="run only this bench_attn case")
@@ -225,6 +225,8 @@ def main():
             r = bench_multi8(torch, L, randn, cos_t, sin_t, gamma, work, gen, stream, timed, args)
         elif args.only == "attn":
             r = bench_attn(torch, L, randn, gen, timed, args)
+        elif args.only == "gemm":
+            r = bench_gemm(torch, L, gen, timed, work, args)
         else:
             r = bench_stress(torch, L, randn, cos_t, sin_t, gamma, stream)
         print(json.dumps({"only": args.only, "detail": r}), flush=True)
@@ -262,6 +264,10 @@ def main():
         log("split-KV decode attention over the paged pool (next row: the KV consumer)")
         result_extra["attn_decode"] = bench_attn(torch, L, randn, gen, timed, args)
         log(json.dumps(result_extra["attn_decode"]))
+
+        log("FP8 GEMMs with the layer ops fused into their epilogues (next row)")
+        result_extra["gemm_fused"] = bench_gemm(torch, L, gen, timed, work, args)
+        log(json.dumps(result_extra["gemm_fused"]))
 
     log("bandwidth probe (achievable read / copy rate on this device)")
     result_extra["probe"] = bench_probe(torch, L, stream, timed)
@@ -442,6 +448,80 @@ def kv_bytes_per_position(bits, group):
     """K row + V row + f32 scales of one KV head at one position."""
     kb, vb = {16: (256, 256), 8: (128, 128), 4: (64, 64), 5: (80, 64)}[bits]
     return kb + vb + (0 if bits == 16 else 2 * 4 * (D // group))
+
+
+FP8_MFMA_PEAK_TFLOPS = 5000.0  # MI355X dense FP8 matrix-core peak
+
+
+def bench_gemm(torch, L, gen, timed, work, args):
+    """FP8 x FP8 GEMMs (granite4_gemm_fp8*) at the layer's shapes, T = 512 and
+    8192: the gate|up projection with SwiGLU -> FP8 fused into its epilogue
+    against the same GEMM storing bf16 gate|up followed by granite4_swiglu_fp8,
+    and the O projection with the residual epilogue + RMSNorm -> FP8 against
+    the GEMM storing the bf16 branch followed by granite4_add_rmsnorm_fp8.
+    Random e4m3 codes (finite), two rotating input sets. TFLOP/s counts 2 M N K
+    per GEMM; the roofline is the 5 PFLOP/s dense FP8 matrix-core peak."""
+    dev = "cuda"
+    out = {}
+
+    def codes(shape):
+        c = torch.randint(0, 0x7F, shape, generator=gen, device=dev, dtype=torch.int32)
+        sign = torch.randint(0, 2, shape, generator=gen, device=dev, dtype=torch.int32) << 7
+        return (c | sign).to(torch.uint8)
+
+    for T in (512, 8192):
+        sets = []
+        for _ in range(2):
+            sets.append({
+                "a": codes((T, H)), "act_a": codes((T, I)),
+                "w_gu": codes((2 * I, H)), "w_o": codes((H, H)), "w_d": codes((H, I)),
+                "act": torch.empty((T, I), dtype=torch.bfloat16, device=dev),
+                "codes_i": torch.empty((T, I), dtype=torch.uint8, device=dev),
+                "gu": torch.empty((T, 2 * I), dtype=torch.bfloat16, device=dev),
+                "hidden": torch.randn((T, H), generator=gen, device=dev).to(torch.bfloat16),
+                "branch": torch.empty((T, H), dtype=torch.bfloat16, device=dev),
+                "res_out": torch.empty((T, H), dtype=torch.bfloat16, device=dev),
+                "codes_h": torch.empty((T, H), dtype=torch.uint8, device=dev),
+                "scale": torch.empty(1, dtype=torch.float32, device=dev),
+                "gamma": torch.ones(H, dtype=torch.bfloat16, device=dev),
+            })
+
+        def gu_fused(s):
+            L.call("granite4_gemm_fp8_swiglu", s["a"], H, 0.01, s["w_gu"], T, I, H, 0.01, 0.01,
+                   s["act"], s["codes_i"], s["scale"], work)
+
+        def gu_unfused(s):
+            L.gemm_fp8(s["a"], 0.01, s["w_gu"], out=s["gu"], scales=(0.01, 0.01, 0.01))
+            L.call("granite4_swiglu_fp8", s["gu"], T, I, s["codes_i"], s["scale"], work, None)
+
+        def o_fused(s):
+            L.call("granite4_gemm_fp8_residual_rmsnorm_fp8", s["a"], H, 0.01, s["w_o"], T, H, H,
+                   0.01, s["hidden"], 1.0, s["gamma"], 1e-5, s["codes_h"], s["scale"], work)
+
+        def o_unfused(s):
+            L.gemm_fp8(s["a"], 0.01, s["w_o"], out=s["branch"], scales=(0.01, 0.01, 0.01))
+            L.call("granite4_add_rmsnorm_fp8", s["hidden"], s["branch"], 1.0, s["gamma"], 1e-5, T,
+                   H, s["res_out"], s["codes_h"], s["scale"], work)
+
+        def down(s):
+            L.gemm_fp8(s["act_a"], 0.01, s["w_d"], out=s["hidden"], out_kind=L.GEMM_RESIDUAL,
+                       scales=(0.01, 0.01, 0.01), residual=s["hidden"])
+
+        steps = 10 if T == 512 else 4
+        res = {}
+        for name, fn, flops in (("gate_up_swiglu_fp8_fused", gu_fused, 2.0 * T * 2 * I * H),
+                                ("gate_up_then_swiglu_fp8", gu_unfused, 2.0 * T * 2 * I * H),
+                                ("o_residual_rmsnorm_fp8_fused", o_fused, 2.0 * T * H * H),
+                                ("o_then_add_rmsnorm_fp8", o_unfused, 2.0 * T * H * H),
+                                ("down_residual", down, 2.0 * T * H * I)):
+            ms = timed(fn, steps, 2, sets, replays=2)
+            tf = flops / (ms * 1e-3) / 1e12
+            res[name] = {"us": round(ms * 1e3, 2), "TFLOPs": round(tf, 1),
+                         "frac_fp8_peak": round(tf / FP8_MFMA_PEAK_TFLOPS, 4)}
+        out[f"T{T}"] = res
+        del sets
+        torch.cuda.empty_cache()
+    return out
 
 
 def bench_attn(torch, L, randn, gen, timed, args):

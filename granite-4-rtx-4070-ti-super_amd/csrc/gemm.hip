@@ -22,9 +22,12 @@
 // Layout: 256-thread workgroups on 128 x 128 output tiles (swiglu: 64 act
 // columns = 64 gate + 64 up weight rows), 4 waves in 2 x 2, each wave 4 x 4
 // v_mfma_f32_16x16x128_f8f6f4 tiles. K advances 128 bytes per stage through
-// two LDS buffers (rows padded to 144 bytes: the 16 rows a fragment read
-// touches fall on distinct banks); the next stage's global loads are in
-// flight while the current one is multiplied. The grid is persistent (at
+// G4_GEMM_STAGES LDS buffers (32 KB each; 16-byte chunks XOR-swizzled by
+// row) filled by direct-to-LDS global loads (global_load_lds_dwordx4), so the
+// next stage streams in without staging registers while the current one is
+// multiplied. Measured: two stages with two workgroups per CU beat three or
+// four stages with one (M = 8192: 2.38 vs 1.47-1.52 PFLOP/s on the down
+// projection) and the register-staged form (1.79). The grid is persistent (at
 // most the resident workgroups and the 1024 partial slots); tiles run M
 // fastest, so the workgroups sharing a weight tile run together.
 //
@@ -48,8 +51,12 @@ namespace {
 constexpr int kGBM = 128;                 // output rows per tile
 constexpr int kGBN = 128;                 // weight rows per tile
 constexpr int kGBK = 128;                 // k bytes per stage
-constexpr int kGPitch = kGBK + 16;        // LDS row pitch, bytes
-constexpr int kGStage = (kGBM + kGBN) * kGPitch;
+constexpr int kGStage = (kGBM + kGBN) * kGBK;  // bytes per pipeline stage
+#ifndef G4_GEMM_STAGES
+#define G4_GEMM_STAGES 2
+#endif
+constexpr int kGStages = G4_GEMM_STAGES;
+constexpr int kEP = 68;  // f32 pitch of the epilogue's LDS staging rows
 
 enum : int {
   kEpiBf16 = GRANITE4_GEMM_BF16,
@@ -59,6 +66,7 @@ enum : int {
 };
 
 typedef int v8i __attribute__((ext_vector_type(8)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 struct GemmArgs {
@@ -97,62 +105,105 @@ __device__ __forceinline__ int b_row(int wn, int ni) {
   return wn * 64 + ni * 16;
 }
 
-struct StageRegs {
-  uint4 a[4], w[4];
-};
+// Stage layout: [A 128 rows][W 128 rows] x 128 bytes, the eight 16-byte
+// chunks of row r stored at chunk position c ^ (r & 7) (the 16 rows a
+// fragment read touches spread over the banks without padding). A stage is
+// filled by direct-to-LDS loads: 16-byte slot s of a region is written by
+// lane s % 64 of the wave instruction covering slots (s / 64) * 64.., so the
+// lane loads the global chunk that slot s stands for. Rows past M / N load a
+// valid row instead (their results are never stored).
+typedef __attribute__((address_space(3))) void* lds_ptr;
 
 template <int EPI>
-__device__ __forceinline__ void stage_load(const GemmArgs& a, int m0, int tn, int k0,
-                                           StageRegs& r) {
+__device__ __forceinline__ void stage_issue(const GemmArgs& a, int m0, int tn, int k0,
+                                            uint8_t* st) {
+  const int wave = threadIdx.x >> 6;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int c = threadIdx.x + 256 * i;  // 16-byte chunk of the 128 x 128 tile
-    const int row = c >> 3, col = (c & 7) * 16;
-    const int m = m0 + row;
-    r.a[i] = m < a.M ? *reinterpret_cast<const uint4*>(a.A + static_cast<size_t>(m) * a.lda + k0 + col)
-                     : make_uint4(0u, 0u, 0u, 0u);
-    const int n = w_row<EPI>(a, tn, row);
-    r.w[i] = n >= 0 ? *reinterpret_cast<const uint4*>(a.W + static_cast<size_t>(n) * a.K + k0 + col)
-                    : make_uint4(0u, 0u, 0u, 0u);
+    const int slot = i * 256 + threadIdx.x;
+    const int row = slot >> 3, c = (slot & 7) ^ (row & 7);
+    const int m = min(m0 + row, a.M - 1);
+    __builtin_amdgcn_global_load_lds(a.A + static_cast<size_t>(m) * a.lda + k0 + 16 * c,
+                                     (lds_ptr)(st + (i * 256 + wave * 64) * 16), 16,
+                                     0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int slot = i * 256 + threadIdx.x;
+    const int row = slot >> 3, c = (slot & 7) ^ (row & 7);
+    int n = w_row<EPI>(a, tn, row);
+    if (n < 0) n = 0;
+    __builtin_amdgcn_global_load_lds(a.W + static_cast<size_t>(n) * a.K + k0 + 16 * c,
+                                     (lds_ptr)(st + kGBM * kGBK + (i * 256 + wave * 64) * 16),
+                                     16, 0, 0);
   }
 }
 
-__device__ __forceinline__ void stage_store(uint8_t* st, const StageRegs& r) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int c = threadIdx.x + 256 * i;
-    const int row = c >> 3, col = (c & 7) * 16;
-    *reinterpret_cast<uint4*>(st + row * kGPitch + col) = r.a[i];
-    *reinterpret_cast<uint4*>(st + (kGBM + row) * kGPitch + col) = r.w[i];
-  }
+// LDS byte address of a pointer into the workgroup's LDS.
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr)(p)));
 }
 
-__device__ __forceinline__ v8i frag(const uint8_t* p) {
-  const uint4 x = *reinterpret_cast<const uint4*>(p);
-  const uint4 y = *reinterpret_cast<const uint4*>(p + 16);
+// 16-byte LDS read issued as assembly: the compiler's wait insertion would
+// otherwise wait for every direct-to-LDS load in flight (it cannot tell the
+// stage being read from the stages being filled). The caller waits with
+// lds_reads_done() before using the result.
+__device__ __forceinline__ v4u lds_read16(uint32_t addr) {
+  v4u v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+  return v;
+}
+__device__ __forceinline__ void lds_reads_done() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// Fragment of tile row r of a region at LDS address `region`: chunks
+// 2 * (lane / 16) and + 1 of the row, as two 16-byte reads.
+__device__ __forceinline__ void frag_issue(uint32_t region, int r, int lane, v4u& x, v4u& y) {
+  const int c0 = 2 * (lane >> 4);
+  const uint32_t row = region + static_cast<uint32_t>(r * kGBK);
+  x = lds_read16(row + 16u * static_cast<uint32_t>(c0 ^ (r & 7)));
+  y = lds_read16(row + 16u * static_cast<uint32_t>((c0 + 1) ^ (r & 7)));
+}
+
+__device__ __forceinline__ v8i frag_of(const v4u& x, const v4u& y) {
   v8i f;
-  f[0] = static_cast<int>(x.x);
-  f[1] = static_cast<int>(x.y);
-  f[2] = static_cast<int>(x.z);
-  f[3] = static_cast<int>(x.w);
-  f[4] = static_cast<int>(y.x);
-  f[5] = static_cast<int>(y.y);
-  f[6] = static_cast<int>(y.z);
-  f[7] = static_cast<int>(y.w);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[i] = static_cast<int>(x[i]);
+    f[i + 4] = static_cast<int>(y[i]);
+  }
   return f;
+}
+
+__device__ __forceinline__ void wave_lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+__device__ __forceinline__ uint32_t pack_bf16_rne(float lo, float hi) {
+  return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+}
+
+// Waits until at most `later` stages' loads (8 per thread each) are in flight.
+__device__ __forceinline__ void stage_wait(int later) {
+  if (later >= 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  else if (later == 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 template <int EPI>
 __global__ __launch_bounds__(256) void gemm_fp8_kernel(GemmArgs a) {
-  __shared__ __align__(16) uint8_t s_tile[2 * kGStage];
+  __shared__ __align__(16) uint8_t s_tile[kGStages * kGStage];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int ktiles = a.K / kGBK;
   const int tiles = a.mt * a.nt;
   const int fr = lane & 15;          // fragment row
-  const int fk = (lane >> 4) * 32;   // fragment k offset
   float amax = 0.0f;
+  static_assert(kGStages >= 2 && kGStages <= 4, "pipeline depth");
+  // Epilogue geometry: the wave's output block is 64 rows x kWCols columns.
+  constexpr int kWCols = EPI == kEpiSwiglu ? 32 : 64;
+  constexpr int kLanesPerRow = kWCols / 8;
+  constexpr int kRowsPerIter = 64 / kLanesPerRow;
+  constexpr int kIters = 32 / kRowsPerIter;
+  static_assert(4 * 32 * kEP * 4 <= kGStages * kGStage, "epilogue staging fits the stage buffers");
 
   for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
     const int tm = tile % a.mt, tn = tile / a.mt;
@@ -163,72 +214,132 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(GemmArgs a) {
 #pragma unroll
       for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
-    StageRegs r;
-    stage_load<EPI>(a, m0, tn, 0, r);
-    __syncthreads();  // the previous tile's readers are done with both buffers
-    stage_store(s_tile, r);
-    __syncthreads();
-    for (int kt = 0; kt < ktiles; ++kt) {
-      const bool more = kt + 1 < ktiles;
-      if (more) stage_load<EPI>(a, m0, tn, (kt + 1) * kGBK, r);
-      const uint8_t* st = s_tile + (kt & 1) * kGStage;
-      v8i af[4], bf[4];
+    // This wave's output columns [col0, col0 + kWCols) (act columns for swiglu).
+    const int col0 = EPI == kEpiSwiglu ? tn * 64 + wn * 32 : tn * kGBN + wn * 64;
+    const int n_end = EPI == kEpiSwiglu ? a.I : a.N;
+    uint4 res[EPI == kEpiResidual ? 2 * kIters : 1];
+    if (EPI == kEpiResidual) {
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi) af[mi] = frag(st + (wm * 64 + mi * 16 + fr) * kGPitch + fk);
+      for (int j = 0; j < 2 * kIters; ++j) {
+        const int h = j / kIters, it = j % kIters;
+        const int m = m0 + wm * 64 + h * 32 + it * kRowsPerIter + lane / kLanesPerRow;
+        const int n = col0 + (lane % kLanesPerRow) * 8;
+        res[j] = (m < a.M && n < n_end)
+                     ? *reinterpret_cast<const uint4*>(a.ep.residual + static_cast<size_t>(m) * a.ep.ldc + n)
+                     : make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+
+    __syncthreads();  // the previous tile's readers are done with every buffer
+#pragma unroll
+    for (int sidx = 0; sidx < kGStages - 1; ++sidx)
+      if (sidx < ktiles) stage_issue<EPI>(a, m0, tn, sidx * kGBK, s_tile + sidx * kGStage);
+    for (int kt = 0; kt < ktiles; ++kt) {
+      // Stages issued after kt so far: min(kStages - 2, ktiles - 1 - kt).
+      const int later = min(kGStages - 2, ktiles - 1 - kt);
+      stage_wait(later);
+      // Stage kt landed for every wave (each waited for its own loads);
+      // stage kt - 1's reads are done (waited before its MFMAs). No fence:
+      // a workgroup-scope release would wait for the stages still in flight.
+      __builtin_amdgcn_s_barrier();
+      if (kt + kGStages - 1 < ktiles)
+        stage_issue<EPI>(a, m0, tn, (kt + kGStages - 1) * kGBK,
+                         s_tile + ((kt + kGStages - 1) % kGStages) * kGStage);
+      const uint32_t st = lds_addr(s_tile + (kt % kGStages) * kGStage);
+      v4u ax[4], ay[4], bx[4], by[4];
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) frag_issue(st, wm * 64 + mi * 16 + fr, lane, ax[mi], ay[mi]);
 #pragma unroll
       for (int ni = 0; ni < 4; ++ni)
-        bf[ni] = frag(st + (kGBM + b_row<EPI>(wn, ni) + fr) * kGPitch + fk);
+        frag_issue(st + kGBM * kGBK, b_row<EPI>(wn, ni) + fr, lane, bx[ni], by[ni]);
+      lds_reads_done();
+      // The fragments pass through the wait: no use can move above it.
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        asm volatile("" : "+v"(ax[j]), "+v"(ay[j]), "+v"(bx[j]), "+v"(by[j]));
+      }
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
         for (int ni = 0; ni < 4; ++ni)
-          acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[mi], bf[ni], acc[mi][ni],
-                                                                         0, 0, 0, 0, 0, 0);
-      if (more) stage_store(s_tile + ((kt + 1) & 1) * kGStage, r);
-      __syncthreads();
+          acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              frag_of(ax[mi], ay[mi]), frag_of(bx[ni], by[ni]), acc[mi][ni], 0, 0, 0, 0, 0, 0);
     }
 
-    // Epilogue: lane holds rows m0 + wm*64 + mi*16 + 4*(lane/16) + i.
+    // Epilogue through LDS: each wave writes its f32 values (the scaled
+    // GEMM value, or silu(g) * u) 32 rows at a time into its own region and
+    // reads them back row-contiguous, so a lane owns 8 consecutive columns
+    // and every global access is 16 bytes. The residual was prefetched at the
+    // tile's start (a load after a store would wait for the store: the
+    // vector memory counter covers both).
+    __builtin_amdgcn_s_barrier();  // every wave is past its last fragment read
+    float* const sv = reinterpret_cast<float*>(s_tile) + wave * (32 * kEP);
     const Granite4GemmEpilogue& ep = a.ep;
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
+    for (int h = 0; h < 2; ++h) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = m0 + wm * 64 + mi * 16 + 4 * (lane >> 4) + i;
-        if (m >= a.M) continue;
-        if (EPI == kEpiSwiglu) {
+      for (int mj = 0; mj < 2; ++mj) {
+        const int mi = 2 * h + mj;
 #pragma unroll
-          for (int ni = 0; ni < 2; ++ni) {
-            const int c = tn * 64 + wn * 32 + ni * 16 + fr;
-            if (c >= a.I) continue;
-            const float g = acc[mi][ni][i] * (a.a_scale * ep.scale0);
-            const float u = acc[mi][ni + 2][i] * (a.a_scale * ep.scale1);
-            const uint32_t h = f32_to_bf16(silu_mul(g, u));
-            ep.out_bf16[static_cast<size_t>(m) * ep.ldc + c] = static_cast<uint16_t>(h);
-            amax = fmaxf(amax, __uint_as_float((h & 0x7fffu) << 16));
-          }
-        } else {
+        for (int ni = 0; ni < kWCols / 16; ++ni) {
+          const int col = ni * 16 + fr;
 #pragma unroll
-          for (int ni = 0; ni < 4; ++ni) {
-            const int n = tn * kGBN + wn * 64 + ni * 16 + fr;
-            if (n >= a.N) continue;
-            const float y = acc[mi][ni][i] * (a.a_scale * epi_scale(ep, n));
-            const size_t off = static_cast<size_t>(m) * ep.ldc + n;
-            if (EPI == kEpiF32) {
-              ep.out_f32[off] = y;
-            } else if (EPI == kEpiBf16) {
-              ep.out_bf16[off] = static_cast<uint16_t>(f32_to_bf16(y));
+          for (int i = 0; i < 4; ++i) {
+            float v;
+            if (EPI == kEpiSwiglu) {
+              const float g = acc[mi][ni][i] * (a.a_scale * ep.scale0);
+              const float u = acc[mi][ni + 2][i] * (a.a_scale * ep.scale1);
+              v = silu_mul(g, u);
             } else {
-              const float res = __uint_as_float(static_cast<uint32_t>(ep.residual[off]) << 16);
-              ep.out_bf16[off] = static_cast<uint16_t>(f32_to_bf16(res + ep.resid_scale * y));
+              v = acc[mi][ni][i] * (a.a_scale * epi_scale(ep, col0 + col));
             }
+            sv[(mj * 16 + 4 * (lane >> 4) + i) * kEP + col] = v;
           }
         }
       }
+      wave_lds_wait();
+#pragma unroll
+      for (int it = 0; it < kIters; ++it) {
+        const int rl = it * kRowsPerIter + lane / kLanesPerRow;
+        const int ch = lane % kLanesPerRow;
+        const int m = m0 + wm * 64 + h * 32 + rl;
+        const int n = col0 + ch * 8;
+        const float4 lo = *reinterpret_cast<const float4*>(sv + rl * kEP + ch * 8);
+        const float4 hi = *reinterpret_cast<const float4*>(sv + rl * kEP + ch * 8 + 4);
+        if (m >= a.M || n >= n_end) continue;
+        const float y[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        const size_t off = static_cast<size_t>(m) * ep.ldc + n;
+        if (EPI == kEpiF32) {
+          *reinterpret_cast<float4*>(ep.out_f32 + off) = lo;
+          *reinterpret_cast<float4*>(ep.out_f32 + off + 4) = hi;
+          continue;
+        }
+        uint32_t w[4];
+        if (EPI == kEpiResidual) {
+          const uint4 r = res[h * kIters + it];
+          const uint32_t rw[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            w[e] = pack_bf16_rne(lo_bf16(rw[e]) + ep.resid_scale * y[2 * e],
+                                 hi_bf16(rw[e]) + ep.resid_scale * y[2 * e + 1]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[e] = pack_bf16_rne(y[2 * e], y[2 * e + 1]);
+        }
+        if (EPI == kEpiSwiglu) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            amax = fmaxf(amax, fmaxf(lo_bf16(w[e] & 0x7fff7fffu), hi_bf16(w[e] & 0x7fff7fffu)));
+        }
+        *reinterpret_cast<uint4*>(ep.out_bf16 + off) = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+      wave_lds_wait();  // reads done before the next half's writes
     }
   }
   if (EPI == kEpiSwiglu) write_partial(a.partials, amax);
 }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 bool gemm_args_ok(const uint8_t* A, int lda, const uint8_t* W, int M, int N, int K) {
   return A != nullptr && W != nullptr && M > 0 && N > 0 && K > 0 && K % kGBK == 0 && lda >= K &&
@@ -255,11 +366,15 @@ extern "C" {
 
 int granite4_gemm_fp8(int out, const uint8_t* A, int lda, float a_scale, const uint8_t* W, int M,
                       int N, int K, const Granite4GemmEpilogue* ep) {
-  if (!gemm_args_ok(A, lda, W, M, N, K) || ep == nullptr || ep->ldc < N ||
+  if (!gemm_args_ok(A, lda, W, M, N, K) || ep == nullptr || ep->ldc < N || N % 8 != 0 ||
+      ep->ldc % 8 != 0 || !aligned16(ep->out_bf16) || !aligned16(ep->out_f32) ||
+      !aligned16(ep->residual) ||
       !std::isfinite(a_scale) ||
       (out == GRANITE4_GEMM_F32 ? ep->out_f32 == nullptr : ep->out_bf16 == nullptr) ||
       (out == GRANITE4_GEMM_RESIDUAL && ep->residual == nullptr) || out < 0 || out > 2) {
-    std::fprintf(stderr, "granite4: granite4_gemm_fp8: invalid arguments (K %% 128 == 0, lda %% 16 == 0)\n");
+    std::fprintf(stderr,
+                 "granite4: granite4_gemm_fp8: invalid arguments (K %% 128 == 0, lda %% 16 == 0, "
+                 "N %% 8 == 0, ldc %% 8 == 0, 16-byte aligned outputs)\n");
     return -1;
   }
   GemmArgs a{};
@@ -293,7 +408,7 @@ int granite4_gemm_fp8(int out, const uint8_t* A, int lda, float a_scale, const u
 int granite4_gemm_fp8_swiglu(const uint8_t* A, int lda, float a_scale, const uint8_t* W_gu, int M,
                              int I, int K, float gate_scale, float up_scale, uint16_t* act,
                              uint8_t* codes, float* d_scale, void* d_work) {
-  if (!gemm_args_ok(A, lda, W_gu, M, 2 * I, K) || act == nullptr || I % 8 != 0 ||
+  if (!gemm_args_ok(A, lda, W_gu, M, 2 * I, K) || act == nullptr || I % 8 != 0 || !aligned16(act) ||
       !std::isfinite(a_scale) || !std::isfinite(gate_scale) || !std::isfinite(up_scale) ||
       d_work == nullptr || (codes != nullptr && d_scale == nullptr) ||
       static_cast<long long>(M) * I >= INT_MAX) {
@@ -324,6 +439,30 @@ int granite4_gemm_fp8_swiglu(const uint8_t* A, int lda, float a_scale, const uin
   return launch_encode_bf16(act, M, I, work_partials(d_work), static_cast<int>(grid), codes, d_scale)
              ? 0
              : -1;
+}
+
+int granite4_gemm_fp8_residual_rmsnorm_fp8(const uint8_t* A, int lda, float a_scale,
+                                           const uint8_t* W, int M, int H, int K, float w_scale,
+                                           uint16_t* hidden, float resid_scale,
+                                           const uint16_t* gamma, float eps, uint8_t* codes,
+                                           float* d_scale, void* d_work) {
+  if (hidden == nullptr || gamma == nullptr || codes == nullptr || d_scale == nullptr ||
+      d_work == nullptr || !std::isfinite(w_scale) || !std::isfinite(resid_scale)) {
+    std::fprintf(stderr, "granite4: granite4_gemm_fp8_residual_rmsnorm_fp8: invalid arguments\n");
+    return -1;
+  }
+  Granite4GemmEpilogue ep{};
+  ep.scale0 = ep.scale1 = ep.scale2 = w_scale;
+  ep.seg1 = ep.seg2 = H;
+  ep.out_bf16 = hidden;
+  ep.residual = hidden;
+  ep.resid_scale = resid_scale;
+  ep.ldc = H;
+  if (granite4_gemm_fp8(GRANITE4_GEMM_RESIDUAL, A, lda, a_scale, W, M, H, K, &ep) != 0) return -1;
+  // The norm reads only the updated residual (no branch): 2 B read + 1 B
+  // written per element after the GEMM's in-place 2 B + 2 B.
+  return granite4_add_rmsnorm_fp8(hidden, nullptr, 1.0f, gamma, eps, M, H, nullptr, codes, d_scale,
+                                  d_work);
 }
 
 }  // extern "C"

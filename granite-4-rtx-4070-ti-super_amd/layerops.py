@@ -97,6 +97,7 @@ _SIG = {
                                    I],
     "granite4_gemm_fp8": [I, P, I, F, P, I, I, I, _c.POINTER(GemmEpilogue)],
     "granite4_gemm_fp8_swiglu": [P, I, F, P, I, I, I, F, F, P, P, P, P],
+    "granite4_gemm_fp8_residual_rmsnorm_fp8": [P, I, F, P, I, I, I, F, P, F, P, F, P, P, P],
     "granite4_host_fp8_encode": [P, _c.c_size_t, F, P],
     "granite4_host_kv_codes": [P, _c.c_size_t, F, I, P],
     "granite4_selftest_bf16": [P],

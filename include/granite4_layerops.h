@@ -395,8 +395,10 @@ int granite4_attn_paged(const uint16_t* q, int rows, int Hq, int Hk, int d, floa
  * GemmOut / GemmEpilogue (prefill_gemm.h:12-28, epi_store
  * prefill_gemm.cu:69-89); the reference's GEMM takes a bf16 A, this one the
  * FP8 activations of this library. y = acc * (a_scale * w_scale(n)) in f32.
- * Needs K % 128 == 0, lda >= K, lda % 16 == 0, 16-byte aligned A and W,
- * ldc >= N.
+ * Needs K % 128 == 0, lda >= K, lda % 16 == 0, N % 8 == 0, ldc >= N,
+ * ldc % 8 == 0, and 16-byte aligned A, W and outputs (the reference needs
+ * K % 32 == 0 and even N, prefill_gemm.cu:1263-1268; every Granite
+ * projection meets both).
  * ------------------------------------------------------------------------- */
 enum {
   GRANITE4_GEMM_BF16 = 0,     /* out_bf16[m][n] = bf16(y) */
@@ -430,6 +432,18 @@ int granite4_gemm_fp8(int out, const uint8_t* A, int lda, float a_scale, const u
 int granite4_gemm_fp8_swiglu(const uint8_t* A, int lda, float a_scale, const uint8_t* W_gu, int M,
                              int I, int K, float gate_scale, float up_scale, uint16_t* act,
                              uint8_t* codes, float* d_scale, void* d_work);
+
+/* Replaces: the O / down GEMM with the kResidual epilogue followed by the
+ * next RMSNorm (forward_gpu.cu:2834-2836: prefill_gemm(kResidual) +
+ * granite4_kernel_rmsnorm), with the norm's output FP8 for the next GEMM:
+ * hidden[m][n] = bf16(hidden + resid_scale * acc * (a_scale * w_scale)) in
+ * place, then codes / d_scale = the per-tensor FP8 RMSNorm of the updated
+ * hidden (as granite4_add_rmsnorm_fp8 with no branch). H % 8 == 0. */
+int granite4_gemm_fp8_residual_rmsnorm_fp8(const uint8_t* A, int lda, float a_scale,
+                                           const uint8_t* W, int M, int H, int K, float w_scale,
+                                           uint16_t* hidden, float resid_scale,
+                                           const uint16_t* gamma, float eps, uint8_t* codes,
+                                           float* d_scale, void* d_work);
 
 #ifdef __cplusplus
 }  /* extern "C" */

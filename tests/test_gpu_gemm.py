@@ -182,3 +182,44 @@ def test_gemm_fp8_invalid_arguments():
     W = torch.zeros((8, 100), dtype=torch.uint8, device="cuda")
     with pytest.raises(L.Granite4Error):
         L.gemm_fp8(A, 1.0, W)  # K % 128 != 0
+    A = torch.zeros((4, 128), dtype=torch.uint8, device="cuda")
+    W = torch.zeros((12, 128), dtype=torch.uint8, device="cuda")
+    with pytest.raises(L.Granite4Error):
+        L.gemm_fp8(A, 1.0, W)  # N % 8 != 0 (the vector epilogue)
+
+
+@pytest.mark.parametrize("M", [64, 512])
+def test_gemm_fp8_residual_rmsnorm_fp8(M):
+    """O / down GEMM + residual, then the next RMSNorm to FP8: the updated
+    hidden against the oracle (as the residual test), and the codes / scale
+    identical to granite4_add_rmsnorm_fp8 run alone on that hidden."""
+    H, K = 4096, 4096
+    note(f"gemm_fp8_residual_rmsnorm_fp8 M={M}")
+    A = ol.fp8_codes(0x7C + M, (M, K))
+    W = ol.fp8_codes(0x7D, (H, K), std=0.5)
+    res = ol.normal_bf16(0x7E, 0.0, 1.0, M * H).reshape(M, H)
+    gamma = ol.normal_bf16(0x7F, 1.0, 0.1, H)
+    rs, a_s, w_s = 0.22, 0.05, 0.003
+    dA, dW, hid, dg = dev(A), dev(W), dev(res), dev(gamma)
+    codes = torch.empty((M, H), dtype=torch.uint8, device="cuda")
+    scale = torch.empty(1, dtype=torch.float32, device="cuda")
+    work = L.fp8_workspace(rows=M)
+    L.call("granite4_gemm_fp8_residual_rmsnorm_fp8", dA, K, a_s, dW, M, H, K, w_s, hid, rs, dg,
+           1e-5, codes, scale, work)
+    got = host(hid)
+    y = ol.gemm_fp8(A, a_s, W, scales=(w_s, w_s, w_s))
+    want_f32 = (ol.bf16_to_f32(res) + np.float32(rs) * y).astype(np.float32)
+    bad, d = bf16_ok(got, want_f32, abs_bound(A, W, a_s * w_s) * rs)
+    assert not bad.any()
+    codes2 = torch.empty_like(codes)
+    scale2 = torch.empty_like(scale)
+    L.call("granite4_add_rmsnorm_fp8", hid, None, 1.0, dg, 1e-5, M, H, None, codes2, scale2, work)
+    np.testing.assert_array_equal(host(codes), host(codes2))
+    assert host(scale)[0] == host(scale2)[0]
+    # and the norm itself against the oracle (<= 1 ulp) through the bf16 form
+    normed = torch.empty_like(hid)
+    L.call("granite4_kernel_rmsnorm", hid, dg, 1e-5, M, H, normed)
+    assert ulp_diff(host(normed), ol.rmsnorm(got, gamma, 1e-5)).max() <= 1
+    want_codes, want_scale = ol.fp8_quantize(host(normed))
+    assert host(scale)[0] == np.float32(want_scale)
+    np.testing.assert_array_equal(host(codes), want_codes)
