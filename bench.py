@@ -486,25 +486,27 @@ def bench_gemm(torch, L, gen, timed, work, args):
                 "gamma": torch.ones(H, dtype=torch.bfloat16, device=dev),
             })
 
+        a_sc = torch.full((1,), 0.01, dtype=torch.float32, device=dev)
+
         def gu_fused(s):
-            L.call("granite4_gemm_fp8_swiglu", s["a"], H, 0.01, s["w_gu"], T, I, H, 0.01, 0.01,
+            L.call("granite4_gemm_fp8_swiglu", s["a"], H, a_sc, s["w_gu"], T, I, H, 0.01, 0.01,
                    s["act"], s["codes_i"], s["scale"], work)
 
         def gu_unfused(s):
-            L.gemm_fp8(s["a"], 0.01, s["w_gu"], out=s["gu"], scales=(0.01, 0.01, 0.01))
+            L.gemm_fp8(s["a"], a_sc, s["w_gu"], out=s["gu"], scales=(0.01, 0.01, 0.01))
             L.call("granite4_swiglu_fp8", s["gu"], T, I, s["codes_i"], s["scale"], work, None)
 
         def o_fused(s):
-            L.call("granite4_gemm_fp8_residual_rmsnorm_fp8", s["a"], H, 0.01, s["w_o"], T, H, H,
+            L.call("granite4_gemm_fp8_residual_rmsnorm_fp8", s["a"], H, a_sc, s["w_o"], T, H, H,
                    0.01, s["hidden"], 1.0, s["gamma"], 1e-5, s["codes_h"], s["scale"], work)
 
         def o_unfused(s):
-            L.gemm_fp8(s["a"], 0.01, s["w_o"], out=s["branch"], scales=(0.01, 0.01, 0.01))
+            L.gemm_fp8(s["a"], a_sc, s["w_o"], out=s["branch"], scales=(0.01, 0.01, 0.01))
             L.call("granite4_add_rmsnorm_fp8", s["hidden"], s["branch"], 1.0, s["gamma"], 1e-5, T,
                    H, s["res_out"], s["codes_h"], s["scale"], work)
 
         def down(s):
-            L.gemm_fp8(s["act_a"], 0.01, s["w_d"], out=s["hidden"], out_kind=L.GEMM_RESIDUAL,
+            L.gemm_fp8(s["act_a"], a_sc, s["w_d"], out=s["hidden"], out_kind=L.GEMM_RESIDUAL,
                        scales=(0.01, 0.01, 0.01), residual=s["hidden"])
 
         steps = 10 if T == 512 else 4

@@ -3,7 +3,7 @@
 //
 // C[m][n] = a_scale * w_scale(n) * sum_k A[m][k] * W[n][k], A fp8 e4m3 codes
 // [M][K] (row pitch lda bytes; the FP8 output of add+RMSNorm / SwiGLU with
-// its per-tensor scale), W fp8 e4m3 [N][K] row-major with per-tensor scales
+// its per-tensor scale, read from device memory as those ops write it), W fp8 e4m3 [N][K] row-major with per-tensor scales
 // by column segment (scale0 / scale1 / scale2 split at seg1 / seg2, as the
 // reference's GemmEpilogue, prefill_gemm.h:12-28). Products of two e4m3
 // values are exact in f32; the sum runs in f32 in the matrix cores' order.
@@ -72,7 +72,7 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 struct GemmArgs {
   const uint8_t* A;
   int lda;
-  float a_scale;
+  const float* a_scale;  // device: the activation's per-tensor scale
   const uint8_t* W;
   int M, N, K;  // N: weight rows (swiglu: 2I)
   int I;        // swiglu: act columns
@@ -196,6 +196,7 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(GemmArgs a) {
   const int ktiles = a.K / kGBK;
   const int tiles = a.mt * a.nt;
   const int fr = lane & 15;          // fragment row
+  const float a_scale = *a.a_scale;
   float amax = 0.0f;
   static_assert(kGStages >= 2 && kGStages <= 4, "pipeline depth");
   // Epilogue geometry: the wave's output block is 64 rows x kWCols columns.
@@ -287,11 +288,11 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(GemmArgs a) {
           for (int i = 0; i < 4; ++i) {
             float v;
             if (EPI == kEpiSwiglu) {
-              const float g = acc[mi][ni][i] * (a.a_scale * ep.scale0);
-              const float u = acc[mi][ni + 2][i] * (a.a_scale * ep.scale1);
+              const float g = acc[mi][ni][i] * (a_scale * ep.scale0);
+              const float u = acc[mi][ni + 2][i] * (a_scale * ep.scale1);
               v = silu_mul(g, u);
             } else {
-              v = acc[mi][ni][i] * (a.a_scale * epi_scale(ep, col0 + col));
+              v = acc[mi][ni][i] * (a_scale * epi_scale(ep, col0 + col));
             }
             sv[(mj * 16 + 4 * (lane >> 4) + i) * kEP + col] = v;
           }
@@ -364,12 +365,12 @@ using namespace g4;
 
 extern "C" {
 
-int granite4_gemm_fp8(int out, const uint8_t* A, int lda, float a_scale, const uint8_t* W, int M,
-                      int N, int K, const Granite4GemmEpilogue* ep) {
+int granite4_gemm_fp8(int out, const uint8_t* A, int lda, const float* d_a_scale, const uint8_t* W,
+                      int M, int N, int K, const Granite4GemmEpilogue* ep) {
   if (!gemm_args_ok(A, lda, W, M, N, K) || ep == nullptr || ep->ldc < N || N % 8 != 0 ||
       ep->ldc % 8 != 0 || !aligned16(ep->out_bf16) || !aligned16(ep->out_f32) ||
       !aligned16(ep->residual) ||
-      !std::isfinite(a_scale) ||
+      d_a_scale == nullptr ||
       (out == GRANITE4_GEMM_F32 ? ep->out_f32 == nullptr : ep->out_bf16 == nullptr) ||
       (out == GRANITE4_GEMM_RESIDUAL && ep->residual == nullptr) || out < 0 || out > 2) {
     std::fprintf(stderr,
@@ -380,7 +381,7 @@ int granite4_gemm_fp8(int out, const uint8_t* A, int lda, float a_scale, const u
   GemmArgs a{};
   a.A = A;
   a.lda = lda;
-  a.a_scale = a_scale;
+  a.a_scale = d_a_scale;
   a.W = W;
   a.M = M;
   a.N = N;
@@ -405,11 +406,12 @@ int granite4_gemm_fp8(int out, const uint8_t* A, int lda, float a_scale, const u
   return launch_status("granite4_gemm_fp8");
 }
 
-int granite4_gemm_fp8_swiglu(const uint8_t* A, int lda, float a_scale, const uint8_t* W_gu, int M,
-                             int I, int K, float gate_scale, float up_scale, uint16_t* act,
-                             uint8_t* codes, float* d_scale, void* d_work) {
+int granite4_gemm_fp8_swiglu(const uint8_t* A, int lda, const float* d_a_scale,
+                             const uint8_t* W_gu, int M, int I, int K, float gate_scale,
+                             float up_scale, uint16_t* act, uint8_t* codes, float* d_scale,
+                             void* d_work) {
   if (!gemm_args_ok(A, lda, W_gu, M, 2 * I, K) || act == nullptr || I % 8 != 0 || !aligned16(act) ||
-      !std::isfinite(a_scale) || !std::isfinite(gate_scale) || !std::isfinite(up_scale) ||
+      d_a_scale == nullptr || !std::isfinite(gate_scale) || !std::isfinite(up_scale) ||
       d_work == nullptr || (codes != nullptr && d_scale == nullptr) ||
       static_cast<long long>(M) * I >= INT_MAX) {
     std::fprintf(stderr, "granite4: granite4_gemm_fp8_swiglu: invalid arguments\n");
@@ -418,7 +420,7 @@ int granite4_gemm_fp8_swiglu(const uint8_t* A, int lda, float a_scale, const uin
   GemmArgs a{};
   a.A = A;
   a.lda = lda;
-  a.a_scale = a_scale;
+  a.a_scale = d_a_scale;
   a.W = W_gu;
   a.M = M;
   a.N = 2 * I;
@@ -441,7 +443,7 @@ int granite4_gemm_fp8_swiglu(const uint8_t* A, int lda, float a_scale, const uin
              : -1;
 }
 
-int granite4_gemm_fp8_residual_rmsnorm_fp8(const uint8_t* A, int lda, float a_scale,
+int granite4_gemm_fp8_residual_rmsnorm_fp8(const uint8_t* A, int lda, const float* d_a_scale,
                                            const uint8_t* W, int M, int H, int K, float w_scale,
                                            uint16_t* hidden, float resid_scale,
                                            const uint16_t* gamma, float eps, uint8_t* codes,
@@ -458,7 +460,7 @@ int granite4_gemm_fp8_residual_rmsnorm_fp8(const uint8_t* A, int lda, float a_sc
   ep.residual = hidden;
   ep.resid_scale = resid_scale;
   ep.ldc = H;
-  if (granite4_gemm_fp8(GRANITE4_GEMM_RESIDUAL, A, lda, a_scale, W, M, H, K, &ep) != 0) return -1;
+  if (granite4_gemm_fp8(GRANITE4_GEMM_RESIDUAL, A, lda, d_a_scale, W, M, H, K, &ep) != 0) return -1;
   // The norm reads only the updated residual (no branch): 2 B read + 1 B
   // written per element after the GEMM's in-place 2 B + 2 B.
   return granite4_add_rmsnorm_fp8(hidden, nullptr, 1.0f, gamma, eps, M, H, nullptr, codes, d_scale,

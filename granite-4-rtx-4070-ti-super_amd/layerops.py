@@ -95,9 +95,9 @@ _SIG = {
     "granite4_prefill_attn": [P, I, I, I, I, F, P, P, P, P, I, I, I, I, P, I, P],
     "granite4_prefill_attention": [P, P, P, F, I, I, I, I, I, I, P, P, P, P, P, I, P, P, I, P, I,
                                    I],
-    "granite4_gemm_fp8": [I, P, I, F, P, I, I, I, _c.POINTER(GemmEpilogue)],
-    "granite4_gemm_fp8_swiglu": [P, I, F, P, I, I, I, F, F, P, P, P, P],
-    "granite4_gemm_fp8_residual_rmsnorm_fp8": [P, I, F, P, I, I, I, F, P, F, P, F, P, P, P],
+    "granite4_gemm_fp8": [I, P, I, P, P, I, I, I, _c.POINTER(GemmEpilogue)],
+    "granite4_gemm_fp8_swiglu": [P, I, P, P, I, I, I, F, F, P, P, P, P],
+    "granite4_gemm_fp8_residual_rmsnorm_fp8": [P, I, P, P, I, I, I, F, P, F, P, F, P, P, P],
     "granite4_host_fp8_encode": [P, _c.c_size_t, F, P],
     "granite4_host_kv_codes": [P, _c.c_size_t, F, I, P],
     "granite4_selftest_bf16": [P],
@@ -209,12 +209,21 @@ def add_rmsnorm_fp8(res, branch, w, eps, work, resid_mult=1.0, res_out=None, cod
     return res_out, codes, scale
 
 
+def _scale_tensor(a_scale, device):
+    """A device f32 [1] for an activation scale given as a tensor or a number."""
+    if isinstance(a_scale, torch.Tensor):
+        return a_scale
+    return torch.tensor([float(a_scale)], dtype=torch.float32, device=device)
+
+
 def gemm_fp8(A, a_scale, W, out_kind=GEMM_BF16, scales=(1.0, 1.0, 1.0), segs=None, out=None,
              residual=None, resid_scale=1.0):
-    """granite4_gemm_fp8: A [M][K] and W [N][K] e4m3 codes (uint8 tensors).
-    Returns out [M][N] (bf16, or f32 for GEMM_F32; in place for
-    GEMM_RESIDUAL when out is residual)."""
+    """granite4_gemm_fp8: A [M][K] and W [N][K] e4m3 codes (uint8 tensors);
+    a_scale a device f32 [1] (or a number, copied to the device). Returns out
+    [M][N] (bf16, or f32 for GEMM_F32; in place for GEMM_RESIDUAL when out is
+    residual)."""
     M, K = A.shape
+    a_scale = _scale_tensor(a_scale, A.device)
     N = W.shape[0]
     if out is None:
         out = torch.empty((M, N), dtype=torch.float32 if out_kind == GEMM_F32 else torch.bfloat16,
@@ -225,18 +234,19 @@ def gemm_fp8(A, a_scale, W, out_kind=GEMM_BF16, scales=(1.0, 1.0, 1.0), segs=Non
                       out.data_ptr() if out_kind == GEMM_F32 else None,
                       None if residual is None else residual.data_ptr(), float(resid_scale),
                       out.stride(0))
-    call("granite4_gemm_fp8", out_kind, A, A.stride(0), float(a_scale), W, M, N, K, ep)
+    call("granite4_gemm_fp8", out_kind, A, A.stride(0), a_scale, W, M, N, K, ep)
     return out
 
 
 def gemm_fp8_swiglu(A, a_scale, W_gu, gate_scale, up_scale, work, act=None, fp8=True):
     """granite4_gemm_fp8_swiglu: returns act (and codes, scale when fp8)."""
     M, K = A.shape
+    a_scale = _scale_tensor(a_scale, A.device)
     I_ = W_gu.shape[0] // 2
     act = torch.empty((M, I_), dtype=torch.bfloat16, device=A.device) if act is None else act
     codes = torch.empty((M, I_), dtype=torch.uint8, device=A.device) if fp8 else None
     scale = torch.empty(1, dtype=torch.float32, device=A.device) if fp8 else None
-    call("granite4_gemm_fp8_swiglu", A, A.stride(0), float(a_scale), W_gu, M, I_, K,
+    call("granite4_gemm_fp8_swiglu", A, A.stride(0), a_scale, W_gu, M, I_, K,
          float(gate_scale), float(up_scale), act, codes, scale, work)
     return (act, codes, scale) if fp8 else act
 

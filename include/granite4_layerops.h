@@ -390,7 +390,9 @@ int granite4_attn_paged(const uint16_t* q, int rows, int Hq, int Hk, int d, floa
  *
  * C[m][n] = a_scale * w_scale(n) * sum_k A[m][k] W[n][k]: A e4m3 codes [M][K]
  * (row pitch lda bytes, the FP8 output of granite4_add_rmsnorm_fp8 /
- * granite4_swiglu_fp8 with its per-tensor scale), W e4m3 [N][K] row-major.
+ * granite4_swiglu_fp8), a_scale its per-tensor scale read from device memory
+ * (d_a_scale: the d_scale those ops write, so no host round trip and the
+ * calls stay graph-capturable), W e4m3 [N][K] row-major.
  * The epilogue kinds and the per-segment weight scales are the reference's
  * GemmOut / GemmEpilogue (prefill_gemm.h:12-28, epi_store
  * prefill_gemm.cu:69-89); the reference's GEMM takes a bf16 A, this one the
@@ -418,8 +420,8 @@ typedef struct Granite4GemmEpilogue {
 
 /* Replaces: granite4::prefill_gemm (prefill_gemm.h:37-39) for FP8
  * activations; `out` is one of GRANITE4_GEMM_*. */
-int granite4_gemm_fp8(int out, const uint8_t* A, int lda, float a_scale, const uint8_t* W, int M,
-                      int N, int K, const Granite4GemmEpilogue* ep);
+int granite4_gemm_fp8(int out, const uint8_t* A, int lda, const float* d_a_scale, const uint8_t* W,
+                      int M, int N, int K, const Granite4GemmEpilogue* ep);
 
 /* Replaces: the gate|up GEMM with the kF32 epilogue followed by
  * granite4::prefill_silu_mul (forward_gpu.cu:2837-2839, prefill_gemm.cu:
@@ -429,9 +431,10 @@ int granite4_gemm_fp8(int out, const uint8_t* A, int lda, float a_scale, const u
  * it is also quantised to FP8 e4m3 under the per-tensor scale amax / 448
  * (written to d_scale), exactly as granite4_swiglu_fp8 quantises its act.
  * d_work: the FP8 workspace (GRANITE4_FP8_WORK_BYTES(0) bytes at least). */
-int granite4_gemm_fp8_swiglu(const uint8_t* A, int lda, float a_scale, const uint8_t* W_gu, int M,
-                             int I, int K, float gate_scale, float up_scale, uint16_t* act,
-                             uint8_t* codes, float* d_scale, void* d_work);
+int granite4_gemm_fp8_swiglu(const uint8_t* A, int lda, const float* d_a_scale,
+                             const uint8_t* W_gu, int M, int I, int K, float gate_scale,
+                             float up_scale, uint16_t* act, uint8_t* codes, float* d_scale,
+                             void* d_work);
 
 /* Replaces: the O / down GEMM with the kResidual epilogue followed by the
  * next RMSNorm (forward_gpu.cu:2834-2836: prefill_gemm(kResidual) +
@@ -439,7 +442,7 @@ int granite4_gemm_fp8_swiglu(const uint8_t* A, int lda, float a_scale, const uin
  * hidden[m][n] = bf16(hidden + resid_scale * acc * (a_scale * w_scale)) in
  * place, then codes / d_scale = the per-tensor FP8 RMSNorm of the updated
  * hidden (as granite4_add_rmsnorm_fp8 with no branch). H % 8 == 0. */
-int granite4_gemm_fp8_residual_rmsnorm_fp8(const uint8_t* A, int lda, float a_scale,
+int granite4_gemm_fp8_residual_rmsnorm_fp8(const uint8_t* A, int lda, const float* d_a_scale,
                                            const uint8_t* W, int M, int H, int K, float w_scale,
                                            uint16_t* hidden, float resid_scale,
                                            const uint16_t* gamma, float eps, uint8_t* codes,

@@ -204,7 +204,8 @@ def test_gemm_fp8_residual_rmsnorm_fp8(M):
     codes = torch.empty((M, H), dtype=torch.uint8, device="cuda")
     scale = torch.empty(1, dtype=torch.float32, device="cuda")
     work = L.fp8_workspace(rows=M)
-    L.call("granite4_gemm_fp8_residual_rmsnorm_fp8", dA, K, a_s, dW, M, H, K, w_s, hid, rs, dg,
+    d_as = torch.tensor([a_s], dtype=torch.float32, device="cuda")
+    L.call("granite4_gemm_fp8_residual_rmsnorm_fp8", dA, K, d_as, dW, M, H, K, w_s, hid, rs, dg,
            1e-5, codes, scale, work)
     got = host(hid)
     y = ol.gemm_fp8(A, a_s, W, scales=(w_s, w_s, w_s))
@@ -223,3 +224,52 @@ def test_gemm_fp8_residual_rmsnorm_fp8(M):
     want_codes, want_scale = ol.fp8_quantize(host(normed))
     assert host(scale)[0] == np.float32(want_scale)
     np.testing.assert_array_equal(host(codes), want_codes)
+
+
+def test_norm_fp8_feeds_gemm_through_device_scale_graph_replay():
+    """add+RMSNorm -> FP8 chained into the GEMM through the device scale the
+    norm writes (no host round trip), captured once as a HIP graph and
+    replayed with new inputs written between replays: every replay matches
+    the oracle GEMM of that replay's codes and scale."""
+    M, H, N = 96, 4096, 256
+    gamma = dev(ol.normal_bf16(0x90, 1.0, 0.1, H))
+    W = ol.fp8_codes(0x91, (N, H), std=0.5)
+    dW = dev(W)
+    res = torch.empty((M, H), dtype=torch.int16, device="cuda")
+    br = torch.empty_like(res)
+    ro = torch.empty_like(res)
+    codes = torch.empty((M, H), dtype=torch.uint8, device="cuda")
+    scale = torch.empty(1, dtype=torch.float32, device="cuda")
+    out = torch.empty((M, N), dtype=torch.int16, device="cuda")
+    work = L.fp8_workspace(rows=M)
+    w_s = 0.004
+
+    def step():
+        L.call("granite4_add_rmsnorm_fp8", res, br, 1.0, gamma, 1e-5, M, H, ro, codes, scale, work)
+        L.gemm_fp8(codes, scale, dW, out=out, scales=(w_s, w_s, w_s))
+
+    def fill(seed):
+        res.copy_(dev(ol.normal_bf16(seed, 0.0, 1.0, M * H).reshape(M, H)))
+        br.copy_(dev(ol.normal_bf16(seed + 1, 0.0, 2.0, M * H).reshape(M, H)))
+
+    fill(0x92)
+    step()
+    torch.cuda.synchronize()
+    cap = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(cap):
+        L.use_stream(cap)
+        with torch.cuda.graph(g, stream=cap):
+            step()
+    L.use_stream()
+    torch.cuda.synchronize()
+    for rep, seed in enumerate((0x93, 0x95, 0x97)):
+        fill(seed)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        c, s = host(codes), host(scale)[0]
+        y = ol.gemm_fp8(c, s, W, scales=(w_s, w_s, w_s))
+        bad, d = bf16_ok(host(out), y, abs_bound(c, W, s * w_s))
+        note(f"  replay {rep}: scale {s:.6g}, max ulp {d.max()}")
+        assert not bad.any()
