@@ -75,6 +75,8 @@ def main():
                     help="run one configuration and print its detail (profiling runs)")
     ap.add_argument("--T", type=int, default=1024, help="token count for --only tN")
     ap.add_argument("--attn-case", default=None, help="run only this bench_attn case")
+    ap.add_argument("--gemm-case", default=None,
+                    help="run only this bench_gemm case, as T512:name or T8192:name")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the non-GEMM layer ops are "
@@ -469,7 +471,10 @@ def bench_gemm(torch, L, gen, timed, work, args):
         sign = torch.randint(0, 2, shape, generator=gen, device=dev, dtype=torch.int32) << 7
         return (c | sign).to(torch.uint8)
 
+    only = getattr(args, "gemm_case", None)
     for T in (512, 8192):
+        if only and not only.startswith(f"T{T}:"):
+            continue
         sets = []
         for _ in range(2):
             sets.append({
@@ -516,6 +521,8 @@ def bench_gemm(torch, L, gen, timed, work, args):
                                 ("o_residual_rmsnorm_fp8_fused", o_fused, 2.0 * T * H * H),
                                 ("o_then_add_rmsnorm_fp8", o_unfused, 2.0 * T * H * H),
                                 ("down_residual", down, 2.0 * T * H * I)):
+            if only and only != f"T{T}:{name}":
+                continue
             ms = timed(fn, steps, 2, sets, replays=2)
             tf = flops / (ms * 1e-3) / 1e12
             res[name] = {"us": round(ms * 1e3, 2), "TFLOPs": round(tf, 1),
