@@ -32,12 +32,21 @@ HIPFLAGS = [
 
 
 def sources():
-    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith((".hip", ".cc")))
+
+
+# Host-only sources (.cc: the KV page-table controller) build with the host
+# compiler; they hold no device code.
+CXX = os.environ.get("CXX", "g++")
+CXXFLAGS = ["-O2", "-std=c++20", "-fPIC", "-Wall", "-I", os.path.join(ROOT, "include")]
 
 
 def compile_one(src):
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *HIPFLAGS, "-c", src, "-o", obj]
+    if src.endswith(".cc"):
+        cmd = [CXX, *CXXFLAGS, "-c", src, "-o", obj]
+    else:
+        cmd = [HIPCC, *HIPFLAGS, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")

@@ -39,6 +39,7 @@ I = _c.c_int
 F = _c.c_float
 D = _c.c_double
 L = _c.c_long
+Z = _c.c_size_t
 
 
 
@@ -98,17 +99,64 @@ _SIG = {
     "granite4_gemm_fp8": [I, P, I, P, P, I, I, I, _c.POINTER(GemmEpilogue)],
     "granite4_gemm_fp8_swiglu": [P, I, P, P, I, I, I, F, F, P, P, P, P],
     "granite4_gemm_fp8_residual_rmsnorm_fp8": [P, I, P, P, I, I, I, F, P, F, P, F, P, P, P],
+    "granite4_kv_layout_offset": [Z, Z, Z, Z, Z, Z, I, Z, Z],
+    "granite4_kv_pool_create": [Z, Z, Z, Z, Z],
+    "granite4_kv_pool_destroy": [P],
+    "granite4_kv_pool_stat": [P, I],
+    "granite4_kv_pool_create_sequence": [P],
+    "granite4_kv_pool_match_prefix": [P, I, P, Z],
+    "granite4_kv_pool_reserve": [P, I, Z, P, Z],
+    "granite4_kv_pool_mark_written": [P, I, Z],
+    "granite4_kv_pool_locate": [P, I, Z, P],
+    "granite4_kv_pool_row_table": [P, I, Z, P],
+    "granite4_kv_pool_reset_sequence": [P, I],
+    "granite4_kv_pool_truncate_sequence": [P, I, Z],
+    "granite4_kv_pool_release": [P, I],
+    "granite4_kv_pool_clear": [P],
+    "granite4_kv_pool_block_table": [P, I, P, Z],
+    "granite4_kv_pool_sequence_tokens": [P, I],
+    "granite4_kv_pool_ref_count": [P, Z],
+    "granite4_kv_pool_page_in_cache": [P, Z],
+    "granite4_kv_ctrl_create": [Z, Z, Z, Z, Z],
+    "granite4_kv_ctrl_destroy": [P],
+    "granite4_kv_ctrl_stat": [P, I],
+    "granite4_kv_ctrl_new_slot": [P],
+    "granite4_kv_ctrl_release_slot": [P, I],
+    "granite4_kv_ctrl_shutdown": [P],
+    "granite4_kv_ctrl_prefill": [P, I, P, Z, P],
+    "granite4_kv_ctrl_commit": [P, I, P, Z],
+    "granite4_kv_ctrl_open_slot": [P],
+    "granite4_kv_ctrl_ensure": [P, I, Z],
+    "granite4_kv_ctrl_trim": [P, I, Z],
+    "granite4_kv_ctrl_drop": [P, I],
+    "granite4_kv_ctrl_pages_missing": [P, I, Z],
+    "granite4_kv_ctrl_slot_pages": [P, I],
+    "granite4_kv_ctrl_row_table": [P, I, Z, P],
+    "granite4_kv_ctrl_committed": [P, I],
+    "granite4_kv_ctrl_last_reused": [P, I],
     "granite4_host_fp8_encode": [P, _c.c_size_t, F, P],
     "granite4_host_kv_codes": [P, _c.c_size_t, F, I, P],
     "granite4_selftest_bf16": [P],
     "granite4_bw_probe": [P, P, _c.c_size_t, I, I],
     "granite4_selftest_fp8": [F, P],
 }
+_RESTYPE = {"granite4_get_stream": P, "granite4_fp8_work_bytes": Z,
+            "granite4_attn_split_scratch_bytes": Z, "granite4_kv_pool_create": P,
+            "granite4_kv_ctrl_create": P}
 for _name, _args in _SIG.items():
     _fn = getattr(_lib, _name)
     _fn.argtypes = _args
-    _fn.restype = {"granite4_get_stream": P, "granite4_fp8_work_bytes": _c.c_size_t,
-                   "granite4_attn_split_scratch_bytes": _c.c_size_t}.get(_name, I)
+    if _name in _RESTYPE:
+        _fn.restype = _RESTYPE[_name]
+    elif _name.endswith(("_destroy", "_reset_sequence", "_truncate_sequence", "_release",
+                         "_clear", "_release_slot", "_shutdown", "_commit", "_trim", "_drop")):
+        _fn.restype = None
+    elif _name.startswith("granite4_kv_") and not _name.endswith(
+            ("_create_sequence", "_reserve", "_mark_written", "_locate", "_row_table",
+             "_page_in_cache", "_new_slot", "_prefill", "_open_slot", "_ensure")):
+        _fn.restype = Z
+    else:
+        _fn.restype = I
 
 lib = _lib
 
@@ -337,3 +385,169 @@ def multi_rows_struct():
                     ("slot", _c.c_int * R), ("tbase", _c.c_int * R),
                     ("tail", (_c.c_int * T) * R)]
     return GpuMultiRows
+
+
+# ----------------------------------------------------------------------------
+# Host page-table controller (include/granite4_kv_pool.h): the reference's
+# PagedKV / KvPoolController (kv_pool.h, kv_pool_controller.h) by name.
+# ----------------------------------------------------------------------------
+
+import numpy as _np  # noqa: E402
+
+KV_STATS = {"pool_pages": 0, "free_pages": 1, "used_pages": 2, "shared_pages": 3,
+            "cached_pages": 4, "retained_pages": 5, "evicted_pages": 6, "live_sequences": 7,
+            "capacity_tokens": 8, "page_bytes": 9, "tokens_per_page": 10}
+NO_INDEX = (1 << (8 * _c.sizeof(Z))) - 1
+
+
+def _ids(tokens):
+    a = _np.ascontiguousarray(_np.asarray(tokens, dtype=_np.uint32))
+    return a, a.ctypes.data, a.size
+
+
+def kv_layout_offset(layers, kv_heads, head_dim, tokens_per_page, token_local, layer, kv, head,
+                     dim):
+    return _lib.granite4_kv_layout_offset(layers, kv_heads, head_dim, tokens_per_page,
+                                          token_local, layer, kv, head, dim)
+
+
+class _Handle:
+    _prefix = ""
+
+    def __getattr__(self, name):
+        if name in KV_STATS:
+            return lambda: getattr(_lib, self._prefix + "stat")(self._h, KV_STATS[name])
+        raise AttributeError(name)
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            getattr(_lib, self._prefix + "destroy")(h)
+            self._h = None
+
+
+class PagedKV(_Handle):
+    """granite4::PagedKV over the C ABI (sized as KvPoolConfig::from_budget)."""
+    _prefix = "granite4_kv_pool_"
+
+    def __init__(self, layers, kv_heads, head_dim, tokens_per_page, budget_bytes):
+        self._h = _lib.granite4_kv_pool_create(layers, kv_heads, head_dim, tokens_per_page,
+                                               budget_bytes)
+        if not self._h:
+            raise Granite4Error("granite4_kv_pool_create failed")
+
+    def create_sequence(self):
+        return _lib.granite4_kv_pool_create_sequence(self._h)
+
+    def match_prefix(self, seq, tokens):
+        _a, p, n = _ids(tokens)
+        return _lib.granite4_kv_pool_match_prefix(self._h, seq, p, n)
+
+    def reserve(self, seq, token_count, tokens):
+        _a, p, n = _ids(tokens)
+        return bool(_lib.granite4_kv_pool_reserve(self._h, seq, token_count, p, n))
+
+    def mark_written(self, seq, page_index):
+        return bool(_lib.granite4_kv_pool_mark_written(self._h, seq, page_index))
+
+    def locate(self, seq, token):
+        out = (Z * 2)()
+        _lib.granite4_kv_pool_locate(self._h, seq, token, out)
+        return (out[0], out[1])
+
+    def row_table(self, seq, n):
+        out = _np.empty(n, _np.int32)
+        if _lib.granite4_kv_pool_row_table(self._h, seq, n, out.ctypes.data) != 0:
+            return None
+        return out
+
+    def reset_sequence(self, seq):
+        _lib.granite4_kv_pool_reset_sequence(self._h, seq)
+
+    def truncate_sequence(self, seq, n_tokens):
+        _lib.granite4_kv_pool_truncate_sequence(self._h, seq, n_tokens)
+
+    def release(self, seq):
+        _lib.granite4_kv_pool_release(self._h, seq)
+
+    def clear(self):
+        _lib.granite4_kv_pool_clear(self._h)
+
+    def block_table(self, seq):
+        n = _lib.granite4_kv_pool_block_table(self._h, seq, None, 0)
+        out = (Z * max(1, n))()
+        _lib.granite4_kv_pool_block_table(self._h, seq, out, n)
+        return [out[i] for i in range(n)]
+
+    def sequence_tokens(self, seq):
+        return _lib.granite4_kv_pool_sequence_tokens(self._h, seq)
+
+    def ref_count(self, page_id):
+        return _lib.granite4_kv_pool_ref_count(self._h, page_id)
+
+    def page_in_cache(self, page_id):
+        return bool(_lib.granite4_kv_pool_page_in_cache(self._h, page_id))
+
+
+class KvPoolController(_Handle):
+    """granite4::KvPoolController over the C ABI."""
+    _prefix = "granite4_kv_ctrl_"
+
+    def __init__(self, layers, kv_heads, head_dim, tokens_per_page, budget_bytes):
+        self._h = _lib.granite4_kv_ctrl_create(layers, kv_heads, head_dim, tokens_per_page,
+                                               budget_bytes)
+        if not self._h:
+            raise Granite4Error("granite4_kv_ctrl_create failed")
+
+    def max_slots(self):
+        return self.pool_pages()
+
+    def new_slot(self):
+        return _lib.granite4_kv_ctrl_new_slot(self._h)
+
+    def release_slot(self, slot):
+        _lib.granite4_kv_ctrl_release_slot(self._h, slot)
+
+    def shutdown(self):
+        _lib.granite4_kv_ctrl_shutdown(self._h)
+
+    def prefill(self, slot, prompt):
+        """Returns (ok, reused)."""
+        _a, p, n = _ids(prompt)
+        reused = Z(0)
+        ok = _lib.granite4_kv_ctrl_prefill(self._h, slot, p, n, _c.byref(reused)) == 0
+        return ok, reused.value
+
+    def commit(self, slot, tokens):
+        _a, p, n = _ids(tokens)
+        _lib.granite4_kv_ctrl_commit(self._h, slot, p, n)
+
+    def open_slot(self):
+        return _lib.granite4_kv_ctrl_open_slot(self._h)
+
+    def ensure(self, slot, n_tokens):
+        return bool(_lib.granite4_kv_ctrl_ensure(self._h, slot, n_tokens))
+
+    def trim(self, slot, n_tokens):
+        _lib.granite4_kv_ctrl_trim(self._h, slot, n_tokens)
+
+    def drop(self, slot):
+        _lib.granite4_kv_ctrl_drop(self._h, slot)
+
+    def pages_missing(self, slot, n_tokens):
+        return _lib.granite4_kv_ctrl_pages_missing(self._h, slot, n_tokens)
+
+    def slot_pages(self, slot):
+        return _lib.granite4_kv_ctrl_slot_pages(self._h, slot)
+
+    def row_table(self, slot, n):
+        out = _np.empty(n, _np.int32)
+        if _lib.granite4_kv_ctrl_row_table(self._h, slot, n, out.ctypes.data) != 0:
+            return None
+        return out
+
+    def committed(self, slot):
+        return _lib.granite4_kv_ctrl_committed(self._h, slot)
+
+    def last_reused(self, slot):
+        return _lib.granite4_kv_ctrl_last_reused(self._h, slot)

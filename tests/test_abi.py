@@ -3,6 +3,7 @@ declares, validates arguments without touching a GPU, and its host-compiled
 copy of the kernels' scalar arithmetic (FP8 encode, KV codes) matches the
 oracle on exhaustive sweeps."""
 import ctypes
+import os
 import re
 
 import numpy as np
@@ -27,6 +28,16 @@ def test_header_symbols_exported():
     assert not missing, missing
     # every declared symbol also has a ctypes signature in the host module
     assert not [s for s in syms if s not in L._SIG], [s for s in syms if s not in L._SIG]
+
+
+def test_kv_pool_header_symbols_exported():
+    """include/granite4_kv_pool.h: every C entry point is exported and bound."""
+    text = open(os.path.join(os.path.dirname(HEADER), "granite4_kv_pool.h")).read()
+    text = text.split('extern "C" {')[-1]
+    syms = sorted(set(re.findall(r"\b(granite4_\w+)\s*\(", text)))
+    assert len(syms) >= 30
+    assert not [s for s in syms if not hasattr(L.lib, s)]
+    assert not [s for s in syms if s not in L._SIG]
 
 
 def test_argument_validation_returns_minus_one():
