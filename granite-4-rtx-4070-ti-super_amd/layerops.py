@@ -134,6 +134,12 @@ _SIG = {
     "granite4_kv_ctrl_row_table": [P, I, Z, P],
     "granite4_kv_ctrl_committed": [P, I],
     "granite4_kv_ctrl_last_reused": [P, I],
+    "granite4_gemv_fp8w": [P, P, F, I, I, P],
+    "granite4_gemv_fp8w_resid": [P, P, F, P, F, I, I, P],
+    "granite4_gemv_qkv": [P, P, P, P, F, F, F, I, I, I, I, P, P, P],
+    "granite4_gemv_rmsnorm_qkv": [P, P, F, P, P, P, F, F, F, I, I, I, I, P, P, P],
+    "granite4_kernel_silu_gate_up": [P, P, P, F, F, I, I, P],
+    "granite4_gemv_rmsnorm_silu_gate_up": [P, P, F, P, P, F, F, I, I, P],
     "granite4_host_fp8_encode": [P, _c.c_size_t, F, P],
     "granite4_host_kv_codes": [P, _c.c_size_t, F, I, P],
     "granite4_selftest_bf16": [P],

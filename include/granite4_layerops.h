@@ -448,6 +448,53 @@ int granite4_gemm_fp8_residual_rmsnorm_fp8(const uint8_t* A, int lda, const floa
                                            const uint16_t* gamma, float eps, uint8_t* codes,
                                            float* d_scale, void* d_work);
 
+/* ---------------------------------------------------------------------------
+ * Batch-1 decode GEMVs (bf16 activation x fp8 e4m3 weight rows [N][K]) with
+ * the decode step's non-GEMM ops fused in. y[n] = scale * sum_k fp8(W[n][k])
+ * * a[k] in f32, as the reference's gemv_row_dequant (forward_gpu.cu:
+ * 934-994). K % 16 == 0, K <= 16384, 16-byte aligned a and W.
+ * ------------------------------------------------------------------------- */
+
+/* Replaces: row_gemm_dequant_kernel launches (forward_gpu.cu:997-1002):
+ * out[n] = bf16(y). */
+int granite4_gemv_fp8w(const uint16_t* d_a, const uint8_t* d_w, float scale, int N, int K,
+                       uint16_t* d_out);
+
+/* Replaces: row_gemm_dequant_resid_kernel (forward_gpu.cu:1004-1013), the O /
+ * down projection: out[n] = bf16(residual[n] + resid_scale * y); out may be
+ * the residual (in place). */
+int granite4_gemv_fp8w_resid(const uint16_t* d_a, const uint8_t* d_w, float scale,
+                             const uint16_t* d_residual, float resid_scale, int N, int K,
+                             uint16_t* d_out);
+
+/* Replaces: row_gemm_dequant_qkv_kernel (forward_gpu.cu:1034-1057): the q, k,
+ * v projections in one launch, each with its own weight, scale and output. */
+int granite4_gemv_qkv(const uint16_t* d_a, const uint8_t* d_wq, const uint8_t* d_wk,
+                      const uint8_t* d_wv, float sq, float sk, float sv, int Nq, int Nk, int Nv,
+                      int K, uint16_t* d_q, uint16_t* d_k, uint16_t* d_v);
+
+/* Replaces: granite4_kernel_rmsnorm (kernels_phase2.cu:910) followed by the
+ * q / k / v GEMV (forward_gpu.cu:2115-2131): d_x is the residual row; every
+ * workgroup computes bf16(x * r * gamma) itself (r from the double sum of
+ * squares, as granite4_kernel_rmsnorm) and multiplies it. */
+int granite4_gemv_rmsnorm_qkv(const uint16_t* d_x, const uint16_t* d_gamma, float eps,
+                              const uint8_t* d_wq, const uint8_t* d_wk, const uint8_t* d_wv,
+                              float sq, float sk, float sv, int Nq, int Nk, int Nv, int K,
+                              uint16_t* d_q, uint16_t* d_k, uint16_t* d_v);
+
+/* Replaces: granite4_kernel_silu_gate_up (kernels_phase2.cu:1217, the same
+ * signature): act[i] = bf16(g * (1 / (1 + exp(-g))) * u), g = scale_g * (gate
+ * row i . x), u = scale_u * (up row i . x). */
+int granite4_kernel_silu_gate_up(const uint8_t* d_wg, const uint8_t* d_wu, const uint16_t* d_x,
+                                 float scale_g, float scale_u, int N, int K, uint16_t* d_out);
+
+/* Replaces: granite4_kernel_rmsnorm followed by granite4_kernel_silu_gate_up
+ * (forward_gpu.cu:2227-2234): d_x is the residual row, normalised in every
+ * workgroup as granite4_gemv_rmsnorm_qkv does. */
+int granite4_gemv_rmsnorm_silu_gate_up(const uint16_t* d_x, const uint16_t* d_gamma, float eps,
+                                       const uint8_t* d_wg, const uint8_t* d_wu, float scale_g,
+                                       float scale_u, int N, int K, uint16_t* d_out);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 

@@ -74,6 +74,11 @@ void g4o_silu_mul_f32(const float* gu, int I, int rows, uint16_t* act);
 void g4o_gemm_fp8(const uint8_t* A, int lda, float a_scale, const uint8_t* W, int M, int N, int K,
                   float scale0, float scale1, float scale2, int seg1, int seg2, float* y);
 
+/* Decode GEMV value before rounding (gemv_row_dequant forward_gpu.cu:934-994):
+ * y[n] = scale * (float)S[n], S = sum_k bf16(a[k]) * fp8(W[n][k]) in double
+ * (products exact). a bf16 [K], W [N][K], y [N]. */
+void g4o_gemv_fp8w(const uint16_t* a, const uint8_t* W, int N, int K, float scale, float* y);
+
 /* RoPE (kernel_math.h:191-219, kernels_phase2.cu:138-162). */
 void g4o_rope_tables(double theta, int head_dim, int max_pos, float* cos_t, float* sin_t);
 void g4o_rope_rows(const uint16_t* x, int rows, int heads, int d, const int* pos,

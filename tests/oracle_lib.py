@@ -50,6 +50,7 @@ def _load():
         "g4o_silu_mul_f32": (None, [f32p, _c.c_int, _c.c_int, u16p]),
         "g4o_gemm_fp8": (None, [u8p, _c.c_int, _c.c_float, u8p, _c.c_int, _c.c_int, _c.c_int,
                                 _c.c_float, _c.c_float, _c.c_float, _c.c_int, _c.c_int, f32p]),
+        "g4o_gemv_fp8w": (None, [u16p, u8p, _c.c_int, _c.c_int, _c.c_float, f32p]),
         "g4o_rope_tables": (None, [_c.c_double, _c.c_int, _c.c_int, f32p, f32p]),
         "g4o_rope_rows": (None, [u16p, _c.c_int, _c.c_int, _c.c_int, i32p, f32p, f32p, u16p]),
         "g4o_kv_scale": (_c.c_float, [_c.c_float, _c.c_int]),
@@ -170,6 +171,16 @@ def gemm_fp8(A, a_scale, W, scales=(1.0, 1.0, 1.0), segs=None):
     y = np.empty((M, N), np.float32)
     lib.g4o_gemm_fp8(_p(A, u8p), K, a_scale, _p(W, u8p), M, N, K, scales[0], scales[1], scales[2],
                      s1, s2, _p(y, f32p))
+    return y
+
+
+def gemv_fp8w(a, W, scale):
+    """y [N] f32 (g4o_gemv_fp8w): bf16 a [K] x e4m3 W [N][K], double sum."""
+    a = np.ascontiguousarray(a, np.uint16)
+    W = np.ascontiguousarray(W, np.uint8)
+    N, K = W.shape
+    y = np.empty(N, np.float32)
+    lib.g4o_gemv_fp8w(_p(a, u16p), _p(W, u8p), N, K, scale, _p(y, f32p))
     return y
 
 

@@ -46,3 +46,12 @@ def test_gemm_oracle_segment_scales():
     np.testing.assert_array_equal(y[:, :4], y1[:, :4])
     np.testing.assert_array_equal(y[:, 4:8], (0.5 * y1[:, 4:8].astype(np.float64)).astype(np.float32))
     np.testing.assert_array_equal(y[:, 8:], (0.25 * y1[:, 8:].astype(np.float64)).astype(np.float32))
+
+
+def test_gemv_oracle_matches_float64_dot():
+    K, N = 256, 24
+    a = ol.normal_bf16(0x66, 0.0, 1.0, K)
+    W = ol.fp8_codes(0x67, (N, K), std=0.5)
+    y = ol.gemv_fp8w(a, W, 0.0123)
+    exact = DEC[W] @ ol.bf16_to_f32(a).astype(np.float64)
+    np.testing.assert_array_equal(y, np.float32(0.0123) * exact.astype(np.float32))
