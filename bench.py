@@ -71,7 +71,7 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline + decode only")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=["t512", "t8192", "decode", "t8", "stress", "tN", "probe",
-                                       "attn", "gemm"],
+                                       "attn", "gemm", "decode_gemv"],
                     help="run one configuration and print its detail (profiling runs)")
     ap.add_argument("--T", type=int, default=1024, help="token count for --only tN")
     ap.add_argument("--attn-case", default=None, help="run only this bench_attn case")
@@ -219,6 +219,8 @@ def main():
         elif args.only == "tN":
             r = measure_ops(args.T, max(2, min(8, 4096 // args.T)), 8, 128, 0, 8, args.steps,
                             args.warmup)
+        elif args.only == "decode_gemv":
+            r = bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream)
         elif args.only == "decode":
             r = {"decode_T1": bench_decode(torch, L, randn, cos_t, sin_t, emb, gamma, stream, args),
                  "decode_T1_with_attention": bench_decode(torch, L, randn, cos_t, sin_t, emb, gamma,
@@ -390,6 +392,128 @@ def bench_decode(torch, L, randn, cos_t, sin_t, emb, gamma, stream, args, layers
             "graph_us_per_step": round(graph_us, 2),
             "eager_us_per_step": round(eager_us, 2), "ideal_bytes": ideal,
             "ideal_us_at_peak": round(ideal / PEAK_GBS / 1e3, 3)}
+
+
+def graph_us(torch, L, stream, step, reps=20):
+    """µs per step() replayed as one HIP graph (captured on a side stream)."""
+    g = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        L.use_stream(cap)
+        step()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=cap):
+            step()
+    L.use_stream(stream)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    del g
+    return e0.elapsed_time(e1) / reps * 1e3
+
+
+def bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream, layers=40):
+    """Batch-1 decode step with its GEMVs (fp8 weight rows of the 8B model:
+    q|k|v 6144 x 4096, o 4096 x 4096, gate and up 12800 x 4096, down 4096 x
+    12800; 199 MB per layer, random e4m3 codes), three ways, each replayed as
+    one HIP graph:
+      plain    the GEMVs alone (no norm, RoPE, KV write, SwiGLU, residual);
+      unfused  the reference's decode order: RMSNorm, q|k|v GEMV, RoPE + bf16
+               KV append, O GEMV + residual, RMSNorm, gate/up GEMV + SwiGLU,
+               down GEMV + residual (7 launches per layer);
+      fused    RMSNorm as the GEMV prologue, SwiGLU and residual as epilogues,
+               RoPE + append still a launch of its own (5 per layer).
+    The non-GEMM overhead of a step is its time minus the plain step's."""
+    dev = "cuda"
+    stride = 8192
+    pos = torch.tensor([4321], dtype=torch.int32, device=dev)
+    toks = torch.randint(0, VOCAB, (8192,), dtype=torch.int32, device=dev)
+    pt = torch.randperm(stride, device=dev).to(torch.int32)
+
+    def codes(*shape):
+        c = torch.randint(0, 0x7F, shape, generator=gen, device=dev, dtype=torch.int32)
+        sign = torch.randint(0, 2, shape, generator=gen, device=dev, dtype=torch.int32) << 7
+        return (c | sign).to(torch.uint8)
+
+    def bf(*shape):
+        return torch.randn(shape, generator=gen, device=dev).to(torch.bfloat16)
+
+    per = []
+    for _ in range(layers):
+        per.append({"wq": codes(HQ * D, H), "wk": codes(HK * D, H), "wv": codes(HK * D, H),
+                    "wo": codes(H, HQ * D), "wg": codes(I, H), "wu": codes(I, H),
+                    "wd": codes(H, I), "arena": L.KvArena(16, HK, stride)})
+    hidden = bf(H)
+    normed = bf(H)
+    q, k, v = bf(HQ * D), bf(HK * D), bf(HK * D)
+    q_rot = bf(HQ * D)
+    attn_out = bf(HQ * D)
+    act = bf(I)
+    g_out, u_out, o_out = bf(I), bf(I), bf(H)
+    sc = 1.0 / 512
+
+    def plain():
+        for p in per:
+            L.call("granite4_gemv_qkv", normed, p["wq"], p["wk"], p["wv"], sc, sc, sc, HQ * D,
+                   HK * D, HK * D, H, q, k, v)
+            L.call("granite4_gemv_fp8w", attn_out, p["wo"], sc, H, HQ * D, o_out)
+            L.call("granite4_gemv_qkv", normed, p["wg"], p["wu"], None, sc, sc, 0.0, I, I, 0, H,
+                   g_out, u_out, None)
+            L.call("granite4_gemv_fp8w", act, p["wd"], sc, H, I, o_out)
+
+    def rope(p):
+        a = p["arena"]
+        L.call("granite4_rope_append_at_pos", q, k, v, cos_t, sin_t, 65536, pos, pt, HQ, HK, D,
+               16, 128, q_rot, a.k, a.v, a.k_scale, a.v_scale, stride)
+
+    def unfused():
+        L.call("granite4_embed_at_pos", toks, pos, emb, VOCAB, H, 1.0, hidden)
+        for p in per:
+            L.call("granite4_kernel_rmsnorm", hidden, gamma, 1e-5, 1, H, normed)
+            L.call("granite4_gemv_qkv", normed, p["wq"], p["wk"], p["wv"], sc, sc, sc, HQ * D,
+                   HK * D, HK * D, H, q, k, v)
+            rope(p)
+            L.call("granite4_gemv_fp8w_resid", attn_out, p["wo"], sc, hidden, 1.0, H, HQ * D,
+                   hidden)
+            L.call("granite4_kernel_rmsnorm", hidden, gamma, 1e-5, 1, H, normed)
+            L.call("granite4_kernel_silu_gate_up", p["wg"], p["wu"], normed, sc, sc, I, H, act)
+            L.call("granite4_gemv_fp8w_resid", act, p["wd"], sc, hidden, 1.0, H, I, hidden)
+
+    def fused():
+        L.call("granite4_embed_at_pos", toks, pos, emb, VOCAB, H, 1.0, hidden)
+        for p in per:
+            L.call("granite4_gemv_rmsnorm_qkv", hidden, gamma, 1e-5, p["wq"], p["wk"], p["wv"],
+                   sc, sc, sc, HQ * D, HK * D, HK * D, H, q, k, v)
+            rope(p)
+            L.call("granite4_gemv_fp8w_resid", attn_out, p["wo"], sc, hidden, 1.0, H, HQ * D,
+                   hidden)
+            L.call("granite4_gemv_rmsnorm_silu_gate_up", hidden, gamma, 1e-5, p["wg"], p["wu"],
+                   sc, sc, I, H, act)
+            L.call("granite4_gemv_fp8w_resid", act, p["wd"], sc, hidden, 1.0, H, I, hidden)
+
+    t_plain = graph_us(torch, L, stream, plain)
+    t_unfused = graph_us(torch, L, stream, unfused)
+    t_fused = graph_us(torch, L, stream, fused)
+    wbytes = layers * (HQ * D + 2 * HK * D + 2 * I) * H + layers * H * (HQ * D + I)
+    del per
+    torch.cuda.empty_cache()
+    return {"layers": layers, "weight_bytes": wbytes,
+            "plain_gemv_us": round(t_plain, 1),
+            "plain_gemv_GBps": round(wbytes / (t_plain * 1e-6) / 1e9, 1),
+            "unfused_us": round(t_unfused, 1), "fused_us": round(t_fused, 1),
+            "non_gemm_overhead_unfused_us": round(t_unfused - t_plain, 1),
+            "non_gemm_overhead_fused_us": round(t_fused - t_plain, 1),
+            "launches_per_step": {"plain": 4 * layers, "unfused": 1 + 7 * layers,
+                                  "fused": 1 + 5 * layers}}
 
 
 def bench_multi8(torch, L, randn, cos_t, sin_t, gamma, work, gen, stream, timed, args):

@@ -15,12 +15,16 @@
 // (kernels_phase2.cu:51-132): every workgroup normalises the whole row for
 // itself (8 KB from L2), which costs less than a separate launch.
 //
-// Layout: 256-thread workgroups, 16 weight rows each (4 per wave); lane l
-// streams bytes [16 l + 1024 j, +16) of its wave's rows (16-byte loads,
-// non-temporal: each weight byte is read once per step) with the next step's
-// loads in flight, and reads the matching 16 activations from LDS (f32). The
-// first weight loads are issued before the prologue, so the norm's latency
-// overlaps them. Sums: per-lane f32 partials, then a DPP wave reduction.
+// Layout: 256-thread workgroups of 16 weight rows (swiglu: 8 gate + the 8
+// matching up rows). The workgroup walks its rows in order with G4_GEMV_DEPTH
+// rows of loads in flight, its 4 waves reading each row together (wave w the
+// quarter [w K/4, (w+1) K/4), 16 bytes per lane per 1024-byte chunk,
+// non-temporal), so each workgroup's accesses stay inside a few contiguous
+// rows. Measured: one row per wave streamed 1 KB at a time left thousands of
+// scattered 1 KB streams open and reached 2.4-3.1 TB/s. A lane's activations
+// are the same for every row (its K positions are fixed), so they live in
+// registers (f32); there is no LDS staging. Sums: per-lane f32 partials, a
+// wave reduction, then the 4 waves' partials in a fixed order.
 
 #include "g4_common.h"
 #include "g4_hw.h"
@@ -37,9 +41,13 @@ namespace {
 enum : int { kProNone = 0, kProNorm = 1 };
 enum : int { kEpiOut = 0, kEpiResid = 1, kEpiSwiglu = 2 };
 
-constexpr int kRowsPerWave = 4;
-constexpr int kRowsPerBlock = 4 * kRowsPerWave;
-constexpr int kMaxK = 16384;  // LDS activation f32 [K]: 64 KB at most
+#ifndef G4_GEMV_DEPTH
+#define G4_GEMV_DEPTH 4
+#endif
+constexpr int kRows = 16;                 // weight rows per workgroup
+constexpr int kDepth = G4_GEMV_DEPTH;     // rows of loads in flight
+constexpr int kMaxChunks = 4;             // 1024-byte chunks per wave per row: K <= 16384
+constexpr int kMaxK = 4 * kMaxChunks * 1024;
 
 struct GemvArgs {
   const uint16_t* x;      // activation, or the residual row to normalise
@@ -79,54 +87,88 @@ __device__ __forceinline__ void fp8x16_to_f32(const uint4& q, float (&f)[16]) {
   }
 }
 
-// Weight row r of the workgroup's 16 (swiglu: rows 0..7 gate, 8..15 up of the
-// same 8 act columns, wave w holding gate c, c+1 and up c, c+1).
+// Weight row r (0..15) of the workgroup, or nullptr past the end (n: its
+// output index). swiglu: rows 0..7 gate, 8..15 up, of the same 8 act columns.
 template <int EPI>
-__device__ __forceinline__ const uint8_t* row_ptr(const GemvArgs& a, int wave, int j, int& n) {
+__device__ __forceinline__ const uint8_t* row_ptr(const GemvArgs& a, int r, int& n) {
   if (EPI == kEpiSwiglu) {
-    const int c = blockIdx.x * 8 + 2 * wave + (j & 1);
+    const int c = blockIdx.x * (kRows / 2) + (r % (kRows / 2));
     n = c;
     if (c >= a.I) return nullptr;
-    return (j < 2 ? a.w[0] : a.w[1]) + static_cast<size_t>(c) * a.K;
+    return (r < kRows / 2 ? a.w[0] : a.w[1]) + static_cast<size_t>(c) * a.K;
   }
-  const int r = blockIdx.x * kRowsPerBlock + wave * kRowsPerWave + j;
-  n = r;
-  if (r >= a.N) return nullptr;
-  if (r < a.seg1) return a.w[0] + static_cast<size_t>(r) * a.K;
-  if (r < a.seg2) return a.w[1] + static_cast<size_t>(r - a.seg1) * a.K;
-  return a.w[2] + static_cast<size_t>(r - a.seg2) * a.K;
+  const int i = blockIdx.x * kRows + r;
+  n = i;
+  if (i >= a.N) return nullptr;
+  if (i < a.seg1) return a.w[0] + static_cast<size_t>(i) * a.K;
+  if (i < a.seg2) return a.w[1] + static_cast<size_t>(i - a.seg1) * a.K;
+  return a.w[2] + static_cast<size_t>(i - a.seg2) * a.K;
 }
 
-template <int PRO, int EPI>
+// Workgroup barrier for LDS exchanges only (waits for this wave's LDS
+// operations, not for its weight loads in flight).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <int PRO, int EPI, int kChunks>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
-  extern __shared__ float s_a[];  // activation, f32 [K]
   __shared__ double s_ss[4];
+  __shared__ float s_part[4][kRows];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int K = a.K;
-  const int steps = (K + 1023) / 1024;
-  const uint8_t* rows[kRowsPerWave];
-  int ns[kRowsPerWave];
+  const int kq = K / 4;                 // bytes of each row this wave reads
+  const int kw = wave * kq;             // its first byte
+  // Lane chunk c covers bytes [kw + 1024 c + 16 lane, +16) of every row.
+  bool cin[kChunks];
+  int koff[kChunks];
 #pragma unroll
-  for (int j = 0; j < kRowsPerWave; ++j) rows[j] = row_ptr<EPI>(a, wave, j, ns[j]);
+  for (int c = 0; c < kChunks; ++c) {
+    const int o = 1024 * c + 16 * lane;
+    cin[c] = o < kq;
+    koff[c] = kw + (cin[c] ? o : 0);  // out-of-range chunks reread the first (zeroed later)
+  }
+  const uint8_t* rows[kRows];
+  int ns[kRows];
+  bool live[kRows];
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) {
+    rows[r] = row_ptr<EPI>(a, r, ns[r]);
+    live[r] = rows[r] != nullptr;
+    if (!live[r]) rows[r] = a.w[0];
+  }
 
-  // First step's weight loads, before the prologue.
-  uint4 wcur[kRowsPerWave];
-  const auto load_step = [&](int st, uint4 (&dst)[kRowsPerWave]) {
-    const int k0 = st * 1024 + 16 * lane;
+  // Rows of weights stream in order, kDepth rows in flight; the 4 waves read
+  // each row together (4 contiguous quarters), so the workgroup's accesses
+  // stay within a few contiguous rows at any time. Every load is
+  // unconditional (out-of-range data is zeroed before use).
+  uint4 buf[kDepth][kChunks];
+  const auto load_row = [&](int r, uint4 (&dst)[kChunks]) {
 #pragma unroll
-    for (int j = 0; j < kRowsPerWave; ++j)
-      dst[j] = (rows[j] != nullptr && k0 < K) ? ld_u4_nt(rows[j] + k0) : make_uint4(0u, 0u, 0u, 0u);
+    for (int c = 0; c < kChunks; ++c) dst[c] = ld_u4_nt(rows[r] + koff[c]);
   };
-  load_step(0, wcur);
+#pragma unroll
+  for (int r = 0; r < kDepth; ++r) load_row(r, buf[r]);
 
-  // Prologue: the activation into LDS as f32.
+  // Prologue: the lane's 16 activations per chunk, in registers (f32).
+  float av[kChunks][16];
+  uint4 xr[kChunks][2];
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    xr[c][0] = *reinterpret_cast<const uint4*>(a.x + koff[c]);
+    xr[c][1] = *reinterpret_cast<const uint4*>(a.x + koff[c] + 8);
+  }
   if (PRO == kProNorm) {
     double ss = 0.0;
-    for (int k = 8 * threadIdx.x; k < K; k += 8 * 256) {
-      const uint4 v = *reinterpret_cast<const uint4*>(a.x + k);
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
+    for (int c = 0; c < kChunks; ++c) {
+      if (!cin[c]) continue;
+      const uint32_t w[8] = {xr[c][0].x, xr[c][0].y, xr[c][0].z, xr[c][0].w,
+                             xr[c][1].x, xr[c][1].y, xr[c][1].z, xr[c][1].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
         const float lo = lo_bf16(w[e]), hi = hi_bf16(w[e]);
         ss += static_cast<double>(lo * lo);
         ss += static_cast<double>(hi * hi);
@@ -134,100 +176,99 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     }
     ss = wave_sum(ss);
     if (lane == 0) s_ss[wave] = ss;
-    __syncthreads();
+    lds_barrier();
     ss = s_ss[0] + s_ss[1] + s_ss[2] + s_ss[3];
-    const float r = 1.0f / sqrtf(static_cast<float>(ss / K) + a.eps);
-    for (int k = 8 * threadIdx.x; k < K; k += 8 * 256) {
-      const uint4 v = *reinterpret_cast<const uint4*>(a.x + k);
-      const uint4 g = *reinterpret_cast<const uint4*>(a.gamma + k);
-      const uint32_t xv[4] = {v.x, v.y, v.z, v.w}, gv[4] = {g.x, g.y, g.z, g.w};
+    const float rr = 1.0f / sqrtf(static_cast<float>(ss / K) + a.eps);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t y = pack_bf16_hw(lo_bf16(xv[e]) * r * lo_bf16(gv[e]),
-                                        hi_bf16(xv[e]) * r * hi_bf16(gv[e]));
-        s_a[k + 2 * e] = lo_bf16(y);
-        s_a[k + 2 * e + 1] = hi_bf16(y);
+    for (int c = 0; c < kChunks; ++c) {
+      const uint4 g0 = *reinterpret_cast<const uint4*>(a.gamma + koff[c]);
+      const uint4 g1 = *reinterpret_cast<const uint4*>(a.gamma + koff[c] + 8);
+      const uint32_t xv[8] = {xr[c][0].x, xr[c][0].y, xr[c][0].z, xr[c][0].w,
+                              xr[c][1].x, xr[c][1].y, xr[c][1].z, xr[c][1].w};
+      const uint32_t gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t y = pack_bf16_hw(lo_bf16(xv[e]) * rr * lo_bf16(gv[e]),
+                                        hi_bf16(xv[e]) * rr * hi_bf16(gv[e]));
+        av[c][2 * e] = lo_bf16(y);
+        av[c][2 * e + 1] = hi_bf16(y);
       }
     }
   } else {
-    for (int k = 8 * threadIdx.x; k < K; k += 8 * 256) {
-      const uint4 v = *reinterpret_cast<const uint4*>(a.x + k);
-      const uint32_t xv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        s_a[k + 2 * e] = lo_bf16(xv[e]);
-        s_a[k + 2 * e + 1] = hi_bf16(xv[e]);
+    for (int c = 0; c < kChunks; ++c) {
+      const uint32_t xv[8] = {xr[c][0].x, xr[c][0].y, xr[c][0].z, xr[c][0].w,
+                              xr[c][1].x, xr[c][1].y, xr[c][1].z, xr[c][1].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        av[c][2 * e] = lo_bf16(xv[e]);
+        av[c][2 * e + 1] = hi_bf16(xv[e]);
       }
     }
   }
-  __syncthreads();
 
-  float acc[kRowsPerWave] = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int st = 0; st < steps; ++st) {
-    uint4 wnext[kRowsPerWave];
-    if (st + 1 < steps) load_step(st + 1, wnext);
-    const int k0 = st * 1024 + 16 * lane;
-    if (k0 < K) {
-      float av[16];
+  float acc[kRows];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float4 f = *reinterpret_cast<const float4*>(s_a + k0 + 4 * q);
-        av[4 * q] = f.x;
-        av[4 * q + 1] = f.y;
-        av[4 * q + 2] = f.z;
-        av[4 * q + 3] = f.w;
-      }
+  for (int r = 0; r < kRows; ++r) {
+    const int slot = r % kDepth;
+    float sum = 0.0f;
 #pragma unroll
-      for (int j = 0; j < kRowsPerWave; ++j) {
-        float wf[16];
-        fp8x16_to_f32(wcur[j], wf);
+    for (int c = 0; c < kChunks; ++c) {
+      uint4 q = buf[slot][c];
+      if (!(cin[c] && live[r])) q = make_uint4(0u, 0u, 0u, 0u);
+      float wf[16];
+      fp8x16_to_f32(q, wf);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) acc[j] = fmaf(wf[e], av[e], acc[j]);
-      }
+      for (int e = 0; e < 16; ++e) sum = fmaf(wf[e], av[c][e], sum);
     }
-    if (st + 1 < steps) {
-#pragma unroll
-      for (int j = 0; j < kRowsPerWave; ++j) wcur[j] = wnext[j];
-    }
+    acc[r] = sum;
+    if (r + kDepth < kRows) load_row(r + kDepth, buf[slot]);
   }
 #pragma unroll
-  for (int j = 0; j < kRowsPerWave; ++j) acc[j] = wave_sum_f32(acc[j]);
-  if (lane != 0) return;
+  for (int r = 0; r < kRows; ++r) acc[r] = wave_sum_f32(acc[r]);
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) s_part[wave][r] = acc[r];
+  }
+  lds_barrier();
+  if (threadIdx.x >= kRows) return;
+  const int r = threadIdx.x;
+  const float tot = (s_part[0][r] + s_part[1][r]) + (s_part[2][r] + s_part[3][r]);
 
   if (EPI == kEpiSwiglu) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int c = ns[t];
-      if (c >= a.I) continue;
-      const float g = a.s[0] * acc[t];
-      const float u = a.s[1] * acc[2 + t];
-      a.o[0][c] = static_cast<uint16_t>(f32_to_bf16(silu_mul(g, u)));
-    }
+    if (r >= kRows / 2) return;
+    const int c = blockIdx.x * (kRows / 2) + r;
+    if (c >= a.I) return;
+    const float gsum = tot;
+    const float usum = (s_part[0][r + kRows / 2] + s_part[1][r + kRows / 2]) +
+                       (s_part[2][r + kRows / 2] + s_part[3][r + kRows / 2]);
+    a.o[0][c] = static_cast<uint16_t>(f32_to_bf16(silu_mul(a.s[0] * gsum, a.s[1] * usum)));
     return;
   }
-#pragma unroll
-  for (int j = 0; j < kRowsPerWave; ++j) {
-    const int n = ns[j];
-    if (n >= a.N) continue;
-    if (EPI == kEpiResid) {
-      const float y = a.s[0] * acc[j];
-      const float res = __uint_as_float(static_cast<uint32_t>(a.residual[n]) << 16);
-      a.o[0][n] = static_cast<uint16_t>(f32_to_bf16(res + a.rs * y));
-    } else {
-      const int seg = n < a.seg1 ? 0 : (n < a.seg2 ? 1 : 2);
-      const int base = seg == 0 ? 0 : (seg == 1 ? a.seg1 : a.seg2);
-      a.o[seg][n - base] = static_cast<uint16_t>(f32_to_bf16(a.s[seg] * acc[j]));
-    }
+  const int n = blockIdx.x * kRows + r;
+  if (n >= a.N) return;
+  if (EPI == kEpiResid) {
+    const float y = a.s[0] * tot;
+    const float res = __uint_as_float(static_cast<uint32_t>(a.residual[n]) << 16);
+    a.o[0][n] = static_cast<uint16_t>(f32_to_bf16(res + a.rs * y));
+  } else {
+    const int seg = n < a.seg1 ? 0 : (n < a.seg2 ? 1 : 2);
+    const int base = seg == 0 ? 0 : (seg == 1 ? a.seg1 : a.seg2);
+    a.o[seg][n - base] = static_cast<uint16_t>(f32_to_bf16(a.s[seg] * tot));
   }
 }
 
-bool gemv_k_ok(int K) { return K > 0 && K % 16 == 0 && K <= kMaxK; }
+bool gemv_k_ok(int K) { return K >= 64 && K % 64 == 0 && K <= kMaxK; }
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Chunks per wave per row: K / 4 bytes in 1024-byte chunks.
 template <int PRO, int EPI>
 int launch_gemv(const GemvArgs& a, unsigned grid, const char* what) {
-  hipLaunchKernelGGL((gemv_kernel<PRO, EPI>), grid, 256, static_cast<size_t>(a.K) * sizeof(float),
-                     stream(), a);
+  const int ch = (a.K / 4 + 1023) / 1024;
+  const hipStream_t st = stream();
+  if (ch <= 1) hipLaunchKernelGGL((gemv_kernel<PRO, EPI, 1>), grid, 256, 0, st, a);
+  else if (ch == 2) hipLaunchKernelGGL((gemv_kernel<PRO, EPI, 2>), grid, 256, 0, st, a);
+  else hipLaunchKernelGGL((gemv_kernel<PRO, EPI, 4>), grid, 256, 0, st, a);
   return launch_status(what);
 }
 
@@ -238,7 +279,7 @@ int gemv_out(int pro, const uint16_t* x, const uint16_t* gamma, float eps,
   if (x == nullptr || !al16(x) || !gemv_k_ok(K) || N <= 0 ||
       (pro == kProNorm && (gamma == nullptr || !al16(gamma) || !std::isfinite(eps))) ||
       static_cast<long long>(N) * K >= (1LL << 40)) {
-    std::fprintf(stderr, "granite4: %s: invalid arguments (K %% 16 == 0, K <= %d)\n", what, kMaxK);
+    std::fprintf(stderr, "granite4: %s: invalid arguments (K %% 64 == 0, K <= %d)\n", what, kMaxK);
     return -1;
   }
   GemvArgs a{};
@@ -258,7 +299,7 @@ int gemv_out(int pro, const uint16_t* x, const uint16_t* gamma, float eps,
   a.seg2 = n[0] + n[1];
   a.N = N;
   a.K = K;
-  const unsigned grid = static_cast<unsigned>((N + kRowsPerBlock - 1) / kRowsPerBlock);
+  const unsigned grid = static_cast<unsigned>((N + kRows - 1) / kRows);
   return pro == kProNorm ? launch_gemv<kProNorm, kEpiOut>(a, grid, what)
                          : launch_gemv<kProNone, kEpiOut>(a, grid, what);
 }
@@ -270,7 +311,7 @@ int gemv_swiglu(int pro, const uint16_t* x, const uint16_t* gamma, float eps, co
       !al16(wu) || !gemv_k_ok(K) || N <= 0 || !std::isfinite(sg) || !std::isfinite(su) ||
       (pro == kProNorm && (gamma == nullptr || !al16(gamma) || !std::isfinite(eps))) ||
       static_cast<long long>(N) * K >= (1LL << 40)) {
-    std::fprintf(stderr, "granite4: %s: invalid arguments (K %% 16 == 0, K <= %d)\n", what, kMaxK);
+    std::fprintf(stderr, "granite4: %s: invalid arguments (K %% 64 == 0, K <= %d)\n", what, kMaxK);
     return -1;
   }
   GemvArgs a{};
@@ -285,7 +326,7 @@ int gemv_swiglu(int pro, const uint16_t* x, const uint16_t* gamma, float eps, co
   a.I = N;
   a.N = N;
   a.K = K;
-  const unsigned grid = static_cast<unsigned>((N + 7) / 8);
+  const unsigned grid = static_cast<unsigned>((N + kRows / 2 - 1) / (kRows / 2));
   return pro == kProNorm ? launch_gemv<kProNorm, kEpiSwiglu>(a, grid, what)
                          : launch_gemv<kProNone, kEpiSwiglu>(a, grid, what);
 }
@@ -325,7 +366,7 @@ int granite4_gemv_fp8w_resid(const uint16_t* d_a, const uint8_t* d_w, float scal
   a.seg1 = a.seg2 = a.N = N;
   a.K = K;
   return launch_gemv<kProNone, kEpiResid>(
-      a, static_cast<unsigned>((N + kRowsPerBlock - 1) / kRowsPerBlock), "granite4_gemv_fp8w_resid");
+      a, static_cast<unsigned>((N + kRows - 1) / kRows), "granite4_gemv_fp8w_resid");
 }
 
 int granite4_gemv_qkv(const uint16_t* d_a, const uint8_t* d_wq, const uint8_t* d_wk,

@@ -452,7 +452,7 @@ int granite4_gemm_fp8_residual_rmsnorm_fp8(const uint8_t* A, int lda, const floa
  * Batch-1 decode GEMVs (bf16 activation x fp8 e4m3 weight rows [N][K]) with
  * the decode step's non-GEMM ops fused in. y[n] = scale * sum_k fp8(W[n][k])
  * * a[k] in f32, as the reference's gemv_row_dequant (forward_gpu.cu:
- * 934-994). K % 16 == 0, K <= 16384, 16-byte aligned a and W.
+ * 934-994). K % 64 == 0, K <= 16384, 16-byte aligned a and W.
  * ------------------------------------------------------------------------- */
 
 /* Replaces: row_gemm_dequant_kernel launches (forward_gpu.cu:997-1002):

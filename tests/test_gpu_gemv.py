@@ -67,7 +67,7 @@ def check_bf16(got, y, bnd):
     assert not bad.any(), np.argwhere(bad)[:5]
 
 
-@pytest.mark.parametrize("N,K", [(100, 4096), (4096, 4096), (4096, 12800), (16, 16)])
+@pytest.mark.parametrize("N,K", [(100, 4096), (4096, 4096), (4096, 12800), (16, 64), (40, 2112)])
 def test_gemv_plain(N, K):
     print(f"gemv N={N} K={K}", flush=True)
     a = ol.normal_bf16(0xA1 + K, 0.0, 1.0, K)
@@ -149,4 +149,4 @@ def test_gemv_invalid_arguments():
     a = torch.zeros(100, dtype=torch.int16, device="cuda")
     W = torch.zeros((4, 100), dtype=torch.uint8, device="cuda")
     with pytest.raises(L.Granite4Error):
-        L.call("granite4_gemv_fp8w", a, W, 1.0, 4, 100, empty16(4))  # K % 16 != 0
+        L.call("granite4_gemv_fp8w", a, W, 1.0, 4, 100, empty16(4))  # K % 64 != 0
