@@ -15,8 +15,9 @@
 // (kernels_phase2.cu:51-132): every workgroup normalises the whole row for
 // itself (8 KB from L2), which costs less than a separate launch.
 //
-// Layout: 256-thread workgroups of 16 weight rows (swiglu: 8 gate + the 8
-// matching up rows). The workgroup walks its rows in order with G4_GEMV_DEPTH
+// Layout: 256-thread workgroups of 16 weight rows (8 when 16 would leave
+// fewer than two workgroups per CU; swiglu: half gate rows, half the matching
+// up rows). The workgroup walks its rows in order with G4_GEMV_DEPTH
 // rows of loads in flight, its 4 waves reading each row together (wave w the
 // quarter [w K/4, (w+1) K/4), 16 bytes per lane per 1024-byte chunk,
 // non-temporal), so each workgroup's accesses stay inside a few contiguous
@@ -31,6 +32,7 @@
 #include "g4_math.h"
 #include "g4_wave.h"
 #include "granite4_layerops.h"
+#include "rope_unit.h"
 
 #include <cmath>
 #include <cstdio>
@@ -44,7 +46,6 @@ enum : int { kEpiOut = 0, kEpiResid = 1, kEpiSwiglu = 2 };
 #ifndef G4_GEMV_DEPTH
 #define G4_GEMV_DEPTH 4
 #endif
-constexpr int kRows = 16;                 // weight rows per workgroup
 constexpr int kDepth = G4_GEMV_DEPTH;     // rows of loads in flight
 constexpr int kMaxChunks = 4;             // 1024-byte chunks per wave per row: K <= 16384
 constexpr int kMaxK = 4 * kMaxChunks * 1024;
@@ -87,9 +88,10 @@ __device__ __forceinline__ void fp8x16_to_f32(const uint4& q, float (&f)[16]) {
   }
 }
 
-// Weight row r (0..15) of the workgroup, or nullptr past the end (n: its
-// output index). swiglu: rows 0..7 gate, 8..15 up, of the same 8 act columns.
-template <int EPI>
+// Weight row r (0 .. kRows - 1) of the workgroup, or nullptr past the end (n:
+// its output index). swiglu: the first half gate rows, the second half the up
+// rows of the same act columns.
+template <int EPI, int kRows>
 __device__ __forceinline__ const uint8_t* row_ptr(const GemvArgs& a, int r, int& n) {
   if (EPI == kEpiSwiglu) {
     const int c = blockIdx.x * (kRows / 2) + (r % (kRows / 2));
@@ -113,7 +115,7 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <int PRO, int EPI, int kChunks>
+template <int PRO, int EPI, int kChunks, int kRows>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   __shared__ double s_ss[4];
   __shared__ float s_part[4][kRows];
@@ -135,7 +137,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   bool live[kRows];
 #pragma unroll
   for (int r = 0; r < kRows; ++r) {
-    rows[r] = row_ptr<EPI>(a, r, ns[r]);
+    rows[r] = row_ptr<EPI, kRows>(a, r, ns[r]);
     live[r] = rows[r] != nullptr;
     if (!live[r]) rows[r] = a.w[0];
   }
@@ -154,11 +156,15 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 
   // Prologue: the lane's 16 activations per chunk, in registers (f32).
   float av[kChunks][16];
-  uint4 xr[kChunks][2];
+  uint4 xr[kChunks][2], gr[kChunks][2];
 #pragma unroll
   for (int c = 0; c < kChunks; ++c) {
     xr[c][0] = *reinterpret_cast<const uint4*>(a.x + koff[c]);
     xr[c][1] = *reinterpret_cast<const uint4*>(a.x + koff[c] + 8);
+    if (PRO == kProNorm) {  // issued with x: one memory round trip, not two
+      gr[c][0] = *reinterpret_cast<const uint4*>(a.gamma + koff[c]);
+      gr[c][1] = *reinterpret_cast<const uint4*>(a.gamma + koff[c] + 8);
+    }
   }
   if (PRO == kProNorm) {
     double ss = 0.0;
@@ -181,8 +187,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     const float rr = 1.0f / sqrtf(static_cast<float>(ss / K) + a.eps);
 #pragma unroll
     for (int c = 0; c < kChunks; ++c) {
-      const uint4 g0 = *reinterpret_cast<const uint4*>(a.gamma + koff[c]);
-      const uint4 g1 = *reinterpret_cast<const uint4*>(a.gamma + koff[c] + 8);
+      const uint4 g0 = gr[c][0], g1 = gr[c][1];
       const uint32_t xv[8] = {xr[c][0].x, xr[c][0].y, xr[c][0].z, xr[c][0].w,
                               xr[c][1].x, xr[c][1].y, xr[c][1].z, xr[c][1].w};
       const uint32_t gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
@@ -258,17 +263,138 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Decode q|k|v GEMV with the RMSNorm prologue and RoPE + the quantised KV
+// write as its epilogue: one 1024-thread workgroup per head (128 weight rows:
+// Hq query heads, then Hk key heads, then Hk value heads), each wave reading
+// whole rows (chunk c of a row = lane bytes [16 l + 1024 c, +16)). The head's
+// 128 outputs gather in LDS as bf16 and one 16-lane row applies rope_unit to
+// them, exactly as the append kernel does to a stored q|k|v row.
+//
+// Sums in the order of gemv_kernel (one partial per 1024-byte chunk, reduced
+// across lanes, then (c0 + c1) + (c2 + c3)), and the norm's sum of squares in
+// the same order, so the outputs are bit-identical to
+// granite4_gemv_rmsnorm_qkv followed by granite4_rope_append_at_pos.
+// ---------------------------------------------------------------------------
+constexpr int kHeadWaves = 16;
+constexpr int kHeadRowsPerWave = 128 / kHeadWaves;
+
+template <int BITS, int GROUP>
+__global__ __launch_bounds__(1024) void gemv_qkv_rope_kernel(GemvArgs g, RopeArgs ra) {
+  __shared__ uint16_t s_head[128];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int u = blockIdx.x;  // head unit
+  const int Hq = ra.Hq, Hk = ra.Hk;
+  const int seg = u < Hq ? 0 : (u < Hq + Hk ? 1 : 2);
+  const int h = seg == 0 ? u : (seg == 1 ? u - Hq : u - Hq - Hk);
+  const uint8_t* wbase = g.w[seg] + static_cast<size_t>(h) * 128 * 4096;
+  const float scale = g.s[seg];
+
+  // Weights: rows 8 wave .. 8 wave + 7 of the head, 2 rows in flight.
+  uint4 buf[2][4];
+  const auto load_row = [&](int j, uint4 (&dst)[4]) {
+    const uint8_t* row = wbase + static_cast<size_t>(kHeadRowsPerWave * wave + j) * 4096;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) dst[c] = ld_u4_nt(row + 1024 * c + 16 * lane);
+  };
+  load_row(0, buf[0]);
+  load_row(1, buf[1]);
+
+  // Norm prologue over the whole row (K = 4096): chunk c = bytes 1024 c + 16 l
+  // of the bf16 row, as wave c of gemv_kernel holds them.
+  uint32_t av[4][8];  // the lane's normalised activations, bf16 pairs
+  {
+    uint4 xr[4][2], gr[4][2];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int k = 1024 * c + 16 * lane;
+      xr[c][0] = *reinterpret_cast<const uint4*>(g.x + k);
+      xr[c][1] = *reinterpret_cast<const uint4*>(g.x + k + 8);
+      gr[c][0] = *reinterpret_cast<const uint4*>(g.gamma + k);
+      gr[c][1] = *reinterpret_cast<const uint4*>(g.gamma + k + 8);
+    }
+    double ssc[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t w[8] = {xr[c][0].x, xr[c][0].y, xr[c][0].z, xr[c][0].w,
+                             xr[c][1].x, xr[c][1].y, xr[c][1].z, xr[c][1].w};
+      double ss = 0.0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float lo = lo_bf16(w[e]), hi = hi_bf16(w[e]);
+        ss += static_cast<double>(lo * lo);
+        ss += static_cast<double>(hi * hi);
+      }
+      ssc[c] = wave_sum(ss);
+    }
+    const double ss = ssc[0] + ssc[1] + ssc[2] + ssc[3];
+    const float rr = 1.0f / sqrtf(static_cast<float>(ss / 4096) + g.eps);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t xv[8] = {xr[c][0].x, xr[c][0].y, xr[c][0].z, xr[c][0].w,
+                              xr[c][1].x, xr[c][1].y, xr[c][1].z, xr[c][1].w};
+      const uint32_t gv[8] = {gr[c][0].x, gr[c][0].y, gr[c][0].z, gr[c][0].w,
+                              gr[c][1].x, gr[c][1].y, gr[c][1].z, gr[c][1].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        av[c][e] = pack_bf16_hw(lo_bf16(xv[e]) * rr * lo_bf16(gv[e]),
+                                hi_bf16(xv[e]) * rr * hi_bf16(gv[e]));
+      }
+    }
+  }
+
+#pragma unroll
+  for (int j = 0; j < kHeadRowsPerWave; ++j) {
+    float part[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float wf[16];
+      fp8x16_to_f32(buf[j & 1][c], wf);
+      float sum = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        sum = fmaf(wf[e], (e & 1) ? hi_bf16(av[c][e >> 1]) : lo_bf16(av[c][e >> 1]), sum);
+      part[c] = sum;
+    }
+    if (j + 2 < kHeadRowsPerWave) load_row(j + 2, buf[j & 1]);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) part[c] = wave_sum_f32(part[c]);
+    if (lane == 0)
+      s_head[kHeadRowsPerWave * wave + j] =
+          static_cast<uint16_t>(f32_to_bf16(scale * ((part[0] + part[1]) + (part[2] + part[3]))));
+  }
+  __syncthreads();
+  if (threadIdx.x >= 16) return;
+  const int lane16 = threadIdx.x;
+  rope_unit<BITS, GROUP>(ra, 0, u, lane16, [&](const uint16_t*) {
+    const uint4 v = *reinterpret_cast<const uint4*>(s_head + 8 * lane16);
+    return V8{{v.x, v.y, v.z, v.w}};
+  });
+}
+
 bool gemv_k_ok(int K) { return K >= 64 && K % 64 == 0 && K <= kMaxK; }
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Chunks per wave per row: K / 4 bytes in 1024-byte chunks.
+// Chunks per wave per row: K / 4 bytes in 1024-byte chunks. Rows per
+// workgroup: 16, or 8 when 16 would leave fewer than two workgroups per CU.
 template <int PRO, int EPI>
-int launch_gemv(const GemvArgs& a, unsigned grid, const char* what) {
+int launch_gemv(const GemvArgs& a, const char* what) {
   const int ch = (a.K / 4 + 1023) / 1024;
+  const long long outputs = EPI == kEpiSwiglu ? 2LL * a.I : a.N;
+  const int rows = outputs >= 16LL * 2 * kCUs ? 16 : 8;
+  const unsigned grid = static_cast<unsigned>(EPI == kEpiSwiglu ? (a.I + rows / 2 - 1) / (rows / 2)
+                                                                 : (a.N + rows - 1) / rows);
   const hipStream_t st = stream();
-  if (ch <= 1) hipLaunchKernelGGL((gemv_kernel<PRO, EPI, 1>), grid, 256, 0, st, a);
-  else if (ch == 2) hipLaunchKernelGGL((gemv_kernel<PRO, EPI, 2>), grid, 256, 0, st, a);
-  else hipLaunchKernelGGL((gemv_kernel<PRO, EPI, 4>), grid, 256, 0, st, a);
+  const auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, 256, 0, st, a); };
+  if (rows == 16) {
+    if (ch <= 1) go(gemv_kernel<PRO, EPI, 1, 16>);
+    else if (ch == 2) go(gemv_kernel<PRO, EPI, 2, 16>);
+    else go(gemv_kernel<PRO, EPI, 4, 16>);
+  } else {
+    if (ch <= 1) go(gemv_kernel<PRO, EPI, 1, 8>);
+    else if (ch == 2) go(gemv_kernel<PRO, EPI, 2, 8>);
+    else go(gemv_kernel<PRO, EPI, 4, 8>);
+  }
   return launch_status(what);
 }
 
@@ -299,9 +425,8 @@ int gemv_out(int pro, const uint16_t* x, const uint16_t* gamma, float eps,
   a.seg2 = n[0] + n[1];
   a.N = N;
   a.K = K;
-  const unsigned grid = static_cast<unsigned>((N + kRows - 1) / kRows);
-  return pro == kProNorm ? launch_gemv<kProNorm, kEpiOut>(a, grid, what)
-                         : launch_gemv<kProNone, kEpiOut>(a, grid, what);
+  return pro == kProNorm ? launch_gemv<kProNorm, kEpiOut>(a, what)
+                         : launch_gemv<kProNone, kEpiOut>(a, what);
 }
 
 int gemv_swiglu(int pro, const uint16_t* x, const uint16_t* gamma, float eps, const uint8_t* wg,
@@ -326,9 +451,8 @@ int gemv_swiglu(int pro, const uint16_t* x, const uint16_t* gamma, float eps, co
   a.I = N;
   a.N = N;
   a.K = K;
-  const unsigned grid = static_cast<unsigned>((N + kRows / 2 - 1) / (kRows / 2));
-  return pro == kProNorm ? launch_gemv<kProNorm, kEpiSwiglu>(a, grid, what)
-                         : launch_gemv<kProNone, kEpiSwiglu>(a, grid, what);
+  return pro == kProNorm ? launch_gemv<kProNorm, kEpiSwiglu>(a, what)
+                         : launch_gemv<kProNone, kEpiSwiglu>(a, what);
 }
 
 }  // namespace
@@ -365,8 +489,7 @@ int granite4_gemv_fp8w_resid(const uint16_t* d_a, const uint8_t* d_w, float scal
   a.rs = resid_scale;
   a.seg1 = a.seg2 = a.N = N;
   a.K = K;
-  return launch_gemv<kProNone, kEpiResid>(
-      a, static_cast<unsigned>((N + kRows - 1) / kRows), "granite4_gemv_fp8w_resid");
+  return launch_gemv<kProNone, kEpiResid>(a, "granite4_gemv_fp8w_resid");
 }
 
 int granite4_gemv_qkv(const uint16_t* d_a, const uint8_t* d_wq, const uint8_t* d_wk,
@@ -401,6 +524,56 @@ int granite4_gemv_rmsnorm_silu_gate_up(const uint16_t* d_x, const uint16_t* d_ga
                                        float scale_u, int N, int K, uint16_t* d_out) {
   return gemv_swiglu(kProNorm, d_x, d_gamma, eps, d_wg, d_wu, scale_g, scale_u, N, K, d_out,
                      "granite4_gemv_rmsnorm_silu_gate_up");
+}
+
+int granite4_gemv_rmsnorm_qkv_rope_append(const uint16_t* d_x, const uint16_t* d_gamma,
+                                          float eps, const uint8_t* d_wq, const uint8_t* d_wk,
+                                          const uint8_t* d_wv, float sq, float sk, float sv,
+                                          const float* cos_tbl, const float* sin_tbl, int max_pos,
+                                          const int* d_pos, const int* d_pt, int Hq, int Hk,
+                                          int bits, int group, uint16_t* q_rot, void* cache_k,
+                                          void* cache_v, float* k_scale, float* v_scale,
+                                          int stride) {
+  RopeArgs ra;
+  // q / k / v point at the weights only to pass the builder's null checks:
+  // the head rows come from the GEMV, not from memory.
+  const uint16_t* dummy = d_x;
+  if (d_x == nullptr || d_gamma == nullptr || !al16(d_x) || !al16(d_gamma) || d_wq == nullptr ||
+      d_wk == nullptr || d_wv == nullptr || !al16(d_wq) || !al16(d_wk) || !al16(d_wv) ||
+      !std::isfinite(eps) || !std::isfinite(sq) || !std::isfinite(sk) || !std::isfinite(sv) ||
+      !rope_args_at_pos(ra, dummy, dummy, dummy, cos_tbl, sin_tbl, max_pos, d_pos, d_pt, Hq, Hk,
+                        128, bits, group, q_rot, cache_k, cache_v, k_scale, v_scale, stride)) {
+    std::fprintf(stderr, "granite4: granite4_gemv_rmsnorm_qkv_rope_append: invalid arguments\n");
+    return -1;
+  }
+  GemvArgs g{};
+  g.x = d_x;
+  g.gamma = d_gamma;
+  g.eps = eps;
+  g.w[0] = d_wq;
+  g.w[1] = d_wk;
+  g.w[2] = d_wv;
+  g.s[0] = sq;
+  g.s[1] = sk;
+  g.s[2] = sv;
+  g.K = 4096;
+  const unsigned grid = static_cast<unsigned>(Hq + 2 * Hk);
+  const hipStream_t st = stream();
+  const int grp = bits == 16 ? 128 : group;
+  const auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, 1024, 0, st, g, ra); };
+  switch (bits * 1000 + grp) {
+    case 16128: go(gemv_qkv_rope_kernel<16, 128>); break;
+    case 8128: go(gemv_qkv_rope_kernel<8, 128>); break;
+    case 8064: go(gemv_qkv_rope_kernel<8, 64>); break;
+    case 8032: go(gemv_qkv_rope_kernel<8, 32>); break;
+    case 4128: go(gemv_qkv_rope_kernel<4, 128>); break;
+    case 4064: go(gemv_qkv_rope_kernel<4, 64>); break;
+    case 4032: go(gemv_qkv_rope_kernel<4, 32>); break;
+    case 5128: go(gemv_qkv_rope_kernel<5, 128>); break;
+    case 5064: go(gemv_qkv_rope_kernel<5, 64>); break;
+    default: go(gemv_qkv_rope_kernel<5, 32>); break;
+  }
+  return launch_status("granite4_gemv_rmsnorm_qkv_rope_append");
 }
 
 }  // extern "C"

@@ -23,43 +23,13 @@
 #include "g4_math.h"
 #include "g4_wave.h"
 #include "granite4_layerops.h"
+#include "rope_unit.h"
 
 #include <map>
 #include <mutex>
 
 namespace g4 {
 
-struct RopeArgs {
-  const uint16_t* q;
-  long long q_stride;
-  const uint16_t* k;
-  long long k_stride;
-  const uint16_t* v;
-  long long v_stride;
-  const float* cos_t;
-  const float* sin_t;
-  int max_pos;
-  int rows, Hq, Hk, d;
-  int base_pos;
-  const int* pos_rows;    // per-row KV position
-  const int* pos_ptr;     // decode: *pos_ptr
-  const int* pt;          // position -> arena row
-  const int* arena_rows;  // per-row arena row
-  const GpuMultiRows* mr;
-  int rope_by_row;  // 1: RoPE table row r for row r (verify tables), KV at base_pos + r
-  uint16_t* q_rot;
-  long long q_rot_stride;
-  uint16_t* k_rot;  // optional bf16 rotated K [rows][Hk d]
-  void* cache_k;
-  void* cache_v;
-  float* k_scale;
-  float* v_scale;
-  int stride;
-  int rotate_k;
-  int k_round;
-  int units_per_row;  // Hq + (kv ? 2 Hk : Hk)
-  int has_kv;         // 0: rotate only (K heads go to k_rot)
-};
 
 // Table-size registry for tables this library allocated, so the reference's
 // entry points (which carry no table length) still get a position bound.
@@ -84,94 +54,6 @@ void table_forget(const float* t) {
 
 namespace {
 
-// RoPE table row of row r.
-__device__ __forceinline__ int rope_pos(const RopeArgs& a, int r) {
-  if (a.mr != nullptr) return a.mr->pos[r];
-  if (a.rope_by_row) return r;
-  return a.pos_rows != nullptr ? a.pos_rows[r] : (a.pos_ptr != nullptr ? *a.pos_ptr : a.base_pos + r);
-}
-
-// Arena row that row r's K / V go to (only K / V units ask, so query heads
-// never wait on the page-table load).
-__device__ __forceinline__ int arena_row(const RopeArgs& a, int r) {
-  if (a.mr != nullptr) {
-    const int pos = a.mr->pos[r];
-    const int slot = a.mr->tree ? a.mr->slot[r] : pos;
-    const int* pt = a.mr->pt[r];
-    return pt != nullptr ? pt[slot] : slot;
-  }
-  if (a.arena_rows != nullptr) return a.arena_rows[r];
-  const int pos =
-      a.pos_rows != nullptr ? a.pos_rows[r] : (a.pos_ptr != nullptr ? *a.pos_ptr : a.base_pos + r);
-  return a.pt != nullptr ? a.pt[pos] : pos;
-}
-
-// Rotates the lane's 8 dims; cs / sn are the lane's cos / sin (dims mod 64).
-__device__ __forceinline__ void rotate8(const V8& x, const float* cs, const float* sn,
-                                        bool first_half, float* out) {
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const uint32_t pw = dpp_u32<kDppRor8>(x.w[e]);
-    const float a0 = lo_bf16(x.w[e]), a1 = hi_bf16(x.w[e]);
-    float b0 = lo_bf16(pw), b1 = hi_bf16(pw);
-    if (first_half) {
-      b0 = -b0;
-      b1 = -b1;
-    }
-    out[2 * e] = a0 * cs[2 * e] + b0 * sn[2 * e];
-    out[2 * e + 1] = a1 * cs[2 * e + 1] + b1 * sn[2 * e + 1];
-  }
-}
-
-__device__ __forceinline__ V8 to_bf16x8(const float* f) {
-  V8 v;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) v.w[e] = pack_bf16_hw(f[2 * e], f[2 * e + 1]);
-  return v;
-}
-
-template <int BITS, int GROUP>
-__device__ __forceinline__ void store_quant(const RopeArgs& a, const float* val, bool is_k,
-                                            long long slot, int lane16) {
-  constexpr int GL = GROUP / 8;
-  float am = 0.0f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf(val[e]));
-  am = group_max<GL>(am);
-  const int qmax = BITS == 8 ? 127 : ((BITS == 5 && is_k) ? 15 : 7);
-  const float s = am / static_cast<float>(qmax);
-  float* scales = is_k ? a.k_scale : a.v_scale;
-  if (lane16 % GL == 0) scales[slot * (128 / GROUP) + lane16 / GL] = s;
-  const float inv = 1.0f / s;
-  int c[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) c[e] = kv_code_inv(val[e], s, inv, qmax);
-  uint8_t* cache = static_cast<uint8_t*>(is_k ? a.cache_k : a.cache_v);
-  if (BITS == 8) {
-    uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      w0 |= (static_cast<uint32_t>(c[e]) & 0xffu) << (8 * e);
-      w1 |= (static_cast<uint32_t>(c[e + 4]) & 0xffu) << (8 * e);
-    }
-    *reinterpret_cast<uint2*>(cache + slot * 128 + 8 * lane16) = make_uint2(w0, w1);
-    return;
-  }
-  uint32_t nib = 0, plane = 0;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const uint32_t code = static_cast<uint32_t>(c[e] + qmax + 1);
-    nib |= (code & 0xfu) << (4 * e);
-    plane |= ((code >> 4) & 1u) << e;
-  }
-  if (BITS == 5 && is_k) {
-    *reinterpret_cast<uint32_t*>(cache + slot * 80 + 4 * lane16) = nib;
-    cache[slot * 80 + 64 + lane16] = static_cast<uint8_t>(plane);
-  } else {
-    *reinterpret_cast<uint32_t*>(cache + slot * 64 + 4 * lane16) = nib;
-  }
-}
-
 template <int BITS, int GROUP>
 __global__ __launch_bounds__(kBlock) void rope_append_kernel(RopeArgs a) {
   const int lane16 = threadIdx.x & 15;
@@ -180,63 +62,7 @@ __global__ __launch_bounds__(kBlock) void rope_append_kernel(RopeArgs a) {
   if (unit >= static_cast<unsigned>(a.rows) * static_cast<unsigned>(a.units_per_row)) return;  // whole DPP rows
   const int r = static_cast<int>(unit / static_cast<unsigned>(a.units_per_row));
   const int u = static_cast<int>(unit - static_cast<unsigned>(r) * static_cast<unsigned>(a.units_per_row));
-  const bool first_half = lane16 < 8;
-
-  if (u < a.Hq + a.Hk && (u < a.Hq || a.rotate_k)) {
-    // Rotated unit: a query head, or a key head that needs RoPE.
-    const int rp = rope_pos(a, r);
-    if (rp < 0 || rp >= a.max_pos) return;
-    const bool is_q = u < a.Hq;
-    const int h = is_q ? u : u - a.Hq;
-    const uint16_t* src = is_q ? a.q + r * a.q_stride + h * 128LL
-                               : a.k + r * a.k_stride + h * 128LL;
-    const V8 x = ld8_nt(src + 8 * lane16);
-    const float* cp = a.cos_t + static_cast<long long>(rp) * 64 + 8 * (lane16 & 7);
-    const float* sp = a.sin_t + static_cast<long long>(rp) * 64 + 8 * (lane16 & 7);
-    float cs[8], sn[8];
-    *reinterpret_cast<float4*>(cs) = *reinterpret_cast<const float4*>(cp);
-    *reinterpret_cast<float4*>(cs + 4) = *reinterpret_cast<const float4*>(cp + 4);
-    *reinterpret_cast<float4*>(sn) = *reinterpret_cast<const float4*>(sp);
-    *reinterpret_cast<float4*>(sn + 4) = *reinterpret_cast<const float4*>(sp + 4);
-    float rot[8];
-    rotate8(x, cs, sn, first_half, rot);
-    const V8 rb = to_bf16x8(rot);
-    if (is_q) {
-      st8_nt(a.q_rot + r * a.q_rot_stride + h * 128LL + 8 * lane16, rb);
-      return;
-    }
-    if (a.k_rot != nullptr) st8(a.k_rot + (static_cast<long long>(r) * a.Hk + h) * 128 + 8 * lane16, rb);
-    if (!a.has_kv) return;
-    const int row = arena_row(a, r);
-    if (row < 0 || row >= a.stride) return;
-    const long long slot = static_cast<long long>(h) * a.stride + row;
-    if (BITS == 16) {
-      st8(static_cast<uint16_t*>(a.cache_k) + slot * 128 + 8 * lane16, rb);
-      return;
-    }
-    float val[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) val[e] = a.k_round ? v8_get(rb, e) : rot[e];
-    store_quant<BITS, GROUP>(a, val, true, slot, lane16);
-    return;
-  }
-  // Unrotated K (already rotated by the caller) or V.
-  if (!a.has_kv) return;
-  const int row = arena_row(a, r);
-  if (row < 0 || row >= a.stride) return;
-  const bool is_k = u < a.Hq + a.Hk;
-  const int h = is_k ? u - a.Hq : u - a.Hq - a.Hk;
-  const uint16_t* src = is_k ? a.k + r * a.k_stride + h * 128LL : a.v + r * a.v_stride + h * 128LL;
-  const V8 x = ld8_nt(src + 8 * lane16);
-  const long long slot = static_cast<long long>(h) * a.stride + row;
-  if (BITS == 16) {
-    st8(static_cast<uint16_t*>(is_k ? a.cache_k : a.cache_v) + slot * 128 + 8 * lane16, x);
-    return;
-  }
-  float val[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) val[e] = v8_get(x, e);
-  store_quant<BITS, GROUP>(a, val, is_k, slot, lane16);
+  rope_unit<BITS, GROUP>(a, r, u, lane16, [&](const uint16_t* head) { return ld8_nt(head + 8 * lane16); });
 }
 
 // Any head dim (even, <= 1024; quantised forms one scale per row): one
@@ -413,6 +239,47 @@ int launch_embed(const int32_t* tokens, int start, const int* d_pos, int rows,
 }
 
 }  // namespace
+bool rope_args_at_pos(RopeArgs& a, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                      const float* cos_tbl, const float* sin_tbl, int max_pos, const int* d_pos,
+                      const int* d_pt, int Hq, int Hk, int d, int bits, int group, uint16_t* q_rot,
+                      void* cache_k, void* cache_v, float* k_scale, float* v_scale, int stride) {
+  if (d_pos == nullptr || q == nullptr || Hq <= 0 || d != 128 || k == nullptr || v == nullptr ||
+      cos_tbl == nullptr || sin_tbl == nullptr || max_pos <= 0 || q_rot == nullptr ||
+      cache_k == nullptr || cache_v == nullptr || Hk <= 0 || stride <= 0 ||
+      (bits != 16 && bits != 8 && bits != 4 && bits != 5) ||
+      (bits != 16 && (group != 32 && group != 64 && group != 128)) ||
+      (bits != 16 && (k_scale == nullptr || v_scale == nullptr)))
+    return false;
+  a = rope_args_zero();
+  a.q = q;
+  a.q_stride = static_cast<long long>(Hq) * d;
+  a.k = k;
+  a.k_stride = static_cast<long long>(Hk) * d;
+  a.v = v;
+  a.v_stride = a.k_stride;
+  a.cos_t = cos_tbl;
+  a.sin_t = sin_tbl;
+  a.max_pos = max_pos;
+  a.rows = 1;
+  a.Hq = Hq;
+  a.Hk = Hk;
+  a.d = d;
+  a.pos_ptr = d_pos;
+  a.pt = d_pt;
+  a.q_rot = q_rot;
+  a.q_rot_stride = a.q_stride;
+  a.cache_k = cache_k;
+  a.cache_v = cache_v;
+  a.k_scale = k_scale;
+  a.v_scale = v_scale;
+  a.stride = stride;
+  a.rotate_k = 1;
+  a.k_round = 1;
+  a.has_kv = 1;
+  a.units_per_row = Hq + 2 * Hk;
+  return true;
+}
+
 }  // namespace g4
 
 using namespace g4;
@@ -843,41 +710,12 @@ int granite4_rope_append_at_pos(const uint16_t* q, const uint16_t* k, const uint
                                 const int* d_pos, const int* d_pt, int Hq, int Hk, int d,
                                 int bits, int group, uint16_t* q_rot, void* cache_k,
                                 void* cache_v, float* k_scale, float* v_scale, int stride) {
-  if (d_pos == nullptr || q == nullptr || Hq <= 0 || d != 128 || k == nullptr || v == nullptr ||
-      cos_tbl == nullptr || sin_tbl == nullptr || max_pos <= 0 || q_rot == nullptr ||
-      cache_k == nullptr || cache_v == nullptr || Hk <= 0 || stride <= 0 ||
-      (bits != 16 && bits != 8 && bits != 4 && bits != 5) ||
-      (bits != 16 && (group != 32 && group != 64 && group != 128)) ||
-      (bits != 16 && (k_scale == nullptr || v_scale == nullptr))) {
+  RopeArgs a;
+  if (!rope_args_at_pos(a, q, k, v, cos_tbl, sin_tbl, max_pos, d_pos, d_pt, Hq, Hk, d, bits, group,
+                        q_rot, cache_k, cache_v, k_scale, v_scale, stride)) {
     std::fprintf(stderr, "granite4: granite4_rope_append_at_pos: invalid arguments\n");
     return -1;
   }
-  RopeArgs a = rope_args_zero();
-  a.q = q;
-  a.q_stride = static_cast<long long>(Hq) * d;
-  a.k = k;
-  a.k_stride = static_cast<long long>(Hk) * d;
-  a.v = v;
-  a.v_stride = a.k_stride;
-  a.cos_t = cos_tbl;
-  a.sin_t = sin_tbl;
-  a.max_pos = max_pos;
-  a.rows = 1;
-  a.Hq = Hq;
-  a.Hk = Hk;
-  a.d = d;
-  a.pos_ptr = d_pos;
-  a.pt = d_pt;
-  a.q_rot = q_rot;
-  a.q_rot_stride = a.q_stride;
-  a.cache_k = cache_k;
-  a.cache_v = cache_v;
-  a.k_scale = k_scale;
-  a.v_scale = v_scale;
-  a.stride = stride;
-  a.rotate_k = 1;
-  a.k_round = 1;
-  a.has_kv = 1;
   return launch_rope_append(a, bits, bits == 16 ? 128 : group, "granite4_rope_append_at_pos");
 }
 

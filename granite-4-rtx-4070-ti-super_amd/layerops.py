@@ -140,6 +140,8 @@ _SIG = {
     "granite4_gemv_rmsnorm_qkv": [P, P, F, P, P, P, F, F, F, I, I, I, I, P, P, P],
     "granite4_kernel_silu_gate_up": [P, P, P, F, F, I, I, P],
     "granite4_gemv_rmsnorm_silu_gate_up": [P, P, F, P, P, F, F, I, I, P],
+    "granite4_gemv_rmsnorm_qkv_rope_append": [P, P, F, P, P, P, F, F, F, P, P, I, P, P, I, I, I, I,
+                                              P, P, P, P, P, I],
     "granite4_host_fp8_encode": [P, _c.c_size_t, F, P],
     "granite4_host_kv_codes": [P, _c.c_size_t, F, I, P],
     "granite4_selftest_bf16": [P],

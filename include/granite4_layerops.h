@@ -495,6 +495,23 @@ int granite4_gemv_rmsnorm_silu_gate_up(const uint16_t* d_x, const uint16_t* d_ga
                                        const uint8_t* d_wg, const uint8_t* d_wu, float scale_g,
                                        float scale_u, int N, int K, uint16_t* d_out);
 
+/* Replaces: granite4_kernel_rmsnorm + the q / k / v GEMV + the RoPE and KV
+ * append of the decode step (forward_gpu.cu:2115-2157), in one launch: the
+ * residual row d_x (K = 4096) is normalised in every workgroup, the q|k|v
+ * projections (Hq / Hk / Hk heads of 128 rows) are computed one head per
+ * workgroup, and each head is rotated at *d_pos and written exactly as
+ * granite4_rope_append_at_pos writes it (q_rot; K / V into the pool row
+ * d_pt[*d_pos], quantised per bits / group). Outputs are bit-identical to
+ * granite4_gemv_rmsnorm_qkv followed by granite4_rope_append_at_pos. */
+int granite4_gemv_rmsnorm_qkv_rope_append(const uint16_t* d_x, const uint16_t* d_gamma,
+                                          float eps, const uint8_t* d_wq, const uint8_t* d_wk,
+                                          const uint8_t* d_wv, float sq, float sk, float sv,
+                                          const float* cos_tbl, const float* sin_tbl, int max_pos,
+                                          const int* d_pos, const int* d_pt, int Hq, int Hk,
+                                          int bits, int group, uint16_t* q_rot, void* cache_k,
+                                          void* cache_v, float* k_scale, float* v_scale,
+                                          int stride);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 

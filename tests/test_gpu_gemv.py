@@ -150,3 +150,42 @@ def test_gemv_invalid_arguments():
     W = torch.zeros((4, 100), dtype=torch.uint8, device="cuda")
     with pytest.raises(L.Granite4Error):
         L.call("granite4_gemv_fp8w", a, W, 1.0, 4, 100, empty16(4))  # K % 64 != 0
+
+
+@pytest.mark.parametrize("bits,group", [(16, 128), (8, 128), (5, 32)])
+def test_rmsnorm_qkv_rope_append_fused(bits, group):
+    """RMSNorm + q|k|v GEMV + RoPE + KV append in one launch: q_rot, the pool
+    row and its scales bit-identical to granite4_gemv_rmsnorm_qkv followed by
+    granite4_rope_append_at_pos (same position, same page table)."""
+    print(f"qkv rope append fused bits={bits} group={group}", flush=True)
+    K, Hq, Hk, D = 4096, 32, 8, 128
+    x = dev(ol.normal_bf16(0xC1, 0.0, 1.0, K))
+    gamma = dev(ol.normal_bf16(0xC2, 1.0, 0.1, K))
+    Wq, Wk, Wv = (dev(ol.fp8_codes(0xC3 + i, (n, K), std=0.5)) for i, n in
+                  enumerate((Hq * D, Hk * D, Hk * D)))
+    sc = (0.004, 0.005, 0.006)
+    cos_t, sin_t = ol.rope_tables(1e7, D, 8192)
+    dcos, dsin = dev(cos_t), dev(sin_t)
+    stride = 256
+    pos = dev(np.array([5000], np.int32))
+    pt = dev(np.random.default_rng(3).permutation(8192).astype(np.int32) % stride)
+    outs = []
+    for fused in (False, True):
+        arena = L.KvArena(bits, Hk, stride, group=group)
+        q_rot = empty16(Hq * D)
+        if fused:
+            L.call("granite4_gemv_rmsnorm_qkv_rope_append", x, gamma, 1e-5, Wq, Wk, Wv, *sc, dcos,
+                   dsin, 8192, pos, pt, Hq, Hk, bits, group, q_rot, arena.k, arena.v,
+                   arena.k_scale, arena.v_scale, stride)
+        else:
+            q, k, v = empty16(Hq * D), empty16(Hk * D), empty16(Hk * D)
+            L.call("granite4_gemv_rmsnorm_qkv", x, gamma, 1e-5, Wq, Wk, Wv, *sc, Hq * D, Hk * D,
+                   Hk * D, K, q, k, v)
+            L.call("granite4_rope_append_at_pos", q, k, v, dcos, dsin, 8192, pos, pt, Hq, Hk, D,
+                   bits, group, q_rot, arena.k, arena.v, arena.k_scale, arena.v_scale, stride)
+        outs.append([host(q_rot), host(arena.k), host(arena.v), host(arena.k_scale),
+                     host(arena.v_scale)])
+    for a, b in zip(*outs):
+        np.testing.assert_array_equal(a, b)
+    row = int(host(pt)[5000])
+    assert np.any(outs[1][1].reshape(Hk, stride, -1)[:, row] != 0)  # the row was written
