@@ -431,7 +431,10 @@ def bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream, layers=40
                KV append, O GEMV + residual, RMSNorm, gate/up GEMV + SwiGLU,
                down GEMV + residual (7 launches per layer);
       fused    RMSNorm as the GEMV prologue, SwiGLU and residual as epilogues,
-               RoPE + append still a launch of its own (5 per layer).
+               RoPE + KV append a launch of its own (5 per layer). Also timed:
+               the same without the RoPE launches, and with RoPE + append in
+               the q|k|v GEMV's epilogue (one workgroup per head: 48 of them,
+               slower than the separate launch).
     The non-GEMM overhead of a step is its time minus the plain step's."""
     dev = "cuda"
     stride = 8192
@@ -491,18 +494,36 @@ def bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream, layers=40
     def fused():
         L.call("granite4_embed_at_pos", toks, pos, emb, VOCAB, H, 1.0, hidden)
         for p in per:
-            L.call("granite4_gemv_rmsnorm_qkv", hidden, gamma, 1e-5, p["wq"], p["wk"], p["wv"],
-                   sc, sc, sc, HQ * D, HK * D, HK * D, H, q, k, v)
-            rope(p)
+            a = p["arena"]
+            L.call("granite4_gemv_rmsnorm_qkv_rope_append", hidden, gamma, 1e-5, p["wq"], p["wk"],
+                   p["wv"], sc, sc, sc, cos_t, sin_t, 65536, pos, pt, HQ, HK, 16, 128, q_rot,
+                   a.k, a.v, a.k_scale, a.v_scale, stride)
             L.call("granite4_gemv_fp8w_resid", attn_out, p["wo"], sc, hidden, 1.0, H, HQ * D,
                    hidden)
             L.call("granite4_gemv_rmsnorm_silu_gate_up", hidden, gamma, 1e-5, p["wg"], p["wu"],
                    sc, sc, I, H, act)
             L.call("granite4_gemv_fp8w_resid", act, p["wd"], sc, hidden, 1.0, H, I, hidden)
 
+    def fused_split(with_rope):
+        def step():
+            L.call("granite4_embed_at_pos", toks, pos, emb, VOCAB, H, 1.0, hidden)
+            for p in per:
+                L.call("granite4_gemv_rmsnorm_qkv", hidden, gamma, 1e-5, p["wq"], p["wk"], p["wv"],
+                       sc, sc, sc, HQ * D, HK * D, HK * D, H, q, k, v)
+                if with_rope:
+                    rope(p)
+                L.call("granite4_gemv_fp8w_resid", attn_out, p["wo"], sc, hidden, 1.0, H, HQ * D,
+                       hidden)
+                L.call("granite4_gemv_rmsnorm_silu_gate_up", hidden, gamma, 1e-5, p["wg"],
+                       p["wu"], sc, sc, I, H, act)
+                L.call("granite4_gemv_fp8w_resid", act, p["wd"], sc, hidden, 1.0, H, I, hidden)
+        return step
+
     t_plain = graph_us(torch, L, stream, plain)
     t_unfused = graph_us(torch, L, stream, unfused)
-    t_fused = graph_us(torch, L, stream, fused)
+    t_qkv_rope_kernel = graph_us(torch, L, stream, fused)
+    t_fused_norope = graph_us(torch, L, stream, fused_split(False))
+    t_fused = graph_us(torch, L, stream, fused_split(True))
     wbytes = layers * (HQ * D + 2 * HK * D + 2 * I) * H + layers * H * (HQ * D + I)
     del per
     torch.cuda.empty_cache()
@@ -512,6 +533,9 @@ def bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream, layers=40
             "unfused_us": round(t_unfused, 1), "fused_us": round(t_fused, 1),
             "non_gemm_overhead_unfused_us": round(t_unfused - t_plain, 1),
             "non_gemm_overhead_fused_us": round(t_fused - t_plain, 1),
+            "fused_gemvs_without_rope_us": round(t_fused_norope, 1),
+            "rope_append_launches_us": round(t_fused - t_fused_norope, 1),
+            "fused_qkv_rope_one_launch_us": round(t_qkv_rope_kernel, 1),
             "launches_per_step": {"plain": 4 * layers, "unfused": 1 + 7 * layers,
                                   "fused": 1 + 5 * layers}}
 
