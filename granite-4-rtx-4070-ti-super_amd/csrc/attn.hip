@@ -37,6 +37,7 @@
 #include "g4_hw.h"
 #include "g4_math.h"
 #include "granite4_layerops.h"
+#include "rope_unit.h"
 
 #include <climits>
 #include <cmath>
@@ -74,6 +75,12 @@ struct AttnArgs {
   float2* part_ml;  // [rows][Hq][nblk]
   float* part_o;    // [rows][Hq][nblk][128]
   uint16_t* out;    // [rows][Hq][128]
+  // Decode append (one row at *d_pos): q, k, v are the raw bf16 projections
+  // (ra.q / ra.k / ra.v); q is rotated in registers, and the wave whose split
+  // holds the position rotates, quantises and writes that position's K / V
+  // row (rope_unit, as the append kernels) before reading its tiles.
+  int fuse_append;
+  RopeArgs ra;
 };
 
 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
@@ -263,13 +270,61 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
   const int t_first = max(t_begin, (lo_min / kTile) * kTile);
   const int* pt = a.row_pt != nullptr ? a.row_pt[r0] : a.d_pt;
 
+  if (a.fuse_append) {
+    // The new position's K / V row, written by the one wave that reads it.
+    if (active && base >= t_begin && base < t_end_max && lane < 32) {
+      const int l16 = lane & 15;
+      rope_unit<BITS, GROUP>(a.ra, 0, (lane < 16 ? a.ra.Hq : a.ra.Hq + a.ra.Hk) + hkv, l16,
+                             [&](const uint16_t* head) { return ld8(head + 8 * l16); });
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the row is written before any tile load
+  }
+
   // This lane's query column.
   const int rr = n >> 2, hq = hkv * kGq + (n & 3);
   const bool live = rr < nr;
   const int my_len = live ? row_len(rr) : 0;
   const int my_lo = live ? row_lo(rr) : 0;
   bf16x8_t qb[4];
-  {
+  if (a.fuse_append) {
+    // Raw q rotated at the position: the lane's dims 32 s + 8 g + j pair with
+    // 32 (s + 2) + 8 g + j, so the rotation is lane-local; the same products
+    // and roundings as the append kernels' rotate8 (out = a c + b' s with b'
+    // the negated or plain partner), then bf16 RNE.
+    const uint16_t* qp = a.ra.q + static_cast<size_t>(hq) * kHd;
+    const int rp = base;
+    const bool ok = live && active && rp >= 0 && rp < a.ra.max_pos;
+    u32x4_t raw[4];
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+      raw[s4] = u32x4_t{0u, 0u, 0u, 0u};
+      if (ok) raw[s4] = *reinterpret_cast<const u32x4_t*>(qp + 32 * s4 + 8 * g);
+    }
+    uint32_t rot[4][4];
+#pragma unroll
+    for (int s4 = 0; s4 < 2; ++s4) {
+      const float* cp = a.ra.cos_t + static_cast<long long>(ok ? rp : 0) * 64 + 32 * s4 + 8 * g;
+      const float* sp = a.ra.sin_t + static_cast<long long>(ok ? rp : 0) * 64 + 32 * s4 + 8 * g;
+      float cs[8], sn[8];
+      *reinterpret_cast<float4*>(cs) = *reinterpret_cast<const float4*>(cp);
+      *reinterpret_cast<float4*>(cs + 4) = *reinterpret_cast<const float4*>(cp + 4);
+      *reinterpret_cast<float4*>(sn) = *reinterpret_cast<const float4*>(sp);
+      *reinterpret_cast<float4*>(sn + 4) = *reinterpret_cast<const float4*>(sp + 4);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t xa = raw[s4][w], xb = raw[s4 + 2][w];
+        const float a0 = lo_bf16(xa), a1 = hi_bf16(xa), b0 = lo_bf16(xb), b1 = hi_bf16(xb);
+        rot[s4][w] = pack_bf16_hw(a0 * cs[2 * w] + (-b0) * sn[2 * w],
+                                  a1 * cs[2 * w + 1] + (-b1) * sn[2 * w + 1]);
+        rot[s4 + 2][w] = pack_bf16_hw(b0 * cs[2 * w] + a0 * sn[2 * w],
+                                      b1 * cs[2 * w + 1] + a1 * sn[2 * w + 1]);
+      }
+    }
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4)
+      qb[s4] = ok ? as_bf16x8(rot[s4][0], rot[s4][1], rot[s4][2], rot[s4][3])
+                  : as_bf16x8(0u, 0u, 0u, 0u);
+  } else {
     const uint16_t* qp = a.q + (static_cast<size_t>(r0 + (live ? rr : 0)) * a.Hq + hq) * kHd;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
@@ -1004,6 +1059,53 @@ int granite4_attn_paged(const uint16_t* q, int rows, int Hq, int Hk, int d, floa
   if (launch_status("granite4_attn_paged (split)") != 0) return -1;
   hipLaunchKernelGGL(attn_combine_kernel, dim3(Hq, rows), kCombineThreads, 0, st, a);
   return launch_status("granite4_attn_paged (combine)");
+}
+
+int granite4_attn_decode_append(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                const float* cos_tbl, const float* sin_tbl, int max_pos,
+                                const int* d_pos, const int* d_pt, int Hq, int Hk, float scale,
+                                void* cache_k, void* cache_v, float* k_scale, float* v_scale,
+                                int bits, int group, int stride, void* scratch, uint16_t* out) {
+  RopeArgs ra;
+  // q_rot is never written here (only the K / V units run): q stands in for it.
+  if (scratch == nullptr || out == nullptr || !std::isfinite(scale) || Hq != kGq * Hk ||
+      !rope_args_at_pos(ra, q, k, v, cos_tbl, sin_tbl, max_pos, d_pos, d_pt, Hq, Hk, kHd, bits,
+                        bits == 16 ? kHd : group, const_cast<uint16_t*>(q), cache_k, cache_v,
+                        k_scale, v_scale, stride)) {
+    std::fprintf(stderr, "granite4: granite4_attn_decode_append: invalid arguments\n");
+    return -1;
+  }
+  const int grp = bits == 16 ? kHd : group;
+  AttnArgs a{};
+  a.k = static_cast<const uint8_t*>(cache_k);
+  a.v = static_cast<const uint8_t*>(cache_v);
+  a.ksc = k_scale;
+  a.vsc = v_scale;
+  a.scale = scale;
+  a.Hq = Hq;
+  a.stride = stride;
+  a.rows = 1;
+  a.tps = attn_tps(stride);
+  a.splits = attn_splits(stride);
+  a.d_pos = d_pos;
+  a.d_pt = d_pt;
+  a.nblk = (a.splits + kAttnWaves - 1) / kAttnWaves;
+  a.part_ml = static_cast<float2*>(scratch);
+  a.part_o = reinterpret_cast<float*>(a.part_ml + static_cast<size_t>(Hq) * a.nblk);
+  a.out = out;
+  a.fuse_append = 1;
+  a.ra = ra;
+  const dim3 grid(Hk, a.nblk, 1);
+  const hipStream_t st = stream();
+  switch (bits) {
+    case 16: launch_attn_bits<16>(a, grp, grid, st); break;
+    case 8: launch_attn_bits<8>(a, grp, grid, st); break;
+    case 4: launch_attn_bits<4>(a, grp, grid, st); break;
+    default: launch_attn_bits<5>(a, grp, grid, st); break;
+  }
+  if (launch_status("granite4_attn_decode_append (split)") != 0) return -1;
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(Hq, 1), kCombineThreads, 0, st, a);
+  return launch_status("granite4_attn_decode_append (combine)");
 }
 
 int granite4_attn_split(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cache_v,

@@ -94,6 +94,7 @@ _SIG = {
                             P, P, P, I, P, P, I, I, I],
     "granite4_attn_paged": [P, I, I, I, I, F, P, P, P, P, I, I, I, I, P, P, P, P, I, I, P, P],
     "granite4_prefill_attn": [P, I, I, I, I, F, P, P, P, P, I, I, I, I, P, I, P],
+    "granite4_attn_decode_append": [P, P, P, P, P, I, P, P, I, I, F, P, P, P, P, I, I, I, P, P],
     "granite4_prefill_attention": [P, P, P, F, I, I, I, I, I, I, P, P, P, P, P, I, P, P, I, P, I,
                                    I],
     "granite4_gemm_fp8": [I, P, I, P, P, I, I, I, _c.POINTER(GemmEpilogue)],

@@ -512,6 +512,21 @@ int granite4_gemv_rmsnorm_qkv_rope_append(const uint16_t* d_x, const uint16_t* d
                                           void* cache_v, float* k_scale, float* v_scale,
                                           int stride);
 
+/* Replaces: the decode step's RoPE + KV append (forward_gpu.cu:2132-2157)
+ * followed by the split-KV attention (attention_split.cu:1083-1255), in the
+ * attention launches: q / k / v are the raw bf16 projections of one token
+ * at *d_pos; q is rotated in registers, and the workgroup whose split holds
+ * the position rotates, quantises and writes that position's K / V row into
+ * the pool (row d_pt[*d_pos]) before reading it. The pool and the output
+ * are bit-identical to granite4_rope_append_at_pos followed by
+ * granite4_attn_paged (rows = 1). scratch: granite4_attn_split_scratch_bytes
+ * (Hq, 1, stride) bytes. */
+int granite4_attn_decode_append(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                const float* cos_tbl, const float* sin_tbl, int max_pos,
+                                const int* d_pos, const int* d_pt, int Hq, int Hk, float scale,
+                                void* cache_k, void* cache_v, float* k_scale, float* v_scale,
+                                int bits, int group, int stride, void* scratch, uint16_t* out);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 
