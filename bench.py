@@ -519,7 +519,60 @@ def bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream, layers=40
                 L.call("granite4_gemv_fp8w_resid", act, p["wd"], sc, hidden, 1.0, H, I, hidden)
         return step
 
+    attn_scr = torch.empty(L.call_size("granite4_attn_split_scratch_bytes", HQ, 1, stride),
+                           dtype=torch.uint8, device=dev)
+
+    def attn(p, qq):
+        a = p["arena"]
+        L.call("granite4_attn_paged", qq, 1, HQ, HK, D, 1.0 / 128, a.k, a.v, None, None, 16, 128,
+               stride, 0, pos, pt, None, None, 0, 0, attn_scr, attn_out)
+
+    def plain_attn():
+        # the GEMVs and the attention alone: no norm, RoPE, KV append, SwiGLU, residual
+        for p in per:
+            L.call("granite4_gemv_qkv", normed, p["wq"], p["wk"], p["wv"], sc, sc, sc, HQ * D,
+                   HK * D, HK * D, H, q, k, v)
+            attn(p, q)
+            L.call("granite4_gemv_fp8w", attn_out, p["wo"], sc, H, HQ * D, o_out)
+            L.call("granite4_gemv_qkv", normed, p["wg"], p["wu"], None, sc, sc, 0.0, I, I, 0, H,
+                   g_out, u_out, None)
+            L.call("granite4_gemv_fp8w", act, p["wd"], sc, H, I, o_out)
+
+    def unfused_attn():
+        L.call("granite4_embed_at_pos", toks, pos, emb, VOCAB, H, 1.0, hidden)
+        for p in per:
+            L.call("granite4_kernel_rmsnorm", hidden, gamma, 1e-5, 1, H, normed)
+            L.call("granite4_gemv_qkv", normed, p["wq"], p["wk"], p["wv"], sc, sc, sc, HQ * D,
+                   HK * D, HK * D, H, q, k, v)
+            rope(p)
+            attn(p, q_rot)
+            L.call("granite4_gemv_fp8w_resid", attn_out, p["wo"], sc, hidden, 1.0, H, HQ * D,
+                   hidden)
+            L.call("granite4_kernel_rmsnorm", hidden, gamma, 1e-5, 1, H, normed)
+            L.call("granite4_kernel_silu_gate_up", p["wg"], p["wu"], normed, sc, sc, I, H, act)
+            L.call("granite4_gemv_fp8w_resid", act, p["wd"], sc, hidden, 1.0, H, I, hidden)
+
+    def fused_attn():
+        # every non-GEMM op inside a GEMV or the attention launch: norm prologues,
+        # RoPE + KV append in the attention, SwiGLU and residual epilogues
+        L.call("granite4_embed_at_pos", toks, pos, emb, VOCAB, H, 1.0, hidden)
+        for p in per:
+            a = p["arena"]
+            L.call("granite4_gemv_rmsnorm_qkv", hidden, gamma, 1e-5, p["wq"], p["wk"], p["wv"],
+                   sc, sc, sc, HQ * D, HK * D, HK * D, H, q, k, v)
+            L.call("granite4_attn_decode_append", q, k, v, cos_t, sin_t, 65536, pos, pt, HQ, HK,
+                   1.0 / 128, a.k, a.v, a.k_scale, a.v_scale, 16, 128, stride, attn_scr,
+                   attn_out)
+            L.call("granite4_gemv_fp8w_resid", attn_out, p["wo"], sc, hidden, 1.0, H, HQ * D,
+                   hidden)
+            L.call("granite4_gemv_rmsnorm_silu_gate_up", hidden, gamma, 1e-5, p["wg"], p["wu"],
+                   sc, sc, I, H, act)
+            L.call("granite4_gemv_fp8w_resid", act, p["wd"], sc, hidden, 1.0, H, I, hidden)
+
     t_plain = graph_us(torch, L, stream, plain)
+    t_plain_attn = graph_us(torch, L, stream, plain_attn)
+    t_unfused_attn = graph_us(torch, L, stream, unfused_attn)
+    t_fused_attn = graph_us(torch, L, stream, fused_attn)
     t_unfused = graph_us(torch, L, stream, unfused)
     t_qkv_rope_kernel = graph_us(torch, L, stream, fused)
     t_fused_norope = graph_us(torch, L, stream, fused_split(False))
@@ -536,6 +589,14 @@ def bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream, layers=40
             "fused_gemvs_without_rope_us": round(t_fused_norope, 1),
             "rope_append_launches_us": round(t_fused - t_fused_norope, 1),
             "fused_qkv_rope_one_launch_us": round(t_qkv_rope_kernel, 1),
+            "with_attention": {
+                "context": int(pos.item()) + 1, "kv": "bf16",
+                "plain_gemv_attn_us": round(t_plain_attn, 1),
+                "unfused_us": round(t_unfused_attn, 1), "fused_us": round(t_fused_attn, 1),
+                "non_gemm_overhead_unfused_us": round(t_unfused_attn - t_plain_attn, 1),
+                "non_gemm_overhead_fused_us": round(t_fused_attn - t_plain_attn, 1),
+                "launches_per_step": {"plain": 5 * layers, "unfused": 1 + 8 * layers,
+                                      "fused": 1 + 5 * layers}},
             "launches_per_step": {"plain": 4 * layers, "unfused": 1 + 7 * layers,
                                   "fused": 1 + 5 * layers}}
 
