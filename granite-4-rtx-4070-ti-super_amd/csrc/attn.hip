@@ -77,13 +77,16 @@ struct AttnArgs {
   uint16_t* out;    // [rows][Hq][128]
   // Decode append (one row at *d_pos): q, k, v are the raw bf16 projections
   // (ra.q / ra.k / ra.v); q is rotated in registers, and the wave whose split
-  // holds the position rotates, quantises and writes that position's K / V
-  // row (rope_unit, as the append kernels) before reading its tiles.
-  int fuse_append;
+  // holds the position rotates and quantises that position's K / V row (the
+  // append kernels' arithmetic) into LDS, reads the key from there, and
+  // copies the row to the pool when its work is done.
   RopeArgs ra;
 };
 
 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+// The page tables are device (global) memory; typed so, their loads are
+// global_load (vmcnt only) rather than flat (which LDS waits would include).
+typedef __attribute__((address_space(1))) const int g4_global_i32;
 
 // Four bf16 of a row-major LDS tile, transposed across each 16-lane group
 // (ds_read_b64_tr_b16): lane i of a group receives element i % 4 of the
@@ -181,20 +184,22 @@ __device__ __forceinline__ void v_load(const uint8_t* vbase, int prow,
   for (int i = 0; i < VS::kSteps; ++i) {
     const int key = i * (64 / VS::kChunks) + lane / VS::kChunks, c = lane % VS::kChunks;
     const int pr = __shfl(prow, key);
-    const uint32_t z = BITS == 16 || BITS == 8 ? 0u : 0x88888888u;  // int4 code 8 = value 0
-    raw[i] = u32x4_t{z, z, z, z};
-    if (pr >= 0) raw[i] = *reinterpret_cast<const u32x4_t*>(vbase + static_cast<size_t>(pr) * VS::kRowB + 16 * c);
+    // Unconditional (row 0 for keys without a row); v_store zeroes those.
+    raw[i] = *reinterpret_cast<const u32x4_t*>(vbase + static_cast<size_t>(pr >= 0 ? pr : 0) * VS::kRowB + 16 * c);
   }
 }
 
+// valid: bit k set when key k of the tile has an arena row (others store 0).
 template <int BITS>
-__device__ __forceinline__ void v_store(const u32x4_t (&raw)[VStage<BITS>::kSteps], uint16_t* vl) {
+__device__ __forceinline__ void v_store(const u32x4_t (&raw)[VStage<BITS>::kSteps], uint16_t* vl,
+                                        unsigned long long valid) {
   using VS = VStage<BITS>;
   const int lane = threadIdx.x & 63;
+  const uint32_t z = BITS == 16 || BITS == 8 ? 0u : 0x88888888u;  // int4 code 8 = value 0
 #pragma unroll
   for (int i = 0; i < VS::kSteps; ++i) {
     const int key = i * (64 / VS::kChunks) + lane / VS::kChunks, c = lane % VS::kChunks;
-    const u32x4_t u = raw[i];
+    const u32x4_t u = ((valid >> key) & 1ull) ? raw[i] : u32x4_t{z, z, z, z};
     if constexpr (BITS == 16) {
       *reinterpret_cast<u32x4_t*>(vl + key * kVPitch + 8 * c) = u;
     } else if constexpr (BITS == 8) {
@@ -229,7 +234,9 @@ __device__ __forceinline__ void v_store(const u32x4_t (&raw)[VStage<BITS>::kStep
 // (each wave owns its LDS tile, so no workgroup barrier is needed).
 __device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-template <int BITS, int GROUP>
+// FUSE: the decode append form (granite4_attn_decode_append); a template
+// parameter so that the plain kernels carry none of its registers.
+template <int BITS, int GROUP, bool FUSE>
 __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a) {
   constexpr bool kQuant = BITS != 16;
   constexpr int kNgrp = kQuant ? kHd / GROUP : 1;
@@ -251,8 +258,11 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
   const int base = a.row_pos != nullptr ? 0 : (a.d_pos != nullptr ? *a.d_pos : a.kv_base);
   // Causal length, clamped to the arena (a position read from device memory
   // never sends the page-table reads past the arena's positions).
+  // Multi-sequence rows (row_pos) take one row per wave, so only rr = 0 is
+  // ever asked for there: one scalar load.
+  const int row_pos0 = a.row_pos != nullptr ? a.row_pos[r0] : 0;
   auto row_len = [&](int rr) {
-    const int len = a.row_pos != nullptr ? a.row_pos[r0 + rr] + 1 : base + r0 + rr + 1;
+    const int len = a.row_pos != nullptr ? row_pos0 + 1 : base + r0 + rr + 1;
     return min(max(len, 0), a.stride);
   };
   auto row_lo = [&](int rr) { return a.window > 0 ? max(0, row_len(rr) - a.window) : 0; };
@@ -269,16 +279,24 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
   const bool active = split < a.splits && t_begin < kv_max && t_end_max > lo_min;
   const int t_first = max(t_begin, (lo_min / kTile) * kTile);
   const int* pt = a.row_pt != nullptr ? a.row_pt[r0] : a.d_pt;
+  const g4_global_i32* ptg = (const g4_global_i32*)pt;  // global loads, not flat
 
-  if (a.fuse_append) {
-    // The new position's K / V row, written by the one wave that reads it.
-    if (active && base >= t_begin && base < t_end_max && lane < 32) {
-      const int l16 = lane & 15;
-      rope_unit<BITS, GROUP>(a.ra, 0, (lane < 16 ? a.ra.Hq : a.ra.Hq + a.ra.Hk) + hkv, l16,
-                             [&](const uint16_t* head) { return ld8(head + 8 * l16); });
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the row is written before any tile load
-  }
+  const uint8_t* kbase = a.k + static_cast<size_t>(hkv) * a.stride * kKb;
+  const uint8_t* vbase = a.v + static_cast<size_t>(hkv) * a.stride * kVb;
+  const float* kscb = kQuant ? a.ksc + static_cast<size_t>(hkv) * a.stride * kNgrp : nullptr;
+  const float* vscb = kQuant ? a.vsc + static_cast<size_t>(hkv) * a.stride * kNgrp : nullptr;
+
+  // Page-table entry of position p, loaded unconditionally from a clamped
+  // index (a guarded load would be waited for inside its branch), and the
+  // arena row it gives: -1 past the split's end or outside [0, stride)
+  // (skipped like the append kernels skip them).
+  const int p_last = max(t_end_max - 1, 0);
+  auto pt_entry = [&](int p) { return pt != nullptr ? ptg[min(p, p_last)] : p; };
+  auto arena_row_of = [&](int p, int r) { return (p < t_end_max && r >= 0 && r < a.stride) ? r : -1; };
+  // Every load that depends only on the position is issued before the first
+  // wait: the first tile's page-table entries, this lane's q (and, fused,
+  // its cos / sin).
+  int pt_next = active ? pt_entry(t_first + lane) : -1;
 
   // This lane's query column.
   const int rr = n >> 2, hq = hkv * kGq + (n & 3);
@@ -286,78 +304,101 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
   const int my_len = live ? row_len(rr) : 0;
   const int my_lo = live ? row_lo(rr) : 0;
   bf16x8_t qb[4];
-  if (a.fuse_append) {
-    // Raw q rotated at the position: the lane's dims 32 s + 8 g + j pair with
-    // 32 (s + 2) + 8 g + j, so the rotation is lane-local; the same products
-    // and roundings as the append kernels' rotate8 (out = a c + b' s with b'
-    // the negated or plain partner), then bf16 RNE.
-    const uint16_t* qp = a.ra.q + static_cast<size_t>(hq) * kHd;
-    const int rp = base;
-    const bool ok = live && active && rp >= 0 && rp < a.ra.max_pos;
-    u32x4_t raw[4];
+  u32x4_t raw[4];
+  float cs[2][8], sn[2][8];
+  const bool q_ok = FUSE ? (live && active && base >= 0 && base < a.ra.max_pos)
+                                  : (live && active);
+  {
+    const uint16_t* qp = FUSE
+                             ? a.ra.q + static_cast<size_t>(hq) * kHd
+                             : a.q + (static_cast<size_t>(r0 + (live ? rr : 0)) * a.Hq + hq) * kHd;
 #pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) {
-      raw[s4] = u32x4_t{0u, 0u, 0u, 0u};
-      if (ok) raw[s4] = *reinterpret_cast<const u32x4_t*>(qp + 32 * s4 + 8 * g);
-    }
-    uint32_t rot[4][4];
+    for (int s4 = 0; s4 < 4; ++s4) raw[s4] = *reinterpret_cast<const u32x4_t*>(qp + 32 * s4 + 8 * g);
+    if constexpr (FUSE) {
+      const long long rp = q_ok ? base : 0;
 #pragma unroll
-    for (int s4 = 0; s4 < 2; ++s4) {
-      const float* cp = a.ra.cos_t + static_cast<long long>(ok ? rp : 0) * 64 + 32 * s4 + 8 * g;
-      const float* sp = a.ra.sin_t + static_cast<long long>(ok ? rp : 0) * 64 + 32 * s4 + 8 * g;
-      float cs[8], sn[8];
-      *reinterpret_cast<float4*>(cs) = *reinterpret_cast<const float4*>(cp);
-      *reinterpret_cast<float4*>(cs + 4) = *reinterpret_cast<const float4*>(cp + 4);
-      *reinterpret_cast<float4*>(sn) = *reinterpret_cast<const float4*>(sp);
-      *reinterpret_cast<float4*>(sn + 4) = *reinterpret_cast<const float4*>(sp + 4);
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const uint32_t xa = raw[s4][w], xb = raw[s4 + 2][w];
-        const float a0 = lo_bf16(xa), a1 = hi_bf16(xa), b0 = lo_bf16(xb), b1 = hi_bf16(xb);
-        rot[s4][w] = pack_bf16_hw(a0 * cs[2 * w] + (-b0) * sn[2 * w],
-                                  a1 * cs[2 * w + 1] + (-b1) * sn[2 * w + 1]);
-        rot[s4 + 2][w] = pack_bf16_hw(b0 * cs[2 * w] + a0 * sn[2 * w],
-                                      b1 * cs[2 * w + 1] + a1 * sn[2 * w + 1]);
+      for (int s4 = 0; s4 < 2; ++s4) {
+        const float* cp = a.ra.cos_t + rp * 64 + 32 * s4 + 8 * g;
+        const float* sp = a.ra.sin_t + rp * 64 + 32 * s4 + 8 * g;
+        *reinterpret_cast<float4*>(cs[s4]) = *reinterpret_cast<const float4*>(cp);
+        *reinterpret_cast<float4*>(cs[s4] + 4) = *reinterpret_cast<const float4*>(cp + 4);
+        *reinterpret_cast<float4*>(sn[s4]) = *reinterpret_cast<const float4*>(sp);
+        *reinterpret_cast<float4*>(sn[s4] + 4) = *reinterpret_cast<const float4*>(sp + 4);
       }
-    }
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4)
-      qb[s4] = ok ? as_bf16x8(rot[s4][0], rot[s4][1], rot[s4][2], rot[s4][3])
-                  : as_bf16x8(0u, 0u, 0u, 0u);
-  } else {
-    const uint16_t* qp = a.q + (static_cast<size_t>(r0 + (live ? rr : 0)) * a.Hq + hq) * kHd;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      u32x4_t u = {0u, 0u, 0u, 0u};
-      if (live && active) u = *reinterpret_cast<const u32x4_t*>(qp + 32 * s + 8 * g);
-      qb[s] = __builtin_bit_cast(bf16x8_t, u);
     }
   }
 
-  const uint8_t* kbase = a.k + static_cast<size_t>(hkv) * a.stride * kKb;
-  const uint8_t* vbase = a.v + static_cast<size_t>(hkv) * a.stride * kVb;
-  const float* kscb = kQuant ? a.ksc + static_cast<size_t>(hkv) * a.stride * kNgrp : nullptr;
-  const float* vscb = kQuant ? a.vsc + static_cast<size_t>(hkv) * a.stride * kNgrp : nullptr;
+  // Decode append: the one wave whose split holds the new position writes
+  // its K / V row to the pool and keeps the same bytes in LDS, inside the
+  // tile that holds the position once that tile's loads are in flight (its
+  // own loads overlap them). The tile then takes the key from LDS: its pool
+  // loads were issued before the store. A position outside the RoPE table
+  // leaves K unwritten (as the append kernels do), so only V is taken.
+  __shared__ __align__(16) uint8_t mir_k[kAttnWaves][2 * kHd];
+  __shared__ __align__(16) uint8_t mir_v[kAttnWaves][2 * kHd];
+  __shared__ float mir_s[kAttnWaves][2][kNgrp];
+  const bool own_new = FUSE && active && base >= t_begin && base < t_end_max;
 
+  // q for the MFMAs: fused, rotated at the position, done in the first tile
+  // once its loads are in flight (the cos / sin wait then overlaps them).
+  auto make_q = [&] {
+    if constexpr (FUSE) {
+      // Raw q rotated at the position: the lane's dims 32 s + 8 g + j pair with
+      // 32 (s + 2) + 8 g + j, so the rotation is lane-local; the same products
+      // and roundings as the append kernels' rotate8 (out = a c + b' s with b'
+      // the negated or plain partner), then bf16 RNE.
+      uint32_t rot[4][4];
+#pragma unroll
+      for (int s4 = 0; s4 < 2; ++s4) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const uint32_t xa = raw[s4][w], xb = raw[s4 + 2][w];
+          const float a0 = lo_bf16(xa), a1 = hi_bf16(xa), b0 = lo_bf16(xb), b1 = hi_bf16(xb);
+          rot[s4][w] = pack_bf16_hw(a0 * cs[s4][2 * w] + (-b0) * sn[s4][2 * w],
+                                    a1 * cs[s4][2 * w + 1] + (-b1) * sn[s4][2 * w + 1]);
+          rot[s4 + 2][w] = pack_bf16_hw(b0 * cs[s4][2 * w] + a0 * sn[s4][2 * w],
+                                        b1 * cs[s4][2 * w + 1] + a1 * sn[s4][2 * w + 1]);
+        }
+      }
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4)
+        qb[s4] = q_ok ? as_bf16x8(rot[s4][0], rot[s4][1], rot[s4][2], rot[s4][3])
+                      : as_bf16x8(0u, 0u, 0u, 0u);
+    } else {
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4)
+        qb[s4] = __builtin_bit_cast(bf16x8_t, q_ok ? raw[s4] : u32x4_t{0u, 0u, 0u, 0u});
+    }
+  };
   f32x4_t o[8];
 #pragma unroll
   for (int nb = 0; nb < 8; ++nb) o[nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   float m = -INFINITY, l = 0.0f;
-
-  // Page-table entry of position p (-1 past the split's end; arena rows
-  // outside [0, stride) are skipped like the append kernels skip them).
-  auto arena_row_of = [&](int p) {
-    if (p >= t_end_max) return -1;
-    const int r = pt != nullptr ? pt[p] : p;
-    return (r >= 0 && r < a.stride) ? r : -1;
-  };
-  int prow_next = active ? arena_row_of(t_first + lane) : -1;
+  int new_row = -1;  // arena row of the appended key once its LDS copy is made
   for (int t0 = active ? t_first : t_end_max; t0 < t_end_max; t0 += kTile) {
     // Arena row of key t0 + lane; the next tile's entry is fetched a tile ahead.
-    const int prow = prow_next;
-    prow_next = arena_row_of(t0 + kTile + lane);
+    const int prow = arena_row_of(t0 + lane, pt_next);
+    if (t0 + kTile < t_end_max) pt_next = pt_entry(t0 + kTile + lane);
     // Every K and V load of the tile first (one memory round trip), then V
     // and the scales to LDS.
+    // The appended row's inputs, issued before the tile's loads so that the
+    // wait for them does not include the tile: lanes 0-15 the key head (and
+    // its cos / sin), 16-31 the value head, 8 dims per lane, no branch.
+    const bool new_tile = own_new && base >= t0 && base < t0 + kTile;  // wave-uniform
+    V8 nx;
+    float ncs[8], nsn[8];
+    if (new_tile) {
+      const int l16 = lane & 15;
+      const uint16_t* src = (lane < 16 ? a.ra.k : a.ra.v) + hkv * kHd + 8 * l16;
+      nx = ld8(src);
+      const long long rp = base < a.ra.max_pos ? base : 0;
+      const float* cp = a.ra.cos_t + rp * 64 + 8 * (l16 & 7);
+      const float* sp = a.ra.sin_t + rp * 64 + 8 * (l16 & 7);
+      *reinterpret_cast<float4*>(ncs) = *reinterpret_cast<const float4*>(cp);
+      *reinterpret_cast<float4*>(ncs + 4) = *reinterpret_cast<const float4*>(cp + 4);
+      *reinterpret_cast<float4*>(nsn) = *reinterpret_cast<const float4*>(sp);
+      *reinterpret_cast<float4*>(nsn + 4) = *reinterpret_cast<const float4*>(sp + 4);
+    }
     u32x4_t vraw[VStage<BITS>::kSteps];
     v_load<BITS>(vbase, prow, vraw);
     u32x4_t kraw[4][4];
@@ -368,23 +409,79 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
 #pragma unroll
       for (int s = 0; s < 4; ++s) kraw[mb][s] = load_k_raw<BITS>(krow, 32 * s + 8 * g);
     }
+    if (t0 == t_first) make_q();
     float ksr[kNgrp], vsr[kNgrp];
     if constexpr (kQuant) {
 #pragma unroll
       for (int gi = 0; gi < kNgrp; ++gi) {
-        ksr[gi] = prow >= 0 ? kscb[static_cast<size_t>(prow) * kNgrp + gi] : 0.0f;
-        vsr[gi] = prow >= 0 ? vscb[static_cast<size_t>(prow) * kNgrp + gi] : 0.0f;
+        const size_t si = static_cast<size_t>(prow >= 0 ? prow : 0) * kNgrp + gi;
+        ksr[gi] = kscb[si];
+        vsr[gi] = vscb[si];
       }
     }
-    v_store<BITS>(vraw, vl);
-    if constexpr (kQuant) {
+    if (new_tile) {
+      // The appended key: K rotated as the append kernels' rope_unit does it
+      // (rotate8, bf16, then the code of the rotated value or of its bf16
+      // rounding), V as is, both quantised by store_quant into this wave's
+      // LDS copy of the row. Lanes 32-63 compute the same and write nothing.
+      const int j = base - t0;
+      const int pj = __shfl(prow, j);
+      const int l16 = lane & 15;
+      const bool is_k = lane < 16;
+      float rot[8];
+      rotate8(nx, ncs, nsn, l16 < 8, rot);
+      const V8 rb = to_bf16x8(rot);
+      if (lane < 32) {
+        if constexpr (BITS == 16) {
+          st8(reinterpret_cast<uint16_t*>(is_k ? mir_k[wave] : mir_v[wave]) + 8 * l16, is_k ? rb : nx);
+        } else {
+          float val[8];
 #pragma unroll
-      for (int gi = 0; gi < kNgrp; ++gi) {
-        ksc_l[lane * kNgrp + gi] = ksr[gi];
-        vsc_l[lane * kNgrp + gi] = vsr[gi];
+          for (int e = 0; e < 8; ++e)
+            val[e] = is_k ? (a.ra.k_round ? v8_get(rb, e) : rot[e]) : v8_get(nx, e);
+          store_quant<BITS, GROUP>(a.ra, val, is_k, 0, l16,
+                                   RowSink{mir_k[wave], mir_v[wave], mir_s[wave][0], mir_s[wave][1]});
+        }
+      }
+      wave_lds_sync();
+      const bool k_new = base < a.ra.max_pos;
+      new_row = pj;
+      if (pj >= 0) {
+        if (k_new) {
+#pragma unroll
+          for (int mb = 0; mb < 4; ++mb) {
+            if (mb == (j >> 4) && n == (j & 15)) {
+#pragma unroll
+              for (int s = 0; s < 4; ++s) kraw[mb][s] = load_k_raw<BITS>(mir_k[wave], 32 * s + 8 * g);
+            }
+          }
+        }
+        using VS = VStage<BITS>;
+#pragma unroll
+        for (int i = 0; i < VS::kSteps; ++i) {
+          const int key = i * (64 / VS::kChunks) + lane / VS::kChunks, c = lane % VS::kChunks;
+          if (key == j) vraw[i] = *reinterpret_cast<const u32x4_t*>(mir_v[wave] + 16 * c);
+        }
+        if constexpr (kQuant) {
+          if (lane == j) {
+#pragma unroll
+            for (int gi = 0; gi < kNgrp; ++gi) {
+              if (k_new) ksr[gi] = mir_s[wave][0][gi];
+              vsr[gi] = mir_s[wave][1][gi];
+            }
+          }
+        }
       }
     }
     const unsigned long long kvalid = __ballot(prow >= 0);
+    v_store<BITS>(vraw, vl, kvalid);
+    if constexpr (kQuant) {
+#pragma unroll
+      for (int gi = 0; gi < kNgrp; ++gi) {
+        ksc_l[lane * kNgrp + gi] = prow >= 0 ? ksr[gi] : 0.0f;
+        vsc_l[lane * kNgrp + gi] = prow >= 0 ? vsr[gi] : 0.0f;
+      }
+    }
     wave_lds_sync();  // V tile and scales in LDS
     // S^T = K Q^T per 16-key block mb: lane l holds keys 16 mb + 4 g + i.
     float sv[4][4];
@@ -495,6 +592,27 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
   {
     const int col = threadIdx.x >> 4, dc = threadIdx.x & 15;  // 16 columns x 8 dims each
     const int crr = col >> 2, chq = hkv * kGq + (col & 3);
+    if (new_row >= 0) {
+      // The appended row from LDS to the pool, last: nothing in this wave
+      // waits for these stores (k: lanes 0-15, v: 16-31, scales: 32-39).
+      const size_t slot = static_cast<size_t>(hkv) * a.stride + new_row;
+      const bool k_new = base < a.ra.max_pos;
+      if (lane < 16) {
+        if (k_new && 16 * lane < kKb)
+          *reinterpret_cast<u32x4_t*>(static_cast<uint8_t*>(a.ra.cache_k) + slot * kKb + 16 * lane) =
+              *reinterpret_cast<const u32x4_t*>(mir_k[wave] + 16 * lane);
+      } else if (lane < 32) {
+        const int c = lane - 16;
+        if (16 * c < kVb)
+          *reinterpret_cast<u32x4_t*>(static_cast<uint8_t*>(a.ra.cache_v) + slot * kVb + 16 * c) =
+              *reinterpret_cast<const u32x4_t*>(mir_v[wave] + 16 * c);
+      } else if (kQuant && lane < 32 + 2 * kNgrp) {
+        const int gi = (lane - 32) % kNgrp;
+        const bool is_k = lane - 32 < kNgrp;
+        if (is_k ? k_new : true)
+          (is_k ? a.ra.k_scale : a.ra.v_scale)[slot * kNgrp + gi] = mir_s[wave][is_k ? 0 : 1][gi];
+      }
+    }
     if (crr >= nr) return;
     float M = -INFINITY;
 #pragma unroll
@@ -899,15 +1017,15 @@ int attn_splits(int max_len) {
   return (tiles + tps - 1) / tps;
 }
 
-template <int BITS>
+template <int BITS, bool FUSE>
 void launch_attn_bits(const AttnArgs& a, int group, dim3 grid, hipStream_t st) {
   if constexpr (BITS == 16) {
     (void)group;
-    hipLaunchKernelGGL((attn_split_kernel<16, kHd>), grid, kAttnWaves * 64, 0, st, a);
+    hipLaunchKernelGGL((attn_split_kernel<16, kHd, FUSE>), grid, kAttnWaves * 64, 0, st, a);
   } else {
-    if (group == kHd) hipLaunchKernelGGL((attn_split_kernel<BITS, kHd>), grid, kAttnWaves * 64, 0, st, a);
-    else if (group == 64) hipLaunchKernelGGL((attn_split_kernel<BITS, 64>), grid, kAttnWaves * 64, 0, st, a);
-    else hipLaunchKernelGGL((attn_split_kernel<BITS, 32>), grid, kAttnWaves * 64, 0, st, a);
+    if (group == kHd) hipLaunchKernelGGL((attn_split_kernel<BITS, kHd, FUSE>), grid, kAttnWaves * 64, 0, st, a);
+    else if (group == 64) hipLaunchKernelGGL((attn_split_kernel<BITS, 64, FUSE>), grid, kAttnWaves * 64, 0, st, a);
+    else hipLaunchKernelGGL((attn_split_kernel<BITS, 32, FUSE>), grid, kAttnWaves * 64, 0, st, a);
   }
 }
 
@@ -1051,10 +1169,10 @@ int granite4_attn_paged(const uint16_t* q, int rows, int Hq, int Hk, int d, floa
   const dim3 grid(Hk, a.nblk, nz);
   const hipStream_t st = stream();
   switch (bits) {
-    case 16: launch_attn_bits<16>(a, group, grid, st); break;
-    case 8: launch_attn_bits<8>(a, group, grid, st); break;
-    case 4: launch_attn_bits<4>(a, group, grid, st); break;
-    default: launch_attn_bits<5>(a, group, grid, st); break;
+    case 16: launch_attn_bits<16, false>(a, group, grid, st); break;
+    case 8: launch_attn_bits<8, false>(a, group, grid, st); break;
+    case 4: launch_attn_bits<4, false>(a, group, grid, st); break;
+    default: launch_attn_bits<5, false>(a, group, grid, st); break;
   }
   if (launch_status("granite4_attn_paged (split)") != 0) return -1;
   hipLaunchKernelGGL(attn_combine_kernel, dim3(Hq, rows), kCombineThreads, 0, st, a);
@@ -1093,15 +1211,14 @@ int granite4_attn_decode_append(const uint16_t* q, const uint16_t* k, const uint
   a.part_ml = static_cast<float2*>(scratch);
   a.part_o = reinterpret_cast<float*>(a.part_ml + static_cast<size_t>(Hq) * a.nblk);
   a.out = out;
-  a.fuse_append = 1;
   a.ra = ra;
   const dim3 grid(Hk, a.nblk, 1);
   const hipStream_t st = stream();
   switch (bits) {
-    case 16: launch_attn_bits<16>(a, grp, grid, st); break;
-    case 8: launch_attn_bits<8>(a, grp, grid, st); break;
-    case 4: launch_attn_bits<4>(a, grp, grid, st); break;
-    default: launch_attn_bits<5>(a, grp, grid, st); break;
+    case 16: launch_attn_bits<16, true>(a, grp, grid, st); break;
+    case 8: launch_attn_bits<8, true>(a, grp, grid, st); break;
+    case 4: launch_attn_bits<4, true>(a, grp, grid, st); break;
+    default: launch_attn_bits<5, true>(a, grp, grid, st); break;
   }
   if (launch_status("granite4_attn_decode_append (split)") != 0) return -1;
   hipLaunchKernelGGL(attn_combine_kernel, dim3(Hq, 1), kCombineThreads, 0, st, a);

@@ -91,9 +91,35 @@ __device__ __forceinline__ V8 to_bf16x8(const float* f) {
   return v;
 }
 
-template <int BITS, int GROUP>
+// Where store_quant puts a row: the pool (PoolSink), or a caller's copy of
+// the row in the pool's byte layout (RowSink: k / v one row each, ks / vs
+// its group scales; the decode attention keeps the row it appends in LDS).
+struct PoolSink {
+  static constexpr bool kPool = true;
+  __device__ __forceinline__ void bytes8(bool, int, uint2) const {}
+  __device__ __forceinline__ void bytes4(bool, int, uint32_t) const {}
+  __device__ __forceinline__ void bytes1(bool, int, uint8_t) const {}
+  __device__ __forceinline__ void scale(bool, int, float) const {}
+};
+struct RowSink {
+  static constexpr bool kPool = false;
+  uint8_t* k;
+  uint8_t* v;
+  float* ks;
+  float* vs;
+  __device__ __forceinline__ void bytes8(bool is_k, int off, uint2 x) const {
+    *reinterpret_cast<uint2*>((is_k ? k : v) + off) = x;
+  }
+  __device__ __forceinline__ void bytes4(bool is_k, int off, uint32_t x) const {
+    *reinterpret_cast<uint32_t*>((is_k ? k : v) + off) = x;
+  }
+  __device__ __forceinline__ void bytes1(bool is_k, int off, uint8_t x) const { (is_k ? k : v)[off] = x; }
+  __device__ __forceinline__ void scale(bool is_k, int gi, float x) const { (is_k ? ks : vs)[gi] = x; }
+};
+
+template <int BITS, int GROUP, class Sink = PoolSink>
 __device__ __forceinline__ void store_quant(const RopeArgs& a, const float* val, bool is_k,
-                                            long long slot, int lane16) {
+                                            long long slot, int lane16, const Sink& sink = Sink{}) {
   constexpr int GL = GROUP / 8;
   float am = 0.0f;
 #pragma unroll
@@ -102,7 +128,10 @@ __device__ __forceinline__ void store_quant(const RopeArgs& a, const float* val,
   const int qmax = BITS == 8 ? 127 : ((BITS == 5 && is_k) ? 15 : 7);
   const float s = am / static_cast<float>(qmax);
   float* scales = is_k ? a.k_scale : a.v_scale;
-  if (lane16 % GL == 0) scales[slot * (128 / GROUP) + lane16 / GL] = s;
+  if (lane16 % GL == 0) {
+    if constexpr (Sink::kPool) scales[slot * (128 / GROUP) + lane16 / GL] = s;
+    else sink.scale(is_k, lane16 / GL, s);
+  }
   const float inv = 1.0f / s;
   int c[8];
 #pragma unroll
@@ -115,7 +144,8 @@ __device__ __forceinline__ void store_quant(const RopeArgs& a, const float* val,
       w0 |= (static_cast<uint32_t>(c[e]) & 0xffu) << (8 * e);
       w1 |= (static_cast<uint32_t>(c[e + 4]) & 0xffu) << (8 * e);
     }
-    *reinterpret_cast<uint2*>(cache + slot * 128 + 8 * lane16) = make_uint2(w0, w1);
+    if constexpr (Sink::kPool) *reinterpret_cast<uint2*>(cache + slot * 128 + 8 * lane16) = make_uint2(w0, w1);
+    else sink.bytes8(is_k, 8 * lane16, make_uint2(w0, w1));
     return;
   }
   uint32_t nib = 0, plane = 0;
@@ -125,7 +155,10 @@ __device__ __forceinline__ void store_quant(const RopeArgs& a, const float* val,
     nib |= (code & 0xfu) << (4 * e);
     plane |= ((code >> 4) & 1u) << e;
   }
-  if (BITS == 5 && is_k) {
+  if constexpr (!Sink::kPool) {
+    sink.bytes4(is_k, 4 * lane16, nib);
+    if (BITS == 5 && is_k) sink.bytes1(true, 64 + lane16, static_cast<uint8_t>(plane));
+  } else if (BITS == 5 && is_k) {
     *reinterpret_cast<uint32_t*>(cache + slot * 80 + 4 * lane16) = nib;
     cache[slot * 80 + 64 + lane16] = static_cast<uint8_t>(plane);
   } else {

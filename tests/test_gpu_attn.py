@@ -265,22 +265,27 @@ def test_prefill_attn_t512_from_zero_and_reference_entry_point():
     np.testing.assert_array_equal(host(out).view(np.uint16), got)
 
 
+@pytest.mark.parametrize("pos_v,max_pos", [(1000, 4096), (0, 4096), (1023, 4096), (1279, 4096),
+                                           (1000, 512)])
 @pytest.mark.parametrize("bits,group", [(16, 128), (8, 128), (5, 32), (4, 64)])
-def test_attn_decode_append_fused(bits, group):
+def test_attn_decode_append_fused(bits, group, pos_v, max_pos):
     """RoPE + KV append folded into the attention launch: the output and the
     whole pool bit-identical to granite4_rope_append_at_pos followed by
-    granite4_attn_paged at the same position and page table."""
-    note(f"attn decode append bits={bits} group={group}")
+    granite4_attn_paged at the same position and page table. Positions at the
+    first / a middle / the last key of a tile and the arena's last row (the
+    appended key is read from the wave's LDS copy), and one past the RoPE
+    table (K not written, V read back from the pool)."""
+    note(f"attn decode append bits={bits} group={group} pos={pos_v} max_pos={max_pos}")
     pages = 80
     stride = 16 * pages
     ck, cv, ks, vs = make_cache(bits, group, stride, 0xF1 + bits)
     rng = np.random.default_rng(bits + group)
     pt = dev(ol.row_table(rng.permutation(pages).astype(np.int32), stride))
-    pos = dev(np.array([1000], np.int32))
+    pos = dev(np.array([pos_v], np.int32))
     q = dev(ol.normal_bf16(0xF2, 0.0, 1.0, HQ * D))
     k = dev(ol.normal_bf16(0xF3, 0.0, 1.0, HK * D))
     v = dev(ol.normal_bf16(0xF4, 0.0, 1.0, HK * D))
-    cos_t, sin_t = ol.rope_tables(1e7, D, 4096)
+    cos_t, sin_t = ol.rope_tables(1e7, D, max_pos)
     dcos, dsin = dev(cos_t), dev(sin_t)
     scratch = torch.empty(L.call_size("granite4_attn_split_scratch_bytes", HQ, 1, stride),
                           dtype=torch.uint8, device="cuda")
@@ -289,11 +294,13 @@ def test_attn_decode_append_fused(bits, group):
         pool = [dev(ck), dev(cv), None if ks is None else dev(ks), None if vs is None else dev(vs)]
         out = torch.empty(HQ * D, dtype=torch.int16, device="cuda")
         if fused:
-            L.call("granite4_attn_decode_append", q, k, v, dcos, dsin, 4096, pos, pt, HQ, HK,
+            L.call("granite4_attn_decode_append", q, k, v, dcos, dsin, max_pos, pos, pt, HQ, HK,
                    1.0 / 16, *pool, bits, group, stride, scratch, out)
         else:
-            q_rot = torch.empty(HQ * D, dtype=torch.int16, device="cuda")
-            L.call("granite4_rope_append_at_pos", q, k, v, dcos, dsin, 4096, pos, pt, HQ, HK, D,
+            # zeros: a position past the table leaves q_rot unwritten, and the
+            # fused form then attends with a zero query
+            q_rot = torch.zeros(HQ * D, dtype=torch.int16, device="cuda")
+            L.call("granite4_rope_append_at_pos", q, k, v, dcos, dsin, max_pos, pos, pt, HQ, HK, D,
                    bits, group, q_rot, *pool, stride)
             L.call("granite4_attn_paged", q_rot, 1, HQ, HK, D, 1.0 / 16, *pool, bits, group, stride,
                    0, pos, pt, None, None, 0, 0, scratch, out)
