@@ -151,21 +151,26 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int c = 0; c < kChunks; ++c) dst[c] = ld_u4_nt(rows[r] + koff[c]);
   };
-#pragma unroll
-  for (int r = 0; r < kDepth; ++r) load_row(r, buf[r]);
-
-  // Prologue: the lane's 16 activations per chunk, in registers (f32).
+  // Prologue loads: the lane's activations (and norm weights) first, then
+  // the first kDepth weight rows, all issued before any is used (vmcnt is in
+  // order: x is waited for while the rows are still in flight, so the norm
+  // overlaps the weight fetch). Without the scheduling barrier the compiler
+  // unpacks x between the row loads and the wait holds the later rows back
+  // by a round trip.
   float av[kChunks][16];
   uint4 xr[kChunks][2], gr[kChunks][2];
 #pragma unroll
   for (int c = 0; c < kChunks; ++c) {
     xr[c][0] = *reinterpret_cast<const uint4*>(a.x + koff[c]);
     xr[c][1] = *reinterpret_cast<const uint4*>(a.x + koff[c] + 8);
-    if (PRO == kProNorm) {  // issued with x: one memory round trip, not two
+    if (PRO == kProNorm) {
       gr[c][0] = *reinterpret_cast<const uint4*>(a.gamma + koff[c]);
       gr[c][1] = *reinterpret_cast<const uint4*>(a.gamma + koff[c] + 8);
     }
   }
+#pragma unroll
+  for (int r = 0; r < kDepth; ++r) load_row(r, buf[r]);
+  __builtin_amdgcn_sched_barrier(0);
   if (PRO == kProNorm) {
     double ss = 0.0;
 #pragma unroll
