@@ -54,6 +54,7 @@ struct GemvArgs {
   const uint16_t* x;      // activation, or the residual row to normalise
   const uint16_t* gamma;  // norm weight (kProNorm)
   float eps;
+  double inv_k;           // 1 / K when K is a power of two, else 0
   const uint8_t* w[3];    // weight segments [n_i][K]
   float s[3];             // their scales
   uint16_t* o[3];         // their outputs (kEpiOut); o[0] = out / act otherwise
@@ -73,6 +74,30 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
   return v;
+}
+
+// Sum of squares of the 16 bf16 in w[8], in double, as a pairwise tree
+// (each square of a bf16 is exact in f32, so only the additions round; the
+// tree keeps the dependent chain 4 additions long instead of 16).
+__device__ __forceinline__ double sumsq16(const uint32_t (&w)[8]) {
+  double d[16];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float lo = lo_bf16(w[e]), hi = hi_bf16(w[e]);
+    d[2 * e] = static_cast<double>(lo * lo);
+    d[2 * e + 1] = static_cast<double>(hi * hi);
+  }
+#pragma unroll
+  for (int w2 = 8; w2 > 0; w2 >>= 1)
+#pragma unroll
+    for (int i = 0; i < w2; ++i) d[i] = d[2 * i] + d[2 * i + 1];
+  return d[0];
+}
+
+// mean = ss / K as the reference computes it (double division): a multiply
+// by the exact 1 / K when K is a power of two (inv_k != 0).
+__device__ __forceinline__ double mean_of(double ss, int K, double inv_k) {
+  return inv_k != 0.0 ? ss * inv_k : ss / K;
 }
 
 __device__ __forceinline__ void fp8x16_to_f32(const uint4& q, float (&f)[16]) {
@@ -178,18 +203,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
       if (!cin[c]) continue;
       const uint32_t w[8] = {xr[c][0].x, xr[c][0].y, xr[c][0].z, xr[c][0].w,
                              xr[c][1].x, xr[c][1].y, xr[c][1].z, xr[c][1].w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float lo = lo_bf16(w[e]), hi = hi_bf16(w[e]);
-        ss += static_cast<double>(lo * lo);
-        ss += static_cast<double>(hi * hi);
-      }
+      ss += sumsq16(w);
     }
     ss = wave_sum(ss);
     if (lane == 0) s_ss[wave] = ss;
     lds_barrier();
     ss = s_ss[0] + s_ss[1] + s_ss[2] + s_ss[3];
-    const float rr = 1.0f / sqrtf(static_cast<float>(ss / K) + a.eps);
+    const float rr = 1.0f / sqrtf(static_cast<float>(mean_of(ss, K, a.inv_k)) + a.eps);
 #pragma unroll
     for (int c = 0; c < kChunks; ++c) {
       const uint4 g0 = gr[c][0], g1 = gr[c][1];
@@ -323,17 +343,10 @@ __global__ __launch_bounds__(1024) void gemv_qkv_rope_kernel(GemvArgs g, RopeArg
     for (int c = 0; c < 4; ++c) {
       const uint32_t w[8] = {xr[c][0].x, xr[c][0].y, xr[c][0].z, xr[c][0].w,
                              xr[c][1].x, xr[c][1].y, xr[c][1].z, xr[c][1].w};
-      double ss = 0.0;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float lo = lo_bf16(w[e]), hi = hi_bf16(w[e]);
-        ss += static_cast<double>(lo * lo);
-        ss += static_cast<double>(hi * hi);
-      }
-      ssc[c] = wave_sum(ss);
+      ssc[c] = wave_sum(sumsq16(w));
     }
     const double ss = ssc[0] + ssc[1] + ssc[2] + ssc[3];
-    const float rr = 1.0f / sqrtf(static_cast<float>(ss / 4096) + g.eps);
+    const float rr = 1.0f / sqrtf(static_cast<float>(ss * (1.0 / 4096)) + g.eps);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const uint32_t xv[8] = {xr[c][0].x, xr[c][0].y, xr[c][0].z, xr[c][0].w,
@@ -430,6 +443,7 @@ int gemv_out(int pro, const uint16_t* x, const uint16_t* gamma, float eps,
   a.seg2 = n[0] + n[1];
   a.N = N;
   a.K = K;
+  a.inv_k = (K & (K - 1)) == 0 ? 1.0 / K : 0.0;
   return pro == kProNorm ? launch_gemv<kProNorm, kEpiOut>(a, what)
                          : launch_gemv<kProNone, kEpiOut>(a, what);
 }
@@ -456,6 +470,7 @@ int gemv_swiglu(int pro, const uint16_t* x, const uint16_t* gamma, float eps, co
   a.I = N;
   a.N = N;
   a.K = K;
+  a.inv_k = (K & (K - 1)) == 0 ? 1.0 / K : 0.0;
   return pro == kProNorm ? launch_gemv<kProNorm, kEpiSwiglu>(a, what)
                          : launch_gemv<kProNone, kEpiSwiglu>(a, what);
 }
@@ -494,6 +509,7 @@ int granite4_gemv_fp8w_resid(const uint16_t* d_a, const uint8_t* d_w, float scal
   a.rs = resid_scale;
   a.seg1 = a.seg2 = a.N = N;
   a.K = K;
+  a.inv_k = (K & (K - 1)) == 0 ? 1.0 / K : 0.0;
   return launch_gemv<kProNone, kEpiResid>(a, "granite4_gemv_fp8w_resid");
 }
 
