@@ -572,7 +572,26 @@ def bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream, layers=40
     t_plain = graph_us(torch, L, stream, plain)
     t_plain_attn = graph_us(torch, L, stream, plain_attn)
     t_unfused_attn = graph_us(torch, L, stream, unfused_attn)
-    t_fused_attn = graph_us(torch, L, stream, fused_attn)
+    k_rot = bf(HK * D)
+
+    def fused_attn_rot():
+        # RoPE in the q|k|v GEMV epilogue, the KV append in the attention
+        L.call("granite4_embed_at_pos", toks, pos, emb, VOCAB, H, 1.0, hidden)
+        for p in per:
+            a = p["arena"]
+            L.call("granite4_gemv_rmsnorm_qkv_rope", hidden, gamma, 1e-5, p["wq"], p["wk"],
+                   p["wv"], sc, sc, sc, cos_t, sin_t, 65536, pos, HQ, HK, H, q_rot, k_rot, v)
+            L.call("granite4_attn_decode_append_rotated", q_rot, k_rot, v, 65536, pos, pt, HQ, HK,
+                   1.0 / 128, a.k, a.v, a.k_scale, a.v_scale, 16, 128, stride, attn_scr,
+                   attn_out)
+            L.call("granite4_gemv_fp8w_resid", attn_out, p["wo"], sc, hidden, 1.0, H, HQ * D,
+                   hidden)
+            L.call("granite4_gemv_rmsnorm_silu_gate_up", hidden, gamma, 1e-5, p["wg"], p["wu"],
+                   sc, sc, I, H, act)
+            L.call("granite4_gemv_fp8w_resid", act, p["wd"], sc, hidden, 1.0, H, I, hidden)
+
+    t_fused_attn_ropeattn = graph_us(torch, L, stream, fused_attn)
+    t_fused_attn = graph_us(torch, L, stream, fused_attn_rot)
     t_unfused = graph_us(torch, L, stream, unfused)
     t_qkv_rope_kernel = graph_us(torch, L, stream, fused)
     t_fused_norope = graph_us(torch, L, stream, fused_split(False))
@@ -595,6 +614,7 @@ def bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream, layers=40
                 "unfused_us": round(t_unfused_attn, 1), "fused_us": round(t_fused_attn, 1),
                 "non_gemm_overhead_unfused_us": round(t_unfused_attn - t_plain_attn, 1),
                 "non_gemm_overhead_fused_us": round(t_fused_attn - t_plain_attn, 1),
+                "fused_rope_in_attention_us": round(t_fused_attn_ropeattn, 1),
                 "launches_per_step": {"plain": 5 * layers, "unfused": 1 + 8 * layers,
                                       "fused": 1 + 5 * layers}},
             "launches_per_step": {"plain": 4 * layers, "unfused": 1 + 7 * layers,

@@ -50,6 +50,7 @@ constexpr int kHd = 128;         // head dim
 constexpr int kGq = 4;           // query heads per KV head
 constexpr int kRowsPerWave = 4;  // query rows per wave (x 4 heads = 16 MFMA rows)
 constexpr int kAttnMaxSplits = 256;
+enum : int { kAttnPlain = 0, kAttnRopeAppend = 1, kAttnAppend = 2 };
 constexpr int kAttnWaves = 4;  // splits per workgroup, merged before the combine
 constexpr int kVPitch = kHd + 16;  // LDS V row pitch (bf16): 288 B, rows 8 banks apart
 
@@ -234,9 +235,13 @@ __device__ __forceinline__ void v_store(const u32x4_t (&raw)[VStage<BITS>::kStep
 // (each wave owns its LDS tile, so no workgroup barrier is needed).
 __device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-// FUSE: the decode append form (granite4_attn_decode_append); a template
+// MODE: kAttnPlain; kAttnRopeAppend (granite4_attn_decode_append: raw q, k
+// rotated here, the new K / V row appended); kAttnAppend
+// (granite4_attn_decode_append_rotated: q and k already rotated, the new row
+// appended). A template parameter so that the plain kernels carry none of
+// the append's registers.
 // parameter so that the plain kernels carry none of its registers.
-template <int BITS, int GROUP, bool FUSE>
+template <int BITS, int GROUP, int MODE>
 __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a) {
   constexpr bool kQuant = BITS != 16;
   constexpr int kNgrp = kQuant ? kHd / GROUP : 1;
@@ -306,6 +311,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
   bf16x8_t qb[4];
   u32x4_t raw[4];
   float cs[2][8], sn[2][8];
+  constexpr bool FUSE = MODE == kAttnRopeAppend;  // q rotated here
   const bool q_ok = FUSE ? (live && active && base >= 0 && base < a.ra.max_pos)
                                   : (live && active);
   {
@@ -337,7 +343,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
   __shared__ __align__(16) uint8_t mir_k[kAttnWaves][2 * kHd];
   __shared__ __align__(16) uint8_t mir_v[kAttnWaves][2 * kHd];
   __shared__ float mir_s[kAttnWaves][2][kNgrp];
-  const bool own_new = FUSE && active && base >= t_begin && base < t_end_max;
+  const bool own_new = MODE != kAttnPlain && active && base >= t_begin && base < t_end_max;
 
   // q for the MFMAs: fused, rotated at the position, done in the first tile
   // once its loads are in flight (the cos / sin wait then overlaps them).
@@ -391,13 +397,15 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
       const int l16 = lane & 15;
       const uint16_t* src = (lane < 16 ? a.ra.k : a.ra.v) + hkv * kHd + 8 * l16;
       nx = ld8(src);
-      const long long rp = base < a.ra.max_pos ? base : 0;
-      const float* cp = a.ra.cos_t + rp * 64 + 8 * (l16 & 7);
-      const float* sp = a.ra.sin_t + rp * 64 + 8 * (l16 & 7);
-      *reinterpret_cast<float4*>(ncs) = *reinterpret_cast<const float4*>(cp);
-      *reinterpret_cast<float4*>(ncs + 4) = *reinterpret_cast<const float4*>(cp + 4);
-      *reinterpret_cast<float4*>(nsn) = *reinterpret_cast<const float4*>(sp);
-      *reinterpret_cast<float4*>(nsn + 4) = *reinterpret_cast<const float4*>(sp + 4);
+      if constexpr (FUSE) {
+        const long long rp = base < a.ra.max_pos ? base : 0;
+        const float* cp = a.ra.cos_t + rp * 64 + 8 * (l16 & 7);
+        const float* sp = a.ra.sin_t + rp * 64 + 8 * (l16 & 7);
+        *reinterpret_cast<float4*>(ncs) = *reinterpret_cast<const float4*>(cp);
+        *reinterpret_cast<float4*>(ncs + 4) = *reinterpret_cast<const float4*>(cp + 4);
+        *reinterpret_cast<float4*>(nsn) = *reinterpret_cast<const float4*>(sp);
+        *reinterpret_cast<float4*>(nsn + 4) = *reinterpret_cast<const float4*>(sp + 4);
+      }
     }
     u32x4_t vraw[VStage<BITS>::kSteps];
     v_load<BITS>(vbase, prow, vraw);
@@ -428,9 +436,17 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
       const int pj = __shfl(prow, j);
       const int l16 = lane & 15;
       const bool is_k = lane < 16;
+      // kAttnAppend: k is the rotated bf16 row already (its code is that of
+      // the bf16 value, the decode append's rounding).
       float rot[8];
-      rotate8(nx, ncs, nsn, l16 < 8, rot);
-      const V8 rb = to_bf16x8(rot);
+      V8 rb = nx;
+      if constexpr (FUSE) {
+        rotate8(nx, ncs, nsn, l16 < 8, rot);
+        rb = to_bf16x8(rot);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) rot[e] = v8_get(nx, e);
+      }
       if (lane < 32) {
         if constexpr (BITS == 16) {
           st8(reinterpret_cast<uint16_t*>(is_k ? mir_k[wave] : mir_v[wave]) + 8 * l16, is_k ? rb : nx);
@@ -1017,7 +1033,7 @@ int attn_splits(int max_len) {
   return (tiles + tps - 1) / tps;
 }
 
-template <int BITS, bool FUSE>
+template <int BITS, int FUSE>
 void launch_attn_bits(const AttnArgs& a, int group, dim3 grid, hipStream_t st) {
   if constexpr (BITS == 16) {
     (void)group;
@@ -1169,32 +1185,39 @@ int granite4_attn_paged(const uint16_t* q, int rows, int Hq, int Hk, int d, floa
   const dim3 grid(Hk, a.nblk, nz);
   const hipStream_t st = stream();
   switch (bits) {
-    case 16: launch_attn_bits<16, false>(a, group, grid, st); break;
-    case 8: launch_attn_bits<8, false>(a, group, grid, st); break;
-    case 4: launch_attn_bits<4, false>(a, group, grid, st); break;
-    default: launch_attn_bits<5, false>(a, group, grid, st); break;
+    case 16: launch_attn_bits<16, kAttnPlain>(a, group, grid, st); break;
+    case 8: launch_attn_bits<8, kAttnPlain>(a, group, grid, st); break;
+    case 4: launch_attn_bits<4, kAttnPlain>(a, group, grid, st); break;
+    default: launch_attn_bits<5, kAttnPlain>(a, group, grid, st); break;
   }
   if (launch_status("granite4_attn_paged (split)") != 0) return -1;
   hipLaunchKernelGGL(attn_combine_kernel, dim3(Hq, rows), kCombineThreads, 0, st, a);
   return launch_status("granite4_attn_paged (combine)");
 }
 
-int granite4_attn_decode_append(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+}  // extern "C"
+
+namespace {
+
+template <int M>
+int attn_decode_append(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                 const float* cos_tbl, const float* sin_tbl, int max_pos,
                                 const int* d_pos, const int* d_pt, int Hq, int Hk, float scale,
                                 void* cache_k, void* cache_v, float* k_scale, float* v_scale,
-                                int bits, int group, int stride, void* scratch, uint16_t* out) {
+                                int bits, int group, int stride, void* scratch, uint16_t* out,
+                                const char* what) {
   RopeArgs ra;
   // q_rot is never written here (only the K / V units run): q stands in for it.
   if (scratch == nullptr || out == nullptr || !std::isfinite(scale) || Hq != kGq * Hk ||
       !rope_args_at_pos(ra, q, k, v, cos_tbl, sin_tbl, max_pos, d_pos, d_pt, Hq, Hk, kHd, bits,
                         bits == 16 ? kHd : group, const_cast<uint16_t*>(q), cache_k, cache_v,
                         k_scale, v_scale, stride)) {
-    std::fprintf(stderr, "granite4: granite4_attn_decode_append: invalid arguments\n");
+    std::fprintf(stderr, "granite4: %s: invalid arguments\n", what);
     return -1;
   }
   const int grp = bits == 16 ? kHd : group;
   AttnArgs a{};
+  a.q = q;  // kAttnAppend reads the rotated q here
   a.k = static_cast<const uint8_t*>(cache_k);
   a.v = static_cast<const uint8_t*>(cache_v);
   a.ksc = k_scale;
@@ -1215,15 +1238,46 @@ int granite4_attn_decode_append(const uint16_t* q, const uint16_t* k, const uint
   const dim3 grid(Hk, a.nblk, 1);
   const hipStream_t st = stream();
   switch (bits) {
-    case 16: launch_attn_bits<16, true>(a, grp, grid, st); break;
-    case 8: launch_attn_bits<8, true>(a, grp, grid, st); break;
-    case 4: launch_attn_bits<4, true>(a, grp, grid, st); break;
-    default: launch_attn_bits<5, true>(a, grp, grid, st); break;
+    case 16: launch_attn_bits<16, M>(a, grp, grid, st); break;
+    case 8: launch_attn_bits<8, M>(a, grp, grid, st); break;
+    case 4: launch_attn_bits<4, M>(a, grp, grid, st); break;
+    default: launch_attn_bits<5, M>(a, grp, grid, st); break;
   }
-  if (launch_status("granite4_attn_decode_append (split)") != 0) return -1;
+  if (launch_status(what) != 0) return -1;
   hipLaunchKernelGGL(attn_combine_kernel, dim3(Hq, 1), kCombineThreads, 0, st, a);
-  return launch_status("granite4_attn_decode_append (combine)");
+  return launch_status(what);
 }
+
+}  // namespace
+
+extern "C" {
+
+int granite4_attn_decode_append(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                const float* cos_tbl, const float* sin_tbl, int max_pos,
+                                const int* d_pos, const int* d_pt, int Hq, int Hk, float scale,
+                                void* cache_k, void* cache_v, float* k_scale, float* v_scale,
+                                int bits, int group, int stride, void* scratch, uint16_t* out) {
+  return attn_decode_append<kAttnRopeAppend>(q, k, v, cos_tbl, sin_tbl, max_pos, d_pos, d_pt, Hq,
+                                             Hk, scale, cache_k, cache_v, k_scale, v_scale, bits,
+                                             group, stride, scratch, out,
+                                             "granite4_attn_decode_append");
+}
+
+int granite4_attn_decode_append_rotated(const uint16_t* q_rot, const uint16_t* k_rot,
+                                        const uint16_t* v, int max_pos, const int* d_pos,
+                                        const int* d_pt, int Hq, int Hk, float scale,
+                                        void* cache_k, void* cache_v, float* k_scale,
+                                        float* v_scale, int bits, int group, int stride,
+                                        void* scratch, uint16_t* out) {
+  // No table is read in this form: q_rot stands in for the cos / sin
+  // pointers in the shared argument checks.
+  const float* none = reinterpret_cast<const float*>(q_rot);
+  return attn_decode_append<kAttnAppend>(q_rot, k_rot, v, none, none, max_pos, d_pos, d_pt, Hq,
+                                         Hk, scale, cache_k, cache_v, k_scale, v_scale, bits,
+                                         group, stride, scratch, out,
+                                         "granite4_attn_decode_append_rotated");
+}
+
 
 int granite4_attn_split(const uint16_t* q, const uint16_t* cache_k, const uint16_t* cache_v,
                         float scale, int Hq, int Hk, int d, int kv_base, const int* d_pos,

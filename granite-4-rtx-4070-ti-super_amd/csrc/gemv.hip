@@ -41,7 +41,7 @@ namespace g4 {
 namespace {
 
 enum : int { kProNone = 0, kProNorm = 1 };
-enum : int { kEpiOut = 0, kEpiResid = 1, kEpiSwiglu = 2 };
+enum : int { kEpiOut = 0, kEpiResid = 1, kEpiSwiglu = 2, kEpiRope = 3 };
 
 #ifndef G4_GEMV_DEPTH
 #define G4_GEMV_DEPTH 4
@@ -63,6 +63,11 @@ struct GemvArgs {
   const uint16_t* residual;  // kEpiResid (may alias o[0])
   float rs;
   int I;                  // kEpiSwiglu: act columns (w[0] gate, w[1] up)
+  // kEpiRope: segments 0 and 1 (q, k heads of 128 rows) rotated at *d_pos
+  const float* cos_t;
+  const float* sin_t;
+  int max_pos;
+  const int* d_pos;
 };
 
 __device__ __forceinline__ uint4 ld_u4_nt(const uint8_t* p) {
@@ -116,6 +121,23 @@ __device__ __forceinline__ void fp8x16_to_f32(const uint4& q, float (&f)[16]) {
 // Weight row r (0 .. kRows - 1) of the workgroup, or nullptr past the end (n:
 // its output index). swiglu: the first half gate rows, the second half the up
 // rows of the same act columns.
+// kEpiRope (kRows = 8): the rotated segments [0, seg2) go 16 blocks per head,
+// block j of a head holding dims 4j .. 4j + 3 (rows r < 4) and their RoPE
+// partners 64 + 4j .. 64 + 4j + 3 (rows r >= 4), so each rotation pair is in
+// one workgroup; the rows past seg2 (v) follow in order.
+template <int EPI, int kRows>
+__device__ __forceinline__ int out_row(const GemvArgs& a, int r) {
+  if (EPI == kEpiRope) {
+    const int nrot = a.seg2 / 8;
+    if (static_cast<int>(blockIdx.x) < nrot) {
+      const int h = blockIdx.x / 16, j = blockIdx.x % 16;
+      return h * 128 + 4 * j + (r & 3) + (r >= 4 ? 64 : 0);
+    }
+    return a.seg2 + (blockIdx.x - nrot) * kRows + r;
+  }
+  return blockIdx.x * kRows + r;
+}
+
 template <int EPI, int kRows>
 __device__ __forceinline__ const uint8_t* row_ptr(const GemvArgs& a, int r, int& n) {
   if (EPI == kEpiSwiglu) {
@@ -124,7 +146,7 @@ __device__ __forceinline__ const uint8_t* row_ptr(const GemvArgs& a, int r, int&
     if (c >= a.I) return nullptr;
     return (r < kRows / 2 ? a.w[0] : a.w[1]) + static_cast<size_t>(c) * a.K;
   }
-  const int i = blockIdx.x * kRows + r;
+  const int i = out_row<EPI, kRows>(a, r);
   n = i;
   if (i >= a.N) return nullptr;
   if (i < a.seg1) return a.w[0] + static_cast<size_t>(i) * a.K;
@@ -196,6 +218,17 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 #pragma unroll
   for (int r = 0; r < kDepth; ++r) load_row(r, buf[r]);
   __builtin_amdgcn_sched_barrier(0);
+  // kEpiRope: this thread's cos / sin (as output row threadIdx.x % 8), loaded
+  // unconditionally from a clamped position, used in the epilogue.
+  int rpos = 0;
+  float rc = 0.0f, rsn = 0.0f;
+  if (EPI == kEpiRope) {
+    rpos = *a.d_pos;
+    const int i = out_row<EPI, kRows>(a, threadIdx.x % kRows) % 128;
+    const long long cp = static_cast<long long>(min(max(rpos, 0), a.max_pos - 1)) * 64 + (i & 63);
+    rc = a.cos_t[cp];
+    rsn = a.sin_t[cp];
+  }
   if (PRO == kProNorm) {
     double ss = 0.0;
 #pragma unroll
@@ -275,8 +308,23 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     a.o[0][c] = static_cast<uint16_t>(f32_to_bf16(silu_mul(a.s[0] * gsum, a.s[1] * usum)));
     return;
   }
-  const int n = blockIdx.x * kRows + r;
+  const int n = out_row<EPI, kRows>(a, r);
   if (n >= a.N) return;
+  if (EPI == kEpiRope && n < a.seg2) {
+    // y = bf16(s tot) for this row and its partner (r ^ 4), then the append
+    // kernels' rotation (rotate8: a c + b' s, b' the partner, negated in the
+    // first half of the head) and bf16. A position outside the table leaves
+    // the output unwritten, as the append kernels leave q_rot.
+    const int seg = n < a.seg1 ? 0 : 1;
+    const int base = seg == 0 ? 0 : a.seg1;
+    const int p = r ^ 4;
+    const float tp = (s_part[0][p] + s_part[1][p]) + (s_part[2][p] + s_part[3][p]);
+    const float ya = bf16_to_f32(f32_to_bf16(a.s[seg] * tot));
+    const float yp = bf16_to_f32(f32_to_bf16(a.s[seg] * tp));
+    const float b = r < 4 ? -yp : yp;
+    if (rpos >= 0 && rpos < a.max_pos) a.o[seg][n - base] = static_cast<uint16_t>(f32_to_bf16(ya * rc + b * rsn));
+    return;
+  }
   if (EPI == kEpiResid) {
     const float y = a.s[0] * tot;
     const float res = __uint_as_float(static_cast<uint32_t>(a.residual[n]) << 16);
@@ -399,7 +447,7 @@ template <int PRO, int EPI>
 int launch_gemv(const GemvArgs& a, const char* what) {
   const int ch = (a.K / 4 + 1023) / 1024;
   const long long outputs = EPI == kEpiSwiglu ? 2LL * a.I : a.N;
-  const int rows = outputs >= 16LL * 2 * kCUs ? 16 : 8;
+  const int rows = EPI != kEpiRope && outputs >= 16LL * 2 * kCUs ? 16 : 8;
   const unsigned grid = static_cast<unsigned>(EPI == kEpiSwiglu ? (a.I + rows / 2 - 1) / (rows / 2)
                                                                  : (a.N + rows - 1) / rows);
   const hipStream_t st = stream();
@@ -446,6 +494,47 @@ int gemv_out(int pro, const uint16_t* x, const uint16_t* gamma, float eps,
   a.inv_k = (K & (K - 1)) == 0 ? 1.0 / K : 0.0;
   return pro == kProNorm ? launch_gemv<kProNorm, kEpiOut>(a, what)
                          : launch_gemv<kProNone, kEpiOut>(a, what);
+}
+
+// q|k|v with RoPE on q and k (Hq, Hk heads of 128): kRows 8, head-paired rows.
+int gemv_qkv_rope(int pro, const uint16_t* x, const uint16_t* gamma, float eps,
+                  const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, float sq, float sk,
+                  float sv, const float* cos_t, const float* sin_t, int max_pos, const int* d_pos,
+                  int Hq, int Hk, int K, uint16_t* q_rot, uint16_t* k_rot, uint16_t* v,
+                  const char* what) {
+  if (x == nullptr || !al16(x) || !gemv_k_ok(K) || Hq <= 0 || Hk <= 0 || cos_t == nullptr ||
+      sin_t == nullptr || max_pos <= 0 || d_pos == nullptr || wq == nullptr || wk == nullptr ||
+      wv == nullptr || !al16(wq) || !al16(wk) || !al16(wv) || q_rot == nullptr ||
+      k_rot == nullptr || v == nullptr || !std::isfinite(sq) || !std::isfinite(sk) ||
+      !std::isfinite(sv) || (pro == kProNorm && (gamma == nullptr || !al16(gamma) || !std::isfinite(eps))) ||
+      static_cast<long long>(Hq + 2 * Hk) * 128 * K >= (1LL << 40)) {
+    std::fprintf(stderr, "granite4: %s: invalid arguments\n", what);
+    return -1;
+  }
+  GemvArgs a{};
+  a.x = x;
+  a.gamma = gamma;
+  a.eps = eps;
+  a.w[0] = wq;
+  a.w[1] = wk;
+  a.w[2] = wv;
+  a.s[0] = sq;
+  a.s[1] = sk;
+  a.s[2] = sv;
+  a.o[0] = q_rot;
+  a.o[1] = k_rot;
+  a.o[2] = v;
+  a.seg1 = Hq * 128;
+  a.seg2 = (Hq + Hk) * 128;
+  a.N = (Hq + 2 * Hk) * 128;
+  a.K = K;
+  a.inv_k = (K & (K - 1)) == 0 ? 1.0 / K : 0.0;
+  a.cos_t = cos_t;
+  a.sin_t = sin_t;
+  a.max_pos = max_pos;
+  a.d_pos = d_pos;
+  return pro == kProNorm ? launch_gemv<kProNorm, kEpiRope>(a, what)
+                         : launch_gemv<kProNone, kEpiRope>(a, what);
 }
 
 int gemv_swiglu(int pro, const uint16_t* x, const uint16_t* gamma, float eps, const uint8_t* wg,
@@ -532,6 +621,26 @@ int granite4_gemv_rmsnorm_qkv(const uint16_t* d_x, const uint16_t* d_gamma, floa
   uint16_t* const o[3] = {d_q, d_k, d_v};
   const int n[3] = {Nq, Nk, Nv};
   return gemv_out(kProNorm, d_x, d_gamma, eps, w, s, o, n, K, "granite4_gemv_rmsnorm_qkv");
+}
+
+int granite4_gemv_qkv_rope(const uint16_t* d_a, const uint8_t* d_wq, const uint8_t* d_wk,
+                           const uint8_t* d_wv, float sq, float sk, float sv, const float* cos_tbl,
+                           const float* sin_tbl, int max_pos, const int* d_pos, int Hq, int Hk,
+                           int K, uint16_t* d_q_rot, uint16_t* d_k_rot, uint16_t* d_v) {
+  return gemv_qkv_rope(kProNone, d_a, nullptr, 0.0f, d_wq, d_wk, d_wv, sq, sk, sv, cos_tbl,
+                       sin_tbl, max_pos, d_pos, Hq, Hk, K, d_q_rot, d_k_rot, d_v,
+                       "granite4_gemv_qkv_rope");
+}
+
+int granite4_gemv_rmsnorm_qkv_rope(const uint16_t* d_x, const uint16_t* d_gamma, float eps,
+                                   const uint8_t* d_wq, const uint8_t* d_wk, const uint8_t* d_wv,
+                                   float sq, float sk, float sv, const float* cos_tbl,
+                                   const float* sin_tbl, int max_pos, const int* d_pos, int Hq,
+                                   int Hk, int K, uint16_t* d_q_rot, uint16_t* d_k_rot,
+                                   uint16_t* d_v) {
+  return gemv_qkv_rope(kProNorm, d_x, d_gamma, eps, d_wq, d_wk, d_wv, sq, sk, sv, cos_tbl,
+                       sin_tbl, max_pos, d_pos, Hq, Hk, K, d_q_rot, d_k_rot, d_v,
+                       "granite4_gemv_rmsnorm_qkv_rope");
 }
 
 int granite4_kernel_silu_gate_up(const uint8_t* d_wg, const uint8_t* d_wu, const uint16_t* d_x,

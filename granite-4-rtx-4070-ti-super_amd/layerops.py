@@ -95,6 +95,7 @@ _SIG = {
     "granite4_attn_paged": [P, I, I, I, I, F, P, P, P, P, I, I, I, I, P, P, P, P, I, I, P, P],
     "granite4_prefill_attn": [P, I, I, I, I, F, P, P, P, P, I, I, I, I, P, I, P],
     "granite4_attn_decode_append": [P, P, P, P, P, I, P, P, I, I, F, P, P, P, P, I, I, I, P, P],
+    "granite4_attn_decode_append_rotated": [P, P, P, I, P, P, I, I, F, P, P, P, P, I, I, I, P, P],
     "granite4_prefill_attention": [P, P, P, F, I, I, I, I, I, I, P, P, P, P, P, I, P, P, I, P, I,
                                    I],
     "granite4_gemm_fp8": [I, P, I, P, P, I, I, I, _c.POINTER(GemmEpilogue)],
@@ -139,6 +140,8 @@ _SIG = {
     "granite4_gemv_fp8w_resid": [P, P, F, P, F, I, I, P],
     "granite4_gemv_qkv": [P, P, P, P, F, F, F, I, I, I, I, P, P, P],
     "granite4_gemv_rmsnorm_qkv": [P, P, F, P, P, P, F, F, F, I, I, I, I, P, P, P],
+    "granite4_gemv_rmsnorm_qkv_rope": [P, P, F, P, P, P, F, F, F, P, P, I, P, I, I, I, P, P, P],
+    "granite4_gemv_qkv_rope": [P, P, P, P, F, F, F, P, P, I, P, I, I, I, P, P, P],
     "granite4_kernel_silu_gate_up": [P, P, P, F, F, I, I, P],
     "granite4_gemv_rmsnorm_silu_gate_up": [P, P, F, P, P, F, F, I, I, P],
     "granite4_gemv_rmsnorm_qkv_rope_append": [P, P, F, P, P, P, F, F, F, P, P, I, P, P, I, I, I, I,

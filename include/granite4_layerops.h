@@ -527,6 +527,41 @@ int granite4_attn_decode_append(const uint16_t* q, const uint16_t* k, const uint
                                 void* cache_k, void* cache_v, float* k_scale, float* v_scale,
                                 int bits, int group, int stride, void* scratch, uint16_t* out);
 
+/* Replaces: granite4_kernel_rmsnorm + the q / k / v GEMV + the RoPE of the
+ * decode step (forward_gpu.cu:2115-2131, rope_at_pos_qk_kernel :857-886):
+ * q_rot and k_rot are the q and k projections (Hq / Hk heads of 128 rows)
+ * rotated at *d_pos, v the v projection; each rotation pair (dims i, i + 64)
+ * is computed in one workgroup from the bf16 projections, with the append
+ * kernels' products and roundings, so the outputs are bit-identical to the
+ * GEMV followed by the rotation. A position outside [0, max_pos) leaves
+ * q_rot and k_rot unwritten (as granite4_rope_append_at_pos leaves q_rot). */
+int granite4_gemv_rmsnorm_qkv_rope(const uint16_t* d_x, const uint16_t* d_gamma, float eps,
+                                   const uint8_t* d_wq, const uint8_t* d_wk, const uint8_t* d_wv,
+                                   float sq, float sk, float sv, const float* cos_tbl,
+                                   const float* sin_tbl, int max_pos, const int* d_pos, int Hq,
+                                   int Hk, int K, uint16_t* d_q_rot, uint16_t* d_k_rot,
+                                   uint16_t* d_v);
+/* The same without the norm prologue: d_a is the GEMV input itself. */
+int granite4_gemv_qkv_rope(const uint16_t* d_a, const uint8_t* d_wq, const uint8_t* d_wk,
+                           const uint8_t* d_wv, float sq, float sk, float sv, const float* cos_tbl,
+                           const float* sin_tbl, int max_pos, const int* d_pos, int Hq, int Hk,
+                           int K, uint16_t* d_q_rot, uint16_t* d_k_rot, uint16_t* d_v);
+
+/* Replaces: the KV append of the decode step (kv_append_*_kernel,
+ * forward_gpu.cu:104-277) followed by granite4_attn_split (rows = 1), in one
+ * attention launch, for q and k already rotated (granite4_gemv_rmsnorm_qkv_rope):
+ * the split holding *d_pos quantises k_rot and v into that position's pool
+ * row (the decode append's codes of the bf16 rotated K) and attends with it.
+ * Bit-identical to granite4_kernel_kv_append*_batched at *d_pos then
+ * granite4_attn_paged. A position outside [0, max_pos) writes V only, as the
+ * append kernels do. scratch: granite4_attn_split_scratch_bytes(Hq, 1, stride). */
+int granite4_attn_decode_append_rotated(const uint16_t* q_rot, const uint16_t* k_rot,
+                                        const uint16_t* v, int max_pos, const int* d_pos,
+                                        const int* d_pt, int Hq, int Hk, float scale,
+                                        void* cache_k, void* cache_v, float* k_scale,
+                                        float* v_scale, int bits, int group, int stride,
+                                        void* scratch, uint16_t* out);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 

@@ -189,3 +189,74 @@ def test_rmsnorm_qkv_rope_append_fused(bits, group):
         np.testing.assert_array_equal(a, b)
     row = int(host(pt)[5000])
     assert np.any(outs[1][1].reshape(Hk, stride, -1)[:, row] != 0)  # the row was written
+
+
+def _fill_pool(arena, seed):
+    """Seeded pool contents in the format's range: bf16 N(0,1) values, or
+    random codes with positive scales."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    if arena.bits == 16:
+        vals = torch.randn(arena.k.numel() // 2, generator=g, device="cuda").to(torch.bfloat16)
+        arena.k.copy_(vals.view(torch.uint8).view(arena.k.shape))
+        vals = torch.randn(arena.v.numel() // 2, generator=g, device="cuda").to(torch.bfloat16)
+        arena.v.copy_(vals.view(torch.uint8).view(arena.v.shape))
+        return
+    arena.k.copy_(torch.randint(0, 256, arena.k.shape, generator=g, device="cuda").to(torch.uint8))
+    arena.v.copy_(torch.randint(0, 256, arena.v.shape, generator=g, device="cuda").to(torch.uint8))
+    if arena.bits == 8:  # int8 codes stay within +-127
+        arena.k[arena.k == 0x80] = 0x81
+        arena.v[arena.v == 0x80] = 0x81
+    arena.k_scale.copy_(torch.rand(arena.k_scale.shape, generator=g, device="cuda") * 0.02)
+    arena.v_scale.copy_(torch.rand(arena.v_scale.shape, generator=g, device="cuda") * 0.02)
+
+
+@pytest.mark.parametrize("pos_v,max_pos", [(5000, 8192), (4095, 8192), (5000, 4096)])
+@pytest.mark.parametrize("bits,group", [(16, 128), (8, 128), (5, 32), (4, 64)])
+def test_rmsnorm_qkv_rope_then_append_attention(bits, group, pos_v, max_pos):
+    """The decode step's q|k|v side in two launches: granite4_gemv_rmsnorm_qkv_rope
+    (RoPE in the GEMV epilogue) then granite4_attn_decode_append_rotated (the
+    append in the attention). q_rot, the attention output and the whole pool
+    bit-identical to granite4_gemv_rmsnorm_qkv + granite4_rope_append_at_pos +
+    granite4_attn_paged; also at a position past the RoPE table (q_rot and K
+    not written, V appended)."""
+    print(f"qkv rope + append attention bits={bits} group={group} pos={pos_v} "
+          f"max_pos={max_pos}", flush=True)
+    K, Hq, Hk, D = 4096, 32, 8, 128
+    x = dev(ol.normal_bf16(0xD1, 0.0, 1.0, K))
+    gamma = dev(ol.normal_bf16(0xD2, 1.0, 0.1, K))
+    Wq, Wk, Wv = (dev(ol.fp8_codes(0xD3 + i, (n, K), std=0.5)) for i, n in
+                  enumerate((Hq * D, Hk * D, Hk * D)))
+    sc = (0.004, 0.005, 0.006)
+    cos_t, sin_t = ol.rope_tables(1e7, D, max_pos)
+    dcos, dsin = dev(cos_t), dev(sin_t)
+    stride = 8192
+    pos = dev(np.array([pos_v], np.int32))
+    pt = dev(np.random.default_rng(7).permutation(stride).astype(np.int32))
+    scratch = torch.empty(L.call_size("granite4_attn_split_scratch_bytes", Hq, 1, stride),
+                          dtype=torch.uint8, device="cuda")
+    outs = []
+    for fused in (False, True):
+        arena = L.KvArena(bits, Hk, stride, group=group)
+        _fill_pool(arena, 0xD9)
+        pool = [arena.k, arena.v, arena.k_scale, arena.v_scale]
+        q_rot = torch.zeros(Hq * D, dtype=torch.int16, device="cuda")
+        out = empty16(Hq * D)
+        if fused:
+            k_rot, v = empty16(Hk * D), empty16(Hk * D)
+            L.call("granite4_gemv_rmsnorm_qkv_rope", x, gamma, 1e-5, Wq, Wk, Wv, *sc, dcos, dsin,
+                   max_pos, pos, Hq, Hk, K, q_rot, k_rot, v)
+            L.call("granite4_attn_decode_append_rotated", q_rot, k_rot, v, max_pos, pos, pt, Hq,
+                   Hk, 1.0 / 16, *pool, bits, group, stride, scratch, out)
+        else:
+            q, k, v = empty16(Hq * D), empty16(Hk * D), empty16(Hk * D)
+            L.call("granite4_gemv_rmsnorm_qkv", x, gamma, 1e-5, Wq, Wk, Wv, *sc, Hq * D, Hk * D,
+                   Hk * D, K, q, k, v)
+            L.call("granite4_rope_append_at_pos", q, k, v, dcos, dsin, max_pos, pos, pt, Hq, Hk, D,
+                   bits, group, q_rot, *pool, stride)
+            L.call("granite4_attn_paged", q_rot, 1, Hq, Hk, D, 1.0 / 16, *pool, bits, group,
+                   stride, 0, pos, pt, None, None, 0, 0, scratch, out)
+        outs.append([host(q_rot), host(out)] + [host(t) for t in pool])
+    for a, b in zip(*outs):
+        np.testing.assert_array_equal(a, b)
+    if pos_v < max_pos:
+        assert np.any(outs[1][0] != 0)  # q_rot was written
