@@ -206,6 +206,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   // by a round trip.
   float av[kChunks][16];
   uint4 xr[kChunks][2], gr[kChunks][2];
+  // kEpiRope's position, loaded first as a vector load (a scalar load would
+  // be scheduled after the weight rows, and its wait would hold the norm).
+  int rpos = 0;
+  if (EPI == kEpiRope) {
+    int z;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+    rpos = a.d_pos[z];
+  }
 #pragma unroll
   for (int c = 0; c < kChunks; ++c) {
     xr[c][0] = *reinterpret_cast<const uint4*>(a.x + koff[c]);
@@ -220,10 +228,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   __builtin_amdgcn_sched_barrier(0);
   // kEpiRope: this thread's cos / sin (as output row threadIdx.x % 8), loaded
   // unconditionally from a clamped position, used in the epilogue.
-  int rpos = 0;
   float rc = 0.0f, rsn = 0.0f;
   if (EPI == kEpiRope) {
-    rpos = *a.d_pos;
     const int i = out_row<EPI, kRows>(a, threadIdx.x % kRows) % 128;
     const long long cp = static_cast<long long>(min(max(rpos, 0), a.max_pos - 1)) * 64 + (i & 63);
     rc = a.cos_t[cp];
