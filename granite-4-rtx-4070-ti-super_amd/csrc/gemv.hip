@@ -228,6 +228,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   __builtin_amdgcn_sched_barrier(0);
   // kEpiRope: this thread's cos / sin (as output row threadIdx.x % 8), loaded
   // unconditionally from a clamped position, used in the epilogue.
+  // kEpiResid: the residual of this thread's output row (threads < kRows),
+  // loaded now so the epilogue does not wait a round trip for it.
+  uint32_t res_bits = 0;
+  if (EPI == kEpiResid) {
+    const int n = min(static_cast<int>(blockIdx.x * kRows + threadIdx.x % kRows), a.N - 1);
+    res_bits = a.residual[n];
+  }
   float rc = 0.0f, rsn = 0.0f;
   if (EPI == kEpiRope) {
     const int i = out_row<EPI, kRows>(a, threadIdx.x % kRows) % 128;
@@ -333,7 +340,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   }
   if (EPI == kEpiResid) {
     const float y = a.s[0] * tot;
-    const float res = __uint_as_float(static_cast<uint32_t>(a.residual[n]) << 16);
+    const float res = __uint_as_float(res_bits << 16);
     a.o[0][n] = static_cast<uint16_t>(f32_to_bf16(res + a.rs * y));
   } else {
     const int seg = n < a.seg1 ? 0 : (n < a.seg2 ? 1 : 2);
