@@ -590,6 +590,30 @@ def bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream, layers=40
                    sc, sc, I, H, act)
             L.call("granite4_gemv_fp8w_resid", act, p["wd"], sc, hidden, 1.0, H, I, hidden)
 
+    def fused_attn_parts(rope_gemv):
+        # breakdown: the fused GEMVs with plain attention (no KV append);
+        # rope_gemv selects the q|k|v GEMV with the RoPE epilogue
+        def step():
+            L.call("granite4_embed_at_pos", toks, pos, emb, VOCAB, H, 1.0, hidden)
+            for p in per:
+                if rope_gemv:
+                    L.call("granite4_gemv_rmsnorm_qkv_rope", hidden, gamma, 1e-5, p["wq"],
+                           p["wk"], p["wv"], sc, sc, sc, cos_t, sin_t, 65536, pos, HQ, HK, H,
+                           q_rot, k_rot, v)
+                    attn(p, q_rot)
+                else:
+                    L.call("granite4_gemv_rmsnorm_qkv", hidden, gamma, 1e-5, p["wq"], p["wk"],
+                           p["wv"], sc, sc, sc, HQ * D, HK * D, HK * D, H, q, k, v)
+                    attn(p, q)
+                L.call("granite4_gemv_fp8w_resid", attn_out, p["wo"], sc, hidden, 1.0, H,
+                       HQ * D, hidden)
+                L.call("granite4_gemv_rmsnorm_silu_gate_up", hidden, gamma, 1e-5, p["wg"],
+                       p["wu"], sc, sc, I, H, act)
+                L.call("granite4_gemv_fp8w_resid", act, p["wd"], sc, hidden, 1.0, H, I, hidden)
+        return step
+
+    t_parts_norope = graph_us(torch, L, stream, fused_attn_parts(False))
+    t_parts_rope = graph_us(torch, L, stream, fused_attn_parts(True))
     t_fused_attn_ropeattn = graph_us(torch, L, stream, fused_attn)
     t_fused_attn = graph_us(torch, L, stream, fused_attn_rot)
     t_unfused = graph_us(torch, L, stream, unfused)
@@ -615,6 +639,10 @@ def bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream, layers=40
                 "non_gemm_overhead_unfused_us": round(t_unfused_attn - t_plain_attn, 1),
                 "non_gemm_overhead_fused_us": round(t_fused_attn - t_plain_attn, 1),
                 "fused_rope_in_attention_us": round(t_fused_attn_ropeattn, 1),
+                "breakdown_us": {
+                    "norm_swiglu_resid_embed": round(t_parts_norope - t_plain_attn, 1),
+                    "rope_epilogue": round(t_parts_rope - t_parts_norope, 1),
+                    "kv_append_in_attention": round(t_fused_attn - t_parts_rope, 1)},
                 "launches_per_step": {"plain": 5 * layers, "unfused": 1 + 8 * layers,
                                       "fused": 1 + 5 * layers}},
             "launches_per_step": {"plain": 4 * layers, "unfused": 1 + 7 * layers,

@@ -154,6 +154,27 @@ __device__ __forceinline__ const uint8_t* row_ptr(const GemvArgs& a, int r, int&
   return a.w[2] + static_cast<size_t>(i - a.seg2) * a.K;
 }
 
+// Row r's offset (in rows) from row 0 within its segment when every row of
+// the workgroup lies in one segment: r (swiglu: r for the gate half and
+// r - kRows / 2 for the up half, each from its own matrix, so that case
+// keeps the general path), or the head-paired kEpiRope order.
+template <int EPI, int kRows>
+__device__ __forceinline__ int row_offset(int r) {
+  if (EPI == kEpiRope) return (r & 3) + (r >= 4 ? 64 : 0);
+  return r;
+}
+
+template <int EPI, int kRows>
+__device__ __forceinline__ bool rows_in_one_segment(const GemvArgs& a) {
+  if (EPI == kEpiSwiglu) return false;
+  const int first = out_row<EPI, kRows>(a, 0);
+  const int last = out_row<EPI, kRows>(a, kRows - 1);
+  if (last >= a.N || last - first != row_offset<EPI, kRows>(kRows - 1)) return false;
+  const int sf = first < a.seg1 ? 0 : (first < a.seg2 ? 1 : 2);
+  const int sl = last < a.seg1 ? 0 : (last < a.seg2 ? 1 : 2);
+  return sf == sl;
+}
+
 // Workgroup barrier for LDS exchanges only (waits for this wave's LDS
 // operations, not for its weight loads in flight).
 __device__ __forceinline__ void lds_barrier() {
@@ -182,11 +203,26 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   const uint8_t* rows[kRows];
   int ns[kRows];
   bool live[kRows];
+  if (rows_in_one_segment<EPI, kRows>(a)) {
+    // Every row of the workgroup exists and lies in one weight segment (all
+    // but the last workgroup of a segment): row r at a fixed offset from the
+    // first, straight-line address arithmetic.
+    int n0;
+    const uint8_t* p0 = row_ptr<EPI, kRows>(a, 0, n0);
 #pragma unroll
-  for (int r = 0; r < kRows; ++r) {
-    rows[r] = row_ptr<EPI, kRows>(a, r, ns[r]);
-    live[r] = rows[r] != nullptr;
-    if (!live[r]) rows[r] = a.w[0];
+    for (int r = 0; r < kRows; ++r) {
+      const int off = row_offset<EPI, kRows>(r);
+      rows[r] = p0 + static_cast<size_t>(off) * a.K;
+      ns[r] = n0 + off;
+      live[r] = true;
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+      rows[r] = row_ptr<EPI, kRows>(a, r, ns[r]);
+      live[r] = rows[r] != nullptr;
+      if (!live[r]) rows[r] = a.w[0];
+    }
   }
 
   // Rows of weights stream in order, kDepth rows in flight; the 4 waves read
