@@ -250,6 +250,11 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
   __shared__ __align__(16) uint16_t vl_all[kAttnWaves][kTile * kVPitch];
   __shared__ float ksc_all[kAttnWaves][kTile * kNgrp], vsc_all[kAttnWaves][kTile * kNgrp];
 
+  // The kernel arguments of the prologue fetched together (one scalar-cache
+  // miss instead of a chain of them before the position is even requested).
+  asm volatile("" ::"s"(a.d_pos), "s"(a.d_pt), "s"(a.row_pos), "s"(a.row_pt), "s"(a.rows),
+               "s"(a.stride), "s"(a.tps), "s"(a.splits), "s"(a.window), "s"(a.kv_base),
+               "s"(a.q), "s"(a.k), "s"(a.v), "s"(a.Hq));
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   uint16_t* vl = vl_all[wave];
   float* ksc_l = ksc_all[wave];
@@ -260,12 +265,20 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
   const int per = a.row_pos != nullptr ? 1 : kRowsPerWave;
   const int r0 = blockIdx.z * per;
   const int nr = min(per, a.rows - r0);
-  const int base = a.row_pos != nullptr ? 0 : (a.d_pos != nullptr ? *a.d_pos : a.kv_base);
+  // The position, the row's position and the row's page table, loaded at
+  // once and unconditionally (absent ones read the q buffer and are unused),
+  // so that no wait for one sits in a branch ahead of the others.
+  const void* qv = a.q;
+  const int pos_raw = *(a.d_pos != nullptr ? a.d_pos : static_cast<const int*>(qv));
+  const int rpos_raw = *(a.row_pos != nullptr ? a.row_pos + r0 : static_cast<const int*>(qv));
+  const int* const rpt_raw =
+      *(a.row_pt != nullptr ? a.row_pt + r0 : static_cast<const int* const*>(qv));
+  const int base = a.row_pos != nullptr ? 0 : (a.d_pos != nullptr ? pos_raw : a.kv_base);
   // Causal length, clamped to the arena (a position read from device memory
   // never sends the page-table reads past the arena's positions).
   // Multi-sequence rows (row_pos) take one row per wave, so only rr = 0 is
   // ever asked for there: one scalar load.
-  const int row_pos0 = a.row_pos != nullptr ? a.row_pos[r0] : 0;
+  const int row_pos0 = a.row_pos != nullptr ? rpos_raw : 0;
   auto row_len = [&](int rr) {
     const int len = a.row_pos != nullptr ? row_pos0 + 1 : base + r0 + rr + 1;
     return min(max(len, 0), a.stride);
@@ -283,7 +296,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
   const int t_end_max = min(kv_max, t_begin + span);
   const bool active = split < a.splits && t_begin < kv_max && t_end_max > lo_min;
   const int t_first = max(t_begin, (lo_min / kTile) * kTile);
-  const int* pt = a.row_pt != nullptr ? a.row_pt[r0] : a.d_pt;
+  const int* pt = a.row_pt != nullptr ? rpt_raw : a.d_pt;
   const g4_global_i32* ptg = (const g4_global_i32*)pt;  // global loads, not flat
 
   const uint8_t* kbase = a.k + static_cast<size_t>(hkv) * a.stride * kKb;

@@ -187,6 +187,11 @@ template <int PRO, int EPI, int kChunks, int kRows>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   __shared__ double s_ss[4];
   __shared__ float s_part[4][kRows];
+  // Every kernel argument the prologue needs, fetched together: otherwise the
+  // compiler loads them where each is first used, one dependent scalar-cache
+  // miss after another before the first weight load.
+  asm volatile("" ::"s"(a.N), "s"(a.K), "s"(a.seg1), "s"(a.seg2), "s"(a.I), "s"(a.w[0]),
+               "s"(a.w[1]), "s"(a.w[2]), "s"(a.x), "s"(a.gamma), "s"(a.d_pos));
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int K = a.K;
   const int kq = K / 4;                 // bytes of each row this wave reads
@@ -203,7 +208,18 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   const uint8_t* rows[kRows];
   int ns[kRows];
   bool live[kRows];
-  if (rows_in_one_segment<EPI, kRows>(a)) {
+  if (EPI == kEpiSwiglu && static_cast<int>(blockIdx.x + 1) * (kRows / 2) <= a.I) {
+    // Every act column of the workgroup exists: gate rows c0 .. c0 + kRows / 2
+    // - 1, then the same up rows.
+    const int c0 = blockIdx.x * (kRows / 2);
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+      const int c = c0 + r % (kRows / 2);
+      rows[r] = (r < kRows / 2 ? a.w[0] : a.w[1]) + static_cast<size_t>(c) * a.K;
+      ns[r] = c;
+      live[r] = true;
+    }
+  } else if (rows_in_one_segment<EPI, kRows>(a)) {
     // Every row of the workgroup exists and lies in one weight segment (all
     // but the last workgroup of a segment): row r at a fixed offset from the
     // first, straight-line address arithmetic.
