@@ -273,6 +273,11 @@ def main():
         result_extra["gemm_fused"] = bench_gemm(torch, L, gen, timed, work, args)
         log(json.dumps(result_extra["gemm_fused"]))
 
+    log("config 1 with the decode GEMVs: non-GEMM overhead of the fused batch-1 decode step")
+    result_extra["decode_T1_gemv"] = bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma,
+                                                       stream)
+    log(json.dumps(result_extra["decode_T1_gemv"]))
+
     log("bandwidth probe (achievable read / copy rate on this device)")
     result_extra["probe"] = bench_probe(torch, L, stream, timed)
     log(json.dumps(result_extra["probe"]))
@@ -307,7 +312,12 @@ def main():
                      "traffic": SWIGLU_FP8_T512_TRAFFIC},
         "cpu_baseline": cpu,
         "measured_probe_GBps": result_extra["probe"],
-        "decode_us_per_step": decode["graph_us_per_step"],
+        "decode_us_per_step": result_extra["decode_T1_gemv"]["with_attention"]["fused_us"],
+        "decode_non_gemm_overhead_us": {
+            "with_attention": result_extra["decode_T1_gemv"]["with_attention"][
+                "non_gemm_overhead_fused_us"],
+            "gemvs_only": result_extra["decode_T1_gemv"]["non_gemm_overhead_fused_us"],
+            "standalone_ops_graph_us": decode["graph_us_per_step"]},
         "detail": result_extra,
     }
     print(json.dumps(line), flush=True)
