@@ -25,6 +25,7 @@
 #include "granite4_layerops.h"
 #include "rope_unit.h"
 
+#include <cstdlib>
 #include <map>
 #include <mutex>
 
@@ -63,6 +64,35 @@ __global__ __launch_bounds__(kBlock) void rope_append_kernel(RopeArgs a) {
   const int r = static_cast<int>(unit / static_cast<unsigned>(a.units_per_row));
   const int u = static_cast<int>(unit - static_cast<unsigned>(r) * static_cast<unsigned>(a.units_per_row));
   rope_unit<BITS, GROUP>(a, r, u, lane16, [&](const uint16_t* head) { return ld8_nt(head + 8 * lane16); });
+}
+
+// One workgroup per token row (units_per_row <= 16 UPL): lane group g owns
+// units g, g + 16, ... of the row. The row's position and arena row are
+// loaded once, then every head row of the group (UPL 16-byte loads per lane
+// in flight together), then the row's cos / sin; the arithmetic is
+// unit_finish's, so the bytes written equal rope_append_kernel's. Measured
+// against one unit per lane group (T=8192, K5V4 group 32): more loads in
+// flight per lane instead of one dependent round trip per unit.
+template <int BITS, int GROUP, int UPL>
+__global__ __launch_bounds__(kBlock) void rope_append_row_kernel(RopeArgs a) {
+  const int lane16 = threadIdx.x & 15, grp = threadIdx.x >> 4;
+  const int r = blockIdx.x;
+  const int nu = a.units_per_row;
+  const int rp = rope_pos(a, r);
+  const int row = a.has_kv ? arena_row(a, r) : -1;
+  V8 x[UPL];
+#pragma unroll
+  for (int j = 0; j < UPL; ++j) {
+    const int u = min(grp + 16 * j, nu - 1);
+    x[j] = ld8_nt(unit_src(a, r, u) + 8 * lane16);
+  }
+  float cs[8], sn[8];
+  unit_trig(a, rp, lane16, cs, sn);
+#pragma unroll
+  for (int j = 0; j < UPL; ++j) {
+    const int u = grp + 16 * j;
+    if (u < nu) unit_finish<BITS, GROUP>(a, r, u, lane16, x[j], cs, sn, rp, row);
+  }
 }
 
 // Any head dim (even, <= 1024; quantised forms one scale per row): one
@@ -134,6 +164,25 @@ __global__ __launch_bounds__(kBlock) void rope_append_generic_kernel(RopeArgs a)
   }
 }
 
+template <int BITS, int GROUP>
+void launch_row_kernel(const RopeArgs& a, int upl) {
+  const hipStream_t st = stream();
+  const dim3 grid(static_cast<unsigned>(a.rows));
+  switch (upl) {
+    case 1: hipLaunchKernelGGL((rope_append_row_kernel<BITS, GROUP, 1>), grid, kBlock, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((rope_append_row_kernel<BITS, GROUP, 2>), grid, kBlock, 0, st, a); break;
+    case 3: hipLaunchKernelGGL((rope_append_row_kernel<BITS, GROUP, 3>), grid, kBlock, 0, st, a); break;
+    default: hipLaunchKernelGGL((rope_append_row_kernel<BITS, GROUP, 4>), grid, kBlock, 0, st, a); break;
+  }
+}
+
+template <int BITS>
+void launch_row_bits(const RopeArgs& a, int group, int upl) {
+  if (BITS == 16 || group == 128) launch_row_kernel<BITS, 128>(a, upl);
+  else if (group == 64) launch_row_kernel<BITS, 64>(a, upl);
+  else launch_row_kernel<BITS, 32>(a, upl);
+}
+
 template <int BITS>
 void launch_fast_bits(const RopeArgs& a, int group, unsigned grid) {
   const hipStream_t st = stream();
@@ -143,6 +192,14 @@ void launch_fast_bits(const RopeArgs& a, int group, unsigned grid) {
 }
 
 }  // namespace
+
+// Per-token workgroups (rope_append_row_kernel) or one unit per lane group
+// (rope_append_kernel); both write the same bytes. G4_ROPE_ROW_KERNEL=0 in
+// the environment selects the latter (A/B measurements).
+const bool g_rope_row_kernel = [] {
+  const char* e = std::getenv("G4_ROPE_ROW_KERNEL");
+  return e == nullptr || e[0] != '0';
+}();
 
 // Validated launch of the fused kernel (d == 128) or the generic one.
 int launch_rope_append(RopeArgs a, int bits, int group, const char* what) {
@@ -156,6 +213,17 @@ int launch_rope_append(RopeArgs a, int bits, int group, const char* what) {
     }
     const long long blocks = (units + (kBlock / 16) - 1) / (kBlock / 16);
     const unsigned grid = static_cast<unsigned>(blocks);
+    const int upl = (a.units_per_row + 15) / 16;
+    if (g_rope_row_kernel && upl <= 4) {
+      switch (bits) {
+        case 16: launch_row_bits<16>(a, 128, upl); break;
+        case 8: launch_row_bits<8>(a, group, upl); break;
+        case 4: launch_row_bits<4>(a, group, upl); break;
+        case 5: launch_row_bits<5>(a, group, upl); break;
+        default: return -1;
+      }
+      return launch_status(what);
+    }
     switch (bits) {
       case 16: launch_fast_bits<16>(a, 128, grid); break;
       case 8: launch_fast_bits<8>(a, group, grid); break;

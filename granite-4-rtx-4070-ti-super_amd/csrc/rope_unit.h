@@ -166,28 +166,46 @@ __device__ __forceinline__ void store_quant(const RopeArgs& a, const float* val,
   }
 }
 
-// One unit (row r, head unit u: Hq query heads, then Hk key heads, then Hk
-// value heads) for the calling 16-lane row. load(head) returns the lane's 8
-// dims of the bf16 head row at global address `head` (or wherever the
-// caller keeps them).
-template <int BITS, int GROUP, class Load>
-__device__ __forceinline__ void rope_unit(const RopeArgs& a, int r, int u, int lane16, Load load) {
-  const bool first_half = lane16 < 8;
+// Whether unit u (Hq query heads, then Hk key heads, then Hk value heads) is
+// rotated here: a query head, or a key head when the call rotates K.
+__device__ __forceinline__ bool unit_rotated(const RopeArgs& a, int u) {
+  return u < a.Hq + a.Hk && (u < a.Hq || a.rotate_k);
+}
 
-  if (u < a.Hq + a.Hk && (u < a.Hq || a.rotate_k)) {
-    // Rotated unit: a query head, or a key head that needs RoPE.
-    const int rp = rope_pos(a, r);
+// The bf16 head row unit u of row r reads.
+__device__ __forceinline__ const uint16_t* unit_src(const RopeArgs& a, int r, int u) {
+  if (u < a.Hq) return a.q + r * a.q_stride + u * 128LL;
+  if (u < a.Hq + a.Hk) return a.k + r * a.k_stride + (u - a.Hq) * 128LL;
+  return a.v + r * a.v_stride + (u - a.Hq - a.Hk) * 128LL;
+}
+
+// The lane's cos / sin (dims mod 64) of table row rp, clamped into [0,
+// max_pos) so that the loads can be issued before rp is checked.
+__device__ __forceinline__ void unit_trig(const RopeArgs& a, int rp, int lane16, float* cs,
+                                          float* sn) {
+  const long long rc = static_cast<long long>(min(max(rp, 0), a.max_pos - 1));
+  const float* cp = a.cos_t + rc * 64 + 8 * (lane16 & 7);
+  const float* sp = a.sin_t + rc * 64 + 8 * (lane16 & 7);
+  *reinterpret_cast<float4*>(cs) = *reinterpret_cast<const float4*>(cp);
+  *reinterpret_cast<float4*>(cs + 4) = *reinterpret_cast<const float4*>(cp + 4);
+  *reinterpret_cast<float4*>(sn) = *reinterpret_cast<const float4*>(sp);
+  *reinterpret_cast<float4*>(sn + 4) = *reinterpret_cast<const float4*>(sp + 4);
+}
+
+// The arithmetic and stores of one unit for the calling 16-lane row, given
+// its loaded head row x (the lane's 8 dims), the lane's cos / sin of table
+// row rp (rotated units) and its arena row (K / V units; arena_row's value).
+// A rotated unit outside the table, or a K / V row outside [0, stride),
+// writes nothing.
+template <int BITS, int GROUP>
+__device__ __forceinline__ void unit_finish(const RopeArgs& a, int r, int u, int lane16,
+                                            const V8& x, const float* cs, const float* sn,
+                                            int rp, int row) {
+  const bool first_half = lane16 < 8;
+  if (unit_rotated(a, u)) {
     if (rp < 0 || rp >= a.max_pos) return;
     const bool is_q = u < a.Hq;
     const int h = is_q ? u : u - a.Hq;
-    const V8 x = load(is_q ? a.q + r * a.q_stride + h * 128LL : a.k + r * a.k_stride + h * 128LL);
-    const float* cp = a.cos_t + static_cast<long long>(rp) * 64 + 8 * (lane16 & 7);
-    const float* sp = a.sin_t + static_cast<long long>(rp) * 64 + 8 * (lane16 & 7);
-    float cs[8], sn[8];
-    *reinterpret_cast<float4*>(cs) = *reinterpret_cast<const float4*>(cp);
-    *reinterpret_cast<float4*>(cs + 4) = *reinterpret_cast<const float4*>(cp + 4);
-    *reinterpret_cast<float4*>(sn) = *reinterpret_cast<const float4*>(sp);
-    *reinterpret_cast<float4*>(sn + 4) = *reinterpret_cast<const float4*>(sp + 4);
     float rot[8];
     rotate8(x, cs, sn, first_half, rot);
     const V8 rb = to_bf16x8(rot);
@@ -197,7 +215,6 @@ __device__ __forceinline__ void rope_unit(const RopeArgs& a, int r, int u, int l
     }
     if (a.k_rot != nullptr) st8(a.k_rot + (static_cast<long long>(r) * a.Hk + h) * 128 + 8 * lane16, rb);
     if (!a.has_kv) return;
-    const int row = arena_row(a, r);
     if (row < 0 || row >= a.stride) return;
     const long long slot = static_cast<long long>(h) * a.stride + row;
     if (BITS == 16) {
@@ -212,11 +229,9 @@ __device__ __forceinline__ void rope_unit(const RopeArgs& a, int r, int u, int l
   }
   // Unrotated K (already rotated by the caller) or V.
   if (!a.has_kv) return;
-  const int row = arena_row(a, r);
   if (row < 0 || row >= a.stride) return;
   const bool is_k = u < a.Hq + a.Hk;
   const int h = is_k ? u - a.Hq : u - a.Hq - a.Hk;
-  const V8 x = load(is_k ? a.k + r * a.k_stride + h * 128LL : a.v + r * a.v_stride + h * 128LL);
   const long long slot = static_cast<long long>(h) * a.stride + row;
   if (BITS == 16) {
     st8(static_cast<uint16_t*>(is_k ? a.cache_k : a.cache_v) + slot * 128 + 8 * lane16, x);
@@ -226,6 +241,26 @@ __device__ __forceinline__ void rope_unit(const RopeArgs& a, int r, int u, int l
 #pragma unroll
   for (int e = 0; e < 8; ++e) val[e] = v8_get(x, e);
   store_quant<BITS, GROUP>(a, val, is_k, slot, lane16);
+}
+
+// One unit (row r, head unit u) for the calling 16-lane row. load(head)
+// returns the lane's 8 dims of the bf16 head row at global address `head`
+// (or wherever the caller keeps them). Only rotated units read the table
+// and only K / V units (with a pool) ask for the arena row, so query heads
+// never wait on the page-table load.
+template <int BITS, int GROUP, class Load>
+__device__ __forceinline__ void rope_unit(const RopeArgs& a, int r, int u, int lane16, Load load) {
+  const bool rot = unit_rotated(a, u);
+  int rp = 0;
+  if (rot) {
+    rp = rope_pos(a, r);
+    if (rp < 0 || rp >= a.max_pos) return;
+  }
+  const V8 x = load(unit_src(a, r, u));
+  float cs[8], sn[8];
+  if (rot) unit_trig(a, rp, lane16, cs, sn);
+  const int row = (u >= a.Hq && a.has_kv) ? arena_row(a, r) : -1;
+  unit_finish<BITS, GROUP>(a, r, u, lane16, x, cs, sn, rp, row);
 }
 
 // Fills a for the decode append at *d_pos (granite4_rope_append_at_pos's
