@@ -23,8 +23,8 @@
 // Same-address atomic counters cost ~8 us.
 //
 // Requirements: every workgroup of the grid resident at once (the host checks
-// the occupancy before choosing this form), at most blockDim.x *
-// kSyncSlotsPerThread workgroups, and one such launch at a time per
+// the occupancy before choosing this form), kSyncThreads-thread workgroups,
+// at most kSyncThreads * kSyncSlotsPerThread of them (GridSync::blocks), and one such launch at a time per
 // workspace. The waits are bounded: a slot or result that never arrives
 // (which those requirements exclude) ends the wait after kSyncSpinLimit
 // polls, and the returned maximum is NaN, so the op reports a NaN scale
@@ -41,24 +41,33 @@ namespace g4 {
 constexpr int kSyncSpinLimit = 1 << 20;
 
 struct GridSync {
-  unsigned long long* slots;   // [gridDim.x] tagged maxima
+  unsigned long long* slots;   // [blocks] tagged maxima
   unsigned* gen;               // generation word
   unsigned long long* result;  // tagged grid maximum (gathered by workgroup 0)
+  int blocks;                  // the launch's grid size (gridDim.x), passed so
+                               // the gather does not read the dispatch packet
 };
+
+// Workgroup size of every launch that synchronises (a constant, so no
+// dispatch-packet load sits on the synchronisation path).
+constexpr int kSyncThreads = 256;
 
 constexpr int kSyncSlotsPerThread = 4;  // kMaxPartials / 256-thread workgroups
 
 // Issued at kernel start (thread 0; the value is used after the compute
 // phase, so the load's latency is hidden).
+// Every thread loads the word (one request per wave): a load in thread 0
+// only would be waited for inside its branch, a round trip before wave 0's
+// first data load.
 __device__ __forceinline__ unsigned grid_sync_tag(const GridSync& gs) {
-  return threadIdx.x == 0 ? __hip_atomic_load(gs.gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u
-                          : 0u;
+  return __hip_atomic_load(gs.gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
 }
 
 // Maximum of m over every thread of the grid (non-negative values; NaN
-// inputs are ignored as fmaxf does). tag0: grid_sync_tag's value (read in
-// thread 0 only). Every thread of the workgroup must call it; blockDim.x *
-// kSyncSlotsPerThread must cover gridDim.x.
+// inputs are ignored as fmaxf does). tag0: grid_sync_tag's value; thread
+// 0's is the one used (it has arrived before thread 0 publishes, so the
+// generation cannot have advanced past it). Every thread of the workgroup
+// must call it; kSyncThreads * kSyncSlotsPerThread must cover gs.blocks.
 //
 // Two levels: workgroups 1.. publish their maximum in their slot; workgroup
 // 0 polls every slot (each thread its <= kSyncSlotsPerThread slots, all
@@ -73,7 +82,7 @@ __device__ __forceinline__ float grid_max(float m, const GridSync& gs, unsigned 
   __shared__ unsigned s_tag;
   __shared__ float s_out;
   const int wave = threadIdx.x >> 6;
-  const int nw = blockDim.x >> 6;
+  constexpr int nw = kSyncThreads / 64;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
   if ((threadIdx.x & 63) == 0) s_red[wave] = m;
@@ -106,8 +115,8 @@ __device__ __forceinline__ float grid_max(float m, const GridSync& gs, unsigned 
   bool need[kSyncSlotsPerThread];
 #pragma unroll
   for (int k = 0; k < kSyncSlotsPerThread; ++k) {
-    const int j = threadIdx.x + k * blockDim.x;
-    need[k] = j > 0 && j < static_cast<int>(gridDim.x);
+    const int j = threadIdx.x + k * kSyncThreads;
+    need[k] = j > 0 && j < gs.blocks;
   }
   int spin = 0;
   bool late = false;
@@ -116,7 +125,7 @@ __device__ __forceinline__ float grid_max(float m, const GridSync& gs, unsigned 
 #pragma unroll
     for (int k = 0; k < kSyncSlotsPerThread; ++k)
       if (need[k])
-        v[k] = __hip_atomic_load(&gs.slots[threadIdx.x + k * blockDim.x], __ATOMIC_RELAXED,
+        v[k] = __hip_atomic_load(&gs.slots[threadIdx.x + k * kSyncThreads], __ATOMIC_RELAXED,
                                  __HIP_MEMORY_SCOPE_AGENT);
     bool any = false;
 #pragma unroll

@@ -355,6 +355,7 @@ __global__ __launch_bounds__(kBlock) void norm_generic_kernel(NormArgs a) {
 template <int VPL, int HR, int HL>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(VPL >= 4 ? 1 : 4)))
 void norm_fp8_fused_kernel(NormArgs a, GridSync gs) {
+  static_assert(kBlock == kSyncThreads, "grid_max assumes kSyncThreads-thread workgroups");
   __shared__ uint4 s_y[HL > 0 ? HL : 1][VPL][kBlock];
   const unsigned tag = grid_sync_tag(gs);
   V8 y[HR > 0 ? HR : 1][VPL];
@@ -489,7 +490,9 @@ bool launch_fused_vpl(const NormArgs& a, const GridSync& gs, int nvec) {
     const int cap = resident < kMaxPartials ? resident : kMaxPartials;
     if (cap <= 0 || a.rows > static_cast<long long>(cap) * (HR + HL)) return false;
     const unsigned grid = static_cast<unsigned>(a.rows < cap ? a.rows : cap);
-    hipLaunchKernelGGL(kern, grid, kBlock, 0, stream(), a, gs);
+    GridSync g = gs;
+    g.blocks = static_cast<int>(grid);
+    hipLaunchKernelGGL(kern, grid, kBlock, 0, stream(), a, g);
     return true;
   };
   if (nvec <= 256) return go(norm_fp8_fused_kernel<1, HR, HL>);
@@ -509,7 +512,7 @@ bool launch_norm_fp8_fused(const uint16_t* x, const uint16_t* branch, float mult
     return false;
   NormArgs a{x, branch, mult, w, eps, rows, cols, res_out, nullptr, codes, scale, nullptr, 0,
              nullptr, 0.0};
-  const GridSync gs{work_slots(work), work_gen(work), work_result(work)};
+  const GridSync gs{work_slots(work), work_gen(work), work_result(work), 0};
   return launch_fused_vpl<kNormHold, 0>(a, gs, nvec) ||
          launch_fused_vpl<kNormDeepHR, kNormDeepHL>(a, gs, nvec);
 }

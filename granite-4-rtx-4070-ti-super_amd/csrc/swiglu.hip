@@ -171,6 +171,7 @@ __global__ __launch_bounds__(kBlock) void encode_bf16_kernel(SwArgs a) {
 // written per element (+2 B with the optional bf16 act), against 9 B for
 // the two-launch form, and one launch instead of two.
 constexpr int kFusedThreads = kBlock;
+static_assert(kFusedThreads == kSyncThreads && kBlock == kSyncThreads, "grid_max assumes kSyncThreads-thread workgroups");
 constexpr int kFusedVpt = 4;
 
 __global__ __launch_bounds__(kFusedThreads) void swiglu_fp8_fused_kernel(SwArgs a, GridSync gs) {
@@ -474,7 +475,8 @@ int granite4_swiglu_fp8(const uint16_t* d_gu, int rows, int I, uint8_t* d_codes,
     f.act = d_act;
     f.codes = d_codes;
     f.scale_out = d_scale;
-    const GridSync gs{work_slots(d_work), work_gen(d_work), work_result(d_work)};
+    const GridSync gs{work_slots(d_work), work_gen(d_work), work_result(d_work),
+                      static_cast<int>(fgrid)};
     hipLaunchKernelGGL(swiglu_fp8_fused_kernel, fgrid, kFusedThreads, 0, stream(), f, gs);
     return launch_status("granite4_swiglu_fp8");
   }
@@ -484,7 +486,8 @@ int granite4_swiglu_fp8(const uint16_t* d_gu, int rows, int I, uint8_t* d_codes,
     h.act = d_act;
     h.codes = d_codes;
     h.scale_out = d_scale;
-    const GridSync gs{work_slots(d_work), work_gen(d_work), work_result(d_work)};
+    const GridSync gs{work_slots(d_work), work_gen(d_work), work_result(d_work),
+                      static_cast<int>(hgrid)};
     hipLaunchKernelGGL(swiglu_fp8_hold_kernel, hgrid, kBlock, 0, stream(), h, gs);
     return launch_status("granite4_swiglu_fp8");
   }

@@ -433,14 +433,16 @@ def _oracle_arena(bits, group, Hk, stride, fill=0xEE):
             np.zeros(Hk * stride * ng, np.float32), np.zeros(Hk * stride * ng, np.float32))
 
 
+@pytest.mark.parametrize("rows", [40, 300])
 @pytest.mark.parametrize("bits", [16, 8, 4, 5])
-def test_prefill_rope_split_append_paged(tables, bits):
+def test_prefill_rope_split_append_paged(tables, bits, rows):
     """The reference's prefill launchers: f32-rotated K quantised, random page table,
-    untouched rows keep their 0xEE fill (test_kernels.cu:730-801)."""
-    note(f"prefill split append bits={bits}")
+    untouched rows keep their 0xEE fill (test_kernels.cu:730-801). 40 rows take the
+    one-unit-per-lane-group kernel, 300 the per-token one."""
+    note(f"prefill split append bits={bits} rows={rows}")
     c, s, dc, ds = tables
-    rows, Hq, Hk, base = 40, 32, 8, 100
-    pages = 16
+    Hq, Hk, base = 32, 8, 100
+    pages = (base + rows + 15) // 16 + 2
     stride = pages * 16
     bt = np.random.default_rng(bits).permutation(pages).astype(np.int32)
     pt = ol.row_table(bt, stride)
@@ -458,18 +460,20 @@ def test_prefill_rope_split_append_paged(tables, bits):
     _arena_compare(arena, want, bits, 128, Hk, stride)
 
 
+@pytest.mark.parametrize("rows", [64, 300])
 @pytest.mark.parametrize("bits,group", [(8, 128), (8, 32), (4, 32), (5, 32), (5, 64), (16, 128)])
-def test_rope_append_fused_entry(tables, bits, group):
-    """granite4_rope_append at config-4 positions (57344..), group scales, per-row arena rows."""
-    note(f"rope_append bits={bits} group={group}")
+def test_rope_append_fused_entry(tables, bits, group, rows):
+    """granite4_rope_append at config-4 positions (57344..), group scales, per-row arena rows
+    (64 rows: one unit per lane group; 300: one workgroup per token)."""
+    note(f"rope_append bits={bits} group={group} rows={rows}")
     c, s, dc, ds = tables
-    rows, Hq, Hk = 64, 32, 8
-    stride = 256
+    Hq, Hk = 32, 8
+    stride = 512
     qkv = _qkv(rows, 0x77 + bits + group)
     d_qkv = dev(qkv)
     q, k, v = d_qkv[:, :Hq * 128], d_qkv[:, Hq * 128:(Hq + Hk) * 128], d_qkv[:, (Hq + Hk) * 128:]
     arena = L.KvArena(bits, Hk, stride, group=group, fill=0xEE)
-    base = 57344 + 8000
+    base = min(57344 + 8000, 65536 - rows)
     arows = np.random.default_rng(group).permutation(stride)[:rows].astype(np.int32)
     for k_round in (False, True):
         q_rot = L.rope_append(arena, q, k, v, dc, ds, base_pos=base, arena_rows=dev(arows),
