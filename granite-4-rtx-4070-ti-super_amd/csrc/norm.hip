@@ -114,7 +114,9 @@ __device__ __forceinline__ void norm_row_load(const NormArgs& a, int rg, NormRow
 // Second half: res' = x + mult * branch (bf16; stored when res_out is given)
 // and the row's r = 1 / rms. Every thread of the workgroup must call it (it
 // synchronises when WPR > 1).
-template <int VPL, int WPR>
+// NT_RES: res' stored non-temporally (a single-launch form never reads it
+// back; the two-launch form's encode pass does, through the caches).
+template <int VPL, int WPR, bool NT_RES = false>
 __device__ __forceinline__ void norm_row_finish(const NormArgs& a, NormRow<VPL, WPR>& t) {
   const int wave = threadIdx.x >> 6;
   double ss = 0.0;
@@ -129,7 +131,8 @@ __device__ __forceinline__ void norm_row_finish(const NormArgs& a, NormRow<VPL, 
       }
       if (t.ok[j] && a.res_out != nullptr) {
         const int vi = (j * WPR + t.part) * 64 + t.lane;
-        st8(a.res_out + t.base + 8 * vi, t.xv[j]);
+        if (NT_RES) st8_nt(a.res_out + t.base + 8 * vi, t.xv[j]);
+        else st8(a.res_out + t.base + 8 * vi, t.xv[j]);
       }
     }
 #pragma unroll
@@ -155,10 +158,10 @@ __device__ __forceinline__ void norm_row_finish(const NormArgs& a, NormRow<VPL, 
 
 // The lane's share of one row of a row group (4 / WPR rows per 256-thread
 // workgroup): res', the gamma vectors, and the row's r = 1 / rms.
-template <int VPL, int WPR>
+template <int VPL, int WPR, bool NT_RES = false>
 __device__ __forceinline__ void norm_row_front(const NormArgs& a, int rg, NormRow<VPL, WPR>& t) {
   norm_row_load<VPL, WPR>(a, rg, t);
-  norm_row_finish<VPL, WPR>(a, t);
+  norm_row_finish<VPL, WPR, NT_RES>(a, t);
 }
 
 // One row group of the workgroup; MODE kOutAmax folds into *m.
@@ -365,7 +368,7 @@ void norm_fp8_fused_kernel(NormArgs a, GridSync gs) {
     const int rg = blockIdx.x + h * gridDim.x;  // uniform over the workgroup
     if (rg >= a.rows) break;
     NormRow<VPL, 4> t;
-    norm_row_front<VPL, 4>(a, rg, t);
+    norm_row_front<VPL, 4, true>(a, rg, t);
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
       V8 yv;
