@@ -316,7 +316,9 @@ def main():
         "decode_non_gemm_overhead_us": {
             "with_attention": result_extra["decode_T1_gemv"]["with_attention"][
                 "non_gemm_overhead_fused_us"],
-            "gemvs_only": result_extra["decode_T1_gemv"]["non_gemm_overhead_fused_us"],
+            "config1_ops_in_gemvs": result_extra["decode_T1_gemv"]["config1_non_gemm_overhead_us"],
+            "gemvs_rope_append_launch": result_extra["decode_T1_gemv"][
+                "non_gemm_overhead_fused_us"],
             "standalone_ops_graph_us": decode["graph_us_per_step"]},
         "detail": result_extra,
     }
@@ -445,6 +447,11 @@ def bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream, layers=40
                the same without the RoPE launches, and with RoPE + append in
                the q|k|v GEMV's epilogue (one workgroup per head: 48 of them,
                slower than the separate launch).
+      config1  BASELINE config 1's ops (embed, add+RMSNorm, SwiGLU, RoPE on
+               Q/K; no KV write) all inside the GEMVs: norm prologues, RoPE in
+               the q|k|v epilogue, SwiGLU and residual epilogues (4 per layer).
+    with attention: the same with the split-KV attention of each layer, the
+    KV append inside the attention launch.
     The non-GEMM overhead of a step is its time minus the plain step's."""
     dev = "cuda"
     stride = 8192
@@ -624,6 +631,20 @@ def bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream, layers=40
 
     t_parts_norope = graph_us(torch, L, stream, fused_attn_parts(False))
     t_parts_rope = graph_us(torch, L, stream, fused_attn_parts(True))
+    def fused_rope_epilogue():
+        # config 1's ops (embed, add+RMSNorm, SwiGLU, RoPE on Q/K) all inside
+        # the decode GEMVs: RoPE in the q|k|v epilogue, no KV write
+        L.call("granite4_embed_at_pos", toks, pos, emb, VOCAB, H, 1.0, hidden)
+        for p in per:
+            L.call("granite4_gemv_rmsnorm_qkv_rope", hidden, gamma, 1e-5, p["wq"], p["wk"],
+                   p["wv"], sc, sc, sc, cos_t, sin_t, 65536, pos, HQ, HK, H, q_rot, k_rot, v)
+            L.call("granite4_gemv_fp8w_resid", attn_out, p["wo"], sc, hidden, 1.0, H, HQ * D,
+                   hidden)
+            L.call("granite4_gemv_rmsnorm_silu_gate_up", hidden, gamma, 1e-5, p["wg"], p["wu"],
+                   sc, sc, I, H, act)
+            L.call("granite4_gemv_fp8w_resid", act, p["wd"], sc, hidden, 1.0, H, I, hidden)
+
+    t_rope_epi = graph_us(torch, L, stream, fused_rope_epilogue)
     t_fused_attn_ropeattn = graph_us(torch, L, stream, fused_attn)
     t_fused_attn = graph_us(torch, L, stream, fused_attn_rot)
     t_unfused = graph_us(torch, L, stream, unfused)
@@ -639,6 +660,8 @@ def bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream, layers=40
             "unfused_us": round(t_unfused, 1), "fused_us": round(t_fused, 1),
             "non_gemm_overhead_unfused_us": round(t_unfused - t_plain, 1),
             "non_gemm_overhead_fused_us": round(t_fused - t_plain, 1),
+            "config1_fused_us": round(t_rope_epi, 1),
+            "config1_non_gemm_overhead_us": round(t_rope_epi - t_plain, 1),
             "fused_gemvs_without_rope_us": round(t_fused_norope, 1),
             "rope_append_launches_us": round(t_fused - t_fused_norope, 1),
             "fused_qkv_rope_one_launch_us": round(t_qkv_rope_kernel, 1),
