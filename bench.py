@@ -433,6 +433,44 @@ def graph_us(torch, L, stream, step, reps=20):
     return e0.elapsed_time(e1) / reps * 1e3
 
 
+def graphs_us(torch, L, stream, steps, rounds=5, reps=20):
+    """µs per step for each of several steps (name -> function), each captured
+    once as a HIP graph on a side stream, then timed round-robin over
+    `rounds` rounds of `reps` replays; the median round of each. Interleaving
+    keeps slow drifts of the clock (and the box) out of the differences
+    between steps."""
+    graphs = {}
+    cap = torch.cuda.Stream()
+    for name, step in steps.items():
+        g = torch.cuda.CUDAGraph()
+        cap.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(cap):
+            L.use_stream(cap)
+            step()
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=cap):
+                step()
+        L.use_stream(stream)
+        torch.cuda.synchronize()
+        graphs[name] = g
+    times = {name: [] for name in steps}
+    for _ in range(rounds):
+        for name, g in graphs.items():
+            for _ in range(3):
+                g.replay()
+            torch.cuda.synchronize()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            times[name].append(e0.elapsed_time(e1) / reps * 1e3)
+    del graphs
+    return {name: sorted(t)[len(t) // 2] for name, t in times.items()}
+
+
 def bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream, layers=40):
     """Batch-1 decode step with its GEMVs (fp8 weight rows of the 8B model:
     q|k|v 6144 x 4096, o 4096 x 4096, gate and up 12800 x 4096, down 4096 x
@@ -586,9 +624,6 @@ def bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream, layers=40
                    sc, sc, I, H, act)
             L.call("granite4_gemv_fp8w_resid", act, p["wd"], sc, hidden, 1.0, H, I, hidden)
 
-    t_plain = graph_us(torch, L, stream, plain)
-    t_plain_attn = graph_us(torch, L, stream, plain_attn)
-    t_unfused_attn = graph_us(torch, L, stream, unfused_attn)
     k_rot = bf(HK * D)
 
     def fused_attn_rot():
@@ -629,8 +664,6 @@ def bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream, layers=40
                 L.call("granite4_gemv_fp8w_resid", act, p["wd"], sc, hidden, 1.0, H, I, hidden)
         return step
 
-    t_parts_norope = graph_us(torch, L, stream, fused_attn_parts(False))
-    t_parts_rope = graph_us(torch, L, stream, fused_attn_parts(True))
     def fused_rope_epilogue():
         # config 1's ops (embed, add+RMSNorm, SwiGLU, RoPE on Q/K) all inside
         # the decode GEMVs: RoPE in the q|k|v epilogue, no KV write
@@ -644,13 +677,17 @@ def bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream, layers=40
                    sc, sc, I, H, act)
             L.call("granite4_gemv_fp8w_resid", act, p["wd"], sc, hidden, 1.0, H, I, hidden)
 
-    t_rope_epi = graph_us(torch, L, stream, fused_rope_epilogue)
-    t_fused_attn_ropeattn = graph_us(torch, L, stream, fused_attn)
-    t_fused_attn = graph_us(torch, L, stream, fused_attn_rot)
-    t_unfused = graph_us(torch, L, stream, unfused)
-    t_qkv_rope_kernel = graph_us(torch, L, stream, fused)
-    t_fused_norope = graph_us(torch, L, stream, fused_split(False))
-    t_fused = graph_us(torch, L, stream, fused_split(True))
+    t = graphs_us(torch, L, stream, {
+        "plain": plain, "plain_attn": plain_attn, "unfused_attn": unfused_attn,
+        "parts_norope": fused_attn_parts(False), "parts_rope": fused_attn_parts(True),
+        "rope_epi": fused_rope_epilogue, "fused_attn_ropeattn": fused_attn,
+        "fused_attn": fused_attn_rot, "unfused": unfused, "qkv_rope_kernel": fused,
+        "fused_norope": fused_split(False), "fused": fused_split(True)})
+    t_plain, t_plain_attn, t_unfused_attn = t["plain"], t["plain_attn"], t["unfused_attn"]
+    t_parts_norope, t_parts_rope, t_rope_epi = t["parts_norope"], t["parts_rope"], t["rope_epi"]
+    t_fused_attn_ropeattn, t_fused_attn = t["fused_attn_ropeattn"], t["fused_attn"]
+    t_unfused, t_qkv_rope_kernel = t["unfused"], t["qkv_rope_kernel"]
+    t_fused_norope, t_fused = t["fused_norope"], t["fused"]
     wbytes = layers * (HQ * D + 2 * HK * D + 2 * I) * H + layers * H * (HQ * D + I)
     del per
     torch.cuda.empty_cache()
