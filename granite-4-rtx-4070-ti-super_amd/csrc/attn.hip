@@ -643,10 +643,12 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
       }
     }
     if (crr >= nr) return;
+    // A block with no key of the row (its positions all unmapped) publishes
+    // (-inf, 0, 0), which the combine weighs with 0, instead of leaving the
+    // previous call's partial in its slot.
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, mml[(w * 16 + col) * 2]);
-    if (M == -INFINITY) return;  // no key of this row in the block
     float L = 0.0f, acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int w = 0; w < kAttnWaves; ++w) {

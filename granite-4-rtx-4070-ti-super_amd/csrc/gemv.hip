@@ -159,8 +159,9 @@ __device__ __forceinline__ const uint8_t* row_ptr(const GemvArgs& a, int r, int&
 // r - kRows / 2 for the up half, each from its own matrix, so that case
 // keeps the general path), or the head-paired kEpiRope order.
 template <int EPI, int kRows>
-__device__ __forceinline__ int row_offset(int r) {
-  if (EPI == kEpiRope) return (r & 3) + (r >= 4 ? 64 : 0);
+__device__ __forceinline__ int row_offset(const GemvArgs& a, int r) {
+  // kEpiRope: head-paired rows in the rotated segments, plain order for v
+  if (EPI == kEpiRope && static_cast<int>(blockIdx.x) < a.seg2 / 8) return (r & 3) + (r >= 4 ? 64 : 0);
   return r;
 }
 
@@ -169,7 +170,7 @@ __device__ __forceinline__ bool rows_in_one_segment(const GemvArgs& a) {
   if (EPI == kEpiSwiglu) return false;
   const int first = out_row<EPI, kRows>(a, 0);
   const int last = out_row<EPI, kRows>(a, kRows - 1);
-  if (last >= a.N || last - first != row_offset<EPI, kRows>(kRows - 1)) return false;
+  if (last >= a.N || last - first != row_offset<EPI, kRows>(a, kRows - 1)) return false;
   const int sf = first < a.seg1 ? 0 : (first < a.seg2 ? 1 : 2);
   const int sl = last < a.seg1 ? 0 : (last < a.seg2 ? 1 : 2);
   return sf == sl;
@@ -227,7 +228,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     const uint8_t* p0 = row_ptr<EPI, kRows>(a, 0, n0);
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
-      const int off = row_offset<EPI, kRows>(r);
+      const int off = row_offset<EPI, kRows>(a, r);
       rows[r] = p0 + static_cast<size_t>(off) * a.K;
       ns[r] = n0 + off;
       live[r] = true;

@@ -249,13 +249,16 @@ unsigned fused_grid(long long vectors) {
 #ifndef G4_SW_HB
 #define G4_SW_HB 4
 #endif
+#ifndef G4_SW_WPE
+#define G4_SW_WPE 4
+#endif
 constexpr int kHoldR = G4_SW_HR;
 constexpr int kHoldL = G4_SW_HL;
 constexpr int kHold = kHoldR + kHoldL;
 constexpr int kHoldBatch = G4_SW_HB;  // held vectors' loads in flight per lane
 constexpr int kStreamU = G4_SW_SU;  // streamed vectors' loads in flight per lane
 
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) void swiglu_fp8_hold_kernel(SwArgs a, GridSync gs) {
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(G4_SW_WPE))) void swiglu_fp8_hold_kernel(SwArgs a, GridSync gs) {
   __shared__ uint4 s_hold[kHoldL > 0 ? kHoldL : 1][kBlock];
   const unsigned tag = grid_sync_tag(gs);
   const int nv = a.I >> 3;

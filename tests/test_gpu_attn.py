@@ -307,3 +307,46 @@ def test_attn_decode_append_fused(bits, group, pos_v, max_pos):
         res.append([host(out)] + [host(t) for t in pool if t is not None])
     for a_, b_ in zip(*res):
         np.testing.assert_array_equal(a_, b_)
+
+
+
+@pytest.mark.parametrize("bits,group", [(8, 128), (16, 128), (5, 32)])
+def test_attn_decode_append_long_context_repeated(bits, group):
+    """The fused decode attention over many split blocks: stride 16384 (256
+    splits, 64 split blocks), positions whose combine covers 1, 17, 64 and 32
+    blocks, called repeatedly on one scratch. Output and pool bit-identical
+    to rope_append_at_pos + granite4_attn_paged every time."""
+    pages = 1024
+    stride = 16 * pages
+    ck, cv, ks, vs = make_cache(bits, group, stride, 0xA1 + bits)
+    rng = np.random.default_rng(bits)
+    pt = dev(ol.row_table(rng.permutation(pages).astype(np.int32), stride))
+    cos_t, sin_t = ol.rope_tables(1e7, D, stride)
+    dcos, dsin = dev(cos_t), dev(sin_t)
+    scratch = torch.empty(L.call_size("granite4_attn_split_scratch_bytes", HQ, 1, stride),
+                          dtype=torch.uint8, device="cuda")
+    for it, pos_v in enumerate((100, 4321, 16383, 255, 8191)):
+        note(f"attn decode long context bits={bits} group={group} pos={pos_v} call={it}")
+        pos = dev(np.array([pos_v], np.int32))
+        q = dev(ol.normal_bf16(0xA2 + it, 0.0, 1.0, HQ * D))
+        k = dev(ol.normal_bf16(0xA3 + it, 0.0, 1.0, HK * D))
+        v = dev(ol.normal_bf16(0xA4 + it, 0.0, 1.0, HK * D))
+        res = []
+        for fused in (False, True):
+            pool = [dev(ck), dev(cv), None if ks is None else dev(ks),
+                    None if vs is None else dev(vs)]
+            out = torch.empty(HQ * D, dtype=torch.int16, device="cuda")
+            if fused:
+                L.call("granite4_attn_decode_append", q, k, v, dcos, dsin, stride, pos, pt, HQ,
+                       HK, 1.0 / 16, *pool, bits, group, stride, scratch, out)
+            else:
+                q_rot = torch.zeros(HQ * D, dtype=torch.int16, device="cuda")
+                L.call("granite4_rope_append_at_pos", q, k, v, dcos, dsin, stride, pos, pt, HQ,
+                       HK, D, bits, group, q_rot, *pool, stride)
+                L.call("granite4_attn_paged", q_rot, 1, HQ, HK, D, 1.0 / 16, *pool, bits, group,
+                       stride, 0, pos, pt, None, None, 0, 0, scratch, out)
+            res.append([host(out)] + [host(t) for t in pool if t is not None])
+        got = (res[1][0].view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+        assert np.isfinite(got).all()
+        for a_, b_ in zip(*res):
+            np.testing.assert_array_equal(a_, b_)
