@@ -495,6 +495,10 @@ void g4o_attn_split(const uint16_t* q, int rows, int Hq, int Hk, int d, float sc
               continue;
             }
             const int arow = pt != NULL && pt[r] != NULL ? pt[r][p] : p;
+            if (arow < 0 || arow >= stride) { /* unmapped position: skipped, as the kernels do */
+              logit[j] = -INFINITY;
+              continue;
+            }
             const uint8_t* krow = (const uint8_t*)cache_k + ((size_t)hk * stride + arow) * kb;
             float dot = 0.0f;
             if (!quant) {

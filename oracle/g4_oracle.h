@@ -109,8 +109,10 @@ void g4o_rope_append(const uint16_t* q, long q_stride, const uint16_t* k, long k
  * by attn_split :1083-1255). Row r (query q[r][Hq][d], Hq = 4 Hk, query head h
  * reads KV head h / 4) sits at position pos[r] and attends to positions
  * [lo, pos[r]], lo = max(0, pos[r] + 1 - window) when window > 0 else 0,
- * found at arena row pt[r][position] (pt[r] NULL: row = position). Cache
- * formats as g4o_rope_append's. Positions are cut into 64-position tiles and
+ * found at arena row pt[r][position] (pt[r] NULL: row = position); a
+ * position whose row is outside [0, stride) is skipped (this library's rule
+ * for unmapped pages; the reference never passes one). Cache formats as
+ * g4o_rope_append's. Positions are cut into 64-position tiles and
  * the tiles into splits of tps tiles; each split keeps its own online
  * softmax, and the splits are combined, as the kernels do:
  *   logit  = bf16(scale * dot), dot = q . k (bf16 K) or sum over scale groups

@@ -121,6 +121,39 @@ def test_attn_contiguous(bits, rows):
     check(got, want, vmax(cv, vs, bits), f"bits {bits} rows {rows}")
 
 
+@pytest.mark.parametrize("bits", [8, 16])
+def test_attn_unmapped_split_block(bits):
+    """A whole split block of positions without an arena row (page-table
+    entries -1 for positions 256..511: one block of 4 splits at this stride)
+    contributes nothing: the block publishes an empty partial rather than
+    leaving the previous call's in its scratch slot (the first call, with
+    every position mapped, fills that slot)."""
+    note(f"attn unmapped split block bits={bits}")
+    pages = 80
+    stride = 16 * pages
+    ck, cv, ks, vs = make_cache(bits, D, stride, 0xE1 + bits)
+    pt = ol.row_table(np.random.default_rng(bits).permutation(pages).astype(np.int32), stride)
+    pt_hole = pt.copy()
+    pt_hole[256:512] = -1
+    q = ol.normal_bf16(0xE2, 0.0, 1.0, HQ * D).reshape(1, HQ * D)
+    pos = dev(np.array([1000], np.int32))
+    scratch = torch.empty(L.call_size("granite4_attn_split_scratch_bytes", HQ, 1, stride),
+                          dtype=torch.uint8, device="cuda")
+    dks = None if ks is None else dev(ks)
+    dvs = None if vs is None else dev(vs)
+    outs = []
+    for table in (pt, pt_hole):
+        out = torch.empty((1, HQ * D), dtype=torch.int16, device="cuda")
+        L.call("granite4_attn_paged", dev(q), 1, HQ, HK, D, 1.0 / 16, dev(ck), dev(cv), dks, dvs,
+               bits, D, stride, 0, pos, dev(table), None, None, 0, 0, scratch, out)
+        outs.append(host(out).view(np.uint16))
+    for got, table in zip(outs, (pt, pt_hole)):
+        want = ol.attn_split(q, ck, cv, ks, vs, bits, D, stride, [1000], pts=[table],
+                             scale=1.0 / 16, Hk=HK)
+        check(got, want, vmax(cv, vs, bits), f"bits {bits} hole={table is pt_hole}")
+    assert not np.array_equal(outs[0], outs[1])
+
+
 @pytest.mark.parametrize("bits,group", [(8, 128), (5, 128), (16, 128), (5, 32), (4, 32), (8, 64)])
 def test_attn_paged_device_pos(bits, group):
     note(f"attn paged bits={bits} group={group}")
