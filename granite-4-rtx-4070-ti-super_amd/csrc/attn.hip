@@ -758,12 +758,11 @@ struct PrefillArgs {
 // ahead (prefill_load, issued before the current tile's compute), then
 // converted into the LDS tile (prefill_store: K codes as exact bf16
 // integers, V as the decode staging does, scales alongside, zeros for keys
-// without a row). Measured against staging each tile after the previous
-// one's compute: T=512 int8 33.7 -> 29.6 us, T=8192 at 57344 K5V4 38.3 ->
-// 35.1 ms. The page-table entries of a tile are
-// loaded a tile before its bytes, so no load waits for another inside the
-// loop. Loads are unconditional (row 0 for keys without a row; masked
-// when stored).
+// without a row). The page-table entries of a tile are loaded a tile before
+// its bytes, so no load waits for another inside the loop. Loads are
+// unconditional (row 0 for keys without a row, masked when stored).
+// Measured against staging each tile after the previous one's compute:
+// T=512 int8 33.7 -> 29.6 us, T=8192 at 57344 K5V4 38.3 -> 35.1 ms.
 template <int BITS, int GROUP>
 struct PrefillRaw {
   static constexpr bool kQuant = BITS != 16;

@@ -155,9 +155,9 @@ __device__ __forceinline__ const uint8_t* row_ptr(const GemvArgs& a, int r, int&
 }
 
 // Row r's offset (in rows) from row 0 within its segment when every row of
-// the workgroup lies in one segment: r (swiglu: r for the gate half and
-// r - kRows / 2 for the up half, each from its own matrix, so that case
-// keeps the general path), or the head-paired kEpiRope order.
+// the workgroup lies in one segment: r, or the head-paired order in
+// kEpiRope's rotated segments. (The swiglu form, whose halves come from two
+// matrices, has a fast path of its own.)
 template <int EPI, int kRows>
 __device__ __forceinline__ int row_offset(const GemvArgs& a, int r) {
   // kEpiRope: head-paired rows in the rotated segments, plain order for v

@@ -70,9 +70,10 @@ __global__ __launch_bounds__(kBlock) void rope_append_kernel(RopeArgs a) {
 // units g, g + 16, ... of the row. The row's position and arena row are
 // loaded once, then every head row of the group (UPL 16-byte loads per lane
 // in flight together), then the row's cos / sin; the arithmetic is
-// unit_finish's, so the bytes written equal rope_append_kernel's. Measured
-// against one unit per lane group (T=8192, K5V4 group 32): more loads in
-// flight per lane instead of one dependent round trip per unit.
+// unit_finish's, so the bytes written equal rope_append_kernel's. One unit
+// per lane group kept one 16-byte load per lane in flight and a dependent
+// page-table / table round trip per unit; measured at T=8192 (K5V4 group
+// 32): 40.3 us there, 32.9 us here.
 template <int BITS, int GROUP, int UPL>
 __global__ __launch_bounds__(kBlock) void rope_append_row_kernel(RopeArgs a) {
   const int lane16 = threadIdx.x & 15, grp = threadIdx.x >> 4;
