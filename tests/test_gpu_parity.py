@@ -79,7 +79,7 @@ def test_selftest_fp8_hw_encoder_exhaustive(scale):
 
 
 # ----------------------------------------------------------------------------- embed
-@pytest.mark.parametrize("rows,mult", [(1, 1.0), (8, 1.0), (512, 1.0), (37, 0.7071)])
+@pytest.mark.parametrize("rows,mult", [(1, 1.0), (8, 1.0), (512, 1.0), (37, 0.7071), (4100, 0.5)])
 def test_embed_rows_bit_exact(rows, mult):
     note(f"embed rows={rows} mult={mult}")
     vocab, H = 1000, 4096
