@@ -539,11 +539,16 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
           for (int i = 0; i < 4; ++i) acc[i] += part[i] * ksc_l[(16 * mb + 4 * g + i) * kNgrp + gi];
         }
       }
+      // logit = bf16(scale * dot), two per hardware conversion (equal to the
+      // integer rounding for every non-NaN value)
+      const uint32_t lg01 = pack_bf16_hw(a.scale * acc[0], a.scale * acc[1]);
+      const uint32_t lg23 = pack_bf16_hw(a.scale * acc[2], a.scale * acc[3]);
+      const float lg[4] = {lo_bf16(lg01), hi_bf16(lg01), lo_bf16(lg23), hi_bf16(lg23)};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int p = t0 + 16 * mb + 4 * g + i;
         const bool ok = live && p < my_len && p >= my_lo && ((kvalid >> (16 * mb + 4 * g + i)) & 1ull);
-        sv[mb][i] = ok ? bf16_to_f32(f32_to_bf16(a.scale * acc[i])) : -INFINITY;
+        sv[mb][i] = ok ? lg[i] : -INFINITY;
       }
     }
     // Online softmax of this lane's query row over the tile.
@@ -1025,11 +1030,14 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_prefill_kernel(PrefillAr
             for (int i = 0; i < 4; ++i) acc[i] += part[i] * ksv[i][gi];
           }
         }
+        const uint32_t lg01 = pack_bf16_hw(a.scale * acc[0], a.scale * acc[1]);
+        const uint32_t lg23 = pack_bf16_hw(a.scale * acc[2], a.scale * acc[3]);
+        const float lg[4] = {lo_bf16(lg01), hi_bf16(lg01), lo_bf16(lg23), hi_bf16(lg23)};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int j = j0 + 16 * mb + 4 * g + i;
           const bool ok = live[cb] && j <= my_pos[cb] && j >= my_lo[cb] && kv_ok[i];
-          e[cb][mb][i] = ok ? bf16_to_f32(f32_to_bf16(a.scale * acc[i])) : -INFINITY;
+          e[cb][mb][i] = ok ? lg[i] : -INFINITY;
         }
       }
     }
