@@ -176,9 +176,9 @@ __device__ __forceinline__ v8i frag_of(const v4u& x, const v4u& y) {
 
 __device__ __forceinline__ void wave_lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-__device__ __forceinline__ uint32_t pack_bf16_rne(float lo, float hi) {
-  return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
-}
+// Two bf16 RNE conversions in one v_cvt_pk_bf16_f32 (equal to the integer
+// rounding for every non-NaN value).
+__device__ __forceinline__ uint32_t pack_bf16_rne(float lo, float hi) { return pack_bf16_hw(lo, hi); }
 
 // Waits until at most `later` stages' loads (8 per thread each) are in flight.
 __device__ __forceinline__ void stage_wait(int later) {
