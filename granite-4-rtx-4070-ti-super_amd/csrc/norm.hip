@@ -226,6 +226,9 @@ __device__ __forceinline__ void norm_rows(const NormArgs& a, int rg, const Fp8En
 
 template <int VPL, int WPR, int MODE>
 __global__ __launch_bounds__(kBlock) void norm_kernel(NormArgs a) {
+  // The arguments of the row loads fetched in one scalar round trip.
+  asm volatile("" ::"s"(a.x), "s"(a.branch), "s"(a.w), "s"(a.rows), "s"(a.cols), "s"(a.mult),
+               "s"(a.res_out), "s"(a.normed), "s"(a.eps));
   constexpr int RPB = 4 / WPR;
   const int nrg = (a.rows + RPB - 1) / RPB;
   Fp8Enc f = fp8_enc_of(0.0f);

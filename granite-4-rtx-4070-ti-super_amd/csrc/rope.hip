@@ -57,6 +57,11 @@ namespace {
 
 template <int BITS, int GROUP>
 __global__ __launch_bounds__(kBlock) void rope_append_kernel(RopeArgs a) {
+  // The kernel arguments the first loads need, fetched in one scalar round
+  // trip (otherwise each is a dependent scalar-cache miss where first used).
+  asm volatile("" ::"s"(a.q), "s"(a.k), "s"(a.v), "s"(a.q_stride), "s"(a.k_stride),
+               "s"(a.v_stride), "s"(a.pos_ptr), "s"(a.pos_rows), "s"(a.pt), "s"(a.arena_rows),
+               "s"(a.mr), "s"(a.rows), "s"(a.units_per_row), "s"(a.Hq), "s"(a.Hk));
   const int lane16 = threadIdx.x & 15;
   // rows * units_per_row < 2^31 (checked on the host), so 32-bit indexing.
   const unsigned unit = blockIdx.x * (kBlock / 16) + (threadIdx.x >> 4);

@@ -251,12 +251,14 @@ __device__ __forceinline__ void unit_finish(const RopeArgs& a, int r, int u, int
 template <int BITS, int GROUP, class Load>
 __device__ __forceinline__ void rope_unit(const RopeArgs& a, int r, int u, int lane16, Load load) {
   const bool rot = unit_rotated(a, u);
+  // The head row first: its address needs no position, so its load overlaps
+  // the position's (and the page table's) instead of waiting behind them.
+  const V8 x = load(unit_src(a, r, u));
   int rp = 0;
   if (rot) {
     rp = rope_pos(a, r);
     if (rp < 0 || rp >= a.max_pos) return;
   }
-  const V8 x = load(unit_src(a, r, u));
   float cs[8], sn[8];
   if (rot) unit_trig(a, rp, lane16, cs, sn);
   const int row = (u >= a.Hq && a.has_kv) ? arena_row(a, r) : -1;

@@ -128,6 +128,8 @@ __device__ __forceinline__ float swiglu_run(const SwArgs& a, const Fp8Enc& f, S&
 
 template <int MODE, bool F32IN>
 __global__ __launch_bounds__(kBlock) void swiglu_kernel(SwArgs a) {
+  // The arguments of the first loads fetched in one scalar round trip.
+  asm volatile("" ::"s"(a.gu), "s"(a.rows), "s"(a.I), "s"(a.act), "s"(a.inv_nv), "s"(a.codes));
   const int nv = a.I >> 3;
   // The FP8 amax pass loads through the caches (the encode pass re-reads
   // the same gate|up right after it, and part of it is still cached: measured
