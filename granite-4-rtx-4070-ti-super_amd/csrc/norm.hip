@@ -362,6 +362,10 @@ template <int VPL, int HR, int HL>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(VPL >= 4 ? 1 : 4)))
 void norm_fp8_fused_kernel(NormArgs a, GridSync gs) {
   static_assert(kBlock == kSyncThreads, "grid_max assumes kSyncThreads-thread workgroups");
+  // Every argument of the first loads fetched in one scalar round trip.
+  asm volatile("" ::"s"(a.x), "s"(a.branch), "s"(a.w), "s"(a.rows), "s"(a.cols), "s"(a.mult),
+               "s"(a.res_out), "s"(a.eps), "s"(gs.gen), "s"(gs.slots), "s"(gs.result),
+               "s"(gs.blocks));
   __shared__ uint4 s_y[HL > 0 ? HL : 1][VPL][kBlock];
   const unsigned tag = grid_sync_tag(gs);
   V8 y[HR > 0 ? HR : 1][VPL];

@@ -177,6 +177,9 @@ static_assert(kFusedThreads == kSyncThreads && kBlock == kSyncThreads, "grid_max
 constexpr int kFusedVpt = 4;
 
 __global__ __launch_bounds__(kFusedThreads) void swiglu_fp8_fused_kernel(SwArgs a, GridSync gs) {
+  // Every argument of the first loads fetched in one scalar round trip.
+  asm volatile("" ::"s"(a.gu), "s"(a.rows), "s"(a.I), "s"(a.inv_nv), "s"(a.act), "s"(a.codes),
+               "s"(gs.gen), "s"(gs.slots), "s"(gs.result), "s"(gs.blocks));
   const unsigned tag = grid_sync_tag(gs);
   const int nv = a.I >> 3;
   const int total = a.rows * nv;
@@ -261,6 +264,8 @@ constexpr int kHoldBatch = G4_SW_HB;  // held vectors' loads in flight per lane
 constexpr int kStreamU = G4_SW_SU;  // streamed vectors' loads in flight per lane
 
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(G4_SW_WPE))) void swiglu_fp8_hold_kernel(SwArgs a, GridSync gs) {
+  asm volatile("" ::"s"(a.gu), "s"(a.rows), "s"(a.I), "s"(a.inv_nv), "s"(a.act), "s"(a.codes),
+               "s"(gs.gen), "s"(gs.slots), "s"(gs.result), "s"(gs.blocks));
   __shared__ uint4 s_hold[kHoldL > 0 ? kHoldL : 1][kBlock];
   const unsigned tag = grid_sync_tag(gs);
   const int nv = a.I >> 3;
