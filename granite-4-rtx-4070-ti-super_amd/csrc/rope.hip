@@ -81,6 +81,9 @@ __global__ __launch_bounds__(kBlock) void rope_append_kernel(RopeArgs a) {
 // 32): 40.3 us there, 32.9 us here.
 template <int BITS, int GROUP, int UPL>
 __global__ __launch_bounds__(kBlock) void rope_append_row_kernel(RopeArgs a) {
+  asm volatile("" ::"s"(a.q), "s"(a.k), "s"(a.v), "s"(a.q_stride), "s"(a.k_stride),
+               "s"(a.v_stride), "s"(a.pos_ptr), "s"(a.pos_rows), "s"(a.pt), "s"(a.arena_rows),
+               "s"(a.mr), "s"(a.units_per_row), "s"(a.Hq), "s"(a.Hk), "s"(a.cos_t), "s"(a.sin_t));
   const int lane16 = threadIdx.x & 15, grp = threadIdx.x >> 4;
   const int r = blockIdx.x;
   const int nu = a.units_per_row;
@@ -303,6 +306,7 @@ template <int NV, int RPW>
 __global__ __launch_bounds__(kBlock) void embed_rows_kernel(const int32_t* tokens, int start,
                                                             int rows, const uint16_t* emb,
                                                             int vocab, float mult, uint16_t* out) {
+  asm volatile("" ::"s"(tokens), "s"(start), "s"(rows), "s"(emb), "s"(vocab), "s"(mult), "s"(out));
   constexpr int H = NV * 8 * kBlock;
   const int r0 = blockIdx.x * RPW;
   int tok[RPW];
