@@ -699,6 +699,9 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(AttnArgs 
   __shared__ float s_w[kAttnMaxSplits / kAttnWaves];
   __shared__ float s_red[kCombineThreads / 64];
   __shared__ float s_half[kHd];
+  // The arguments fetched in one scalar round trip.
+  asm volatile("" ::"s"(a.d_pos), "s"(a.row_pos), "s"(a.part_ml), "s"(a.part_o), "s"(a.out),
+               "s"(a.nblk), "s"(a.tps), "s"(a.stride), "s"(a.window), "s"(a.kv_base), "s"(a.Hq));
   const int h = blockIdx.x, row = blockIdx.y;
   const int len = a.row_pos != nullptr ? a.row_pos[row] + 1
                                        : (a.d_pos != nullptr ? *a.d_pos : a.kv_base) + row + 1;

@@ -277,6 +277,8 @@ __global__ __launch_bounds__(kBlock) void embed_kernel(const int32_t* tokens, in
                                                        const int* d_pos, const uint16_t* emb,
                                                        int vocab, int H, float mult,
                                                        uint16_t* out) {
+  asm volatile("" ::"s"(tokens), "s"(start), "s"(d_pos), "s"(emb), "s"(vocab), "s"(H), "s"(mult),
+               "s"(out));
   const int r = blockIdx.y;
   const int tok = d_pos != nullptr ? tokens[*d_pos] : tokens[start + r];
   const bool valid = vocab < 0 || (tok >= 0 && tok < vocab);
