@@ -3,6 +3,7 @@
 // entry points that run the kernels' scalar arithmetic on the CPU.
 #include "g4_common.h"
 #include "g4_math.h"
+#include "g4_sync.h"
 #include "granite4_layerops.h"
 
 #include <atomic>
@@ -43,6 +44,12 @@ std::atomic<int> g_fp8_mode{[] {
 }  // namespace
 
 int fp8_launch_mode() { return g_fp8_mode.load(std::memory_order_relaxed); }
+
+namespace {
+std::atomic<int> g_spin_limit{kSyncSpinLimit};
+}  // namespace
+
+int fp8_sync_spin_limit() { return g_spin_limit.load(std::memory_order_relaxed); }
 
 int resident_blocks(const void* kernel, int threads) {
   static std::mutex mu;
@@ -168,6 +175,35 @@ int granite4_rope_tables_free(float* d_cos, float* d_sin) {
 int granite4_set_fp8_launch_mode(int mode) {
   if (mode != 0 && mode != 1) return -1;
   return g_fp8_mode.exchange(mode);
+}
+
+int granite4_fp8_sync_status(void* d_work, int clear) {
+  if (d_work == nullptr) return -1;
+  unsigned v = 0;
+  hipStream_t st = stream();
+  bool ok = hipMemcpyAsync(&v, work_err(d_work), sizeof v, hipMemcpyDeviceToHost, st) ==
+                hipSuccess &&
+            hipStreamSynchronize(st) == hipSuccess;
+  if (ok && clear && v != 0) {
+    // A wait that gave up can leave slots tagged for a generation that is
+    // still to come; the whole synchronisation area (slots, generation,
+    // error word, result) goes back to its zero-filled start state.
+    static const std::vector<unsigned char> zeros(kWorkRowOff - kWorkSlotsOff, 0);
+    ok = hipMemcpyAsync(static_cast<char*>(d_work) + kWorkSlotsOff, zeros.data(), zeros.size(),
+                        hipMemcpyHostToDevice, st) == hipSuccess &&
+         hipStreamSynchronize(st) == hipSuccess;
+  }
+  if (!ok) {
+    std::fprintf(stderr, "granite4: granite4_fp8_sync_status: %s\n",
+                 hipGetErrorString(hipGetLastError()));
+    return -1;
+  }
+  return v != 0 ? 1 : 0;
+}
+
+int granite4_debug_set_sync_spin_limit(int limit) {
+  if (limit < 0) return -1;
+  return g_spin_limit.exchange(limit);
 }
 
 size_t granite4_fp8_work_bytes(int rows) {

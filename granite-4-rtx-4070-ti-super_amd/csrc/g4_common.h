@@ -21,7 +21,10 @@ constexpr int kPersistBlocks = kCUs * 8;  // grid cap for grid-stride kernels
 //                      (its grid is capped at kMaxPartials)
 //   [4096, 12288)      u64 tagged slots of the single-launch form's grid
 //                      maximum (one per workgroup, at most kMaxPartials)
-//   [12288, 12544)     u32 generation word of those slots at +0, u64 tagged
+//   [12288, 12544)     u32 generation word of those slots at +0, u32 sticky
+//                      synchronisation-error word at +64 (set to 1 when a
+//                      bounded wait of the single-launch form gave up; read
+//                      and cleared by granite4_fp8_sync_status), u64 tagged
 //                      grid maximum at +128 (+ padding)
 //   [12544, ...)       f32 per row: the norm's 1 / rms from pass 1 to pass 2
 // The slots, the generation word and the grid maximum must start zero-filled.
@@ -35,6 +38,9 @@ __host__ __device__ inline unsigned long long* work_slots(void* w) {
 }
 __host__ __device__ inline unsigned* work_gen(void* w) {
   return reinterpret_cast<unsigned*>(static_cast<char*>(w) + kWorkGenOff);
+}
+__host__ __device__ inline unsigned* work_err(void* w) {
+  return reinterpret_cast<unsigned*>(static_cast<char*>(w) + kWorkGenOff + 64);
 }
 __host__ __device__ inline unsigned long long* work_result(void* w) {
   return reinterpret_cast<unsigned long long*>(static_cast<char*>(w) + kWorkGenOff + 128);
@@ -60,6 +66,11 @@ int resident_blocks(const void* kernel, int threads);
 // Process-wide FP8 launch mode (granite4_set_fp8_launch_mode): 0 = single
 // launch where the tensor fits, 1 = always two launches.
 int fp8_launch_mode();
+
+// Process-wide poll limit of the single-launch forms' bounded waits
+// (granite4_debug_set_sync_spin_limit; default kSyncSpinLimit). 0 makes every
+// wait give up at once: a host-forced failure for testing the error path.
+int fp8_sync_spin_limit();
 
 inline bool fits_int(long long v) { return v >= 0 && v <= INT_MAX; }
 

@@ -26,9 +26,13 @@
 // the occupancy before choosing this form), kSyncThreads-thread workgroups,
 // at most kSyncThreads * kSyncSlotsPerThread of them (GridSync::blocks), and one such launch at a time per
 // workspace. The waits are bounded: a slot or result that never arrives
-// (which those requirements exclude) ends the wait after kSyncSpinLimit
-// polls, and the returned maximum is NaN, so the op reports a NaN scale
-// rather than hang.
+// (which those requirements exclude) ends the wait after gs.spin_limit
+// polls (kSyncSpinLimit unless a test lowers it), the returned maximum is
+// NaN, so the op reports a NaN scale rather than hang, and the workspace's
+// sticky error word is set to 1 for the host to read
+// (granite4_fp8_sync_status). A spin limit of 0 gives up before polling:
+// workgroup 0 publishes a NaN maximum, so every workgroup of the launch
+// deterministically ends with NaN and the error word set.
 #ifndef G4_SYNC_H
 #define G4_SYNC_H
 
@@ -46,6 +50,8 @@ struct GridSync {
   unsigned long long* result;  // tagged grid maximum (gathered by workgroup 0)
   int blocks;                  // the launch's grid size (gridDim.x), passed so
                                // the gather does not read the dispatch packet
+  unsigned* err;               // sticky error word (1: a wait gave up)
+  int spin_limit;              // polls before a wait gives up
 };
 
 // Workgroup size of every launch that synchronises (a constant, so no
@@ -100,11 +106,12 @@ __device__ __forceinline__ float grid_max(float m, const GridSync& gs, unsigned 
       int spin = 0;
       for (;;) {
         v = __hip_atomic_load(gs.result, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (static_cast<unsigned>(v >> 32) == tag || ++spin >= kSyncSpinLimit) break;
+        if (static_cast<unsigned>(v >> 32) == tag || ++spin >= gs.spin_limit) break;
         __builtin_amdgcn_s_sleep(1);
       }
-      s_out = static_cast<unsigned>(v >> 32) == tag ? __uint_as_float(static_cast<unsigned>(v))
-                                                      : __builtin_nanf("");
+      const bool ok = static_cast<unsigned>(v >> 32) == tag;
+      if (!ok) __hip_atomic_store(gs.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_out = ok ? __uint_as_float(static_cast<unsigned>(v)) : __builtin_nanf("");
     }
     __syncthreads();
     return s_out;
@@ -119,8 +126,8 @@ __device__ __forceinline__ float grid_max(float m, const GridSync& gs, unsigned 
     need[k] = j > 0 && j < gs.blocks;
   }
   int spin = 0;
-  bool late = false;
-  for (;;) {
+  bool late = gs.spin_limit <= 0;
+  while (!late) {
     unsigned long long v[kSyncSlotsPerThread];
 #pragma unroll
     for (int k = 0; k < kSyncSlotsPerThread; ++k)
@@ -139,10 +146,7 @@ __device__ __forceinline__ float grid_max(float m, const GridSync& gs, unsigned 
       }
     }
     if (!any) break;
-    if (++spin >= kSyncSpinLimit) {
-      late = true;
-      break;
-    }
+    if (++spin >= gs.spin_limit) late = true;
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) mm = fmaxf(mm, __shfl_xor(mm, o));
@@ -156,7 +160,10 @@ __device__ __forceinline__ float grid_max(float m, const GridSync& gs, unsigned 
       bad |= s_red[i] != s_red[i];
       r = fmaxf(r, s_red[i]);
     }
-    if (bad) r = __builtin_nanf("");
+    if (bad) {
+      r = __builtin_nanf("");
+      __hip_atomic_store(gs.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     __hip_atomic_store(gs.result, (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(r),
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(gs.gen, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

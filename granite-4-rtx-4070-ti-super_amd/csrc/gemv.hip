@@ -538,10 +538,11 @@ int launch_gemv(const GemvArgs& a, const char* what) {
 int gemv_out(int pro, const uint16_t* x, const uint16_t* gamma, float eps,
              const uint8_t* const (&w)[3], const float (&s)[3], uint16_t* const (&o)[3],
              const int (&n)[3], int K, const char* what) {
-  const int N = n[0] + n[1] + n[2];
-  if (x == nullptr || !al16(x) || !gemv_k_ok(K) || N <= 0 ||
+  const long long N = static_cast<long long>(n[0]) + n[1] + n[2];
+  if (x == nullptr || !al16(x) || !gemv_k_ok(K) || N <= 0 || N > INT_MAX || n[0] < 0 ||
+      n[1] < 0 || n[2] < 0 ||
       (pro == kProNorm && (gamma == nullptr || !al16(gamma) || !std::isfinite(eps))) ||
-      static_cast<long long>(N) * K >= (1LL << 40)) {
+      N * K >= (1LL << 40)) {
     std::fprintf(stderr, "granite4: %s: invalid arguments (K %% 64 == 0, K <= %d)\n", what, kMaxK);
     return -1;
   }
@@ -560,7 +561,7 @@ int gemv_out(int pro, const uint16_t* x, const uint16_t* gamma, float eps,
   }
   a.seg1 = n[0];
   a.seg2 = n[0] + n[1];
-  a.N = N;
+  a.N = static_cast<int>(N);
   a.K = K;
   a.inv_k = (K & (K - 1)) == 0 ? 1.0 / K : 0.0;
   return pro == kProNorm ? launch_gemv<kProNorm, kEpiOut>(a, what)
@@ -614,7 +615,7 @@ int gemv_swiglu(int pro, const uint16_t* x, const uint16_t* gamma, float eps, co
   if (x == nullptr || wg == nullptr || wu == nullptr || out == nullptr || !al16(x) || !al16(wg) ||
       !al16(wu) || !gemv_k_ok(K) || N <= 0 || !std::isfinite(sg) || !std::isfinite(su) ||
       (pro == kProNorm && (gamma == nullptr || !al16(gamma) || !std::isfinite(eps))) ||
-      static_cast<long long>(N) * K >= (1LL << 40)) {
+      N * K >= (1LL << 40)) {
     std::fprintf(stderr, "granite4: %s: invalid arguments (K %% 64 == 0, K <= %d)\n", what, kMaxK);
     return -1;
   }
@@ -628,7 +629,7 @@ int gemv_swiglu(int pro, const uint16_t* x, const uint16_t* gamma, float eps, co
   a.s[1] = su;
   a.o[0] = out;
   a.I = N;
-  a.N = N;
+  a.N = static_cast<int>(N);
   a.K = K;
   a.inv_k = (K & (K - 1)) == 0 ? 1.0 / K : 0.0;
   return pro == kProNorm ? launch_gemv<kProNorm, kEpiSwiglu>(a, what)

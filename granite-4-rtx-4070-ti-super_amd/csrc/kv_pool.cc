@@ -197,12 +197,22 @@ bool PagedKV::reserve(int seq, std::size_t token_count, const Tokens& tokens) {
   const std::size_t need = (beyond + B - 1) / B;
   // Fail before changing anything (no partial eviction).
   if (free_.size() + lru_.size() < need) return false;
+  if (s.filled < held && pages_[s.pages.back()].cached) {
+    // The sequence was truncated inside a cached (shared, full) page: its
+    // rows already hold the page's tokens, so growing back over them is
+    // bookkeeping only. Different tokens would overwrite shared rows: refused.
+    const Page& p = pages_[s.pages.back()];
+    const std::size_t base = held - B, upto = std::min(held, token_count);
+    for (std::size_t i = s.filled; i < upto; ++i)
+      if (p.tokens[i - base] != tokens[i]) return false;
+  }
   while (free_.size() < need) evict_lru();
 
   if (s.filled < held) {  // top up the partial tail page first: pages stay dense
     Page& p = pages_[s.pages.back()];
     const std::size_t upto = std::min(held, token_count);
-    p.tokens.insert(p.tokens.end(), tokens.begin() + s.filled, tokens.begin() + upto);
+    if (!p.cached)  // a cached tail already holds these ids (checked above)
+      p.tokens.insert(p.tokens.end(), tokens.begin() + s.filled, tokens.begin() + upto);
     s.filled = upto;
   }
   while (s.filled < token_count) {
@@ -267,13 +277,18 @@ void PagedKV::truncate_sequence(int seq, std::size_t n_tokens) {
   Seq& s = seqs_[seq];
   const std::size_t B = config_.tokens_per_page;
   const std::size_t keep = (n_tokens + B - 1) / B;
+  const bool dropped = s.pages.size() > keep;
   for (std::size_t i = keep; i < s.pages.size(); ++i) put_ref(s.pages[i]);
-  if (s.pages.size() > keep) s.pages.resize(keep);
+  if (dropped) s.pages.resize(keep);
   s.filled = std::min(s.filled, n_tokens);
   if (keep > 0 && !s.pages.empty()) {
     Page& last = pages_[s.pages.back()];
     if (last.cached) {
-      s.filled = s.pages.size() * B;  // a cached page is full and shared: kept whole
+      // A cached page is full and shared: its ids stay whole. When pages were
+      // dropped the sequence keeps the whole page (as the reference does);
+      // otherwise the count is trimmed, and reserve regrows it only with the
+      // page's own tokens.
+      if (dropped) s.filled = s.pages.size() * B;
     } else {
       const std::size_t in_last = s.filled > (s.pages.size() - 1) * B ? s.filled - (s.pages.size() - 1) * B : 0;
       if (last.tokens.size() > in_last) last.tokens.resize(in_last);

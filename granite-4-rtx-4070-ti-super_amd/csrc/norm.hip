@@ -522,7 +522,8 @@ bool launch_norm_fp8_fused(const uint16_t* x, const uint16_t* branch, float mult
     return false;
   NormArgs a{x, branch, mult, w, eps, rows, cols, res_out, nullptr, codes, scale, nullptr, 0,
              nullptr, 0.0};
-  const GridSync gs{work_slots(work), work_gen(work), work_result(work), 0};
+  const GridSync gs{work_slots(work), work_gen(work), work_result(work), 0, work_err(work),
+                    fp8_sync_spin_limit()};
   return launch_fused_vpl<kNormHold, 0>(a, gs, nvec) ||
          launch_fused_vpl<kNormDeepHR, kNormDeepHL>(a, gs, nvec);
 }

@@ -301,7 +301,8 @@ __global__ __launch_bounds__(kBlock) void embed_kernel(const int32_t* tokens, in
   }
 }
 
-// Whole rows, RPW tokens per workgroup, for H = 2048 NV: the token ids
+// Whole rows, RPW tokens per workgroup, for H = NV * 8 * kBlock (NV = 2:
+// H = 4096, the width the host dispatch checks): the token ids
 // first, then every vector of the workgroup's rows in flight (NV per row per
 // thread), then the stores; the arithmetic is embed_kernel's.
 template <int NV, int RPW>

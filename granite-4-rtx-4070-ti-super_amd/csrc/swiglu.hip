@@ -486,7 +486,7 @@ int granite4_swiglu_fp8(const uint16_t* d_gu, int rows, int I, uint8_t* d_codes,
     f.codes = d_codes;
     f.scale_out = d_scale;
     const GridSync gs{work_slots(d_work), work_gen(d_work), work_result(d_work),
-                      static_cast<int>(fgrid)};
+                      static_cast<int>(fgrid), work_err(d_work), fp8_sync_spin_limit()};
     hipLaunchKernelGGL(swiglu_fp8_fused_kernel, fgrid, kFusedThreads, 0, stream(), f, gs);
     return launch_status("granite4_swiglu_fp8");
   }
@@ -497,7 +497,7 @@ int granite4_swiglu_fp8(const uint16_t* d_gu, int rows, int I, uint8_t* d_codes,
     h.codes = d_codes;
     h.scale_out = d_scale;
     const GridSync gs{work_slots(d_work), work_gen(d_work), work_result(d_work),
-                      static_cast<int>(hgrid)};
+                      static_cast<int>(hgrid), work_err(d_work), fp8_sync_spin_limit()};
     hipLaunchKernelGGL(swiglu_fp8_hold_kernel, hgrid, kBlock, 0, stream(), h, gs);
     return launch_status("granite4_swiglu_fp8");
   }

@@ -89,6 +89,8 @@ _SIG = {
     "granite4_row_table": [P, I, I, P],
     "granite4_fp8_work_bytes": [I],
     "granite4_set_fp8_launch_mode": [I],
+    "granite4_fp8_sync_status": [P, I],
+    "granite4_debug_set_sync_spin_limit": [I],
     "granite4_attn_split_scratch_bytes": [I, I, I],
     "granite4_attn_split": [P, P, P, F, I, I, I, I, P, I, I, P, P, P, P, P, P, I, P, P, I, P, I,
                             P, P, P, I, P, P, I, I, I],
@@ -210,6 +212,23 @@ def set_fp8_launch_mode(mode):
     prev = _lib.granite4_set_fp8_launch_mode(mode)
     if prev < 0:
         raise ValueError(f"FP8 launch mode {mode}")
+    return prev
+
+
+def fp8_sync_status(work, clear=False):
+    """granite4_fp8_sync_status: 0 if no single-launch FP8 call on `work`
+    gave up waiting (NaN scale) since the last clear, 1 if one did."""
+    rc = _lib.granite4_fp8_sync_status(_ptr(work), int(bool(clear)))
+    if rc < 0:
+        raise Granite4Error("granite4_fp8_sync_status failed")
+    return rc
+
+
+def set_sync_spin_limit(limit):
+    """granite4_debug_set_sync_spin_limit (test hook). Returns the previous limit."""
+    prev = _lib.granite4_debug_set_sync_spin_limit(int(limit))
+    if prev < 0:
+        raise ValueError(f"spin limit {limit}")
     return prev
 
 

@@ -241,8 +241,32 @@ size_t granite4_fp8_work_bytes(int rows);
  * resident grid, else two; 1 = always two launches (also selected at load by
  * the environment variable G4_FP8_SINGLE_LAUNCH=0). Both forms give identical
  * codes and scales. Returns the previous mode, -1 for another value. No
- * reference counterpart (a tuning switch). */
+ * reference counterpart (a tuning switch).
+ *
+ * The single-launch form's workgroups meet once inside the launch, so it
+ * needs every workgroup of its grid resident at the same time. The library
+ * sizes the grid from the occupancy query, which holds when the call has the
+ * device to itself. Another stream's kernels (or another process's) holding
+ * CUs for longer than the bounded wait (about 2^20 polls), or two
+ * single-launch calls in flight at once on different streams, break that.
+ * The wait then gives up instead of hanging: the scale written is NaN, and
+ * the workspace's sticky error word is set. A caller that overlaps streams on
+ * one device selects mode 1, whose two launches need no co-residency. */
 int granite4_set_fp8_launch_mode(int mode);
+/* Reads the workspace's sticky synchronisation-error word: 0 if no
+ * single-launch FP8 call on d_work gave up waiting since the last clear, 1
+ * if one did (its scale is NaN), -1 on a HIP error. clear != 0 resets the
+ * word and the workspace's synchronisation slots to their zero-filled start
+ * (a wait that gave up can leave a slot tagged for a later call; until the
+ * clear, later calls on the workspace are not reliable). Synchronises the calling thread's stream (not for use inside graph
+ * capture). No reference counterpart. */
+int granite4_fp8_sync_status(void* d_work, int clear);
+/* Test hook: sets the process-wide poll limit of the single-launch forms'
+ * bounded waits (default 2^20) and returns the previous one, -1 for a
+ * negative limit. 0 makes every wait give up at once, so a test can drive
+ * the error path while every kernel still exits normally. No reference
+ * counterpart. */
+int granite4_debug_set_sync_spin_limit(int limit);
 int granite4_add_rmsnorm_fp8(const uint16_t* d_res, const uint16_t* d_branch, float resid_mult,
                              const uint16_t* d_w, float eps, int rows, int cols,
                              uint16_t* d_res_out, uint8_t* d_codes, float* d_scale,

@@ -57,6 +57,11 @@ def test_argument_validation_returns_minus_one():
                                     None, None, 8, 48, 0, 1, 8, 4096, 8, 8, 8, 8, 16) == -1  # group
     assert lib.granite4_embed_rows(8, 0, 8, 100, 4096, 1.0, 8) == -1
     assert lib.granite4_rope_tables_build(1e7, 127, 16, None, None) == -1
+    # a negative segment is rejected even when the total is positive
+    assert lib.granite4_gemv_qkv(256, 256, 256, 256, 1.0, 1.0, 1.0, -8, 16, 0, 4096, 256, 256,
+                                 256) == -1
+    assert lib.granite4_fp8_sync_status(None, 0) == -1
+    assert lib.granite4_debug_set_sync_spin_limit(-1) == -1
 
 
 def test_row_table_host_matches_oracle_and_golden():

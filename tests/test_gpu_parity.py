@@ -627,3 +627,54 @@ def test_out_of_range_rows_are_skipped(tables):
     k = host(arena.k)
     assert (k[:, 1:5] == 0xEE).all() and (k[:, 6:] == 0xEE).all()
     assert not (k[:, 0] == 0xEE).all() and not (k[:, 5] == 0xEE).all()
+
+
+# ----------------------------------------------------------------------------- grid-sync failure
+@pytest.mark.parametrize("op,rows", [("norm", 512), ("norm", 8192), ("swiglu", 512),
+                                     ("swiglu", 2048)])
+def test_fp8_single_launch_wait_give_up_is_reported(op, rows):
+    """The single-launch FP8 forms' bounded wait, forced by the host to give
+    up at once (spin limit 0: workgroup 0 publishes a NaN maximum without
+    polling, so every kernel exits normally): the scale is NaN, the sticky
+    error word reads 1 until cleared, and after the clear the same workspace
+    gives correct results again."""
+    note(f"fp8 sync give-up {op} rows={rows}")
+    work = L.fp8_workspace()
+    assert L.fp8_sync_status(work) == 0
+    if op == "norm":
+        cols = 4096
+        x = dev(_hidden(rows, cols, 0xD1))
+        w_h = ol.normal_bf16(0xD2, 1.0, 0.1, cols)
+        w = dev(w_h)
+        codes = torch.empty((rows, cols), dtype=torch.uint8, device="cuda")
+
+        def run(scale):
+            L.call("granite4_add_rmsnorm_fp8", x, None, 1.0, w, 1e-5, rows, cols, None, codes,
+                   scale, work)
+    else:
+        I_ = 12800
+        gu = dev(ol.normal_bf16(0xD3, 0.0, 1.0, rows * 2 * I_).reshape(rows, 2 * I_))
+        codes = torch.empty((rows, I_), dtype=torch.uint8, device="cuda")
+
+        def run(scale):
+            L.call("granite4_swiglu_fp8", gu, rows, I_, codes, scale, work, None)
+    good = torch.empty(1, dtype=torch.float32, device="cuda")
+    run(good)
+    good_codes = host(codes).copy()
+    assert L.fp8_sync_status(work) == 0
+    prev = L.set_sync_spin_limit(0)
+    try:
+        bad = torch.empty(1, dtype=torch.float32, device="cuda")
+        run(bad)
+        torch.cuda.synchronize()
+    finally:
+        L.set_sync_spin_limit(prev)
+    assert np.isnan(host(bad)[0])
+    assert L.fp8_sync_status(work) == 1
+    assert L.fp8_sync_status(work, clear=True) == 1
+    assert L.fp8_sync_status(work) == 0
+    again = torch.empty(1, dtype=torch.float32, device="cuda")
+    run(again)
+    assert host(again)[0] == host(good)[0]
+    np.testing.assert_array_equal(host(codes), good_codes)
+    assert L.fp8_sync_status(work) == 0

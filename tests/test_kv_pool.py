@@ -210,6 +210,26 @@ def test_truncate_keeps_cached_pages_whole():
     assert p.mark_written(q, 1)  # the regrown page is complete again
 
 
+def test_truncate_inside_cached_tail_without_drop():
+    """No page dropped: the count is min(filled, n) as in the reference
+    (kv_pool.cc:319-321), even when the tail page is cached. Growing back
+    over the cached page's own tokens is allowed; other tokens would
+    overwrite shared rows and are refused with nothing changed."""
+    p = small_pool()
+    s = p.create_sequence()
+    t = toks(0, 8)
+    assert p.reserve(s, 8, t)
+    assert p.mark_written(s, 0) and p.mark_written(s, 1)
+    p.truncate_sequence(s, 6)
+    assert p.sequence_tokens(s) == 6 and len(p.block_table(s)) == 2
+    free = p.free_pages()
+    assert not p.reserve(s, 8, t[:6] + [901, 902])
+    assert p.sequence_tokens(s) == 6 and p.free_pages() == free
+    assert p.reserve(s, 10, t + [5, 6])  # the page's own ids, then a new page
+    assert p.sequence_tokens(s) == 10 and len(p.block_table(s)) == 3
+    assert p.page_in_cache(p.block_table(s)[1])
+
+
 # --------------------------------------------------------- KvPoolController
 
 def test_slot_capacity():

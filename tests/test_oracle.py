@@ -20,6 +20,17 @@ from oracle_lib import lib
 G = np.load(os.path.join(os.path.dirname(__file__), "golden", "golden.npz"))
 
 
+@pytest.fixture
+def ref():
+    """The reference-host-math shim (oracle/_ref). Loaded only when a test that
+    uses it runs, never at collection: oracle/_ref is built in the container
+    from the reference tree and does not travel to the GPU box."""
+    r = ol.ref_lib()
+    if r is None:
+        pytest.skip("oracle/_ref not built (no reference tree)")
+    return r
+
+
 # --------------------------------------------------------------------------- rng / bf16
 def test_rng_matches_reference_stream():
     for seed in (0x4242, 0x1337, 0):
@@ -110,9 +121,7 @@ def test_fp8_quantize_zero_tensor_and_saturation():
     assert codes[2] == 0
 
 
-@pytest.mark.skipif(ol.ref_lib() is None, reason="oracle/_ref not built (no reference tree)")
-def test_fp8_encode_random_doubles_vs_reference_shim():
-    ref = ol.ref_lib()
+def test_fp8_encode_random_doubles_vs_reference_shim(ref):
     rs = np.random.default_rng(0xC0FFEE)
     xs = np.concatenate([rs.normal(0, 100, 100000), np.exp2(rs.uniform(-20, 10, 100000))])
     for x in xs:
@@ -154,9 +163,7 @@ def test_rmsnorm_closed_forms():
     assert np.all(np.abs(got - ref) <= np.abs(ref) * 2**-7 + 1e-30)
 
 
-@pytest.mark.skipif(ol.ref_lib() is None, reason="oracle/_ref not built (no reference tree)")
-def test_rmsnorm_vs_reference_shim_outliers():
-    ref = ol.ref_lib()
+def test_rmsnorm_vs_reference_shim_outliers(ref):
     rows, cols = 16, 4096
     x = ol.normal_bf16(11, 0.0, 1.0, rows * cols).reshape(rows, cols)
     xf = ol.bf16_to_f32(x) * np.where(np.arange(cols) % 97 == 0, 20.0, 1.0)
