@@ -178,6 +178,7 @@ int granite4_set_fp8_launch_mode(int mode) {
 }
 
 int granite4_fp8_sync_status(void* d_work, int clear) {
+  if (d_work == nullptr) d_work = static_scratch("granite4_fp8_sync_status");
   if (d_work == nullptr) return -1;
   unsigned v = 0;
   hipStream_t st = stream();

@@ -67,6 +67,10 @@ int resident_blocks(const void* kernel, int threads);
 // launch where the tensor fits, 1 = always two launches.
 int fp8_launch_mode();
 
+// The current device's static FP8 scratch (granite4_add_rmsnorm_fp8_noalloc):
+// its device address, set up on first use; nullptr on failure.
+void* static_scratch(const char* what);
+
 // Process-wide poll limit of the single-launch forms' bounded waits
 // (granite4_debug_set_sync_spin_limit; default kSyncSpinLimit). 0 makes every
 // wait give up at once: a host-forced failure for testing the error path.

@@ -32,6 +32,7 @@
 #include "granite4_layerops.h"
 
 #include <cstdlib>
+#include <mutex>
 #include <type_traits>
 
 static_assert(g4::kMaxPartials == GRANITE4_FP8_MAX_PARTIALS, "workspace layout");
@@ -545,7 +546,90 @@ int rmsnorm_ref_api(const uint16_t* d_x, const uint16_t* d_w, float eps, int row
   return launch_norm<kOutBf16>(a, what);
 }
 
+int add_rmsnorm_fp8_impl(const uint16_t* d_res, const uint16_t* d_branch, float resid_mult,
+                         const uint16_t* d_w, float eps, int rows, int cols, uint16_t* d_res_out,
+                         uint8_t* d_codes, float* d_scale, void* d_work, const char* what) {
+  if (!norm_args_ok(d_res, d_w, eps, rows, cols) || !std::isfinite(resid_mult) ||
+      d_codes == nullptr || d_scale == nullptr || d_work == nullptr) {
+    std::fprintf(stderr, "granite4: %s: invalid arguments\n", what);
+    return -1;
+  }
+  uint16_t* res_out = d_branch != nullptr ? d_res_out : nullptr;
+  if (launch_norm_fp8_fused(d_res, d_branch, resid_mult, d_w, eps, rows, cols, res_out, d_codes,
+                            d_scale, d_work))
+    return launch_status(what);
+  NormArgs p1{d_res, d_branch, resid_mult, d_w, eps, rows, cols,
+              res_out, nullptr, nullptr, nullptr, work_partials(d_work), 0,
+              work_row_r(d_work), 0.0};
+  if (launch_norm<kOutAmax>(p1, "granite4_add_rmsnorm_fp8 (amax)") != 0) return -1;
+  // Pass 2 reads the stored residual when there is one (it may alias d_res).
+  NormArgs p2 = p1;
+  if (res_out != nullptr) {
+    p2.x = res_out;
+    p2.branch = nullptr;
+  }
+  p2.res_out = nullptr;
+  p2.codes = d_codes;
+  p2.scale_out = d_scale;
+  return launch_norm<kOutFp8>(p2, "granite4_add_rmsnorm_fp8 (encode)");
+}
+
 }  // namespace
+
+// ---------------------------------------------------------------------------
+// Static scratch for granite4_add_rmsnorm_fp8_noalloc: the FP8 workspace
+// (partials, synchronisation slots, generation / error / result words, one
+// f32 1 / rms per row) for up to kNoAllocMaxRows rows, in device memory the
+// code object reserves, so the entry point never allocates. Each GPU holds
+// its own copy (at its own address) until the process ends; every call on a
+// GPU shares it, so calls that overlap on one GPU race.
+constexpr int kNoAllocMaxRows = 65536;
+constexpr size_t kNoAllocScratchBytes = kWorkRowOff + 4u * kNoAllocMaxRows;  // 274,688 B
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+
+namespace {
+// Zero-fills n 32-bit words (a kernel rather than hipMemsetAsync, so a
+// caller may capture it in a graph).
+__global__ __launch_bounds__(kBlock) void scratch_clear_kernel(unsigned* p, int n) {
+  for (int i = blockIdx.x * kBlock + threadIdx.x; i < n; i += gridDim.x * kBlock) p[i] = 0u;
+}
+}  // namespace
+
+// The device address of the current device's `scratch` (the host-side name
+// is only a stand-in), looked up once per device with that device current;
+// the first call on a device also zero-fills its synchronisation area on the
+// calling stream (the slots and generation word must start zero). The
+// per-row and partial areas need no clearing: each call writes them before
+// reading them. nullptr (with a message) on failure.
+void* static_scratch(const char* what) {
+  static std::mutex mu;
+  static void* ptrs[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    std::fprintf(stderr, "granite4: %s: no usable current device\n", what);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (ptrs[dev] != nullptr) return ptrs[dev];
+  void* ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || ptr == nullptr) {
+    (void)hipGetLastError();
+    std::fprintf(stderr, "granite4: %s: hipGetSymbolAddress(scratch) failed: %s\n", what,
+                 hipGetErrorString(e));
+    return nullptr;
+  }
+  constexpr int words = static_cast<int>(kNoAllocScratchBytes / 4);
+  hipLaunchKernelGGL(scratch_clear_kernel, (words + kBlock - 1) / kBlock, kBlock, 0, stream(),
+                     static_cast<unsigned*>(ptr), words);
+  if (launch_status(what) != 0) return nullptr;
+  ptrs[dev] = ptr;
+  return ptr;
+}
+
 }  // namespace g4
 
 using namespace g4;
@@ -581,29 +665,25 @@ int granite4_add_rmsnorm_fp8(const uint16_t* d_res, const uint16_t* d_branch, fl
                              const uint16_t* d_w, float eps, int rows, int cols,
                              uint16_t* d_res_out, uint8_t* d_codes, float* d_scale,
                              void* d_work) {
-  if (!norm_args_ok(d_res, d_w, eps, rows, cols) || !std::isfinite(resid_mult) ||
-      d_codes == nullptr || d_scale == nullptr || d_work == nullptr) {
-    std::fprintf(stderr, "granite4: granite4_add_rmsnorm_fp8: invalid arguments\n");
+  return add_rmsnorm_fp8_impl(d_res, d_branch, resid_mult, d_w, eps, rows, cols, d_res_out, d_codes,
+                              d_scale, d_work, "granite4_add_rmsnorm_fp8");
+}
+
+int granite4_add_rmsnorm_fp8_noalloc(const uint16_t* d_res, const uint16_t* d_branch,
+                                     float resid_mult, const uint16_t* d_w, float eps, int rows,
+                                     int cols, uint16_t* d_res_out, uint8_t* d_codes,
+                                     float* d_scale) {
+  if (rows > kNoAllocMaxRows) {
+    std::fprintf(stderr,
+                 "granite4: granite4_add_rmsnorm_fp8_noalloc: %d rows exceed the static "
+                 "scratch's maximum of %d (use granite4_add_rmsnorm_fp8 with a workspace)\n",
+                 rows, kNoAllocMaxRows);
     return -1;
   }
-  uint16_t* res_out = d_branch != nullptr ? d_res_out : nullptr;
-  if (launch_norm_fp8_fused(d_res, d_branch, resid_mult, d_w, eps, rows, cols, res_out, d_codes,
-                            d_scale, d_work))
-    return launch_status("granite4_add_rmsnorm_fp8");
-  NormArgs p1{d_res, d_branch, resid_mult, d_w, eps, rows, cols,
-              res_out, nullptr, nullptr, nullptr, work_partials(d_work), 0,
-              work_row_r(d_work), 0.0};
-  if (launch_norm<kOutAmax>(p1, "granite4_add_rmsnorm_fp8 (amax)") != 0) return -1;
-  // Pass 2 reads the stored residual when there is one (it may alias d_res).
-  NormArgs p2 = p1;
-  if (res_out != nullptr) {
-    p2.x = res_out;
-    p2.branch = nullptr;
-  }
-  p2.res_out = nullptr;
-  p2.codes = d_codes;
-  p2.scale_out = d_scale;
-  return launch_norm<kOutFp8>(p2, "granite4_add_rmsnorm_fp8 (encode)");
+  void* work = static_scratch("granite4_add_rmsnorm_fp8_noalloc");
+  if (work == nullptr) return -1;
+  return add_rmsnorm_fp8_impl(d_res, d_branch, resid_mult, d_w, eps, rows, cols, d_res_out, d_codes,
+                              d_scale, work, "granite4_add_rmsnorm_fp8_noalloc");
 }
 
 }  // extern "C"

@@ -81,6 +81,7 @@ _SIG = {
     "granite4_embed_at_pos": [P, P, P, I, I, F, P],
     "granite4_add_rmsnorm": [P, P, F, P, F, I, I, P, P],
     "granite4_add_rmsnorm_fp8": [P, P, F, P, F, I, I, P, P, P, P],
+    "granite4_add_rmsnorm_fp8_noalloc": [P, P, F, P, F, I, I, P, P, P],
     "granite4_swiglu": [P, I, I, P],
     "granite4_swiglu_fp8": [P, I, I, P, P, P, P],
     "granite4_rope_append": [P, L, P, L, P, L, P, P, I, I, I, I, I, I, P, P, P, I, I, I, I, P, L,

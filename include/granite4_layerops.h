@@ -259,7 +259,8 @@ int granite4_set_fp8_launch_mode(int mode);
  * word and the workspace's synchronisation slots to their zero-filled start
  * (a wait that gave up can leave a slot tagged for a later call; until the
  * clear, later calls on the workspace are not reliable). Synchronises the calling thread's stream (not for use inside graph
- * capture). No reference counterpart. */
+ * capture). d_work NULL reads the current device's static scratch of
+ * granite4_add_rmsnorm_fp8_noalloc. No reference counterpart. */
 int granite4_fp8_sync_status(void* d_work, int clear);
 /* Test hook: sets the process-wide poll limit of the single-launch forms'
  * bounded waits (default 2^20) and returns the previous one, -1 for a
@@ -271,6 +272,21 @@ int granite4_add_rmsnorm_fp8(const uint16_t* d_res, const uint16_t* d_branch, fl
                              const uint16_t* d_w, float eps, int rows, int cols,
                              uint16_t* d_res_out, uint8_t* d_codes, float* d_scale,
                              void* d_work);
+
+/* No reference counterpart: for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). granite4_add_rmsnorm_fp8 without the d_work argument: its
+ * workspace is a static device array in the library (274,688 bytes per GPU,
+ * held until the process ends), so the call allocates nothing. rows <= 65536
+ * (-1 with a message beyond that). Every call on one GPU shares that array:
+ * calls that overlap on one GPU (other streams, other host threads) race and
+ * must be serialised by the caller. The first call on a device zero-fills
+ * the array's synchronisation area with a kernel on the calling stream.
+ * granite4_fp8_sync_status(NULL, clear) reads its error word. */
+int granite4_add_rmsnorm_fp8_noalloc(const uint16_t* d_res, const uint16_t* d_branch,
+                                     float resid_mult, const uint16_t* d_w, float eps, int rows,
+                                     int cols, uint16_t* d_res_out, uint8_t* d_codes,
+                                     float* d_scale);
 
 /* SwiGLU from bf16 gate|up rows gu [rows][2I] (gate at [r][i], up at
  * [r][I + i]; prefill_gemm.cu:1194-1203 with bf16 inputs):
