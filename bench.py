@@ -46,13 +46,23 @@ B_ROPE = {16: B_ROPE_COMMON + 2 * HK * D * 2,
           "k5v4g32": B_ROPE_COMMON + HK * (80 + 64) + 2 * HK * 4 * 4}
 
 
-# HBM bytes per swiglu_fp8 call at T=512 (one launch, swiglu_fp8_fused_kernel),
-# measured with two rocprofv3 --pmc runs of `bench.py --only t512` (FETCH_SIZE,
-# then WRITE_SIZE, KiB per dispatch): fetch 12925.4 KiB x 2.0 + write 6432.1
-# KiB x 1.0. The factors are what the same counters read for the known-size
-# copy probe (`bench.py --only probe`): FETCH_SIZE half the bytes, WRITE_SIZE
-# all of them.
-SWIGLU_FP8_T512_TRAFFIC = int(12925.4 * 2.0 * 1024 + 6432.1 * 1024)
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "layerops_prefill_T512_hbm_traffic.md")
+
+
+def profiled_traffic(kernel, path=TRAFFIC_PROFILE):
+    """HBM bytes per dispatch of `kernel` from the committed rocprofv3 summary
+    (two --pmc runs of `bench.py --only t512`: FETCH_SIZE, then WRITE_SIZE, KiB
+    per dispatch). The table's scaled columns (MiB fetched x2.0 and written
+    x1.0, the factors the known-size copy probe gives these counters) are
+    summed. None if the summary has no row for the kernel."""
+    try:
+        for line in open(path):
+            cells = [c.strip() for c in line.strip().strip("|").split("|")]
+            if len(cells) >= 6 and cells[0].strip("`").startswith(kernel):
+                return int((float(cells[4]) + float(cells[5])) * (1 << 20))
+    except (OSError, ValueError):
+        pass
+    return None
 
 
 def per_launch_extra(op):
@@ -70,7 +80,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline + decode only")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["t512", "t8192", "decode", "t8", "stress", "tN", "probe",
+    ap.add_argument("--only", choices=["t512", "t8192", "decode", "t8", "stress", "tN", "probe", "floor", "t1",
                                        "attn", "gemm", "decode_gemv"],
                     help="run one configuration and print its detail (profiling runs)")
     ap.add_argument("--T", type=int, default=1024, help="token count for --only tN")
@@ -216,6 +226,10 @@ def main():
             r = measure_ops(8192, 2, 5, 32, 57344, "k5v4g32", args.steps, args.warmup)
         elif args.only == "probe":
             r = bench_probe(torch, L, stream, timed)
+        elif args.only == "t1":
+            r = bench_t1_ops(torch, L, randn, timed, cos_t, sin_t, emb, gamma)
+        elif args.only == "floor":
+            r = bench_floor(torch, L, timed, work)
         elif args.only == "tN":
             r = measure_ops(args.T, max(2, min(8, 4096 // args.T)), 8, 128, 0, 8, args.steps,
                             args.warmup)
@@ -247,6 +261,14 @@ def main():
     decode = bench_decode(torch, L, randn, cos_t, sin_t, emb, gamma, stream, args)
     log(json.dumps(decode))
     result_extra["decode_T1"] = decode
+
+    log("config 1: each op alone at T=1")
+    result_extra["decode_T1_ops"] = bench_t1_ops(torch, L, randn, timed, cos_t, sin_t, emb, gamma)
+    log(json.dumps(result_extra["decode_T1_ops"]))
+
+    log("the fixed floor under the T=512 ops (launch, grid synchronisation, same-size copies)")
+    result_extra["floor_T512"] = bench_floor(torch, L, timed, work)
+    log(json.dumps(result_extra["floor_T512"]))
 
     if not args.quick:
         log("config 1 + attention: the decode step with the split-KV attention per layer")
@@ -309,9 +331,14 @@ def main():
         "roofline": {"bound": "hbm", "kernel": "swiglu_fp8 (single launch: swiglu_fp8_fused_kernel)",
                      "achieved": dom["GBps"], "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom["GBps"] / PEAK_GBS, 4),
-                     "traffic": SWIGLU_FP8_T512_TRAFFIC},
+                     "traffic": profiled_traffic("swiglu_fp8_fused_kernel"),
+                     "traffic_source": "profiles/layerops_prefill_T512_hbm_traffic.md"},
         "cpu_baseline": cpu,
         "measured_probe_GBps": result_extra["probe"],
+        "T1_ops": {k: {"us": v["us"], "GBps": v["GBps"], "frac_peak": v["frac_peak"]}
+                   for k, v in result_extra["decode_T1_ops"].items()},
+        "T512_ops": {k: {"us": v["us"], "GBps": v["GBps"], "frac_peak": v.get("frac_peak")}
+                     for k, v in c3.items()},
         "decode_us_per_step": result_extra["decode_T1_gemv"]["with_attention"]["fused_us"],
         "decode_non_gemm_overhead_us": {
             "with_attention": result_extra["decode_T1_gemv"]["with_attention"][
@@ -404,6 +431,47 @@ def bench_decode(torch, L, randn, cos_t, sin_t, emb, gamma, stream, args, layers
             "graph_us_per_step": round(graph_us, 2),
             "eager_us_per_step": round(eager_us, 2), "ideal_bytes": ideal,
             "ideal_us_at_peak": round(ideal / PEAK_GBS / 1e3, 3)}
+
+
+def bench_t1_ops(torch, L, randn, timed, cos_t, sin_t, emb, gamma, nsets=8):
+    """BASELINE config 1's ops one at a time at T = 1 (bf16 outputs), each
+    timed as the prefill ops are (a graph of back-to-back calls over rotating
+    input sets): µs per call, algorithmic bytes and GB/s. At this size every
+    op is one launch's fixed cost (see bench_floor)."""
+    dev = "cuda"
+    stride = 8192
+    toks = torch.randint(0, VOCAB, (8192,), dtype=torch.int32, device=dev)
+    pt = torch.randperm(stride, device=dev).to(torch.int32)
+    sets = []
+    for i in range(nsets):
+        sets.append({"pos": torch.tensor([1000 + 7 * i], dtype=torch.int32, device=dev),
+                     "res": randn((1, H)), "br": randn((1, H)),
+                     "res_out": torch.empty((1, H), dtype=torch.bfloat16, device=dev),
+                     "normed": torch.empty((1, H), dtype=torch.bfloat16, device=dev),
+                     "gu": randn((1, 2 * I)), "act": torch.empty((1, I), dtype=torch.bfloat16,
+                                                                 device=dev),
+                     "q": randn((1, HQ * D)), "k": randn((1, HK * D)), "v": randn((1, HK * D)),
+                     "q_rot": torch.empty((1, HQ * D), dtype=torch.bfloat16, device=dev),
+                     "arena": L.KvArena(16, HK, stride)})
+    ops = {
+        "embed": (lambda s: L.call("granite4_embed_at_pos", toks, s["pos"], emb, VOCAB, H, 1.0,
+                                   s["res_out"]), B_EMBED),
+        "add_rmsnorm": (lambda s: L.call("granite4_add_rmsnorm", s["res"], s["br"], 1.0, gamma,
+                                         1e-5, 1, H, s["res_out"], s["normed"]),
+                        B_NORM_BF16 + per_launch_extra("norm_bf16")),
+        "swiglu": (lambda s: L.call("granite4_swiglu", s["gu"], 1, I, s["act"]), B_SWIGLU_BF16),
+        "rope_append_bf16": (lambda s: L.call(
+            "granite4_rope_append_at_pos", s["q"], s["k"], s["v"], cos_t, sin_t, 65536, s["pos"],
+            pt, HQ, HK, D, 16, 128, s["q_rot"], s["arena"].k, s["arena"].v, None, None, stride),
+            B_ROPE[16]),
+    }
+    out = {}
+    for name, (fn, b) in ops.items():
+        ms = timed(fn, 40, 4, sets)
+        gbs = b / (ms * 1e-3) / 1e9
+        out[name] = {"us": round(ms * 1e3, 3), "bytes": int(b), "GBps": round(gbs, 2),
+                     "frac_peak": round(gbs / PEAK_GBS, 5)}
+    return out
 
 
 def graph_us(torch, L, stream, step, reps=20):
@@ -987,6 +1055,45 @@ def bench_probe(torch, L, stream, timed):
     return out
 
 
+def bench_floor(torch, L, timed, work, T=512):
+    """The fixed floor under the T=512 ops, each measured as the ops are (a
+    graph of back-to-back calls over 8 rotating buffer sets): an empty launch;
+    one grid synchronisation with no data; and, per op, a kernel that only
+    reads the op's input bytes and writes its output bytes in one launch
+    (1024 workgroups, every load in flight), without and with one grid
+    synchronisation between the loads and the stores."""
+    out = {}
+    steps = 40
+    one = torch.zeros(16, dtype=torch.uint8, device="cuda")
+    for blocks in (1, 512, 1024):
+        ms = timed(lambda st, b=blocks: L.call("granite4_floor_probe", None, 0, None, 0, None, 0, b),
+                   steps, 4, [None])
+        out[f"empty_{blocks}wg_us"] = round(ms * 1e3, 3)
+    for blocks in (512, 1024):
+        ms = timed(lambda st, b=blocks: L.call("granite4_floor_probe", one, 0, one, 0, work, 2, b),
+                   steps, 4, [None])
+        out[f"sync_only_{blocks}wg_us"] = round(ms * 1e3, 3)
+    ops = {"embed": (2 * H * T, 2 * H * T),
+           "add_rmsnorm_fp8": (4 * H * T + 2 * H, 3 * H * T),
+           "swiglu_fp8": (4 * I * T, I * T),
+           "rope_append_8": (((HQ + 2 * HK) * D * 2 + 512 + 4) * T,
+                             (HQ * D * 2 + 2 * HK * D + 2 * HK * 4) * T)}
+    for name, (rb, wb) in ops.items():
+        rb16, wb16 = (rb + 15) // 16 * 16, (wb + 15) // 16 * 16
+        sets = [(torch.ones(rb16, dtype=torch.uint8, device="cuda"),
+                 torch.empty(wb16, dtype=torch.uint8, device="cuda")) for _ in range(8)]
+        r = {"read_B": rb, "write_B": wb}
+        for mode, key in ((1, "copy"), (2, "copy_sync")):
+            ms = timed(lambda st, m=mode: L.call("granite4_floor_probe", st[0], rb16, st[1], wb16,
+                                                  work, m, 1024), steps, 4, sets)
+            r[f"{key}_us"] = round(ms * 1e3, 3)
+            r[f"{key}_frac_peak"] = round((rb + wb) / (ms * 1e-3) / 1e9 / PEAK_GBS, 4)
+        out[name] = r
+        del sets
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_stress(torch, L, randn, cos_t, sin_t, gamma, stream, layers=40, T=32768):
     dev = "cuda"
     res = randn((T, H))
@@ -1023,58 +1130,36 @@ def bench_stress(torch, L, randn, cos_t, sin_t, gamma, stream, layers=40, T=3276
             "frac_peak": round(total / (ms * 1e-3) / 1e9 / PEAK_GBS, 4)}
 
 
-def cpu_baseline(budget_s=12.0):
-    """The oracle (scalar C) on a bounded sample of the headline workload: the
-    T=512 step's four ops over `rows`-token samples for about budget_s seconds,
-    half on one thread and half on one thread per core of the box's share;
-    GB/s in the same ideal-byte units (value = all cores)."""
+def cpu_baseline(budget_s=16.0):
+    """The oracle (scalar C, oracle/g4_cpu_step.c) on the headline workload
+    itself: the whole T=512 step (embed from the full 100352-row table,
+    add+RMSNorm -> FP8, SwiGLU -> FP8, RoPE + int8 KV), about budget_s / 2
+    seconds on one thread, then the same on every core of the box's share,
+    the step split by token rows with the FP8 scales agreed between two
+    barriers. Inputs are built before the timed loop; GB/s in the GPU's
+    ideal-byte units (value = all cores)."""
+    import ctypes
     import oracle_lib as ol
-    rows = 16
-    rs = 0x5EED
-    emb = ol.normal_bf16(rs, 0.0, 0.02, 4096 * H).reshape(4096, H)
-    tok = (ol.u32(rs + 1, rows) % 4096).astype(np.int32)
-    res = ol.normal_bf16(rs + 2, 0.0, 1.0, rows * H).reshape(rows, H)
-    br = ol.normal_bf16(rs + 3, 0.0, 1.0, rows * H).reshape(rows, H)
-    w = ol.normal_bf16(rs + 4, 1.0, 0.1, H)
-    gu = ol.normal_bf16(rs + 5, 0.0, 1.0, rows * 2 * I).reshape(rows, 2 * I)
-    qkv = ol.normal_bf16(rs + 6, 0.0, 1.0, rows * 48 * D).reshape(rows, 48 * D)
-    c, s = ol.rope_tables(1e7, D, 1024)
-    stride = 1024
-    pos = np.arange(rows)
-
-    def step():
-        ol.embed_rows(tok, emb, 1.0)
-        ro, no = ol.add_rmsnorm(res, br, 1.0, w, 1e-5)
-        ol.fp8_quantize(no)
-        ol.fp8_quantize(ol.swiglu(gu))
-        ol.rope_append(qkv[:, :HQ * D], qkv[:, HQ * D:40 * D], qkv[:, 40 * D:], c, s, pos, pos, 8,
-                       128, stride, HK)
-
-    def run(budget):
-        n = 0
-        t0 = time.perf_counter()
-        while time.perf_counter() - t0 < budget:
-            step()
-            n += 1
-        return n, time.perf_counter() - t0
-
-    step()
-    step_bytes = rows * (B_EMBED + B_NORM_FP8 + B_SWIGLU_FP8 + B_ROPE[8])
-    # One thread, then one independent sample per thread on every core of the
-    # box's share (the oracle's C calls release the GIL).
-    n1, t1 = run(budget_s / 2)
+    fn = ol.lib.g4o_cpu_step_bench
+    fn.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_double, ctypes.POINTER(ctypes.c_double)]
+    fn.restype = ctypes.c_int
+    T = 512
+    step_bytes = T * (B_EMBED + B_NORM_FP8 + B_SWIGLU_FP8 + B_ROPE[8]) + \
+        per_launch_extra("norm_fp8") + per_launch_extra("swiglu_fp8")
     try:
-        cores = len(os.sched_getaffinity(0))
+        avail = len(os.sched_getaffinity(0))
     except AttributeError:
-        cores = os.cpu_count() or 1
-    cores = max(1, min(cores, 16))
-    import concurrent.futures as cf
-    with cf.ThreadPoolExecutor(cores) as ex:
-        outs = list(ex.map(run, [budget_s / 2] * cores))
-    nt = sum(o[0] for o in outs)
-    tt = max(o[1] for o in outs)
-    gbs1 = step_bytes * n1 / t1 / 1e9
-    gbst = step_bytes * nt / tt / 1e9
+        avail = os.cpu_count() or 1
+    # The GPU box's CPU share is 16 cores per GPU: use all of them (fewer if
+    # the process may run on fewer).
+    cores = max(1, min(avail, 16))
+    wall = ctypes.c_double()
+    n1 = fn(T, 1, budget_s / 2, ctypes.byref(wall))
+    t1 = wall.value
+    nt = fn(T, cores, budget_s / 2, ctypes.byref(wall))
+    tt = wall.value
+    if n1 <= 0 or nt <= 0:
+        return None
     model = "unknown"
     try:
         for line in open("/proc/cpuinfo"):
@@ -1083,13 +1168,16 @@ def cpu_baseline(budget_s=12.0):
                 break
     except OSError:
         pass
-    return {"value": round(gbst, 3), "unit": "GB/s", "cores": cores,
-            "kind": "port", "cpu": model, "one_core_GBps": round(gbs1, 3),
-            "ms_per_token_one_core": round(t1 / n1 / rows * 1e3, 4),
-            "sample": f"the T=512 step's four ops (embed, add_rmsnorm+FP8 quantise, SwiGLU+FP8 "
-                      f"quantise, RoPE+int8 KV) on {rows}-token samples: scalar C oracle, "
-                      f"{n1} samples on one thread in {t1:.1f}s, then {nt} on {cores} threads "
-                      f"(one sample stream each) in {tt:.1f}s"}
+    return {"value": round(step_bytes * nt / tt / 1e9, 3), "unit": "GB/s", "cores": cores,
+            "kind": "port", "cpu": model, "hardware_concurrency": os.cpu_count(),
+            "affinity_cores": avail,
+            "one_core_GBps": round(step_bytes * n1 / t1 / 1e9, 3),
+            "ms_per_step_one_core": round(t1 / n1 * 1e3, 2),
+            "ms_per_step_all_cores": round(tt / nt * 1e3, 2),
+            "sample": f"the full T=512 step (BASELINE config 3: embed from the [100352][4096] "
+                      f"table, add_rmsnorm + FP8, SwiGLU + FP8, RoPE + int8 paged KV) with the "
+                      f"scalar C oracle: {n1} steps on one thread in {t1:.1f} s, then {nt} steps "
+                      f"on {cores} threads (rows split across threads) in {tt:.1f} s"}
 
 
 if __name__ == "__main__":

@@ -3,6 +3,7 @@
 // HBM rate on this device, measured rather than assumed, and the known-size
 // kernels that calibrate rocprof's FETCH_SIZE / WRITE_SIZE counters.
 #include "g4_common.h"
+#include "g4_sync.h"
 #include "granite4_layerops.h"
 
 namespace g4 {
@@ -57,6 +58,34 @@ __global__ __launch_bounds__(kBlock) void read_kernel(const uint4* src, long lon
   if (acc == 0x9e3779b9u) sink[0] = acc;  // keeps the loads live; practically never stored
 }
 
+__global__ __launch_bounds__(kBlock) void empty_kernel() {}
+
+// The floor of a layer op that reads R bytes and writes W bytes in one launch:
+// every lane loads its share of src (up to kFloorVpl 16-byte vectors, all in
+// flight, non-temporal), optionally meets the grid once (grid_max, as the
+// single-launch FP8 forms do), then writes its share of dst (non-temporal).
+constexpr int kFloorVpl = 8;
+template <bool SYNC>
+__global__ __launch_bounds__(kBlock) void floor_kernel(const uint4* src, long long nr, uint4* dst,
+                                                       long long nw, GridSync gs) {
+  const unsigned tag = SYNC ? grid_sync_tag(gs) : 0u;
+  const long long lanes = static_cast<long long>(gridDim.x) * kBlock;
+  const long long lane = static_cast<long long>(blockIdx.x) * kBlock + threadIdx.x;
+  uint4 v[kFloorVpl];
+#pragma unroll
+  for (int u = 0; u < kFloorVpl; ++u) {
+    const long long i = lane + u * lanes;
+    v[u] = i < nr ? ld_nt(src + i) : make_uint4(0, 0, 0, 0);
+  }
+  unsigned acc = 0;
+#pragma unroll
+  for (int u = 0; u < kFloorVpl; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  float m = __uint_as_float(acc & 0x3f7fffffu);
+  if (SYNC) m = grid_max(m, gs, tag);
+  const unsigned x = __float_as_uint(m) ^ acc;
+  for (long long i = lane; i < nw; i += lanes) st_nt(dst + i, make_uint4(x, x + 1, x + 2, x + 3));
+}
+
 }  // namespace
 }  // namespace g4
 
@@ -81,6 +110,35 @@ int granite4_bw_probe(const void* src, void* dst, size_t bytes, int mode, int bl
     default: return -1;
   }
   return launch_status("granite4_bw_probe");
+}
+
+int granite4_floor_probe(const void* src, size_t read_bytes, void* dst, size_t write_bytes,
+                         void* d_work, int mode, int blocks) {
+  const hipStream_t st = stream();
+  if (mode == 0) {  // an empty kernel of `blocks` workgroups: the launch floor
+    if (blocks <= 0) return -1;
+    hipLaunchKernelGGL(empty_kernel, blocks, kBlock, 0, st);
+    return launch_status("granite4_floor_probe");
+  }
+  if ((mode != 1 && mode != 2) || src == nullptr || dst == nullptr ||
+      (read_bytes & 15) != 0 || (write_bytes & 15) != 0 || (mode == 2 && d_work == nullptr))
+    return -1;
+  const int resident = resident_blocks(reinterpret_cast<const void*>(floor_kernel<true>), kBlock);
+  const int cap = resident < kMaxPartials ? resident : kMaxPartials;
+  const long long nr = static_cast<long long>(read_bytes / 16);
+  const long long nw = static_cast<long long>(write_bytes / 16);
+  if (blocks <= 0 || blocks > cap ||
+      nr > static_cast<long long>(blocks) * kBlock * kFloorVpl)
+    return -1;
+  const GridSync gs{work_slots(d_work), work_gen(d_work), work_result(d_work), blocks,
+                    work_err(d_work), fp8_sync_spin_limit()};
+  if (mode == 2)
+    hipLaunchKernelGGL(floor_kernel<true>, blocks, kBlock, 0, st, static_cast<const uint4*>(src),
+                       nr, static_cast<uint4*>(dst), nw, gs);
+  else
+    hipLaunchKernelGGL(floor_kernel<false>, blocks, kBlock, 0, st, static_cast<const uint4*>(src),
+                       nr, static_cast<uint4*>(dst), nw, gs);
+  return launch_status("granite4_floor_probe");
 }
 
 }  // extern "C"

@@ -153,6 +153,7 @@ _SIG = {
     "granite4_host_kv_codes": [P, _c.c_size_t, F, I, P],
     "granite4_selftest_bf16": [P],
     "granite4_bw_probe": [P, P, _c.c_size_t, I, I],
+    "granite4_floor_probe": [P, Z, P, Z, P, I, I],
     "granite4_selftest_fp8": [F, P],
 }
 _RESTYPE = {"granite4_get_stream": P, "granite4_fp8_work_bytes": Z,

@@ -349,6 +349,15 @@ int granite4_host_kv_codes(const float* x, size_t n, float scale, int qmax, int3
  * 4 a copy with one vector per lane per iteration, 5 a non-temporal copy with
  * eight; `blocks` 256-thread workgroups in a grid-stride loop. */
 int granite4_bw_probe(const void* src, void* dst, size_t bytes, int mode, int blocks);
+/* The floor of a one-launch layer op (bench infrastructure, no reference
+ * counterpart). mode 0: an empty kernel of `blocks` workgroups. mode 1: each
+ * lane of `blocks` 256-thread workgroups loads its share of read_bytes (at
+ * most 8 16-byte vectors per lane), then writes its share of write_bytes.
+ * mode 2: as 1 with one grid synchronisation between the loads and the
+ * stores (d_work: an FP8 workspace), the single-launch FP8 forms' structure.
+ * blocks must not exceed the resident grid (at most 1024). */
+int granite4_floor_probe(const void* src, size_t read_bytes, void* dst, size_t write_bytes,
+                         void* d_work, int mode, int blocks);
 
 /* Device self-tests of the hardware conversions the kernels use, against the
  * library's exact software arithmetic (the pattern of the reference's

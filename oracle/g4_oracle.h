@@ -144,6 +144,13 @@ void g4o_prefill_attn(const uint16_t* q, int rows, int Hq, int Hk, int d, float 
 /* Paged pool: position -> arena row (kv_pool.cc:285-297). */
 void g4o_row_table(const int32_t* block_table, int n, int page, int32_t* out);
 
+/* bench.py's CPU baseline (g4_cpu_step.c): the T-token one-layer step of
+ * BASELINE config 3 (embed from the full 100352-row table, add+RMSNorm ->
+ * FP8, SwiGLU -> FP8, RoPE + int8 KV) with the functions above, split by rows
+ * over `threads` host threads, repeated for about `seconds`. Returns the
+ * steps done and their wall time in *wall_s; -1 on bad arguments. */
+int g4o_cpu_step_bench(int T, int threads, double seconds, double* wall_s);
+
 #ifdef __cplusplus
 }
 #endif
