@@ -694,21 +694,19 @@ def bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream, layers=40
 
     k_rot = bf(HK * D)
 
+    # The library's whole decode step (granite4_decode_step): RoPE in the
+    # q|k|v GEMV epilogue, the KV append in the attention, norm prologues,
+    # SwiGLU and residual epilogues.
+    dstep = L.DecodeStep(
+        [{"attn_norm": gamma, "ffn_norm": gamma, "wq": p["wq"], "wk": p["wk"], "wv": p["wv"],
+          "wo": p["wo"], "wg": p["wg"], "wu": p["wu"], "wd": p["wd"], "sq": sc, "sk": sc,
+          "sv": sc, "so": sc, "sg": sc, "su": sc, "sd": sc, "cache_k": p["arena"].k,
+          "cache_v": p["arena"].v} for p in per],
+        H, I, HQ, HK, VOCAB, emb, cos_t, sin_t, eps=1e-5, emb_mult=1.0, resid_mult=1.0,
+        attn_scale=1.0 / 128, kv_bits=16, kv_group=128, kv_stride=stride)
+
     def fused_attn_rot():
-        # RoPE in the q|k|v GEMV epilogue, the KV append in the attention
-        L.call("granite4_embed_at_pos", toks, pos, emb, VOCAB, H, 1.0, hidden)
-        for p in per:
-            a = p["arena"]
-            L.call("granite4_gemv_rmsnorm_qkv_rope", hidden, gamma, 1e-5, p["wq"], p["wk"],
-                   p["wv"], sc, sc, sc, cos_t, sin_t, 65536, pos, HQ, HK, H, q_rot, k_rot, v)
-            L.call("granite4_attn_decode_append_rotated", q_rot, k_rot, v, 65536, pos, pt, HQ, HK,
-                   1.0 / 128, a.k, a.v, a.k_scale, a.v_scale, 16, 128, stride, attn_scr,
-                   attn_out)
-            L.call("granite4_gemv_fp8w_resid", attn_out, p["wo"], sc, hidden, 1.0, H, HQ * D,
-                   hidden)
-            L.call("granite4_gemv_rmsnorm_silu_gate_up", hidden, gamma, 1e-5, p["wg"], p["wu"],
-                   sc, sc, I, H, act)
-            L.call("granite4_gemv_fp8w_resid", act, p["wd"], sc, hidden, 1.0, H, I, hidden)
+        dstep(toks, pos, pt)
 
     def fused_attn_parts(rope_gemv):
         # breakdown: the fused GEMVs with plain attention (no KV append);

@@ -51,6 +51,29 @@ class GemmEpilogue(_c.Structure):
 
 GEMM_BF16, GEMM_F32, GEMM_RESIDUAL = 0, 1, 2
 
+
+class DecodeLayer(_c.Structure):
+    """Granite4DecodeLayer (include/granite4_layerops.h)."""
+    _fields_ = [("attn_norm", P), ("wq", P), ("wk", P), ("wv", P), ("wo", P), ("ffn_norm", P),
+                ("wg", P), ("wu", P), ("wd", P), ("sq", F), ("sk", F), ("sv", F), ("so", F),
+                ("sg", F), ("su", F), ("sd", F), ("cache_k", P), ("cache_v", P),
+                ("k_scale", P), ("v_scale", P)]
+
+
+class DecodeModel(_c.Structure):
+    """Granite4DecodeModel (include/granite4_layerops.h)."""
+    _fields_ = [("layers", I), ("H", I), ("I", I), ("Hq", I), ("Hk", I), ("vocab", I),
+                ("eps", F), ("emb_mult", F), ("resid_mult", F), ("attn_scale", F),
+                ("emb", P), ("layer", _c.POINTER(DecodeLayer)), ("final_norm", P),
+                ("lm_head", P), ("lm_scale", F), ("cos_tbl", P), ("sin_tbl", P),
+                ("max_pos", I), ("kv_bits", I), ("kv_group", I), ("kv_stride", I)]
+
+
+class DecodeBuffers(_c.Structure):
+    """Granite4DecodeBuffers (include/granite4_layerops.h)."""
+    _fields_ = [("hidden", P), ("q_rot", P), ("k_rot", P), ("v", P), ("attn_out", P),
+                ("act", P), ("attn_scratch", P)]
+
 _SIG = {
     "granite4_set_stream": [P],
     "granite4_get_stream": [],
@@ -149,6 +172,7 @@ _SIG = {
     "granite4_gemv_rmsnorm_silu_gate_up": [P, P, F, P, P, F, F, I, I, P],
     "granite4_gemv_rmsnorm_qkv_rope_append": [P, P, F, P, P, P, F, F, F, P, P, I, P, P, I, I, I, I,
                                               P, P, P, P, P, I],
+    "granite4_decode_step": [_c.POINTER(DecodeModel), _c.POINTER(DecodeBuffers), P, P, P, P, P],
     "granite4_host_fp8_encode": [P, _c.c_size_t, F, P],
     "granite4_host_kv_codes": [P, _c.c_size_t, F, I, P],
     "granite4_selftest_bf16": [P],
@@ -215,6 +239,50 @@ def set_fp8_launch_mode(mode):
     if prev < 0:
         raise ValueError(f"FP8 launch mode {mode}")
     return prev
+
+
+class DecodeStep:
+    """granite4_decode_step over torch tensors: `layers` is a list of dicts
+    with the Granite4DecodeLayer fields (tensors or pointers, floats for the
+    scales); the model fields are keyword arguments. Allocates the step's
+    device buffers once; __call__ launches one step on the current library
+    stream (capturable)."""
+
+    _LAYER_PTRS = ("attn_norm", "wq", "wk", "wv", "wo", "ffn_norm", "wg", "wu", "wd", "cache_k",
+                   "cache_v", "k_scale", "v_scale")
+
+    def __init__(self, layers, H, I, Hq, Hk, vocab, emb, cos, sin, eps=1e-5, emb_mult=1.0,
+                 resid_mult=1.0, attn_scale=1.0 / 128, final_norm=None, lm_head=None,
+                 lm_scale=1.0, kv_bits=16, kv_group=128, kv_stride=0, device="cuda"):
+        self._keep = [layers, emb, cos, sin, final_norm, lm_head]
+        arr = (DecodeLayer * len(layers))()
+        for i, ly in enumerate(layers):
+            for f in self._LAYER_PTRS:
+                setattr(arr[i], f, _ptr(ly.get(f)))
+            for f in ("sq", "sk", "sv", "so", "sg", "su", "sd"):
+                setattr(arr[i], f, float(ly[f]))
+        self._arr = arr
+        self.model = DecodeModel(len(layers), H, I, Hq, Hk, vocab, eps, emb_mult, resid_mult,
+                                 attn_scale, _ptr(emb), arr, _ptr(final_norm), _ptr(lm_head),
+                                 lm_scale, _ptr(cos), _ptr(sin), cos.shape[0], kv_bits, kv_group,
+                                 kv_stride)
+        bf = torch.bfloat16
+        self.hidden = torch.empty(H, dtype=bf, device=device)
+        self.q_rot = torch.empty(Hq * 128, dtype=bf, device=device)
+        self.k_rot = torch.empty(Hk * 128, dtype=bf, device=device)
+        self.v = torch.empty(Hk * 128, dtype=bf, device=device)
+        self.attn_out = torch.empty(Hq * 128, dtype=bf, device=device)
+        self.act = torch.empty(I, dtype=bf, device=device)
+        self.scratch = torch.empty(_lib.granite4_attn_split_scratch_bytes(Hq, 1, kv_stride),
+                                   dtype=torch.uint8, device=device)
+        self.buffers = DecodeBuffers(*[_ptr(t) for t in (self.hidden, self.q_rot, self.k_rot,
+                                                          self.v, self.attn_out, self.act,
+                                                          self.scratch)])
+
+    def __call__(self, tokens, pos, pt=None, hidden_out=None, logits=None):
+        _check(_lib.granite4_decode_step(_c.byref(self.model), _c.byref(self.buffers),
+                                         _ptr(tokens), _ptr(pos), _ptr(pt), _ptr(hidden_out),
+                                         _ptr(logits)), "granite4_decode_step")
 
 
 def fp8_sync_status(work, clear=False):

@@ -611,6 +611,83 @@ int granite4_attn_decode_append_rotated(const uint16_t* q_rot, const uint16_t* k
                                         float* v_scale, int bits, int group, int stride,
                                         void* scratch, uint16_t* out);
 
+/* ---------------------------------------------------------------------------
+ * The batch-1 decode step of the whole model (the reference's
+ * forward_position, forward_gpu.cu:2066-2285, captured once by
+ * capture_decode_graph :2934-2964 and replayed per token).
+ * ------------------------------------------------------------------------- */
+
+/* One layer's weights (fp8 e4m3 rows [N][K] with per-tensor scales, the
+ * reference's LayerView and its sc[0..6]), RMSNorm gammas (bf16 [H]) and KV
+ * arena (as granite4_attn_paged reads it; scales NULL for bits 16). */
+typedef struct Granite4DecodeLayer {
+  const uint16_t* attn_norm;
+  const uint8_t* wq;  /* [Hq * 128][H] */
+  const uint8_t* wk;  /* [Hk * 128][H] */
+  const uint8_t* wv;  /* [Hk * 128][H] */
+  const uint8_t* wo;  /* [H][Hq * 128] */
+  const uint16_t* ffn_norm;
+  const uint8_t* wg;  /* [I][H] */
+  const uint8_t* wu;  /* [I][H] */
+  const uint8_t* wd;  /* [H][I] */
+  float sq, sk, sv, so, sg, su, sd;
+  void* cache_k;
+  void* cache_v;
+  float* k_scale;
+  float* v_scale;
+} Granite4DecodeLayer;
+
+/* The model: dimensions (head_dim 128, Hq a multiple of Hk), the multipliers
+ * of the Granite config (embedding, residual, attention scale), eps, the
+ * embedding table, a host array of `layers` layers, the optional final norm
+ * and LM head, the RoPE tables and the KV format of every layer's arena
+ * (bits 16 / 8 / 4 / 5, group, row stride). */
+typedef struct Granite4DecodeModel {
+  int layers, H, I, Hq, Hk, vocab;
+  float eps, emb_mult, resid_mult, attn_scale;
+  const uint16_t* emb;                /* [vocab][H] bf16 */
+  const Granite4DecodeLayer* layer;   /* host array [layers] */
+  const uint16_t* final_norm;         /* [H] or NULL */
+  const uint8_t* lm_head;             /* [vocab][H] e4m3 or NULL */
+  float lm_scale;
+  const float* cos_tbl;
+  const float* sin_tbl;
+  int max_pos;
+  int kv_bits, kv_group, kv_stride;
+} Granite4DecodeModel;
+
+/* Device scratch of the step, caller-owned: hidden [H] (the residual stream,
+ * written from the embedding at the start of the step), q_rot [Hq * 128],
+ * k_rot and v [Hk * 128], attn_out [Hq * 128], act [I], attn_scratch
+ * granite4_attn_split_scratch_bytes(Hq, 1, kv_stride) bytes. */
+typedef struct Granite4DecodeBuffers {
+  uint16_t* hidden;
+  uint16_t* q_rot;
+  uint16_t* k_rot;
+  uint16_t* v;
+  uint16_t* attn_out;
+  uint16_t* act;
+  void* attn_scratch;
+} Granite4DecodeBuffers;
+
+/* Replaces: forward_position (forward_gpu.cu:2066-2285) for the split-KV
+ * attention path. One token at position *d_pos (token d_tokens[*d_pos]):
+ * embed, then per layer RMSNorm + q|k|v GEMV + RoPE (one launch), KV append
+ * at arena row d_pt[*d_pos] (d_pt NULL: row = position) inside the split-KV
+ * attention, O GEMV + residual, RMSNorm + gate/up GEMV + SwiGLU, down GEMV +
+ * residual; then d_hidden_out = RMSNorm(hidden, final_norm) and d_logits =
+ * bf16(lm_scale * lm_head . RMSNorm(hidden)) where given (NULL skips them).
+ * 5 launches per layer + 1-3. Asynchronous on the calling thread's stream,
+ * no allocation: capturable once in a HIP graph and replayed per token with
+ * *d_pos advanced between replays. Outputs are bit-identical to calling
+ * granite4_embed_at_pos, granite4_gemv_rmsnorm_qkv_rope,
+ * granite4_attn_decode_append_rotated, granite4_gemv_fp8w_resid,
+ * granite4_gemv_rmsnorm_silu_gate_up, granite4_gemv_fp8w_resid,
+ * granite4_kernel_rmsnorm and granite4_gemv_rmsnorm_qkv in that order. */
+int granite4_decode_step(const Granite4DecodeModel* model, const Granite4DecodeBuffers* buffers,
+                         const int32_t* d_tokens, const int* d_pos, const int* d_pt,
+                         uint16_t* d_hidden_out, uint16_t* d_logits);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 
