@@ -615,7 +615,7 @@ int gemv_swiglu(int pro, const uint16_t* x, const uint16_t* gamma, float eps, co
   if (x == nullptr || wg == nullptr || wu == nullptr || out == nullptr || !al16(x) || !al16(wg) ||
       !al16(wu) || !gemv_k_ok(K) || N <= 0 || !std::isfinite(sg) || !std::isfinite(su) ||
       (pro == kProNorm && (gamma == nullptr || !al16(gamma) || !std::isfinite(eps))) ||
-      N * K >= (1LL << 40)) {
+      static_cast<long long>(N) * K >= (1LL << 40)) {
     std::fprintf(stderr, "granite4: %s: invalid arguments (K %% 64 == 0, K <= %d)\n", what, kMaxK);
     return -1;
   }
