@@ -846,6 +846,7 @@ def kv_bytes_per_position(bits, group):
 
 
 FP8_MFMA_PEAK_TFLOPS = 5000.0  # MI355X dense FP8 matrix-core peak
+BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix-core peak
 
 
 def bench_gemm(torch, L, gen, timed, work, args):
@@ -882,6 +883,9 @@ def bench_gemm(torch, L, gen, timed, work, args):
                 "codes_h": torch.empty((T, H), dtype=torch.uint8, device=dev),
                 "scale": torch.empty(1, dtype=torch.float32, device=dev),
                 "gamma": torch.ones(H, dtype=torch.bfloat16, device=dev),
+                "hid_a": torch.randn((T, H), generator=gen, device=dev).to(torch.bfloat16),
+                "qkv_out": torch.empty((T, 6144), dtype=torch.bfloat16, device=dev),
+                "gu_f32": torch.empty((T, 2 * I), dtype=torch.float32, device=dev),
             })
 
         a_sc = torch.full((1,), 0.01, dtype=torch.float32, device=dev)
@@ -907,19 +911,39 @@ def bench_gemm(torch, L, gen, timed, work, args):
             L.gemm_fp8(s["act_a"], a_sc, s["w_d"], out=s["hidden"], out_kind=L.GEMM_RESIDUAL,
                        scales=(0.01, 0.01, 0.01), residual=s["hidden"])
 
+        # The reference's own prefill GEMM form (granite4_prefill_gemm: bf16
+        # activations x fp8 weights), at the same shapes.
+        def ref_qkv(s):
+            L.prefill_gemm(s["hid_a"], s["w_gu"][:6144], out=s["qkv_out"],
+                           scales=(0.01, 0.01, 0.01), segs=(4096, 5120))
+
+        def ref_gu_f32(s):
+            L.prefill_gemm(s["hid_a"], s["w_gu"], out_kind=L.GEMM_F32, out=s["gu_f32"],
+                           scales=(0.01, 0.01, 0.01))
+
+        def ref_down(s):
+            L.prefill_gemm(s["act"], s["w_d"], out_kind=L.GEMM_RESIDUAL, out=s["hidden"],
+                           scales=(0.01, 0.01, 0.01), residual=s["hidden"])
+
         steps = 10 if T == 512 else 4
         res = {}
         for name, fn, flops in (("gate_up_swiglu_fp8_fused", gu_fused, 2.0 * T * 2 * I * H),
                                 ("gate_up_then_swiglu_fp8", gu_unfused, 2.0 * T * 2 * I * H),
                                 ("o_residual_rmsnorm_fp8_fused", o_fused, 2.0 * T * H * H),
                                 ("o_then_add_rmsnorm_fp8", o_unfused, 2.0 * T * H * H),
-                                ("down_residual", down, 2.0 * T * H * I)):
+                                ("down_residual", down, 2.0 * T * H * I),
+                                ("bf16A_qkv_bf16", ref_qkv, 2.0 * T * 6144 * H),
+                                ("bf16A_gate_up_f32", ref_gu_f32, 2.0 * T * 2 * I * H),
+                                ("bf16A_down_residual", ref_down, 2.0 * T * H * I)):
             if only and only != f"T{T}:{name}":
                 continue
             ms = timed(fn, steps, 2, sets, replays=2)
             tf = flops / (ms * 1e-3) / 1e12
-            res[name] = {"us": round(ms * 1e3, 2), "TFLOPs": round(tf, 1),
-                         "frac_fp8_peak": round(tf / FP8_MFMA_PEAK_TFLOPS, 4)}
+            res[name] = {"us": round(ms * 1e3, 2), "TFLOPs": round(tf, 1)}
+            if name.startswith("bf16A"):
+                res[name]["frac_bf16_peak"] = round(tf / BF16_MFMA_PEAK_TFLOPS, 4)
+            else:
+                res[name]["frac_fp8_peak"] = round(tf / FP8_MFMA_PEAK_TFLOPS, 4)
         out[f"T{T}"] = res
         del sets
         torch.cuda.empty_cache()

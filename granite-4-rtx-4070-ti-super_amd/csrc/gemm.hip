@@ -79,6 +79,7 @@ struct GemmArgs {
   Granite4GemmEpilogue ep;
   float* partials;  // swiglu: [gridDim.x] max |act|
   int mt, nt;       // tile counts along M and N
+  bool vec_out;     // 16-byte output rows (pitch and width multiples of 8)
 };
 
 __device__ __forceinline__ float epi_scale(const Granite4GemmEpilogue& ep, int n) {
@@ -187,6 +188,103 @@ __device__ __forceinline__ void stage_wait(int later) {
   else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
+// Epilogue of one output tile through LDS: each wave writes its f32 values
+// (y = acc * (a_scale * w_scale(n)), or silu(g) * u) 32 rows at a time into
+// its own region and reads them back row-contiguous, so a lane owns 8
+// consecutive columns and every global access is 16 bytes (or, where the
+// output pitch or width is not a multiple of 8, element by element). The
+// residual was prefetched at the tile's start (a load after a store would
+// wait for the store: the vector memory counter covers both).
+template <int EPI, int kIters, int kWCols>
+__device__ __forceinline__ void tile_epilogue(const GemmArgs& a, const v4f (&acc)[4][4],
+                                              float a_scale, uint8_t* s_tile, int m0, int col0,
+                                              int n_end, const uint4* res, float& amax) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave >> 1;
+  const int fr = lane & 15;
+  constexpr int kLanesPerRow = kWCols / 8;
+  constexpr int kRowsPerIter = 64 / kLanesPerRow;
+  __builtin_amdgcn_s_barrier();  // every wave is past its last fragment read
+  float* const sv = reinterpret_cast<float*>(s_tile) + wave * (32 * kEP);
+  const Granite4GemmEpilogue& ep = a.ep;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int mj = 0; mj < 2; ++mj) {
+      const int mi = 2 * h + mj;
+#pragma unroll
+      for (int ni = 0; ni < kWCols / 16; ++ni) {
+        const int col = ni * 16 + fr;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float v;
+          if (EPI == kEpiSwiglu) {
+            const float g = acc[mi][ni][i] * (a_scale * ep.scale0);
+            const float u = acc[mi][ni + 2][i] * (a_scale * ep.scale1);
+            v = silu_mul(g, u);
+          } else {
+            v = acc[mi][ni][i] * (a_scale * epi_scale(ep, col0 + col));
+          }
+          sv[(mj * 16 + 4 * (lane >> 4) + i) * kEP + col] = v;
+        }
+      }
+    }
+    wave_lds_wait();
+#pragma unroll
+    for (int it = 0; it < kIters; ++it) {
+      const int rl = it * kRowsPerIter + lane / kLanesPerRow;
+      const int ch = lane % kLanesPerRow;
+      const int m = m0 + wm * 64 + h * 32 + rl;
+      const int n = col0 + ch * 8;
+      const float4 lo = *reinterpret_cast<const float4*>(sv + rl * kEP + ch * 8);
+      const float4 hi = *reinterpret_cast<const float4*>(sv + rl * kEP + ch * 8 + 4);
+      if (m >= a.M || n >= n_end) continue;
+      const float y[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+      const size_t off = static_cast<size_t>(m) * ep.ldc + n;
+      if (EPI != kEpiSwiglu && !a.vec_out) {
+        // Element by element (an output pitch or width that is not a
+        // multiple of 8): the same arithmetic per element.
+        for (int e = 0; e < 8 && n + e < n_end; ++e) {
+          if (EPI == kEpiF32) {
+            ep.out_f32[off + e] = y[e];
+          } else if (EPI == kEpiResidual) {
+            const float r = bf16_to_f32(ep.residual[off + e]);
+            ep.out_bf16[off + e] = static_cast<uint16_t>(f32_to_bf16(r + ep.resid_scale * y[e]));
+          } else {
+            ep.out_bf16[off + e] = static_cast<uint16_t>(f32_to_bf16(y[e]));
+          }
+        }
+        continue;
+      }
+      if (EPI == kEpiF32) {
+        *reinterpret_cast<float4*>(ep.out_f32 + off) = lo;
+        *reinterpret_cast<float4*>(ep.out_f32 + off + 4) = hi;
+        continue;
+      }
+      uint32_t w[4];
+      if (EPI == kEpiResidual) {
+        const uint4 r = res[h * kIters + it];
+        const uint32_t rw[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          w[e] = pack_bf16_rne(lo_bf16(rw[e]) + ep.resid_scale * y[2 * e],
+                               hi_bf16(rw[e]) + ep.resid_scale * y[2 * e + 1]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = pack_bf16_rne(y[2 * e], y[2 * e + 1]);
+      }
+      if (EPI == kEpiSwiglu) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          amax = fmaxf(amax, fmaxf(lo_bf16(w[e] & 0x7fff7fffu), hi_bf16(w[e] & 0x7fff7fffu)));
+      }
+      *reinterpret_cast<uint4*>(ep.out_bf16 + off) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+    wave_lds_wait();  // reads done before the next half's writes
+  }
+}
+
 template <int EPI>
 __global__ __launch_bounds__(256) void gemm_fp8_kernel(GemmArgs a) {
   __shared__ __align__(16) uint8_t s_tile[kGStages * kGStage];
@@ -267,77 +365,167 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(GemmArgs a) {
               frag_of(ax[mi], ay[mi]), frag_of(bx[ni], by[ni]), acc[mi][ni], 0, 0, 0, 0, 0, 0);
     }
 
-    // Epilogue through LDS: each wave writes its f32 values (the scaled
-    // GEMM value, or silu(g) * u) 32 rows at a time into its own region and
-    // reads them back row-contiguous, so a lane owns 8 consecutive columns
-    // and every global access is 16 bytes. The residual was prefetched at the
-    // tile's start (a load after a store would wait for the store: the
-    // vector memory counter covers both).
-    __builtin_amdgcn_s_barrier();  // every wave is past its last fragment read
-    float* const sv = reinterpret_cast<float*>(s_tile) + wave * (32 * kEP);
-    const Granite4GemmEpilogue& ep = a.ep;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-#pragma unroll
-      for (int mj = 0; mj < 2; ++mj) {
-        const int mi = 2 * h + mj;
-#pragma unroll
-        for (int ni = 0; ni < kWCols / 16; ++ni) {
-          const int col = ni * 16 + fr;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float v;
-            if (EPI == kEpiSwiglu) {
-              const float g = acc[mi][ni][i] * (a_scale * ep.scale0);
-              const float u = acc[mi][ni + 2][i] * (a_scale * ep.scale1);
-              v = silu_mul(g, u);
-            } else {
-              v = acc[mi][ni][i] * (a_scale * epi_scale(ep, col0 + col));
-            }
-            sv[(mj * 16 + 4 * (lane >> 4) + i) * kEP + col] = v;
-          }
-        }
-      }
-      wave_lds_wait();
-#pragma unroll
-      for (int it = 0; it < kIters; ++it) {
-        const int rl = it * kRowsPerIter + lane / kLanesPerRow;
-        const int ch = lane % kLanesPerRow;
-        const int m = m0 + wm * 64 + h * 32 + rl;
-        const int n = col0 + ch * 8;
-        const float4 lo = *reinterpret_cast<const float4*>(sv + rl * kEP + ch * 8);
-        const float4 hi = *reinterpret_cast<const float4*>(sv + rl * kEP + ch * 8 + 4);
-        if (m >= a.M || n >= n_end) continue;
-        const float y[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-        const size_t off = static_cast<size_t>(m) * ep.ldc + n;
-        if (EPI == kEpiF32) {
-          *reinterpret_cast<float4*>(ep.out_f32 + off) = lo;
-          *reinterpret_cast<float4*>(ep.out_f32 + off + 4) = hi;
-          continue;
-        }
-        uint32_t w[4];
-        if (EPI == kEpiResidual) {
-          const uint4 r = res[h * kIters + it];
-          const uint32_t rw[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            w[e] = pack_bf16_rne(lo_bf16(rw[e]) + ep.resid_scale * y[2 * e],
-                                 hi_bf16(rw[e]) + ep.resid_scale * y[2 * e + 1]);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) w[e] = pack_bf16_rne(y[2 * e], y[2 * e + 1]);
-        }
-        if (EPI == kEpiSwiglu) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            amax = fmaxf(amax, fmaxf(lo_bf16(w[e] & 0x7fff7fffu), hi_bf16(w[e] & 0x7fff7fffu)));
-        }
-        *reinterpret_cast<uint4*>(ep.out_bf16 + off) = make_uint4(w[0], w[1], w[2], w[3]);
-      }
-      wave_lds_wait();  // reads done before the next half's writes
-    }
+    tile_epilogue<EPI, kIters, kWCols>(a, acc, a_scale, s_tile, m0, col0, n_end, res, amax);
   }
   if (EPI == kEpiSwiglu) write_partial(a.partials, amax);
+}
+
+// ---------------------------------------------------------------------------
+// bf16 A x fp8 W (the reference's prefill_gemm, prefill_gemm.h:34-39):
+// C[m][n] = w_scale(n) * sum_k A[m][k] * W[n][k], A bf16 [M][lda], W e4m3
+// [N][K]. Each product bf16 x e4m3 is exact in f32; the sum runs in f32 in
+// the matrix cores' order (v_mfma_f32_16x16x32_bf16).
+//
+// Same tiling, persistent grid and epilogue as gemm_fp8_kernel; K advances
+// 64 elements per stage. A stage holds A as 128 rows x 128 bytes (the bf16
+// k-slice, eight 16-byte chunks XOR-swizzled by row) and W raw as 128 rows
+// x 64 bytes (four chunks, swizzled by row % 4), both filled by
+// direct-to-LDS loads. Each wave converts its W fragments from e4m3 to bf16
+// as it reads them (exact: an e4m3 value has at most 4 significant bits, so
+// its bf16 is the top half of its f32): one conversion and one byte permute
+// per two elements. A stage whose second 32-element half lies past K (K % 64
+// == 32) loads valid bytes there and skips that half's MFMAs.
+constexpr int kBwK = 64;                          // k elements per stage
+constexpr int kBwARow = 2 * kBwK;                 // A bytes per tile row per stage
+constexpr int kBwWRow = kBwK;                     // W bytes per tile row per stage
+constexpr int kBwStage = kGBM * kBwARow + kGBN * kBwWRow;  // 24 KB
+
+typedef __bf16 bf16x8_g __attribute__((ext_vector_type(8)));
+
+template <int EPI>
+__device__ __forceinline__ void bw_stage_issue(const GemmArgs& a, int m0, int tn, int k0,
+                                               uint8_t* st) {
+  const int wave = threadIdx.x >> 6;
+  const uint16_t* A = reinterpret_cast<const uint16_t*>(a.A);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int slot = i * 256 + threadIdx.x;
+    const int row = slot >> 3, c = (slot & 7) ^ (row & 7);
+    const int m = min(m0 + row, a.M - 1);
+    const int k = k0 + 8 * c < a.K ? k0 + 8 * c : 0;  // past K: a valid chunk, unused
+    __builtin_amdgcn_global_load_lds(A + static_cast<size_t>(m) * a.lda + k,
+                                     (lds_ptr)(st + (i * 256 + wave * 64) * 16), 16, 0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int slot = i * 256 + threadIdx.x;
+    const int row = slot >> 2, c = (slot & 3) ^ (row & 3);
+    int n = w_row<EPI>(a, tn, row);
+    if (n < 0) n = 0;
+    const int k = k0 + 16 * c < a.K ? k0 + 16 * c : 0;
+    __builtin_amdgcn_global_load_lds(a.W + static_cast<size_t>(n) * a.K + k,
+                                     (lds_ptr)(st + kGBM * kBwARow + (i * 256 + wave * 64) * 16),
+                                     16, 0, 0);
+  }
+}
+
+__device__ __forceinline__ uint2 lds_read8(uint32_t addr) {
+  uint2 v;
+  asm volatile("ds_read_b64 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+  return v;
+}
+
+// Eight e4m3 codes -> eight bf16 (exact), in element order.
+__device__ __forceinline__ bf16x8_g fp8x8_to_bf16(uint2 q) {
+  uint32_t w[4];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t x = h ? q.y : q.x;
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(x), false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(x), true);
+    w[2 * h] = __builtin_amdgcn_perm(__float_as_uint(lo[1]), __float_as_uint(lo[0]), 0x07060302u);
+    w[2 * h + 1] = __builtin_amdgcn_perm(__float_as_uint(hi[1]), __float_as_uint(hi[0]), 0x07060302u);
+  }
+  const v4u u = {w[0], w[1], w[2], w[3]};
+  return __builtin_bit_cast(bf16x8_g, u);
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_bf16w_kernel(GemmArgs a) {
+  __shared__ __align__(16) uint8_t s_tile[2 * kBwStage];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int ktiles = (a.K + kBwK - 1) / kBwK;
+  const int tiles = a.mt * a.nt;
+  const int fr = lane & 15;
+  float amax = 0.0f;
+  constexpr int kWCols = 64;
+  constexpr int kLanesPerRow = kWCols / 8;
+  constexpr int kRowsPerIter = 64 / kLanesPerRow;
+  constexpr int kIters = 32 / kRowsPerIter;
+  static_assert(4 * 32 * kEP * 4 <= 2 * kBwStage, "epilogue staging fits the stage buffers");
+
+  for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    const int tm = tile % a.mt, tn = tile / a.mt;
+    const int m0 = tm * kGBM;
+    v4f acc[4][4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    const int col0 = tn * kGBN + wn * 64;
+    const int n_end = a.N;
+    uint4 res[EPI == kEpiResidual ? 2 * kIters : 1];
+    if (EPI == kEpiResidual) {
+#pragma unroll
+      for (int j = 0; j < 2 * kIters; ++j) {
+        const int h = j / kIters, it = j % kIters;
+        const int m = m0 + wm * 64 + h * 32 + it * kRowsPerIter + lane / kLanesPerRow;
+        const int n = col0 + (lane % kLanesPerRow) * 8;
+        res[j] = (a.vec_out && m < a.M && n < n_end)
+                     ? *reinterpret_cast<const uint4*>(a.ep.residual + static_cast<size_t>(m) * a.ep.ldc + n)
+                     : make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+
+    __syncthreads();  // the previous tile's readers are done with both buffers
+    bw_stage_issue<EPI>(a, m0, tn, 0, s_tile);
+    for (int kt = 0; kt < ktiles; ++kt) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      // Stage kt landed for every wave; stage kt - 1's reads are done.
+      __builtin_amdgcn_s_barrier();
+      if (kt + 1 < ktiles) bw_stage_issue<EPI>(a, m0, tn, (kt + 1) * kBwK, s_tile + ((kt + 1) & 1) * kBwStage);
+      const uint32_t st = lds_addr(s_tile + (kt & 1) * kBwStage);
+      const uint32_t sw = st + kGBM * kBwARow;
+      const int halves = a.K - kt * kBwK >= kBwK ? 2 : 1;  // wave-uniform
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        if (s >= halves) break;
+        v4u ax[4];
+        uint2 bq[4];
+        const int ca = 4 * s + (lane >> 4);            // A chunk: elements 32 s + 8 (lane / 16)
+        const int cw = 2 * s + (lane >> 5);            // W chunk: bytes 32 s + 8 (lane / 16)
+        const uint32_t wh = 8u * static_cast<uint32_t>((lane >> 4) & 1);
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi) {
+          const int r = wm * 64 + mi * 16 + fr;
+          ax[mi] = lds_read16(st + static_cast<uint32_t>(r * kBwARow) +
+                              16u * static_cast<uint32_t>(ca ^ (r & 7)));
+        }
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) {
+          const int r = wn * 64 + ni * 16 + fr;
+          bq[ni] = lds_read8(sw + static_cast<uint32_t>(r * kBwWRow) +
+                             16u * static_cast<uint32_t>(cw ^ (r & 3)) + wh);
+        }
+        lds_reads_done();
+#pragma unroll
+        for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(ax[j]), "+v"(bq[j]));
+        bf16x8_g bf[4];
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) bf[ni] = fp8x8_to_bf16(bq[ni]);
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi) {
+          const bf16x8_g af = __builtin_bit_cast(bf16x8_g, ax[mi]);
+#pragma unroll
+          for (int ni = 0; ni < 4; ++ni)
+            acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bf[ni], acc[mi][ni], 0, 0, 0);
+        }
+      }
+    }
+    tile_epilogue<EPI, kIters, kWCols>(a, acc, 1.0f, s_tile, m0, col0, n_end, res, amax);
+  }
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -389,6 +577,7 @@ int granite4_gemm_fp8(int out, const uint8_t* A, int lda, const float* d_a_scale
   a.ep = *ep;
   a.mt = (M + kGBM - 1) / kGBM;
   a.nt = (N + kGBN - 1) / kGBN;
+  a.vec_out = true;
   const long long tiles = static_cast<long long>(a.mt) * a.nt;
   const hipStream_t st = stream();
   switch (out) {
@@ -404,6 +593,72 @@ int granite4_gemm_fp8(int out, const uint8_t* A, int lda, const float* d_a_scale
       break;
   }
   return launch_status("granite4_gemm_fp8");
+}
+
+int granite4_prefill_gemm(int out, const uint16_t* A, int lda, const uint8_t* W, int M, int N,
+                          int K, const Granite4GemmEpilogue* ep, float* ws, size_t ws_bytes) {
+  (void)ws;
+  (void)ws_bytes;
+  // The reference's requirements (prefill_gemm.cu:1264-1271): K % 32 == 0,
+  // lda % 8 == 0, even N and ldc, 16-byte aligned A and W.
+  if (A == nullptr || W == nullptr || ep == nullptr || M <= 0 || N <= 0 || K <= 0 || K % 32 != 0 ||
+      lda % 8 != 0 || lda < K || (N & 1) != 0 || (ep->ldc & 1) != 0 || ep->ldc < N ||
+      !aligned16(A) || !aligned16(W) || out < 0 || out > 2 ||
+      (out == GRANITE4_GEMM_F32 ? ep->out_f32 == nullptr : ep->out_bf16 == nullptr) ||
+      (out == GRANITE4_GEMM_RESIDUAL && ep->residual == nullptr) ||
+      static_cast<long long>(M) * lda >= (1LL << 40) ||
+      static_cast<long long>(N) * K >= (1LL << 40)) {
+    std::fprintf(stderr,
+                 "granite4: granite4_prefill_gemm: invalid arguments (K %% 32 == 0, lda %% 8 == 0, "
+                 "even N and ldc, 16-byte aligned A and W)\n");
+    return -1;
+  }
+  GemmArgs a{};
+  a.A = reinterpret_cast<const uint8_t*>(A);
+  a.lda = lda;
+  a.W = W;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.ep = *ep;
+  a.mt = (M + kGBM - 1) / kGBM;
+  a.nt = (N + kGBN - 1) / kGBN;
+  const void* outp = out == GRANITE4_GEMM_F32 ? static_cast<const void*>(ep->out_f32)
+                                              : static_cast<const void*>(ep->out_bf16);
+  a.vec_out = N % 8 == 0 && ep->ldc % 8 == 0 && aligned16(outp) &&
+              (out != GRANITE4_GEMM_RESIDUAL || aligned16(ep->residual));
+  const long long tiles = static_cast<long long>(a.mt) * a.nt;
+  const hipStream_t st = stream();
+  const auto grid = [&](const void* k) {
+    const int resident = resident_blocks(k, 256);
+    long long g = tiles;
+    if (resident > 0 && g > resident) g = resident;
+    return static_cast<unsigned>(g > 0 ? g : 1);
+  };
+  switch (out) {
+    case GRANITE4_GEMM_BF16:
+      hipLaunchKernelGGL(gemm_bf16w_kernel<kEpiBf16>,
+                         grid(reinterpret_cast<const void*>(gemm_bf16w_kernel<kEpiBf16>)), 256, 0,
+                         st, a);
+      break;
+    case GRANITE4_GEMM_F32:
+      hipLaunchKernelGGL(gemm_bf16w_kernel<kEpiF32>,
+                         grid(reinterpret_cast<const void*>(gemm_bf16w_kernel<kEpiF32>)), 256, 0, st,
+                         a);
+      break;
+    default:
+      hipLaunchKernelGGL(gemm_bf16w_kernel<kEpiResidual>,
+                         grid(reinterpret_cast<const void*>(gemm_bf16w_kernel<kEpiResidual>)), 256,
+                         0, st, a);
+      break;
+  }
+  return launch_status("granite4_prefill_gemm");
+}
+
+size_t granite4_prefill_gemm_workspace_bytes(int M, int N) {
+  (void)M;
+  (void)N;
+  return 0;
 }
 
 int granite4_gemm_fp8_swiglu(const uint8_t* A, int lda, const float* d_a_scale,
@@ -432,6 +687,7 @@ int granite4_gemm_fp8_swiglu(const uint8_t* A, int lda, const float* d_a_scale,
   a.ep.ldc = I;
   a.mt = (M + kGBM - 1) / kGBM;
   a.nt = (I + 63) / 64;
+  a.vec_out = true;
   a.partials = work_partials(d_work);
   const long long tiles = static_cast<long long>(a.mt) * a.nt;
   const unsigned grid = gemm_grid<kEpiSwiglu>(tiles, kMaxPartials);

@@ -125,6 +125,8 @@ _SIG = {
     "granite4_prefill_attention": [P, P, P, F, I, I, I, I, I, I, P, P, P, P, P, I, P, P, I, P, I,
                                    I],
     "granite4_gemm_fp8": [I, P, I, P, P, I, I, I, _c.POINTER(GemmEpilogue)],
+    "granite4_prefill_gemm": [I, P, I, P, I, I, I, _c.POINTER(GemmEpilogue), P, Z],
+    "granite4_prefill_gemm_workspace_bytes": [I, I],
     "granite4_gemm_fp8_swiglu": [P, I, P, P, I, I, I, F, F, P, P, P, P],
     "granite4_gemm_fp8_residual_rmsnorm_fp8": [P, I, P, P, I, I, I, F, P, F, P, F, P, P, P],
     "granite4_kv_layout_offset": [Z, Z, Z, Z, Z, Z, I, Z, Z],
@@ -181,6 +183,7 @@ _SIG = {
     "granite4_selftest_fp8": [F, P],
 }
 _RESTYPE = {"granite4_get_stream": P, "granite4_fp8_work_bytes": Z,
+            "granite4_prefill_gemm_workspace_bytes": Z,
             "granite4_attn_split_scratch_bytes": Z, "granite4_kv_pool_create": P,
             "granite4_kv_ctrl_create": P}
 for _name, _args in _SIG.items():
@@ -384,6 +387,27 @@ def gemm_fp8(A, a_scale, W, out_kind=GEMM_BF16, scales=(1.0, 1.0, 1.0), segs=Non
                       None if residual is None else residual.data_ptr(), float(resid_scale),
                       out.stride(0))
     call("granite4_gemm_fp8", out_kind, A, A.stride(0), a_scale, W, M, N, K, ep)
+    return out
+
+
+def prefill_gemm(A, W, out_kind=GEMM_BF16, scales=(1.0, 1.0, 1.0), segs=None, out=None,
+                 residual=None, resid_scale=1.0):
+    """granite4_prefill_gemm (the reference's prefill_gemm): A [M][K] bf16
+    (row pitch A.stride(0)), W [N][K] e4m3 codes (uint8). Returns out [M][N]
+    (bf16, or f32 for GEMM_F32; in place for GEMM_RESIDUAL when out is
+    residual)."""
+    M, K = A.shape
+    N = W.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32 if out_kind == GEMM_F32 else torch.bfloat16,
+                          device=A.device)
+    s1, s2 = segs if segs is not None else (N, N)
+    ep = GemmEpilogue(float(scales[0]), float(scales[1]), float(scales[2]), int(s1), int(s2),
+                      None if out_kind == GEMM_F32 else out.data_ptr(),
+                      out.data_ptr() if out_kind == GEMM_F32 else None,
+                      None if residual is None else residual.data_ptr(), float(resid_scale),
+                      out.stride(0))
+    call("granite4_prefill_gemm", out_kind, A, A.stride(0), W, M, N, K, ep, None, 0)
     return out
 
 

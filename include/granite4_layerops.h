@@ -472,6 +472,21 @@ typedef struct Granite4GemmEpilogue {
 int granite4_gemm_fp8(int out, const uint8_t* A, int lda, const float* d_a_scale, const uint8_t* W,
                       int M, int N, int K, const Granite4GemmEpilogue* ep);
 
+/* Replaces: granite4::prefill_gemm (prefill_gemm.h:34-39, prefill_gemm.cu:
+ * 1260-1298), the reference's own form: C[m][n] = w_scale(n) * sum_k A[m][k]
+ * W[n][k] with A bf16 [M][lda] and W e4m3 [N][K]; `out` one of
+ * GRANITE4_GEMM_* (kBf16 / kF32 / kResidual, the reference's epi_store,
+ * prefill_gemm.cu:69-89, y = w_scale(n) * acc in f32). The reference's
+ * requirements: K % 32 == 0, lda % 8 == 0, lda >= K, even N and ldc,
+ * ldc >= N, 16-byte aligned A and W (outputs whose pitch or width is not a
+ * multiple of 8 are written element by element). ws / ws_bytes are accepted
+ * and unused: the grid is persistent over 128 x 128 tiles, with no split-K
+ * workspace. */
+int granite4_prefill_gemm(int out, const uint16_t* A, int lda, const uint8_t* W, int M, int N,
+                          int K, const Granite4GemmEpilogue* ep, float* ws, size_t ws_bytes);
+/* prefill_gemm.h:42 (prefill_gemm_workspace_bytes): 0, no workspace is used. */
+size_t granite4_prefill_gemm_workspace_bytes(int M, int N);
+
 /* Replaces: the gate|up GEMM with the kF32 epilogue followed by
  * granite4::prefill_silu_mul (forward_gpu.cu:2837-2839, prefill_gemm.cu:
  * 1194-1203), fused: W_gu is [2I][K] (gate rows, then up rows), act[m][i] =
@@ -694,6 +709,29 @@ int granite4_decode_step(const Granite4DecodeModel* model, const Granite4DecodeB
 /* The reference's C++ launcher names (prefill_gemm.h:41-105,
  * forward_gpu_api.h:219-229), forwarding to the C entry points above. */
 namespace granite4 {
+// prefill_gemm.h:12-39: the reference's GemmOut / GemmEpilogue (same fields
+// and defaults) and prefill_gemm, over granite4_prefill_gemm.
+enum class GemmOut { kBf16 = GRANITE4_GEMM_BF16, kF32 = GRANITE4_GEMM_F32,
+                     kResidual = GRANITE4_GEMM_RESIDUAL };
+struct GemmEpilogue {
+  float scale0 = 1.0f, scale1 = 1.0f, scale2 = 1.0f;
+  int seg1 = INT32_MAX, seg2 = INT32_MAX;
+  uint16_t* out_bf16 = nullptr;
+  float* out_f32 = nullptr;
+  const uint16_t* residual = nullptr;
+  float resid_scale = 1.0f;
+  int ldc = 0;
+};
+inline int prefill_gemm(GemmOut out, const uint16_t* A, int lda, const uint8_t* W, int M, int N,
+                        int K, const GemmEpilogue& ep, float* ws = nullptr,
+                        size_t ws_bytes = 0) {
+  const Granite4GemmEpilogue e{ep.scale0, ep.scale1, ep.scale2, ep.seg1, ep.seg2, ep.out_bf16,
+                               ep.out_f32, ep.residual, ep.resid_scale, ep.ldc};
+  return granite4_prefill_gemm(static_cast<int>(out), A, lda, W, M, N, K, &e, ws, ws_bytes);
+}
+inline size_t prefill_gemm_workspace_bytes(int M, int N) {
+  return granite4_prefill_gemm_workspace_bytes(M, N);
+}
 inline int prefill_embed_rows(const int32_t* d_tokens, int start, int rows, const uint16_t* emb,
                               float mult, uint16_t* out, int H) {
   return granite4_prefill_embed_rows(d_tokens, start, rows, emb, mult, out, H);

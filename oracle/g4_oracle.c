@@ -274,6 +274,22 @@ void g4o_gemm_fp8(const uint8_t* A, int lda, float a_scale, const uint8_t* W, in
   }
 }
 
+void g4o_gemm_bf16w(const uint16_t* A, int lda, const uint8_t* W, int M, int N, int K,
+                    float scale0, float scale1, float scale2, int seg1, int seg2, float* y) {
+  double dec[256];
+  for (int c = 0; c < 256; ++c) dec[c] = g4o_fp8_decode((uint8_t)c);
+  for (int m = 0; m < M; ++m) {
+    const uint16_t* a = A + (size_t)m * (size_t)lda;
+    for (int n = 0; n < N; ++n) {
+      const uint8_t* w = W + (size_t)n * (size_t)K;
+      double acc = 0.0;
+      for (int k = 0; k < K; ++k) acc += (double)g4o_bf16_to_f32(a[k]) * dec[w[k]];
+      const float s = n < seg1 ? scale0 : (n < seg2 ? scale1 : scale2);
+      y[(size_t)m * (size_t)N + n] = (float)((double)s * acc);
+    }
+  }
+}
+
 void g4o_gemv_fp8w(const uint16_t* a, const uint8_t* W, int N, int K, float scale, float* y) {
   double dec[256];
   for (int c = 0; c < 256; ++c) dec[c] = g4o_fp8_decode((uint8_t)c);

@@ -74,6 +74,14 @@ void g4o_silu_mul_f32(const float* gu, int I, int rows, uint16_t* act);
 void g4o_gemm_fp8(const uint8_t* A, int lda, float a_scale, const uint8_t* W, int M, int N, int K,
                   float scale0, float scale1, float scale2, int seg1, int seg2, float* y);
 
+/* The reference's prefill GEMM value before its epilogue rounding
+ * (prefill_gemm.h:34-39, epi_store prefill_gemm.cu:69-89): bf16 A [M][lda]
+ * times fp8 e4m3 W [N][K]^T, y[m][n] = (float)((double)scale(n) * S), S the
+ * exact sum of bf16(a) * fp8(w) products (each exact) accumulated in double;
+ * scale(n) as g4o_gemm_fp8's. */
+void g4o_gemm_bf16w(const uint16_t* A, int lda, const uint8_t* W, int M, int N, int K,
+                    float scale0, float scale1, float scale2, int seg1, int seg2, float* y);
+
 /* Decode GEMV value before rounding (gemv_row_dequant forward_gpu.cu:934-994):
  * y[n] = scale * (float)S[n], S = sum_k bf16(a[k]) * fp8(W[n][k]) in double
  * (products exact). a bf16 [K], W [N][K], y [N]. */

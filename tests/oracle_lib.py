@@ -51,6 +51,8 @@ def _load():
         "g4o_gemm_fp8": (None, [u8p, _c.c_int, _c.c_float, u8p, _c.c_int, _c.c_int, _c.c_int,
                                 _c.c_float, _c.c_float, _c.c_float, _c.c_int, _c.c_int, f32p]),
         "g4o_gemv_fp8w": (None, [u16p, u8p, _c.c_int, _c.c_int, _c.c_float, f32p]),
+        "g4o_gemm_bf16w": (None, [u16p, _c.c_int, u8p, _c.c_int, _c.c_int, _c.c_int, _c.c_float,
+                                  _c.c_float, _c.c_float, _c.c_int, _c.c_int, f32p]),
         "g4o_rope_tables": (None, [_c.c_double, _c.c_int, _c.c_int, f32p, f32p]),
         "g4o_rope_rows": (None, [u16p, _c.c_int, _c.c_int, _c.c_int, i32p, f32p, f32p, u16p]),
         "g4o_kv_scale": (_c.c_float, [_c.c_float, _c.c_int]),
@@ -171,6 +173,20 @@ def gemm_fp8(A, a_scale, W, scales=(1.0, 1.0, 1.0), segs=None):
     y = np.empty((M, N), np.float32)
     lib.g4o_gemm_fp8(_p(A, u8p), K, a_scale, _p(W, u8p), M, N, K, scales[0], scales[1], scales[2],
                      s1, s2, _p(y, f32p))
+    return y
+
+
+def gemm_bf16w(A, W, scales=(1.0, 1.0, 1.0), segs=None):
+    """y [M][N] f32 (g4o_gemm_bf16w): bf16 A [M][K] x e4m3 W [N][K]^T, exact
+    products, double accumulation, scale by column segment."""
+    A = np.ascontiguousarray(A, np.uint16)
+    W = np.ascontiguousarray(W, np.uint8)
+    M, K = A.shape
+    N = W.shape[0]
+    s1, s2 = segs if segs is not None else (N, N)
+    y = np.empty((M, N), np.float32)
+    lib.g4o_gemm_bf16w(_p(A, u16p), K, _p(W, u8p), M, N, K, scales[0], scales[1], scales[2], s1,
+                       s2, _p(y, f32p))
     return y
 
 

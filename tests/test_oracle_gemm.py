@@ -55,3 +55,26 @@ def test_gemv_oracle_matches_float64_dot():
     y = ol.gemv_fp8w(a, W, 0.0123)
     exact = DEC[W] @ ol.bf16_to_f32(a).astype(np.float64)
     np.testing.assert_array_equal(y, np.float32(0.0123) * exact.astype(np.float32))
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 8, 32), (5, 31, 96), (33, 40, 256)])
+def test_gemm_bf16w_oracle_matches_float64_matmul(M, N, K):
+    """The reference prefill GEMM's value (bf16 A x fp8 W): numpy float64
+    matmul of the decoded operands, segment scales applied in double."""
+    A = ol.normal_bf16(0x71 + M, 0.0, 1.0, M * K).reshape(M, K)
+    W = ol.fp8_codes(0x72 + N, (N, K), std=0.5)
+    s1, s2 = N // 3, 2 * N // 3
+    y = ol.gemm_bf16w(A, W, scales=(0.011, 0.5, 3.0), segs=(s1, s2))
+    S = ol.bf16_to_f32(A).astype(np.float64) @ DEC[W].T
+    sc = np.where(np.arange(N) < s1, np.float32(0.011),
+                  np.where(np.arange(N) < s2, np.float32(0.5), np.float32(3.0))).astype(np.float64)
+    np.testing.assert_array_equal(y, (sc * S).astype(np.float32))
+
+
+def test_gemm_bf16w_oracle_one_hot_rows_pick_weight_columns():
+    K, N = 64, 16
+    A = np.zeros((K, K), np.uint16)
+    A[np.arange(K), np.arange(K)] = 0x3F80  # bf16 1.0
+    W = ol.fp8_codes(0x73, (N, K))
+    y = ol.gemm_bf16w(A, W, scales=(0.25, 0.25, 0.25))
+    np.testing.assert_array_equal(y, (0.25 * DEC[W].T).astype(np.float32))
