@@ -16,8 +16,8 @@
 // itself (8 KB from L2), which costs less than a separate launch.
 //
 // Layout: 256-thread workgroups of 16 weight rows (8 when 16 would leave
-// fewer than two workgroups per CU; swiglu: half gate rows, half the matching
-// up rows). The workgroup walks its rows in order with G4_GEMV_DEPTH
+// fewer than two workgroups per CU, 4 then for the forms without a norm
+// prologue; swiglu: half gate rows, half the matching up rows). The workgroup walks its rows in order with G4_GEMV_DEPTH
 // rows of loads in flight, its 4 waves reading each row together (wave w the
 // quarter [w K/4, (w+1) K/4), 16 bytes per lane per 1024-byte chunk,
 // non-temporal), so each workgroup's accesses stay inside a few contiguous
@@ -518,11 +518,27 @@ template <int PRO, int EPI>
 int launch_gemv(const GemvArgs& a, const char* what) {
   const int ch = (a.K / 4 + 1023) / 1024;
   const long long outputs = EPI == kEpiSwiglu ? 2LL * a.I : a.N;
-  const int rows = EPI != kEpiRope && outputs >= 16LL * 2 * kCUs ? 16 : 8;
+  // Rows per workgroup: 16 where that still leaves two workgroups per CU;
+  // otherwise 8, or 4 for the forms without a norm prologue. Measured per
+  // call (40-layer graphs, medians): O + residual 5.68 -> 5.33 us, q|k|v
+  // 6.76 -> 6.44, down + residual 11.81 -> 11.64 with 4 rows; the norm
+  // forms lose with 4 (their per-workgroup row norm is repeated twice as
+  // often: q|k|v 7.18 -> 7.39) and keep 8, as the RoPE form must (head-paired
+  // rows).
+  int rows = EPI != kEpiRope && outputs >= 16LL * 2 * kCUs ? 16 : 8;
+  if (rows == 8 && PRO == kProNone && EPI != kEpiRope && EPI != kEpiSwiglu) rows = 4;
   const unsigned grid = static_cast<unsigned>(EPI == kEpiSwiglu ? (a.I + rows / 2 - 1) / (rows / 2)
                                                                  : (a.N + rows - 1) / rows);
   const hipStream_t st = stream();
   const auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, 256, 0, st, a); };
+  if constexpr (PRO == kProNone && EPI != kEpiRope && EPI != kEpiSwiglu) {
+    if (rows == 4) {
+      if (ch <= 1) go(gemv_kernel<PRO, EPI, 1, 4>);
+      else if (ch == 2) go(gemv_kernel<PRO, EPI, 2, 4>);
+      else go(gemv_kernel<PRO, EPI, 4, 4>);
+      return launch_status(what);
+    }
+  }
   if (rows == 16) {
     if (ch <= 1) go(gemv_kernel<PRO, EPI, 1, 16>);
     else if (ch == 2) go(gemv_kernel<PRO, EPI, 2, 16>);
