@@ -15,9 +15,9 @@
 // (kernels_phase2.cu:51-132): every workgroup normalises the whole row for
 // itself (8 KB from L2), which costs less than a separate launch.
 //
-// Layout: 256-thread workgroups of 16 weight rows (8 when 16 would leave
-// fewer than two workgroups per CU, 4 then for the forms without a norm
-// prologue; swiglu: half gate rows, half the matching up rows). The workgroup walks its rows in order with G4_GEMV_DEPTH
+// Layout: 256-thread workgroups of 8 weight rows (4 for the smaller forms
+// without a norm prologue; swiglu: half gate rows, half the matching up
+// rows). The workgroup walks its rows in order with G4_GEMV_DEPTH
 // rows of loads in flight, its 4 waves reading each row together (wave w the
 // quarter [w K/4, (w+1) K/4), 16 bytes per lane per 1024-byte chunk,
 // non-temporal), so each workgroup's accesses stay inside a few contiguous
@@ -246,11 +246,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   // each row together (4 contiguous quarters), so the workgroup's accesses
   // stay within a few contiguous rows at any time. Every load is
   // unconditional (out-of-range data is zeroed before use).
-  // The 16-row norm-prologue form (gate/up) keeps all 16 rows in flight
-  // before the norm, so its latency overlaps the whole weight fetch.
-  // Measured per decode step: 16 rows in flight -15 us against 4; for the
-  // 8-row forms 8 in flight was +14 us against 4.
-  constexpr int kD = (PRO == kProNorm && kChunks == 1 && kRows == 16) ? 16 : kDepth;
+  // Measured: 8 rows in flight instead of 4 in the 8-row forms cost 14 us
+  // per decode step (all 8 in flight before the SwiGLU form's norm: no
+  // change, 18.7 vs 18.8 us per call).
+  constexpr int kD = kRows < kDepth ? kRows : kDepth;
   uint4 buf[kD][kChunks];
   const auto load_row = [&](int r, uint4 (&dst)[kChunks]) {
 #pragma unroll
@@ -518,15 +517,19 @@ template <int PRO, int EPI>
 int launch_gemv(const GemvArgs& a, const char* what) {
   const int ch = (a.K / 4 + 1023) / 1024;
   const long long outputs = EPI == kEpiSwiglu ? 2LL * a.I : a.N;
-  // Rows per workgroup: 16 where that still leaves two workgroups per CU;
-  // otherwise 8, or 4 for the forms without a norm prologue. Measured per
-  // call (40-layer graphs, medians): O + residual 5.68 -> 5.33 us, q|k|v
-  // 6.76 -> 6.44, down + residual 11.81 -> 11.64 with 4 rows; the norm
-  // forms lose with 4 (their per-workgroup row norm is repeated twice as
-  // often: q|k|v 7.18 -> 7.39) and keep 8, as the RoPE form must (head-paired
-  // rows).
-  int rows = EPI != kEpiRope && outputs >= 16LL * 2 * kCUs ? 16 : 8;
-  if (rows == 8 && PRO == kProNone && EPI != kEpiRope && EPI != kEpiSwiglu) rows = 4;
+  // Rows per workgroup: 8 (swiglu: 4 gate + 4 up rows), or 4 for the forms
+  // without a norm prologue whose outputs number fewer than 8192 (O, q|k|v,
+  // down). Measured per call (40-layer graphs, medians over interleaved
+  // rounds), against the earlier 16 rows for 8192 outputs and up:
+  //   norm + gate/up + SwiGLU   19.5 -> 18.3-18.9 us (4 rows: 27)
+  //   gate|up plain             19.5 -> 18.0-18.3
+  //   O + residual               5.68 -> 5.31 (4 rows)
+  //   q|k|v                      6.76 -> 6.41 (4 rows)
+  //   down + residual           11.81 -> 11.63 (4 rows)
+  // More workgroups hide the weight stream's latency better; the norm forms
+  // keep 8 (with 4 their per-workgroup row norm costs more than it hides:
+  // q|k|v 7.18 -> 7.39), as the RoPE form must (head-paired rows).
+  const int rows = PRO == kProNone && EPI != kEpiRope && EPI != kEpiSwiglu && outputs < 8192 ? 4 : 8;
   const unsigned grid = static_cast<unsigned>(EPI == kEpiSwiglu ? (a.I + rows / 2 - 1) / (rows / 2)
                                                                  : (a.N + rows - 1) / rows);
   const hipStream_t st = stream();
@@ -539,15 +542,9 @@ int launch_gemv(const GemvArgs& a, const char* what) {
       return launch_status(what);
     }
   }
-  if (rows == 16) {
-    if (ch <= 1) go(gemv_kernel<PRO, EPI, 1, 16>);
-    else if (ch == 2) go(gemv_kernel<PRO, EPI, 2, 16>);
-    else go(gemv_kernel<PRO, EPI, 4, 16>);
-  } else {
-    if (ch <= 1) go(gemv_kernel<PRO, EPI, 1, 8>);
-    else if (ch == 2) go(gemv_kernel<PRO, EPI, 2, 8>);
-    else go(gemv_kernel<PRO, EPI, 4, 8>);
-  }
+  if (ch <= 1) go(gemv_kernel<PRO, EPI, 1, 8>);
+  else if (ch == 2) go(gemv_kernel<PRO, EPI, 2, 8>);
+  else go(gemv_kernel<PRO, EPI, 4, 8>);
   return launch_status(what);
 }
 
