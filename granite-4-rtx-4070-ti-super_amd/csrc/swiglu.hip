@@ -30,6 +30,8 @@ namespace {
 
 enum : int { kOutBf16 = 0, kOutAmax = 1, kOutFp8 = 2 };
 
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+
 struct SwArgs {
   const void* gu;  // bf16 [rows][2I] (or f32 for the reference's prefill_silu_mul)
   int rows, I;
@@ -189,7 +191,12 @@ __global__ __launch_bounds__(kFusedThreads) void swiglu_fp8_fused_kernel(SwArgs 
 #pragma unroll
   for (int k = 0; k < kFusedVpt; ++k) x[k] = load_gu<false, true>(a, min(v0 + k * step, total - 1), nv);
   uint32_t w[kFusedVpt][4];
-  float m = 0.0f;
+  // max |act| on the bf16 bit patterns, two per v_pk_max_u16: for
+  // non-negative bf16 values the unsigned order of the patterns is the
+  // numeric order. A NaN pattern (above 0x7f80 once the sign is cleared)
+  // would win that maximum where fmaxf ignores NaN, so a lane that saw one
+  // recomputes its maximum with fmaxf from the values it holds.
+  u16x2_t mk = {0, 0};
 #pragma unroll
   for (int k = 0; k < kFusedVpt; ++k) {
     const int v = v0 + k * step;
@@ -197,6 +204,18 @@ __global__ __launch_bounds__(kFusedThreads) void swiglu_fp8_fused_kernel(SwArgs 
     for (int e = 0; e < 4; ++e) w[k][e] = act_pair<false>(x[k], e);
     if (v < total) {
       if (a.act != nullptr) st8_nt(a.act + 8LL * v, V8{{w[k][0], w[k][1], w[k][2], w[k][3]}});
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        mk = __builtin_elementwise_max(mk, __builtin_bit_cast(u16x2_t, w[k][e] & 0x7fff7fffu));
+    }
+  }
+  const uint32_t mb = mk[0] > mk[1] ? mk[0] : mk[1];
+  float m = __uint_as_float(mb << 16);
+  if (__builtin_expect(mb > 0x7f80u, 0)) {
+    m = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kFusedVpt; ++k) {
+      if (v0 + k * step >= total) break;
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         m = fmaxf(m, fmaxf(lo_bf16(w[k][e] & 0x7fff7fffu), hi_bf16(w[k][e] & 0x7fff7fffu)));

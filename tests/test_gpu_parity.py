@@ -678,3 +678,32 @@ def test_fp8_single_launch_wait_give_up_is_reported(op, rows):
     assert host(again)[0] == host(good)[0]
     np.testing.assert_array_equal(host(codes), good_codes)
     assert L.fp8_sync_status(work) == 0
+
+
+@pytest.mark.parametrize("rows", [8, 512, 2048])
+def test_swiglu_fp8_nan_inputs_are_ignored_by_the_scale(rows):
+    """A NaN act (from a NaN gate) is skipped by the per-tensor maximum, as
+    the reference quantiser's `a > amax` skips it (gpu_pack.cc:44-46); the
+    single-launch forms take that maximum on bf16 bit patterns, where a NaN
+    pattern would otherwise win."""
+    note(f"swiglu_fp8 NaN rows={rows}")
+    I_ = 12800
+    gu = ol.normal_bf16(0xE5 + rows, 0.0, 1.0, rows * 2 * I_).reshape(rows, 2 * I_)
+    gu[rows // 2, 17] = 0x7FC1   # NaN gate
+    gu[0, I_ + 3] = 0xFFC0       # NaN up (negative sign bit)
+    d_gu = dev(gu)
+    act = torch.empty((rows, I_), dtype=torch.int16, device="cuda")
+    L.call("granite4_swiglu", d_gu, rows, I_, act)
+    work = L.fp8_workspace()
+    for mode in (0, 1):
+        prev = L.set_fp8_launch_mode(mode)
+        try:
+            codes = torch.empty((rows, I_), dtype=torch.uint8, device="cuda")
+            scale = torch.empty(1, dtype=torch.float32, device="cuda")
+            L.call("granite4_swiglu_fp8", d_gu, rows, I_, codes, scale, work, None)
+        finally:
+            L.set_fp8_launch_mode(prev)
+        a = host(act)
+        assert np.isnan(ol.bf16_to_f32(a[rows // 2, 17]))
+        _fp8_check(host(codes), host(scale)[0], a)
+        assert np.isfinite(host(scale)[0]) and host(scale)[0] > 0
