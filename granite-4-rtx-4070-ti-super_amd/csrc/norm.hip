@@ -43,6 +43,8 @@ static_assert(g4::kMaxPartials <= g4::kBlock * g4::kSyncSlotsPerThread,
 namespace g4 {
 namespace {
 
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+
 enum : int { kOutBf16 = 0, kOutAmax = 1, kOutFp8 = 2 };
 
 struct NormArgs {
@@ -370,7 +372,11 @@ void norm_fp8_fused_kernel(NormArgs a, GridSync gs) {
   __shared__ uint4 s_y[HL > 0 ? HL : 1][VPL][kBlock];
   const unsigned tag = grid_sync_tag(gs);
   V8 y[HR > 0 ? HR : 1][VPL];
-  float m = 0.0f;
+  // max |y| on the bf16 bit patterns, two per v_pk_max_u16 (for
+  // non-negative bf16 values the unsigned order of the patterns is the
+  // numeric order); a lane that saw a NaN pattern (above 0x7f80 once the
+  // sign is cleared) recomputes its maximum with fmaxf, which skips NaN.
+  u16x2_t mk = {0, 0};
 #pragma unroll
   for (int h = 0; h < HR + HL; ++h) {
     const int rg = blockIdx.x + h * gridDim.x;  // uniform over the workgroup
@@ -385,11 +391,36 @@ void norm_fp8_fused_kernel(NormArgs a, GridSync gs) {
         yv.w[e] = pack_bf16_hw(lo_bf16(t.xv[j].w[e]) * t.r * lo_bf16(t.wv[j].w[e]),
                                hi_bf16(t.xv[j].w[e]) * t.r * hi_bf16(t.wv[j].w[e]));
         // lanes past the row's end hold zeros (x and w load as 0)
-        m = fmaxf(m, lo_bf16(yv.w[e] & 0x7fff7fffu));
-        m = fmaxf(m, hi_bf16(yv.w[e] & 0x7fff7fffu));
+        mk = __builtin_elementwise_max(mk, __builtin_bit_cast(u16x2_t, yv.w[e] & 0x7fff7fffu));
       }
       if (h < HR) y[h < HR ? h : 0][j] = yv;
       else s_y[h >= HR ? h - HR : 0][j][threadIdx.x] = make_uint4(yv.w[0], yv.w[1], yv.w[2], yv.w[3]);
+    }
+  }
+  const uint32_t mb = mk[0] > mk[1] ? mk[0] : mk[1];
+  float m = __uint_as_float(mb << 16);
+  if (__builtin_expect(mb > 0x7f80u, 0)) {
+    m = 0.0f;
+#pragma unroll
+    for (int h = 0; h < HR + HL; ++h) {
+      if (static_cast<int>(blockIdx.x + h * gridDim.x) >= a.rows) break;
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) {
+        uint32_t w4[4];
+        if (h < HR) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w4[e] = y[h < HR ? h : 0][j].w[e];
+        } else {
+          const uint4 q = s_y[h >= HR ? h - HR : 0][j][threadIdx.x];
+          w4[0] = q.x;
+          w4[1] = q.y;
+          w4[2] = q.z;
+          w4[3] = q.w;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          m = fmaxf(m, fmaxf(lo_bf16(w4[e] & 0x7fff7fffu), hi_bf16(w4[e] & 0x7fff7fffu)));
+      }
     }
   }
   const Fp8Enc f = fp8_scale_of(grid_max(m, gs, tag));

@@ -707,3 +707,30 @@ def test_swiglu_fp8_nan_inputs_are_ignored_by_the_scale(rows):
         assert np.isnan(ol.bf16_to_f32(a[rows // 2, 17]))
         _fp8_check(host(codes), host(scale)[0], a)
         assert np.isfinite(host(scale)[0]) and host(scale)[0] > 0
+
+
+@pytest.mark.parametrize("rows", [8, 512, 8192])
+def test_add_rmsnorm_fp8_nan_row_is_ignored_by_the_scale(rows):
+    """A NaN in one residual row makes that row's normed values NaN; the
+    per-tensor maximum skips them (the reference quantiser's `a > amax`), in
+    the single-launch forms as in the two-launch form."""
+    note(f"add_rmsnorm_fp8 NaN rows={rows}")
+    cols = 4096
+    res = _hidden(rows, cols, 0xE9 + rows)
+    res[rows // 2, 100] = 0x7FC0  # NaN
+    w = ol.normal_bf16(0xEA, 1.0, 0.1, cols)
+    d_res, d_w = dev(res), dev(w)
+    no = torch.empty_like(d_res)
+    L.call("granite4_add_rmsnorm", d_res, None, 1.0, d_w, 1e-5, rows, cols, None, no)
+    work = L.fp8_workspace()
+    for mode in (0, 1):
+        prev = L.set_fp8_launch_mode(mode)
+        try:
+            codes = torch.empty((rows, cols), dtype=torch.uint8, device="cuda")
+            scale = torch.empty(1, dtype=torch.float32, device="cuda")
+            L.call("granite4_add_rmsnorm_fp8", d_res, None, 1.0, d_w, 1e-5, rows, cols, None,
+                   codes, scale, work)
+        finally:
+            L.set_fp8_launch_mode(prev)
+        _fp8_check(host(codes), host(scale)[0], host(no))
+        assert np.isfinite(host(scale)[0]) and host(scale)[0] > 0
