@@ -87,23 +87,23 @@ __device__ __forceinline__ float epi_scale(const Granite4GemmEpilogue& ep, int n
 }
 
 // Weight row behind tile row r (0..127) of N tile tn, or -1 past the end.
-template <int EPI>
+template <int EPI, int TN = kGBN>
 __device__ __forceinline__ int w_row(const GemmArgs& a, int tn, int r) {
   if (EPI == kEpiSwiglu) {
     const int c = tn * 64 + (r & 63);
     if (c >= a.I) return -1;
     return r < 64 ? c : a.I + c;
   }
-  const int n = tn * kGBN + r;
+  const int n = tn * TN + r;
   return n < a.N ? n : -1;
 }
 
 // Tile row of the wave's B fragment ni (swiglu: ni 0, 1 gate; 2, 3 the
 // matching up rows, so one lane holds g and u of the same act element).
-template <int EPI>
+template <int EPI, int TN = kGBN>
 __device__ __forceinline__ int b_row(int wn, int ni) {
   if (EPI == kEpiSwiglu) return ni < 2 ? wn * 32 + ni * 16 : 64 + wn * 32 + (ni - 2) * 16;
-  return wn * 64 + ni * 16;
+  return wn * (TN / 2) + ni * 16;
 }
 
 // Stage layout: [A 128 rows][W 128 rows] x 128 bytes, the eight 16-byte
@@ -115,7 +115,7 @@ __device__ __forceinline__ int b_row(int wn, int ni) {
 // valid row instead (their results are never stored).
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
-template <int EPI>
+template <int EPI, int TN = kGBN>
 __device__ __forceinline__ void stage_issue(const GemmArgs& a, int m0, int tn, int k0,
                                             uint8_t* st) {
   const int wave = threadIdx.x >> 6;
@@ -129,10 +129,10 @@ __device__ __forceinline__ void stage_issue(const GemmArgs& a, int m0, int tn, i
                                      0, 0);
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < TN / 32; ++i) {
     const int slot = i * 256 + threadIdx.x;
     const int row = slot >> 3, c = (slot & 7) ^ (row & 7);
-    int n = w_row<EPI>(a, tn, row);
+    int n = w_row<EPI, TN>(a, tn, row);
     if (n < 0) n = 0;
     __builtin_amdgcn_global_load_lds(a.W + static_cast<size_t>(n) * a.K + k0 + 16 * c,
                                      (lds_ptr)(st + kGBM * kGBK + (i * 256 + wave * 64) * 16),
@@ -285,9 +285,15 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, const v4f (&acc
   }
 }
 
-template <int EPI>
+// TN: weight rows per tile, 128, or 64 where 128 x 128 tiles cannot fill the
+// CUs (a short prompt's O and down projections: 128 tiles at M = 512); each
+// wave then owns 64 x 32 outputs (4 x 2 MFMA tiles).
+template <int EPI, int TN = kGBN>
 __global__ __launch_bounds__(256) void gemm_fp8_kernel(GemmArgs a) {
-  __shared__ __align__(16) uint8_t s_tile[kGStages * kGStage];
+  static_assert(TN == kGBN || (TN == 64 && EPI != kEpiSwiglu), "tile width");
+  constexpr int kNI = TN / 32;  // MFMA tiles per wave along N
+  constexpr int kStage = (kGBM + TN) * kGBK;
+  __shared__ __align__(16) uint8_t s_tile[kGStages * kStage];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -298,11 +304,11 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(GemmArgs a) {
   float amax = 0.0f;
   static_assert(kGStages >= 2 && kGStages <= 4, "pipeline depth");
   // Epilogue geometry: the wave's output block is 64 rows x kWCols columns.
-  constexpr int kWCols = EPI == kEpiSwiglu ? 32 : 64;
+  constexpr int kWCols = EPI == kEpiSwiglu ? 32 : TN / 2;
   constexpr int kLanesPerRow = kWCols / 8;
   constexpr int kRowsPerIter = 64 / kLanesPerRow;
   constexpr int kIters = 32 / kRowsPerIter;
-  static_assert(4 * 32 * kEP * 4 <= kGStages * kGStage, "epilogue staging fits the stage buffers");
+  static_assert(4 * 32 * kEP * 4 <= kGStages * kStage, "epilogue staging fits the stage buffers");
 
   for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
     const int tm = tile % a.mt, tn = tile / a.mt;
@@ -314,7 +320,7 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(GemmArgs a) {
       for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
     // This wave's output columns [col0, col0 + kWCols) (act columns for swiglu).
-    const int col0 = EPI == kEpiSwiglu ? tn * 64 + wn * 32 : tn * kGBN + wn * 64;
+    const int col0 = EPI == kEpiSwiglu ? tn * 64 + wn * 32 : tn * TN + wn * (TN / 2);
     const int n_end = EPI == kEpiSwiglu ? a.I : a.N;
     uint4 res[EPI == kEpiResidual ? 2 * kIters : 1];
     if (EPI == kEpiResidual) {
@@ -332,7 +338,7 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(GemmArgs a) {
     __syncthreads();  // the previous tile's readers are done with every buffer
 #pragma unroll
     for (int sidx = 0; sidx < kGStages - 1; ++sidx)
-      if (sidx < ktiles) stage_issue<EPI>(a, m0, tn, sidx * kGBK, s_tile + sidx * kGStage);
+      if (sidx < ktiles) stage_issue<EPI, TN>(a, m0, tn, sidx * kGBK, s_tile + sidx * kStage);
     for (int kt = 0; kt < ktiles; ++kt) {
       // Stages issued after kt so far: min(kStages - 2, ktiles - 1 - kt).
       const int later = min(kGStages - 2, ktiles - 1 - kt);
@@ -342,25 +348,25 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(GemmArgs a) {
       // a workgroup-scope release would wait for the stages still in flight.
       __builtin_amdgcn_s_barrier();
       if (kt + kGStages - 1 < ktiles)
-        stage_issue<EPI>(a, m0, tn, (kt + kGStages - 1) * kGBK,
-                         s_tile + ((kt + kGStages - 1) % kGStages) * kGStage);
-      const uint32_t st = lds_addr(s_tile + (kt % kGStages) * kGStage);
-      v4u ax[4], ay[4], bx[4], by[4];
+        stage_issue<EPI, TN>(a, m0, tn, (kt + kGStages - 1) * kGBK,
+                             s_tile + ((kt + kGStages - 1) % kGStages) * kStage);
+      const uint32_t st = lds_addr(s_tile + (kt % kGStages) * kStage);
+      v4u ax[4], ay[4], bx[kNI], by[kNI];
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi) frag_issue(st, wm * 64 + mi * 16 + fr, lane, ax[mi], ay[mi]);
 #pragma unroll
-      for (int ni = 0; ni < 4; ++ni)
-        frag_issue(st + kGBM * kGBK, b_row<EPI>(wn, ni) + fr, lane, bx[ni], by[ni]);
+      for (int ni = 0; ni < kNI; ++ni)
+        frag_issue(st + kGBM * kGBK, b_row<EPI, TN>(wn, ni) + fr, lane, bx[ni], by[ni]);
       lds_reads_done();
       // The fragments pass through the wait: no use can move above it.
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        asm volatile("" : "+v"(ax[j]), "+v"(ay[j]), "+v"(bx[j]), "+v"(by[j]));
-      }
+      for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(ax[j]), "+v"(ay[j]));
+#pragma unroll
+      for (int j = 0; j < kNI; ++j) asm volatile("" : "+v"(bx[j]), "+v"(by[j]));
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni)
+        for (int ni = 0; ni < kNI; ++ni)
           acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
               frag_of(ax[mi], ay[mi]), frag_of(bx[ni], by[ni]), acc[mi][ni], 0, 0, 0, 0, 0, 0);
     }
@@ -537,9 +543,9 @@ bool gemm_args_ok(const uint8_t* A, int lda, const uint8_t* W, int M, int N, int
          static_cast<long long>(M) * lda < (1LL << 40);
 }
 
-template <int EPI>
+template <int EPI, int TN = kGBN>
 unsigned gemm_grid(long long tiles, int cap) {
-  const int resident = resident_blocks(reinterpret_cast<const void*>(gemm_fp8_kernel<EPI>), 256);
+  const int resident = resident_blocks(reinterpret_cast<const void*>(gemm_fp8_kernel<EPI, TN>), 256);
   long long g = tiles;
   if (resident > 0 && g > resident) g = resident;
   if (g > cap) g = cap;
@@ -576,20 +582,25 @@ int granite4_gemm_fp8(int out, const uint8_t* A, int lda, const float* d_a_scale
   a.K = K;
   a.ep = *ep;
   a.mt = (M + kGBM - 1) / kGBM;
-  a.nt = (N + kGBN - 1) / kGBN;
   a.vec_out = true;
+  // 128 x 64 tiles where 128 x 128 ones would leave CUs idle.
+  const bool narrow = static_cast<long long>(a.mt) * ((N + kGBN - 1) / kGBN) < kCUs;
+  a.nt = narrow ? (N + 63) / 64 : (N + kGBN - 1) / kGBN;
   const long long tiles = static_cast<long long>(a.mt) * a.nt;
   const hipStream_t st = stream();
+  const auto go = [&](auto kern, unsigned grid) { hipLaunchKernelGGL(kern, grid, 256, 0, st, a); };
   switch (out) {
     case GRANITE4_GEMM_BF16:
-      hipLaunchKernelGGL(gemm_fp8_kernel<kEpiBf16>, gemm_grid<kEpiBf16>(tiles, INT_MAX), 256, 0, st, a);
+      if (narrow) go(gemm_fp8_kernel<kEpiBf16, 64>, gemm_grid<kEpiBf16, 64>(tiles, INT_MAX));
+      else go(gemm_fp8_kernel<kEpiBf16>, gemm_grid<kEpiBf16>(tiles, INT_MAX));
       break;
     case GRANITE4_GEMM_F32:
-      hipLaunchKernelGGL(gemm_fp8_kernel<kEpiF32>, gemm_grid<kEpiF32>(tiles, INT_MAX), 256, 0, st, a);
+      if (narrow) go(gemm_fp8_kernel<kEpiF32, 64>, gemm_grid<kEpiF32, 64>(tiles, INT_MAX));
+      else go(gemm_fp8_kernel<kEpiF32>, gemm_grid<kEpiF32>(tiles, INT_MAX));
       break;
     default:
-      hipLaunchKernelGGL(gemm_fp8_kernel<kEpiResidual>, gemm_grid<kEpiResidual>(tiles, INT_MAX), 256,
-                         0, st, a);
+      if (narrow) go(gemm_fp8_kernel<kEpiResidual, 64>, gemm_grid<kEpiResidual, 64>(tiles, INT_MAX));
+      else go(gemm_fp8_kernel<kEpiResidual>, gemm_grid<kEpiResidual>(tiles, INT_MAX));
       break;
   }
   return launch_status("granite4_gemm_fp8");
