@@ -40,6 +40,7 @@
 #include "rope_unit.h"
 
 #include <climits>
+#include <type_traits>
 #include <cmath>
 
 namespace g4 {
@@ -748,6 +749,10 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(AttnArgs 
 // output is bf16(o * (1 / l)) (prefill_gemm.cu:930-940).
 // ---------------------------------------------------------------------------
 constexpr int kKPitch = kHd + 8;  // K tile pitch (bf16): 272 B, 16 rows on distinct banks
+// Waves per prefill workgroup. Staging a tile's K / V into LDS is split over
+// all of them, so more waves sharing a tile cost less staging per score.
+constexpr int kPrefWaves = 8;
+constexpr int kPrefThreads = kPrefWaves * 64;
 
 struct PrefillArgs {
   const uint16_t* q;  // [rows][Hq][128]
@@ -777,9 +782,12 @@ struct PrefillRaw {
   static constexpr int kNgrp = kQuant ? kHd / GROUP : 1;
   static constexpr int kKElems = BITS == 16 ? 8 : BITS == 8 ? 16 : 32;  // per K chunk
   static constexpr int kKRowChunks = kHd / kKElems;
-  static constexpr int kKIt = (kTile * kKRowChunks + kAttnWaves * 64 - 1) / (kAttnWaves * 64);
+  static constexpr int kKIt = (kTile * kKRowChunks + kPrefThreads - 1) / (kPrefThreads);
   static constexpr int kVRowChunks = VStage<BITS>::kChunks;
-  static constexpr int kVIt = (kTile * kVRowChunks + kAttnWaves * 64 - 1) / (kAttnWaves * 64);
+  static constexpr int kVIt = (kTile * kVRowChunks + kPrefThreads - 1) / (kPrefThreads);
+  // V chunks start on the thread after the last K chunk's, so a tile whose K
+  // chunks fill only part of the workgroup puts its V on the idle threads.
+  static constexpr int kVShift = (kTile * kKRowChunks) % kPrefThreads;
   u32x4_t k[kKIt][kKElems / 8];
   u32x4_t v[kVIt];
   float ksc[kKIt][kNgrp], vsc[kKIt][kNgrp];
@@ -792,17 +800,17 @@ __device__ __forceinline__ void prefill_pt(const PrefillArgs& a, int j0, int kv_
                                            int (&ptk)[PrefillRaw<BITS, GROUP>::kKIt],
                                            int (&ptv)[PrefillRaw<BITS, GROUP>::kVIt]) {
   using R = PrefillRaw<BITS, GROUP>;
-  const int t = threadIdx.x;
+  const int t = threadIdx.x, tv = (t + R::kVShift) % kPrefThreads;
   const int last = max(kv_end - 1, 0);
 #pragma unroll
   for (int it = 0; it < R::kKIt; ++it) {
-    const int key = min((t + it * kAttnWaves * 64) / R::kKRowChunks, kTile - 1);
+    const int key = min((t + it * kPrefThreads) / R::kKRowChunks, kTile - 1);
     const int p = j0 + key;
     ptk[it] = a.d_pt != nullptr ? a.d_pt[min(p, last)] : p;
   }
 #pragma unroll
   for (int it = 0; it < R::kVIt; ++it) {
-    const int key = min((t + it * kAttnWaves * 64) / R::kVRowChunks, kTile - 1);
+    const int key = min((tv + it * kPrefThreads) / R::kVRowChunks, kTile - 1);
     const int p = j0 + key;
     ptv[it] = a.d_pt != nullptr ? a.d_pt[min(p, last)] : p;
   }
@@ -817,16 +825,18 @@ __device__ __forceinline__ void prefill_load(const PrefillArgs& a, const uint8_t
                                              PrefillRaw<BITS, GROUP>& raw) {
   using R = PrefillRaw<BITS, GROUP>;
   constexpr int kKb = k_row_bytes(BITS);
-  const int t = threadIdx.x;
+  const int t = threadIdx.x, tv = (t + R::kVShift) % kPrefThreads;
   auto valid = [&](int key, int r) {
     return (j0 + key < kv_end && r >= 0 && r < a.stride) ? r : -1;
   };
 #pragma unroll
   for (int it = 0; it < R::kKIt; ++it) {
-    const int idx = t + it * kAttnWaves * 64;
-    const int key = min(idx / R::kKRowChunks, kTile - 1);
+    const int idx = t + it * kPrefThreads;
+    raw.kr[it] = -1;
+    if (idx >= kTile * R::kKRowChunks) continue;  // no K chunk (whole waves)
+    const int key = idx / R::kKRowChunks;
     const int c = (idx % R::kKRowChunks) * R::kKElems;
-    const int pr = idx < kTile * R::kKRowChunks ? valid(key, ptk[it]) : -1;
+    const int pr = valid(key, ptk[it]);
     raw.kr[it] = pr;
     const uint8_t* row = kbase + static_cast<size_t>(pr >= 0 ? pr : 0) * kKb;
 #pragma unroll
@@ -842,10 +852,12 @@ __device__ __forceinline__ void prefill_load(const PrefillArgs& a, const uint8_t
   }
 #pragma unroll
   for (int it = 0; it < R::kVIt; ++it) {
-    const int idx = t + it * kAttnWaves * 64;
-    const int key = min(idx / R::kVRowChunks, kTile - 1);
+    const int idx = tv + it * kPrefThreads;
+    raw.vr[it] = -1;
+    if (idx >= kTile * R::kVRowChunks) continue;  // no V chunk (whole waves)
+    const int key = idx / R::kVRowChunks;
     const int c = idx % R::kVRowChunks;
-    const int pr = idx < kTile * R::kVRowChunks ? valid(key, ptv[it]) : -1;
+    const int pr = valid(key, ptv[it]);
     raw.vr[it] = pr;
     raw.v[it] = *reinterpret_cast<const u32x4_t*>(
         vbase + static_cast<size_t>(pr >= 0 ? pr : 0) * VStage<BITS>::kRowB + 16 * c);
@@ -855,12 +867,12 @@ __device__ __forceinline__ void prefill_load(const PrefillArgs& a, const uint8_t
 template <int BITS, int GROUP>
 __device__ __forceinline__ void prefill_store(const PrefillRaw<BITS, GROUP>& raw, uint16_t* ks,
                                               uint16_t* vs, float* ksc_l, float* vsc_l,
-                                              unsigned* s_valid) {
+                                              unsigned* s_valid, float kmul) {
   using R = PrefillRaw<BITS, GROUP>;
-  const int t = threadIdx.x;
+  const int t = threadIdx.x, tv = (t + R::kVShift) % kPrefThreads;
 #pragma unroll
   for (int it = 0; it < R::kKIt; ++it) {
-    const int idx = t + it * kAttnWaves * 64;
+    const int idx = t + it * kPrefThreads;
     if (idx >= kTile * R::kKRowChunks) break;
     const int key = idx / R::kKRowChunks, c = (idx % R::kKRowChunks) * R::kKElems;
     const int pr = raw.kr[it];
@@ -875,7 +887,7 @@ __device__ __forceinline__ void prefill_store(const PrefillRaw<BITS, GROUP>& raw
       if constexpr (R::kQuant) {
 #pragma unroll
         for (int gi = 0; gi < R::kNgrp; ++gi) {
-          ksc_l[key * R::kNgrp + gi] = pr >= 0 ? raw.ksc[it][gi] : 0.0f;
+          ksc_l[key * R::kNgrp + gi] = pr >= 0 ? raw.ksc[it][gi] * kmul : 0.0f;
           vsc_l[key * R::kNgrp + gi] = pr >= 0 ? raw.vsc[it][gi] : 0.0f;
         }
       }
@@ -884,7 +896,7 @@ __device__ __forceinline__ void prefill_store(const PrefillRaw<BITS, GROUP>& raw
   }
 #pragma unroll
   for (int it = 0; it < R::kVIt; ++it) {
-    const int idx = t + it * kAttnWaves * 64;
+    const int idx = tv + it * kPrefThreads;
     if (idx >= kTile * R::kVRowChunks) break;
     const int key = idx / R::kVRowChunks, c = idx % R::kVRowChunks;
     const uint32_t z = BITS == 16 || BITS == 8 ? 0u : 0x88888888u;
@@ -923,15 +935,17 @@ __device__ __forceinline__ void prefill_store(const PrefillRaw<BITS, GROUP>& raw
 // fragments read from LDS serve all CB blocks, and a staged tile serves
 // 16 CB positions.
 template <int BITS, int GROUP, int CB>
-__global__ __launch_bounds__(kAttnWaves * 64) void attn_prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(kPrefThreads) void attn_prefill_kernel(PrefillArgs a) {
   constexpr bool kQuant = BITS != 16;
   constexpr int kNgrp = kQuant ? kHd / GROUP : 1;
   constexpr int kKb = k_row_bytes(BITS), kVb = v_row_bytes(BITS);
-  constexpr int kPos = kAttnWaves * 4 * CB;  // positions per workgroup
-  __shared__ __align__(16) uint16_t ks[kTile * kKPitch];
-  __shared__ __align__(16) uint16_t vs[kTile * kVPitch];
-  __shared__ float ksc_l[kTile * kNgrp], vsc_l[kTile * kNgrp];
-  __shared__ unsigned s_valid[kTile];
+  constexpr int kPos = kPrefWaves * 4 * CB;  // positions per workgroup
+  // Two tile buffers: tile t + 1 is staged into one while tile t is read from
+  // the other, with one barrier per tile.
+  __shared__ __align__(16) uint16_t ks2[2][kTile * kKPitch];
+  __shared__ __align__(16) uint16_t vs2[2][kTile * kVPitch];
+  __shared__ float ksc2[2][kTile * kNgrp], vsc2[2][kTile * kNgrp];
+  __shared__ unsigned valid2[2][kTile];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, n = lane & 15;
@@ -977,6 +991,13 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_prefill_kernel(PrefillAr
     l[cb] = 0.0f;
   }
 
+  // The wave's columns span positions [wave_pos_min, wave_pos_min + 4 CB);
+  // the last one's window starts at wave_lo_max.
+  const int wave_row0 = p0 + 4 * CB * wave;
+  const bool wave_live = wave_row0 + 4 * CB - 1 < a.rows;
+  const int wave_pos_min = a.base + wave_row0;
+  const int wave_lo_max = a.window > 0 ? max(0, wave_pos_min + 4 * CB - a.window) : 0;
+
   using Raw = PrefillRaw<BITS, GROUP>;
   Raw raw;
   int ptk[Raw::kKIt], ptv[Raw::kVIt];
@@ -984,123 +1005,157 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_prefill_kernel(PrefillAr
     prefill_pt<BITS, GROUP>(a, j_first, kv_end, ptk, ptv);
     prefill_load<BITS, GROUP>(a, kbase, vbase, kscb, vscb, j_first, kv_end, ptk, ptv, raw);
     prefill_pt<BITS, GROUP>(a, j_first + kTile, kv_end, ptk, ptv);
-  }
-  for (int j0 = j_first; j0 < kv_end; j0 += kTile) {
-    __syncthreads();  // the previous tile's readers are done
-    prefill_store<BITS, GROUP>(raw, ks, vs, ksc_l, vsc_l, s_valid);
-    __syncthreads();
-    if (j0 + kTile < kv_end) {
-      // the next tile's bytes (its page-table entries arrived during this
-      // tile's predecessor), then the entries of the tile after it
-      prefill_load<BITS, GROUP>(a, kbase, vbase, kscb, vscb, j0 + kTile, kv_end, ptk, ptv, raw);
-      prefill_pt<BITS, GROUP>(a, j0 + 2 * kTile, kv_end, ptk, ptv);
+    prefill_store<BITS, GROUP>(raw, ks2[0], vs2[0], ksc2[0], vsc2[0], valid2[0], a.scale);
+    if (j_first + kTile < kv_end) {
+      prefill_load<BITS, GROUP>(a, kbase, vbase, kscb, vscb, j_first + kTile, kv_end, ptk, ptv, raw);
+      prefill_pt<BITS, GROUP>(a, j_first + 2 * kTile, kv_end, ptk, ptv);
     }
-    float e[CB][4][4];
+  }
+  __syncthreads();
+  int buf = 0;
+  for (int j0 = j_first; j0 < kv_end; j0 += kTile, buf ^= 1) {
+    const uint16_t* ks = ks2[buf];
+    const uint16_t* vs = vs2[buf];
+    const float* ksc_l = ksc2[buf];
+    const float* vsc_l = vsc2[buf];
+    const unsigned* s_valid = valid2[buf];
+    // A tile that every column of this wave sees whole (all keys at or below
+    // the wave's first position, at or above its last window start, each with
+    // an arena row) takes the form without the mask.
+    const bool full = wave_live && j0 + kTile - 1 <= wave_pos_min && j0 >= wave_lo_max &&
+                      __all(s_valid[lane] != 0u);
+    auto tile = [&](auto mask_tag) {
+      constexpr bool kMask = decltype(mask_tag)::value;
+      float e[CB][4][4];
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      bf16x8_t ka[4];
+      for (int mb = 0; mb < 4; ++mb) {
+        bf16x8_t ka[4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        ka[s] = *reinterpret_cast<const bf16x8_t*>(ks + (16 * mb + n) * kKPitch + 32 * s + 8 * g);
-      float ksv[4][kNgrp];
-      bool kv_ok[4];
+        for (int s = 0; s < 4; ++s)
+          ka[s] = *reinterpret_cast<const bf16x8_t*>(ks + (16 * mb + n) * kKPitch + 32 * s + 8 * g);
+        float ksv[4][kNgrp];
+        bool kv_ok[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = 16 * mb + 4 * g + i;
-        kv_ok[i] = s_valid[key] != 0u;
+        for (int i = 0; i < 4; ++i) {
+          const int key = 16 * mb + 4 * g + i;
+          kv_ok[i] = kMask ? s_valid[key] != 0u : true;
 #pragma unroll
-        for (int gi = 0; gi < kNgrp; ++gi) ksv[i][gi] = kQuant ? ksc_l[key * kNgrp + gi] : 1.0f;
+          for (int gi = 0; gi < kNgrp; ++gi) ksv[i][gi] = kQuant ? ksc_l[key * kNgrp + gi] : 1.0f;
+        }
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+          // dot * scale: the staged K scales carry the logit scale.
+          f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+          if constexpr (!kQuant || GROUP == kHd) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s], qb[cb][s], acc, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = acc[i] * (kQuant ? ksv[i][0] : a.scale);
+          } else {
+            constexpr int kSteps = GROUP / 32;
+#pragma unroll
+            for (int gi = 0; gi < kNgrp; ++gi) {
+              f32x4_t part = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+              for (int s = gi * kSteps; s < (gi + 1) * kSteps; ++s)
+                part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s], qb[cb][s], part, 0, 0, 0);
+#pragma unroll
+              for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(part[i], ksv[i][gi], acc[i]);
+            }
+          }
+          const uint32_t lg01 = pack_bf16_hw(acc[0], acc[1]);
+          const uint32_t lg23 = pack_bf16_hw(acc[2], acc[3]);
+          const float lg[4] = {lo_bf16(lg01), hi_bf16(lg01), lo_bf16(lg23), hi_bf16(lg23)};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if constexpr (kMask) {
+              const int j = j0 + 16 * mb + 4 * g + i;
+              const bool ok = live[cb] && j <= my_pos[cb] && j >= my_lo[cb] && kv_ok[i];
+              e[cb][mb][i] = ok ? lg[i] : -INFINITY;
+            } else {
+              e[cb][mb][i] = lg[i];
+            }
+          }
+        }
       }
+      // Online softmax per column block (e holds the logits until here).
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb) {
-        f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        if constexpr (!kQuant || GROUP == kHd) {
+        float mx = m[cb];
 #pragma unroll
-          for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s], qb[cb][s], acc, 0, 0, 0);
-          if constexpr (kQuant) {
+        for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[i] = acc[i] * ksv[i][0];
+          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, e[cb][mb][i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        // Where no column's maximum moved, the rescale factor is exactly 1:
+        // skip the multiply of o and l (a wave-uniform branch).
+        if (__any(mx != m[cb])) {
+          const float alpha = mx == -INFINITY ? 1.0f : __expf(m[cb] - mx);
+          m[cb] = mx;
+          l[cb] *= alpha;
+#pragma unroll
+          for (int nb = 0; nb < 8; ++nb) o[cb][nb] *= alpha;
+        }
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if constexpr (kMask) e[cb][mb][i] = mx == -INFINITY ? 0.0f : __expf(e[cb][mb][i] - mx);
+            else e[cb][mb][i] = __expf(e[cb][mb][i] - mx);
+            l[cb] += e[cb][mb][i];
           }
-        } else {
-          constexpr int kSteps = GROUP / 32;
-#pragma unroll
-          for (int gi = 0; gi < kNgrp; ++gi) {
-            f32x4_t part = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int s = gi * kSteps; s < (gi + 1) * kSteps; ++s)
-              part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s], qb[cb][s], part, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[i] += part[i] * ksv[i][gi];
-          }
-        }
-        const uint32_t lg01 = pack_bf16_hw(a.scale * acc[0], a.scale * acc[1]);
-        const uint32_t lg23 = pack_bf16_hw(a.scale * acc[2], a.scale * acc[3]);
-        const float lg[4] = {lo_bf16(lg01), hi_bf16(lg01), lo_bf16(lg23), hi_bf16(lg23)};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int j = j0 + 16 * mb + 4 * g + i;
-          const bool ok = live[cb] && j <= my_pos[cb] && j >= my_lo[cb] && kv_ok[i];
-          e[cb][mb][i] = ok ? lg[i] : -INFINITY;
-        }
       }
-    }
-    // Online softmax per column block (e holds the logits until here).
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb) {
-      float mx = m[cb];
+      for (int s = 0; s < 2; ++s) {
+        float vsv[8][kNgrp];
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
+        for (int jj = 0; jj < 8; ++jj) {
+          const int key = 16 * (2 * s + (jj >> 2)) + 4 * g + (jj & 3);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, e[cb][mb][i]);
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float alpha = mx == -INFINITY ? 1.0f : __expf(m[cb] - mx);
-      m[cb] = mx;
-      l[cb] *= alpha;
-#pragma unroll
-      for (int nb = 0; nb < 8; ++nb) o[cb][nb] *= alpha;
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          e[cb][mb][i] = mx == -INFINITY ? 0.0f : __expf(e[cb][mb][i] - mx);
-          l[cb] += e[cb][mb][i];
+          for (int gi = 0; gi < kNgrp; ++gi) vsv[jj][gi] = kQuant ? vsc_l[key * kNgrp + gi] : 1.0f;
         }
-    }
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      float vsv[8][kNgrp];
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        const int key = 16 * (2 * s + (jj >> 2)) + 4 * g + (jj & 3);
-#pragma unroll
-        for (int gi = 0; gi < kNgrp; ++gi) vsv[jj][gi] = kQuant ? vsc_l[key * kNgrp + gi] : 1.0f;
-      }
-      bf16x8_t pb[CB][kNgrp];
-#pragma unroll
-      for (int cb = 0; cb < CB; ++cb)
-#pragma unroll
-        for (int gi = 0; gi < kNgrp; ++gi) {
-          float pv[8];
-#pragma unroll
-          for (int jj = 0; jj < 8; ++jj) pv[jj] = e[cb][2 * s + (jj >> 2)][jj & 3] * vsv[jj][gi];
-          pb[cb][gi] = as_bf16x8(pack_bf16_hw(pv[0], pv[1]), pack_bf16_hw(pv[2], pv[3]),
-                                 pack_bf16_hw(pv[4], pv[5]), pack_bf16_hw(pv[6], pv[7]));
-        }
-      const int kk = n >> 2, dd = 4 * (n & 3);
-      const uint16_t* r1 = vs + (32 * s + 4 * g + kk) * kVPitch + dd;
-      const uint16_t* r2 = r1 + 16 * kVPitch;
-#pragma unroll
-      for (int nb = 0; nb < 8; ++nb) {
-        const u32x2_t lo2 = lds_read_tr(r1 + 16 * nb);
-        const u32x2_t hi2 = lds_read_tr(r2 + 16 * nb);
-        const bf16x8_t va = as_bf16x8(lo2.x, lo2.y, hi2.x, hi2.y);
-        const int gi = kQuant ? (16 * nb) / GROUP : 0;
+        bf16x8_t pb[CB][kNgrp];
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb)
-          o[cb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[cb][gi], o[cb][nb], 0, 0, 0);
+#pragma unroll
+          for (int gi = 0; gi < kNgrp; ++gi) {
+            float pv[8];
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj)
+              pv[jj] = kQuant ? e[cb][2 * s + (jj >> 2)][jj & 3] * vsv[jj][gi] : e[cb][2 * s + (jj >> 2)][jj & 3];
+            pb[cb][gi] = as_bf16x8(pack_bf16_hw(pv[0], pv[1]), pack_bf16_hw(pv[2], pv[3]),
+                                   pack_bf16_hw(pv[4], pv[5]), pack_bf16_hw(pv[6], pv[7]));
+          }
+        const int kk = n >> 2, dd = 4 * (n & 3);
+        const uint16_t* r1 = vs + (32 * s + 4 * g + kk) * kVPitch + dd;
+        const uint16_t* r2 = r1 + 16 * kVPitch;
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) {
+          const u32x2_t lo2 = lds_read_tr(r1 + 16 * nb);
+          const u32x2_t hi2 = lds_read_tr(r2 + 16 * nb);
+          const bf16x8_t va = as_bf16x8(lo2.x, lo2.y, hi2.x, hi2.y);
+          const int gi = kQuant ? (16 * nb) / GROUP : 0;
+#pragma unroll
+          for (int cb = 0; cb < CB; ++cb)
+            o[cb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[cb][gi], o[cb][nb], 0, 0, 0);
+        }
+      }
+    };
+    if (full) tile(std::false_type{});
+    else tile(std::true_type{});
+    if (j0 + kTile < kv_end) {
+      // Stage the next tile (its bytes were loaded a tile ago) into the other
+      // buffer, whose last readers passed the previous barrier; then load the
+      // bytes of the tile after it and the page-table entries of the third.
+      prefill_store<BITS, GROUP>(raw, ks2[buf ^ 1], vs2[buf ^ 1], ksc2[buf ^ 1], vsc2[buf ^ 1],
+                                 valid2[buf ^ 1], a.scale);
+      if (j0 + 2 * kTile < kv_end) {
+        prefill_load<BITS, GROUP>(a, kbase, vbase, kscb, vscb, j0 + 2 * kTile, kv_end, ptk, ptv, raw);
+        prefill_pt<BITS, GROUP>(a, j0 + 3 * kTile, kv_end, ptk, ptv);
       }
     }
+    __syncthreads();
   }
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) {
@@ -1159,11 +1214,11 @@ void launch_prefill_bits(const PrefillArgs& a, int group, dim3 grid, hipStream_t
   constexpr int CB = kPrefillCb;
   if constexpr (BITS == 16) {
     (void)group;
-    hipLaunchKernelGGL((attn_prefill_kernel<16, kHd, CB>), grid, kAttnWaves * 64, 0, st, a);
+    hipLaunchKernelGGL((attn_prefill_kernel<16, kHd, CB>), grid, kPrefThreads, 0, st, a);
   } else {
-    if (group == kHd) hipLaunchKernelGGL((attn_prefill_kernel<BITS, kHd, CB>), grid, kAttnWaves * 64, 0, st, a);
-    else if (group == 64) hipLaunchKernelGGL((attn_prefill_kernel<BITS, 64, CB>), grid, kAttnWaves * 64, 0, st, a);
-    else hipLaunchKernelGGL((attn_prefill_kernel<BITS, 32, CB>), grid, kAttnWaves * 64, 0, st, a);
+    if (group == kHd) hipLaunchKernelGGL((attn_prefill_kernel<BITS, kHd, CB>), grid, kPrefThreads, 0, st, a);
+    else if (group == 64) hipLaunchKernelGGL((attn_prefill_kernel<BITS, 64, CB>), grid, kPrefThreads, 0, st, a);
+    else hipLaunchKernelGGL((attn_prefill_kernel<BITS, 32, CB>), grid, kPrefThreads, 0, st, a);
   }
 }
 
@@ -1202,7 +1257,7 @@ int granite4_prefill_attn(const uint16_t* q_rot, int rows, int Hq, int Hk, int d
   a.window = window;
   a.d_pt = d_pt;
   a.out = out;
-  constexpr int kPos = kAttnWaves * 4 * kPrefillCb;
+  constexpr int kPos = kPrefWaves * 4 * kPrefillCb;
   const dim3 grid((rows + kPos - 1) / kPos, Hk);
   const hipStream_t st = stream();
   switch (bits) {
