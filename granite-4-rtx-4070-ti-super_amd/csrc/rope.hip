@@ -25,6 +25,7 @@
 #include "granite4_layerops.h"
 #include "rope_unit.h"
 
+#include <atomic>
 #include <cstdlib>
 #include <map>
 #include <mutex>
@@ -34,23 +35,61 @@ namespace g4 {
 
 // Table-size registry for tables this library allocated, so the reference's
 // entry points (which carry no table length) still get a position bound.
+// Lookups run on every launch of those entry points: they scan a fixed array
+// of atomic (table, length) slots without a lock. Registration and removal
+// (once per table) take the mutex; a table registered beyond the slots goes
+// to an overflow map that lookups consult only while it is non-empty.
 namespace {
+constexpr int kTabSlots = 64;
+std::atomic<const float*> g_tab_key[kTabSlots];
+std::atomic<int> g_tab_len[kTabSlots];
+std::atomic<int> g_tab_used{0};      // slots [0, used) may hold tables
+std::atomic<int> g_tab_overflow{0};  // entries in g_tab_more
 std::mutex g_tab_mu;
-std::map<const float*, int> g_tab_len;
+std::map<const float*, int> g_tab_more;
 }  // namespace
 
 int table_bound(const float* t) {
+  const int used = g_tab_used.load(std::memory_order_acquire);
+  for (int i = 0; i < used; ++i)
+    if (g_tab_key[i].load(std::memory_order_acquire) == t)
+      return g_tab_len[i].load(std::memory_order_relaxed);
+  if (g_tab_overflow.load(std::memory_order_acquire) == 0) return INT_MAX;
   std::lock_guard<std::mutex> lk(g_tab_mu);
-  const auto it = g_tab_len.find(t);
-  return it == g_tab_len.end() ? INT_MAX : it->second;
+  const auto it = g_tab_more.find(t);
+  return it == g_tab_more.end() ? INT_MAX : it->second;
 }
 void table_register(const float* t, int max_pos) {
   std::lock_guard<std::mutex> lk(g_tab_mu);
-  g_tab_len[t] = max_pos;
+  int free_slot = -1;
+  const int used = g_tab_used.load(std::memory_order_relaxed);
+  for (int i = 0; i < used; ++i) {
+    const float* k = g_tab_key[i].load(std::memory_order_relaxed);
+    if (k == t) {
+      g_tab_len[i].store(max_pos, std::memory_order_relaxed);
+      return;
+    }
+    if (k == nullptr && free_slot < 0) free_slot = i;
+  }
+  if (free_slot < 0 && used < kTabSlots) free_slot = used;
+  if (free_slot < 0) {
+    g_tab_more[t] = max_pos;
+    g_tab_overflow.store(static_cast<int>(g_tab_more.size()), std::memory_order_release);
+    return;
+  }
+  // The length before the key: a lookup that sees the key sees its length.
+  g_tab_len[free_slot].store(max_pos, std::memory_order_relaxed);
+  g_tab_key[free_slot].store(t, std::memory_order_release);
+  if (free_slot == used) g_tab_used.store(used + 1, std::memory_order_release);
 }
 void table_forget(const float* t) {
   std::lock_guard<std::mutex> lk(g_tab_mu);
-  g_tab_len.erase(t);
+  const int used = g_tab_used.load(std::memory_order_relaxed);
+  for (int i = 0; i < used; ++i)
+    if (g_tab_key[i].load(std::memory_order_relaxed) == t)
+      g_tab_key[i].store(nullptr, std::memory_order_release);
+  if (g_tab_more.erase(t) != 0)
+    g_tab_overflow.store(static_cast<int>(g_tab_more.size()), std::memory_order_release);
 }
 
 namespace {

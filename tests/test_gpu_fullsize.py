@@ -297,6 +297,50 @@ def test_rope_tables_build_allocating_reference_api(tables, max_pos):
     assert L.lib.granite4_rope_tables_build(1e7, 128, 0, ctypes.byref(pc), ctypes.byref(ps)) == -1
 
 
+def test_rope_table_registry_bounds_many_tables():
+    """The length registry behind the reference-signature RoPE launchers,
+    which carry no table length: 70 tables from granite4_rope_tables_build
+    (past the registry's 64 lock-free slots, so the overflow map is used
+    too), max_pos 8 + i. A 80-row granite4_kernel_rope over table i rotates
+    rows < max_pos exactly as the oracle and leaves the rest unwritten; after
+    every table is freed, a freed slot is reused by a new table with its own
+    bound."""
+    note("rope table registry")
+    rows = 80
+    x = ol.uniform_bf16(0x1341, 4.0, rows * 128).reshape(rows, 1, 128)
+    dx = dev(x)
+    built = []
+    try:
+        for i in range(70):
+            pc, ps = ctypes.c_void_p(), ctypes.c_void_p()
+            assert L.lib.granite4_rope_tables_build(1e7, 128, 8 + i, ctypes.byref(pc),
+                                                   ctypes.byref(ps)) == 0
+            built.append((pc.value, ps.value, 8 + i))
+        full_c, full_s = ol.rope_tables(1e7, 128, 80)
+        want_all = ol.rope_rows(x, np.arange(rows), full_c, full_s).reshape(rows, 128)
+        for i in (0, 1, 40, 63, 64, 65, 69):
+            pc, ps, mp = built[i]
+            out = torch.full((rows, 128), 0x7E7E, dtype=torch.int16, device="cuda")
+            L.call("granite4_kernel_rope", dx, pc, ps, rows, 128, out)
+            got = host(out)
+            np.testing.assert_array_equal(got[:mp], want_all[:mp])
+            assert (got[mp:] == 0x7E7E).all(), i
+    finally:
+        for pc, ps, _ in built:
+            assert L.lib.granite4_rope_tables_free(pc, ps) == 0
+    pc, ps = ctypes.c_void_p(), ctypes.c_void_p()
+    assert L.lib.granite4_rope_tables_build(1e7, 128, 20, ctypes.byref(pc), ctypes.byref(ps)) == 0
+    try:
+        out = torch.full((rows, 128), 0x7E7E, dtype=torch.int16, device="cuda")
+        L.call("granite4_kernel_rope", dx, pc.value, ps.value, rows, 128, out)
+        got = host(out)
+        c20, s20 = ol.rope_tables(1e7, 128, 20)
+        np.testing.assert_array_equal(got[:20], ol.rope_rows(x[:20], np.arange(20), c20, s20).reshape(20, 128))
+        assert (got[20:] == 0x7E7E).all()
+    finally:
+        assert L.lib.granite4_rope_tables_free(pc.value, ps.value) == 0
+
+
 @pytest.mark.parametrize("bits", [16, 8, 4, 5])
 def test_multi_kv_append_reference_api(bits):
     """granite4_multi_kv_append (forward_gpu.cu:3915): 8 sessions at random
