@@ -749,10 +749,12 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(AttnArgs 
 // output is bf16(o * (1 / l)) (prefill_gemm.cu:930-940).
 // ---------------------------------------------------------------------------
 constexpr int kKPitch = kHd + 8;  // K tile pitch (bf16): 272 B, 16 rows on distinct banks
-// Waves per prefill workgroup. Staging a tile's K / V into LDS is split over
-// all of them, so more waves sharing a tile cost less staging per score.
-constexpr int kPrefWaves = 8;
-constexpr int kPrefThreads = kPrefWaves * 64;
+// Waves per prefill workgroup (template parameter W): 8, or 4 where 8-wave
+// workgroups would not give every CU one. Staging a tile's K / V into LDS is
+// split over all of them, so more waves sharing a tile cost less staging per
+// score; fewer waves per workgroup give short prompts more workgroups.
+// Measured: T=8192 at 57344 K5V4 8 waves 23.6 ms, 4 waves 48.5 ms; T=512
+// int8 (128 8-wave workgroups) 23.3 us, 4 waves 21.5 us.
 
 struct PrefillArgs {
   const uint16_t* q;  // [rows][Hq][128]
@@ -776,8 +778,9 @@ struct PrefillArgs {
 // unconditional (row 0 for keys without a row, masked when stored).
 // Measured against staging each tile after the previous one's compute:
 // T=512 int8 33.7 -> 29.6 us, T=8192 at 57344 K5V4 38.3 -> 35.1 ms.
-template <int BITS, int GROUP>
+template <int BITS, int GROUP, int W>
 struct PrefillRaw {
+  static constexpr int kPrefThreads = W * 64;
   static constexpr bool kQuant = BITS != 16;
   static constexpr int kNgrp = kQuant ? kHd / GROUP : 1;
   static constexpr int kKElems = BITS == 16 ? 8 : BITS == 8 ? 16 : 32;  // per K chunk
@@ -795,11 +798,12 @@ struct PrefillRaw {
 };
 
 // Page-table entries of tile j0's keys for this thread's K and V chunks.
-template <int BITS, int GROUP>
+template <int BITS, int GROUP, int W>
 __device__ __forceinline__ void prefill_pt(const PrefillArgs& a, int j0, int kv_end,
-                                           int (&ptk)[PrefillRaw<BITS, GROUP>::kKIt],
-                                           int (&ptv)[PrefillRaw<BITS, GROUP>::kVIt]) {
-  using R = PrefillRaw<BITS, GROUP>;
+                                           int (&ptk)[PrefillRaw<BITS, GROUP, W>::kKIt],
+                                           int (&ptv)[PrefillRaw<BITS, GROUP, W>::kVIt]) {
+  using R = PrefillRaw<BITS, GROUP, W>;
+  constexpr int kPrefThreads = R::kPrefThreads;
   const int t = threadIdx.x, tv = (t + R::kVShift) % kPrefThreads;
   const int last = max(kv_end - 1, 0);
 #pragma unroll
@@ -816,14 +820,15 @@ __device__ __forceinline__ void prefill_pt(const PrefillArgs& a, int j0, int kv_
   }
 }
 
-template <int BITS, int GROUP>
+template <int BITS, int GROUP, int W>
 __device__ __forceinline__ void prefill_load(const PrefillArgs& a, const uint8_t* kbase,
                                              const uint8_t* vbase, const float* kscb,
                                              const float* vscb, int j0, int kv_end,
-                                             const int (&ptk)[PrefillRaw<BITS, GROUP>::kKIt],
-                                             const int (&ptv)[PrefillRaw<BITS, GROUP>::kVIt],
-                                             PrefillRaw<BITS, GROUP>& raw) {
-  using R = PrefillRaw<BITS, GROUP>;
+                                             const int (&ptk)[PrefillRaw<BITS, GROUP, W>::kKIt],
+                                             const int (&ptv)[PrefillRaw<BITS, GROUP, W>::kVIt],
+                                             PrefillRaw<BITS, GROUP, W>& raw) {
+  using R = PrefillRaw<BITS, GROUP, W>;
+  constexpr int kPrefThreads = R::kPrefThreads;
   constexpr int kKb = k_row_bytes(BITS);
   const int t = threadIdx.x, tv = (t + R::kVShift) % kPrefThreads;
   auto valid = [&](int key, int r) {
@@ -864,11 +869,12 @@ __device__ __forceinline__ void prefill_load(const PrefillArgs& a, const uint8_t
   }
 }
 
-template <int BITS, int GROUP>
-__device__ __forceinline__ void prefill_store(const PrefillRaw<BITS, GROUP>& raw, uint16_t* ks,
+template <int BITS, int GROUP, int W>
+__device__ __forceinline__ void prefill_store(const PrefillRaw<BITS, GROUP, W>& raw, uint16_t* ks,
                                               uint16_t* vs, float* ksc_l, float* vsc_l,
                                               unsigned* s_valid, float kmul) {
-  using R = PrefillRaw<BITS, GROUP>;
+  using R = PrefillRaw<BITS, GROUP, W>;
+  constexpr int kPrefThreads = R::kPrefThreads;
   const int t = threadIdx.x, tv = (t + R::kVShift) % kPrefThreads;
 #pragma unroll
   for (int it = 0; it < R::kKIt; ++it) {
@@ -934,8 +940,9 @@ __device__ __forceinline__ void prefill_store(const PrefillRaw<BITS, GROUP>& raw
 // CB: column blocks per wave (4 CB positions x 4 heads each); the K and V^T
 // fragments read from LDS serve all CB blocks, and a staged tile serves
 // 16 CB positions.
-template <int BITS, int GROUP, int CB>
-__global__ __launch_bounds__(kPrefThreads) void attn_prefill_kernel(PrefillArgs a) {
+template <int BITS, int GROUP, int CB, int W>
+__global__ __launch_bounds__(W * 64) void attn_prefill_kernel(PrefillArgs a) {
+  constexpr int kPrefWaves = W;
   constexpr bool kQuant = BITS != 16;
   constexpr int kNgrp = kQuant ? kHd / GROUP : 1;
   constexpr int kKb = k_row_bytes(BITS), kVb = v_row_bytes(BITS);
@@ -998,17 +1005,17 @@ __global__ __launch_bounds__(kPrefThreads) void attn_prefill_kernel(PrefillArgs 
   const int wave_pos_min = a.base + wave_row0;
   const int wave_lo_max = a.window > 0 ? max(0, wave_pos_min + 4 * CB - a.window) : 0;
 
-  using Raw = PrefillRaw<BITS, GROUP>;
+  using Raw = PrefillRaw<BITS, GROUP, W>;
   Raw raw;
   int ptk[Raw::kKIt], ptv[Raw::kVIt];
   if (j_first < kv_end) {
-    prefill_pt<BITS, GROUP>(a, j_first, kv_end, ptk, ptv);
-    prefill_load<BITS, GROUP>(a, kbase, vbase, kscb, vscb, j_first, kv_end, ptk, ptv, raw);
-    prefill_pt<BITS, GROUP>(a, j_first + kTile, kv_end, ptk, ptv);
-    prefill_store<BITS, GROUP>(raw, ks2[0], vs2[0], ksc2[0], vsc2[0], valid2[0], a.scale);
+    prefill_pt<BITS, GROUP, W>(a, j_first, kv_end, ptk, ptv);
+    prefill_load<BITS, GROUP, W>(a, kbase, vbase, kscb, vscb, j_first, kv_end, ptk, ptv, raw);
+    prefill_pt<BITS, GROUP, W>(a, j_first + kTile, kv_end, ptk, ptv);
+    prefill_store<BITS, GROUP, W>(raw, ks2[0], vs2[0], ksc2[0], vsc2[0], valid2[0], a.scale);
     if (j_first + kTile < kv_end) {
-      prefill_load<BITS, GROUP>(a, kbase, vbase, kscb, vscb, j_first + kTile, kv_end, ptk, ptv, raw);
-      prefill_pt<BITS, GROUP>(a, j_first + 2 * kTile, kv_end, ptk, ptv);
+      prefill_load<BITS, GROUP, W>(a, kbase, vbase, kscb, vscb, j_first + kTile, kv_end, ptk, ptv, raw);
+      prefill_pt<BITS, GROUP, W>(a, j_first + 2 * kTile, kv_end, ptk, ptv);
     }
   }
   __syncthreads();
@@ -1148,11 +1155,11 @@ __global__ __launch_bounds__(kPrefThreads) void attn_prefill_kernel(PrefillArgs 
       // Stage the next tile (its bytes were loaded a tile ago) into the other
       // buffer, whose last readers passed the previous barrier; then load the
       // bytes of the tile after it and the page-table entries of the third.
-      prefill_store<BITS, GROUP>(raw, ks2[buf ^ 1], vs2[buf ^ 1], ksc2[buf ^ 1], vsc2[buf ^ 1],
+      prefill_store<BITS, GROUP, W>(raw, ks2[buf ^ 1], vs2[buf ^ 1], ksc2[buf ^ 1], vsc2[buf ^ 1],
                                  valid2[buf ^ 1], a.scale);
       if (j0 + 2 * kTile < kv_end) {
-        prefill_load<BITS, GROUP>(a, kbase, vbase, kscb, vscb, j0 + 2 * kTile, kv_end, ptk, ptv, raw);
-        prefill_pt<BITS, GROUP>(a, j0 + 3 * kTile, kv_end, ptk, ptv);
+        prefill_load<BITS, GROUP, W>(a, kbase, vbase, kscb, vscb, j0 + 2 * kTile, kv_end, ptk, ptv, raw);
+        prefill_pt<BITS, GROUP, W>(a, j0 + 3 * kTile, kv_end, ptk, ptv);
       }
     }
     __syncthreads();
@@ -1209,16 +1216,30 @@ void launch_attn_bits(const AttnArgs& a, int group, dim3 grid, hipStream_t st) {
 // cycles per tile), so more registers per wave only cost occupancy.
 constexpr int kPrefillCb = 1;
 
-template <int BITS>
-void launch_prefill_bits(const PrefillArgs& a, int group, dim3 grid, hipStream_t st) {
+template <int BITS, int W>
+void launch_prefill_w(const PrefillArgs& a, int group, dim3 grid, hipStream_t st) {
   constexpr int CB = kPrefillCb;
   if constexpr (BITS == 16) {
     (void)group;
-    hipLaunchKernelGGL((attn_prefill_kernel<16, kHd, CB>), grid, kPrefThreads, 0, st, a);
+    hipLaunchKernelGGL((attn_prefill_kernel<16, kHd, CB, W>), grid, W * 64, 0, st, a);
   } else {
-    if (group == kHd) hipLaunchKernelGGL((attn_prefill_kernel<BITS, kHd, CB>), grid, kPrefThreads, 0, st, a);
-    else if (group == 64) hipLaunchKernelGGL((attn_prefill_kernel<BITS, 64, CB>), grid, kPrefThreads, 0, st, a);
-    else hipLaunchKernelGGL((attn_prefill_kernel<BITS, 32, CB>), grid, kPrefThreads, 0, st, a);
+    if (group == kHd) hipLaunchKernelGGL((attn_prefill_kernel<BITS, kHd, CB, W>), grid, W * 64, 0, st, a);
+    else if (group == 64) hipLaunchKernelGGL((attn_prefill_kernel<BITS, 64, CB, W>), grid, W * 64, 0, st, a);
+    else hipLaunchKernelGGL((attn_prefill_kernel<BITS, 32, CB, W>), grid, W * 64, 0, st, a);
+  }
+}
+
+// 8-wave workgroups (32 positions each) where they give every CU one, else
+// 4-wave workgroups (16 positions) for twice the workgroups.
+template <int BITS>
+void launch_prefill_bits(const PrefillArgs& a, int group, int Hk, hipStream_t st) {
+  const long long wide = static_cast<long long>((a.rows + 8 * 4 * kPrefillCb - 1) / (8 * 4 * kPrefillCb)) * Hk;
+  if (wide >= kCUs) {
+    const dim3 grid((a.rows + 8 * 4 * kPrefillCb - 1) / (8 * 4 * kPrefillCb), Hk);
+    launch_prefill_w<BITS, 8>(a, group, grid, st);
+  } else {
+    const dim3 grid((a.rows + 4 * 4 * kPrefillCb - 1) / (4 * 4 * kPrefillCb), Hk);
+    launch_prefill_w<BITS, 4>(a, group, grid, st);
   }
 }
 
@@ -1257,14 +1278,12 @@ int granite4_prefill_attn(const uint16_t* q_rot, int rows, int Hq, int Hk, int d
   a.window = window;
   a.d_pt = d_pt;
   a.out = out;
-  constexpr int kPos = kPrefWaves * 4 * kPrefillCb;
-  const dim3 grid((rows + kPos - 1) / kPos, Hk);
   const hipStream_t st = stream();
   switch (bits) {
-    case 16: launch_prefill_bits<16>(a, group, grid, st); break;
-    case 8: launch_prefill_bits<8>(a, group, grid, st); break;
-    case 4: launch_prefill_bits<4>(a, group, grid, st); break;
-    default: launch_prefill_bits<5>(a, group, grid, st); break;
+    case 16: launch_prefill_bits<16>(a, group, Hk, st); break;
+    case 8: launch_prefill_bits<8>(a, group, Hk, st); break;
+    case 4: launch_prefill_bits<4>(a, group, Hk, st); break;
+    default: launch_prefill_bits<5>(a, group, Hk, st); break;
   }
   return launch_status("granite4_prefill_attn");
 }

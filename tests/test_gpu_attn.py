@@ -281,6 +281,27 @@ def test_prefill_attn_paged(bits, group, window):
     check(got, want, vmax(cv, vs, bits), f"prefill paged bits {bits} group {group} w {window}")
 
 
+@pytest.mark.parametrize("bits,group,window", [(5, 32, 0), (8, 128, 300)])
+def test_prefill_attn_long_prompt_eight_wave_form(bits, group, window):
+    """1100 rows (8-wave workgroups of 32 positions: enough of them for every
+    CU, where shorter prompts take 4-wave ones), paged, at base 60. Three
+    32-row ranges checked against the oracle run on those rows alone (a row's
+    output depends only on its position and the pool)."""
+    note(f"prefill attn long prompt bits={bits} group={group} window={window}")
+    pages = 80
+    stride = 16 * pages
+    base, rows = 60, 1100
+    ck, cv, ks, vs = make_cache(bits, group, stride, 0xF4 + bits)
+    rng = np.random.default_rng(bits + 99)
+    pt = ol.row_table(rng.permutation(pages).astype(np.int32), stride)
+    q = ol.normal_bf16(0xF5, 0.0, 1.0, rows * HQ * D).reshape(rows, HQ * D)
+    got = run_prefill(q, ck, cv, ks, vs, bits, group, stride, base, d_pt=dev(pt), window=window)
+    for r0 in (0, 530, rows - 32):
+        want = ol.prefill_attn(q[r0:r0 + 32], ck, cv, ks, vs, bits, group, stride, base + r0,
+                               pt=pt, window=window, scale=1.0 / 16, Hk=HK)
+        check(got[r0:r0 + 32], want, vmax(cv, vs, bits), f"prefill rows {r0}.. bits {bits}")
+
+
 def test_prefill_attn_t512_from_zero_and_reference_entry_point():
     """T = 512 from position 0 (BASELINE config 3's prefill shape), int8, and
     the reference-named granite4_prefill_attention on the same inputs."""
