@@ -27,7 +27,10 @@
 // next stage streams in without staging registers while the current one is
 // multiplied. Measured: two stages with two workgroups per CU beat three or
 // four stages with one (M = 8192: 2.38 vs 1.47-1.52 PFLOP/s on the down
-// projection) and the register-staged form (1.79). The grid is persistent (at
+// projection) and the register-staged form (1.79). Where the 128 x 64 tiles
+// give each CU at most one (a short prompt's O and down projections), the
+// workgroup takes six stages instead (T=512 down 64.5 -> 58.5 us), three
+// where two share a CU. The grid is persistent (at
 // most the resident workgroups and the 1024 partial slots); tiles run M
 // fastest, so the workgroups sharing a weight tile run together.
 //
@@ -44,6 +47,7 @@
 
 #include <cmath>
 #include <cstdio>
+#include <type_traits>
 
 namespace g4 {
 namespace {
@@ -181,11 +185,31 @@ __device__ __forceinline__ void wave_lds_wait() { asm volatile("s_waitcnt lgkmcn
 // rounding for every non-NaN value).
 __device__ __forceinline__ uint32_t pack_bf16_rne(float lo, float hi) { return pack_bf16_hw(lo, hi); }
 
-// Waits until at most `later` stages' loads (8 per thread each) are in flight.
-__device__ __forceinline__ void stage_wait(int later) {
-  if (later >= 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-  else if (later == 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+// Waits until at most `later` stages' loads (LPS per thread each) are in
+// flight (vmcnt counts a thread's loads in issue order).
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else if constexpr (N == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+  else if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else if constexpr (N == 12) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+  else if constexpr (N == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  else if constexpr (N == 18) asm volatile("s_waitcnt vmcnt(18)" ::: "memory");
+  else if constexpr (N == 24) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+  else if constexpr (N == 30) asm volatile("s_waitcnt vmcnt(30)" ::: "memory");
+  else if constexpr (N == 32) asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
+  else if constexpr (N == 40) asm volatile("s_waitcnt vmcnt(40)" ::: "memory");
+  else static_assert(N < 0, "add the count");
+}
+template <int LPS>
+__device__ __forceinline__ void stage_wait_n(int later) {
+  if (later >= 5) vm_wait<5 * LPS>();
+  else if (later == 4) vm_wait<4 * LPS>();
+  else if (later == 3) vm_wait<3 * LPS>();
+  else if (later == 2) vm_wait<2 * LPS>();
+  else if (later == 1) vm_wait<LPS>();
+  else vm_wait<0>();
 }
 
 // Epilogue of one output tile through LDS: each wave writes its f32 values
@@ -288,12 +312,15 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, const v4f (&acc
 // TN: weight rows per tile, 128, or 64 where 128 x 128 tiles cannot fill the
 // CUs (a short prompt's O and down projections: 128 tiles at M = 512); each
 // wave then owns 64 x 32 outputs (4 x 2 MFMA tiles).
-template <int EPI, int TN = kGBN>
+// ST: pipeline stages (kGStages, or more where one workgroup per CU leaves
+// it the LDS).
+template <int EPI, int TN = kGBN, int ST = kGStages>
 __global__ __launch_bounds__(256) void gemm_fp8_kernel(GemmArgs a) {
   static_assert(TN == kGBN || (TN == 64 && EPI != kEpiSwiglu), "tile width");
   constexpr int kNI = TN / 32;  // MFMA tiles per wave along N
   constexpr int kStage = (kGBM + TN) * kGBK;
-  __shared__ __align__(16) uint8_t s_tile[kGStages * kStage];
+  __shared__ __align__(16) uint8_t s_tile[ST * kStage];
+  constexpr int kLps = 4 + TN / 32;  // loads per thread per stage
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -302,13 +329,13 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(GemmArgs a) {
   const int fr = lane & 15;          // fragment row
   const float a_scale = *a.a_scale;
   float amax = 0.0f;
-  static_assert(kGStages >= 2 && kGStages <= 4, "pipeline depth");
+  static_assert(ST >= 2 && ST <= 6, "pipeline depth");
   // Epilogue geometry: the wave's output block is 64 rows x kWCols columns.
   constexpr int kWCols = EPI == kEpiSwiglu ? 32 : TN / 2;
   constexpr int kLanesPerRow = kWCols / 8;
   constexpr int kRowsPerIter = 64 / kLanesPerRow;
   constexpr int kIters = 32 / kRowsPerIter;
-  static_assert(4 * 32 * kEP * 4 <= kGStages * kStage, "epilogue staging fits the stage buffers");
+  static_assert(4 * 32 * kEP * 4 <= ST * kStage, "epilogue staging fits the stage buffers");
 
   for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
     const int tm = tile % a.mt, tn = tile / a.mt;
@@ -337,20 +364,20 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(GemmArgs a) {
 
     __syncthreads();  // the previous tile's readers are done with every buffer
 #pragma unroll
-    for (int sidx = 0; sidx < kGStages - 1; ++sidx)
+    for (int sidx = 0; sidx < ST - 1; ++sidx)
       if (sidx < ktiles) stage_issue<EPI, TN>(a, m0, tn, sidx * kGBK, s_tile + sidx * kStage);
     for (int kt = 0; kt < ktiles; ++kt) {
       // Stages issued after kt so far: min(kStages - 2, ktiles - 1 - kt).
-      const int later = min(kGStages - 2, ktiles - 1 - kt);
-      stage_wait(later);
+      const int later = min(ST - 2, ktiles - 1 - kt);
+      stage_wait_n<kLps>(later);
       // Stage kt landed for every wave (each waited for its own loads);
       // stage kt - 1's reads are done (waited before its MFMAs). No fence:
       // a workgroup-scope release would wait for the stages still in flight.
       __builtin_amdgcn_s_barrier();
-      if (kt + kGStages - 1 < ktiles)
-        stage_issue<EPI, TN>(a, m0, tn, (kt + kGStages - 1) * kGBK,
-                             s_tile + ((kt + kGStages - 1) % kGStages) * kStage);
-      const uint32_t st = lds_addr(s_tile + (kt % kGStages) * kStage);
+      if (kt + ST - 1 < ktiles)
+        stage_issue<EPI, TN>(a, m0, tn, (kt + ST - 1) * kGBK,
+                             s_tile + ((kt + ST - 1) % ST) * kStage);
+      const uint32_t st = lds_addr(s_tile + (kt % ST) * kStage);
       v4u ax[4], ay[4], bx[kNI], by[kNI];
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi) frag_issue(st, wm * 64 + mi * 16 + fr, lane, ax[mi], ay[mi]);
@@ -543,9 +570,9 @@ bool gemm_args_ok(const uint8_t* A, int lda, const uint8_t* W, int M, int N, int
          static_cast<long long>(M) * lda < (1LL << 40);
 }
 
-template <int EPI, int TN = kGBN>
+template <int EPI, int TN = kGBN, int ST = kGStages>
 unsigned gemm_grid(long long tiles, int cap) {
-  const int resident = resident_blocks(reinterpret_cast<const void*>(gemm_fp8_kernel<EPI, TN>), 256);
+  const int resident = resident_blocks(reinterpret_cast<const void*>(gemm_fp8_kernel<EPI, TN, ST>), 256);
   long long g = tiles;
   if (resident > 0 && g > resident) g = resident;
   if (g > cap) g = cap;
@@ -589,19 +616,21 @@ int granite4_gemm_fp8(int out, const uint8_t* A, int lda, const float* d_a_scale
   const long long tiles = static_cast<long long>(a.mt) * a.nt;
   const hipStream_t st = stream();
   const auto go = [&](auto kern, unsigned grid) { hipLaunchKernelGGL(kern, grid, 256, 0, st, a); };
+  // 128 x 64 tiles: six stages where every tile has a CU of its own (one
+  // workgroup per CU, 144 KB of LDS), three where two share one (72 KB
+  // each), two otherwise.
+  const int deep = !narrow ? 2 : (tiles <= kCUs ? 6 : (tiles <= 2 * kCUs ? 3 : 2));
+  const auto run = [&](auto e_tag) {
+    constexpr int E = decltype(e_tag)::value;
+    if (!narrow) go(gemm_fp8_kernel<E>, gemm_grid<E>(tiles, INT_MAX));
+    else if (deep == 6) go(gemm_fp8_kernel<E, 64, 6>, gemm_grid<E, 64, 6>(tiles, INT_MAX));
+    else if (deep == 3) go(gemm_fp8_kernel<E, 64, 3>, gemm_grid<E, 64, 3>(tiles, INT_MAX));
+    else go(gemm_fp8_kernel<E, 64>, gemm_grid<E, 64>(tiles, INT_MAX));
+  };
   switch (out) {
-    case GRANITE4_GEMM_BF16:
-      if (narrow) go(gemm_fp8_kernel<kEpiBf16, 64>, gemm_grid<kEpiBf16, 64>(tiles, INT_MAX));
-      else go(gemm_fp8_kernel<kEpiBf16>, gemm_grid<kEpiBf16>(tiles, INT_MAX));
-      break;
-    case GRANITE4_GEMM_F32:
-      if (narrow) go(gemm_fp8_kernel<kEpiF32, 64>, gemm_grid<kEpiF32, 64>(tiles, INT_MAX));
-      else go(gemm_fp8_kernel<kEpiF32>, gemm_grid<kEpiF32>(tiles, INT_MAX));
-      break;
-    default:
-      if (narrow) go(gemm_fp8_kernel<kEpiResidual, 64>, gemm_grid<kEpiResidual, 64>(tiles, INT_MAX));
-      else go(gemm_fp8_kernel<kEpiResidual>, gemm_grid<kEpiResidual>(tiles, INT_MAX));
-      break;
+    case GRANITE4_GEMM_BF16: run(std::integral_constant<int, kEpiBf16>{}); break;
+    case GRANITE4_GEMM_F32: run(std::integral_constant<int, kEpiF32>{}); break;
+    default: run(std::integral_constant<int, kEpiResidual>{}); break;
   }
   return launch_status("granite4_gemm_fp8");
 }
