@@ -39,7 +39,10 @@
 #include "granite4_layerops.h"
 #include "rope_unit.h"
 
+#include <atomic>
 #include <climits>
+#include <cstdlib>
+#include <random>
 #include <type_traits>
 #include <cmath>
 
@@ -53,6 +56,7 @@ constexpr int kRowsPerWave = 4;  // query rows per wave (x 4 heads = 16 MFMA row
 constexpr int kAttnMaxSplits = 256;
 enum : int { kAttnPlain = 0, kAttnRopeAppend = 1, kAttnAppend = 2 };
 constexpr int kAttnWaves = 4;  // splits per workgroup, merged before the combine
+constexpr int kAttnSpinLimit = 1 << 20;  // polls before the combining block gives up
 constexpr int kVPitch = kHd + 16;  // LDS V row pitch (bf16): 288 B, rows 8 banks apart
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -77,6 +81,11 @@ struct AttnArgs {
   float2* part_ml;  // [rows][Hq][nblk]
   float* part_o;    // [rows][Hq][nblk][128]
   uint16_t* out;    // [rows][Hq][128]
+  // Combine inside the split launch: the arrival tag of each split block,
+  // [row groups][Hk][nblk], and this call's tag (never 0). tags == nullptr:
+  // a second launch (attn_combine_kernel) combines.
+  unsigned* tags;
+  unsigned tag;
   // Decode append (one row at *d_pos): q, k, v are the raw bf16 projections
   // (ra.q / ra.k / ra.v); q is rotated in registers, and the wave whose split
   // holds the position rotates and quantises that position's K / V row (the
@@ -236,6 +245,92 @@ __device__ __forceinline__ void v_store(const u32x4_t (&raw)[VStage<BITS>::kStep
 // (each wave owns its LDS tile, so no workgroup barrier is needed).
 __device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// Partials and arrival tags are written and read at device scope (sc1 on
+// gfx950): the workgroup that combines may run on another XCD, whose L2
+// holds none of the writer's lines, and a tag must not be seen before the
+// partial it announces.
+__device__ __forceinline__ void st_dev_u64(void* p, unsigned long long v) {
+  __hip_atomic_store(static_cast<unsigned long long*>(p), v, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long ld_dev_u64(const void* p) {
+  return __hip_atomic_load(static_cast<unsigned long long*>(const_cast<void*>(p)), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long f2_bits(float x, float y) {
+  return static_cast<unsigned long long>(__float_as_uint(x)) |
+         (static_cast<unsigned long long>(__float_as_uint(y)) << 32);
+}
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// The split blocks [s0, used) whose partials make up row `row`: the blocks up
+// to the row's causal length (clamped to the arena), from the block holding
+// the window's first key.
+__device__ __forceinline__ void combine_range(const AttnArgs& a, int row, int& s0, int& used) {
+  const int len = a.row_pos != nullptr ? a.row_pos[row] + 1
+                                       : (a.d_pos != nullptr ? *a.d_pos : a.kv_base) + row + 1;
+  const int span = kAttnWaves * a.tps * kTile;  // positions per split block
+  used = min((min(max(len, 0), a.stride) + span - 1) / span, a.nblk);
+  s0 = a.window > 0 ? max(0, len - a.window) / span : 0;
+}
+
+// One wave combines the split-block partials of one (row, head)
+// (attn_combine_kernel, attention_split.cu:1049-1074): M = max m_b,
+// w_b = exp(m_b - M) (0 for a block without keys of the row), L = sum l_b w_b
+// and out = bf16(sum o_b w_b / L), both sums in block order. Lane j holds
+// block s0 + j's (m, l) (at most 64 blocks: kAttnMaxSplits / kAttnWaves);
+// each lane owns dims 2 lane and 2 lane + 1, whose partials are loaded 16
+// blocks at a time.
+__device__ void combine_wave(const AttnArgs& a, int row, int h) {
+  static_assert(kAttnMaxSplits / kAttnWaves <= 64, "one (m, l) per lane");
+  const int lane = threadIdx.x & 63;
+  constexpr int kChunk = 16;
+  const size_t rbase = (static_cast<size_t>(row) * a.Hq + h) * a.nblk;
+  const float* prow = a.part_o + rbase * kHd + 2 * lane;
+  // The first chunk and the (m, l) loads go out with the row's length, not
+  // after it, from block 0; a window that starts the row's blocks later
+  // loads them again from its first block.
+  unsigned long long ov[kChunk];
+#pragma unroll
+  for (int j = 0; j < kChunk; ++j) ov[j] = ld_dev_u64(prow + static_cast<size_t>(min(j, a.nblk - 1)) * kHd);
+  unsigned long long mlb = ld_dev_u64(a.part_ml + rbase + min(lane, a.nblk - 1));
+  int s0, used;
+  combine_range(a, row, s0, used);
+  if (s0 > 0) {
+    const int sc = min(s0, a.nblk - 1), lc = max(min(used, a.nblk) - 1, sc);
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) ov[j] = ld_dev_u64(prow + static_cast<size_t>(min(sc + j, lc)) * kHd);
+    mlb = ld_dev_u64(a.part_ml + rbase + min(sc + lane, lc));
+  }
+  const int nb = used - s0;  // blocks s0 + j, j < nb (the loads above start at block s0)
+  const float mj = lane < nb ? __uint_as_float(static_cast<unsigned>(mlb)) : -INFINITY;
+  const float lj = lane < nb ? __uint_as_float(static_cast<unsigned>(mlb >> 32)) : 0.0f;
+  float M = mj;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+  const float wj = mj == -INFINITY ? 0.0f : expf(mj - M);
+  float L = 0.0f, acc0 = 0.0f, acc1 = 0.0f;
+  for (int c = 0; c < nb; c += kChunk) {
+    if (c > 0) {
+#pragma unroll
+      for (int j = 0; j < kChunk; ++j)
+        ov[j] = ld_dev_u64(prow + static_cast<size_t>(s0 + min(c + j, nb - 1)) * kHd);
+    }
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) {
+      if (c + j < nb) {
+        const float wb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wj), c + j));
+        const float lb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lj), c + j));
+        L += lb * wb;
+        acc0 += __uint_as_float(static_cast<unsigned>(ov[j])) * wb;
+        acc1 += __uint_as_float(static_cast<unsigned>(ov[j] >> 32)) * wb;
+      }
+    }
+  }
+  *reinterpret_cast<uint32_t*>(a.out + (static_cast<size_t>(row) * a.Hq + h) * kHd + 2 * lane) =
+      f32_to_bf16(acc0 / L) | (f32_to_bf16(acc1 / L) << 16);
+}
+
 // MODE: kAttnPlain; kAttnRopeAppend (granite4_attn_decode_append: raw q, k
 // rotated here, the new K / V row appended); kAttnAppend
 // (granite4_attn_decode_append_rotated: q and k already rotated, the new row
@@ -291,8 +386,15 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
     lo_min = min(lo_min, row_lo(rr));
   }
   const int span = a.tps * kTile;
-  const int blk_begin = blockIdx.y * kAttnWaves * span;
-  if (blk_begin >= kv_max || blk_begin + kAttnWaves * span <= lo_min) return;  // whole block idle
+  const int bspan = kAttnWaves * span;
+  const int blk_begin = blockIdx.y * bspan;
+  // The group's blocks with work, [b_lo, b_hi): the others return at once.
+  // With the combine fused, block 0 of a group with none still combines
+  // (every row then gets the combine's output for no keys).
+  const int b_lo = lo_min / bspan;
+  const int b_hi = min((kv_max + bspan - 1) / bspan, a.nblk);
+  const bool in_range = static_cast<int>(blockIdx.y) >= b_lo && static_cast<int>(blockIdx.y) < b_hi;
+  if (!in_range && !(a.tags != nullptr && b_lo >= b_hi && blockIdx.y == 0)) return;
   const int t_begin = split * span;
   const int t_end_max = min(kv_max, t_begin + span);
   const bool active = split < a.splits && t_begin < kv_max && t_end_max > lo_min;
@@ -648,91 +750,85 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
           (is_k ? a.ra.k_scale : a.ra.v_scale)[slot * kNgrp + gi] = mir_s[wave][is_k ? 0 : 1][gi];
       }
     }
-    if (crr >= nr) return;
     // A block with no key of the row (its positions all unmapped) publishes
     // (-inf, 0, 0), which the combine weighs with 0, instead of leaving the
     // previous call's partial in its slot.
-    float M = -INFINITY;
+    if (crr < nr) {
+      float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, mml[(w * 16 + col) * 2]);
-    float L = 0.0f, acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+      for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, mml[(w * 16 + col) * 2]);
+      float L = 0.0f, acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) {
-      const float mw = mml[(w * 16 + col) * 2];
-      const float wt = mw == -INFINITY ? 0.0f : expf(mw - M);
-      L += mml[(w * 16 + col) * 2 + 1] * wt;
-      const float* ow = mo + (w * 16 + col) * kHd + 8 * dc;
+      for (int w = 0; w < kAttnWaves; ++w) {
+        const float mw = mml[(w * 16 + col) * 2];
+        const float wt = mw == -INFINITY ? 0.0f : expf(mw - M);
+        L += mml[(w * 16 + col) * 2 + 1] * wt;
+        const float* ow = mo + (w * 16 + col) * kHd + 8 * dc;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += ow[e] * wt;
+        for (int e = 0; e < 8; ++e) acc[e] += ow[e] * wt;
+      }
+      const size_t slot = (static_cast<size_t>(r0 + crr) * a.Hq + chq) * a.nblk + blockIdx.y;
+      if (dc == 0) st_dev_u64(a.part_ml + slot, f2_bits(M, L));
+      float* po = a.part_o + slot * kHd + 8 * dc;
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) st_dev_u64(po + e, f2_bits(acc[e], acc[e + 1]));
     }
-    const size_t slot = (static_cast<size_t>(r0 + crr) * a.Hq + chq) * a.nblk + blockIdx.y;
-    if (dc == 0) a.part_ml[slot] = make_float2(M, L);
-    float* po = a.part_o + slot * kHd + 8 * dc;
-    *reinterpret_cast<f32x4_t*>(po) = f32x4_t{acc[0], acc[1], acc[2], acc[3]};
-    *reinterpret_cast<f32x4_t*>(po + 4) = f32x4_t{acc[4], acc[5], acc[6], acc[7]};
   }
-}
+  if (a.tags == nullptr) return;
 
-// One workgroup per (head, row) rescales and sums the row's split-block
-// partials: every (m, l) and partial output is loaded at once (a lane per
-// block for (m, l); each half of the workgroup holds every other block's o
-// for all 128 dims), then M = max m, w = exp(m - M), L = sum l w and
-// out = bf16(sum o w / L).
-constexpr int kCombineThreads = 256;
-
-__device__ __forceinline__ float block_reduce(float v, bool is_max, float* red) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float u = __shfl_xor(v, o);
-    v = is_max ? fmaxf(v, u) : v + u;
+  // Combine fused: the group's last block with work (b_hi - 1; block 0 of a
+  // group with none) combines. The others publish their tag once their
+  // partials are stored and exit; the combining block polls the group's tags
+  // (one per lane, bounded), clears them (so a graph replay, which reuses
+  // the tag, starts from zeros) and combines. Its wait cannot starve the
+  // blocks it waits for: they have lower workgroup ids, and each XCD
+  // dispatches its workgroups in id order, so the lowest unfinished
+  // workgroup of the launch can always be dispatched and depends only on
+  // finished ones. A wait that gives up after the spin limit (which that
+  // excludes) writes NaN outputs rather than hang.
+  const bool combiner = b_lo < b_hi ? static_cast<int>(blockIdx.y) == b_hi - 1 : blockIdx.y == 0;
+  unsigned* gt = a.tags + (static_cast<size_t>(blockIdx.z) * gridDim.x + hkv) * a.nblk;
+  wait_stores();
+  __syncthreads();
+  if (!combiner) {
+    if (threadIdx.x == 0)
+      __hip_atomic_store(gt + blockIdx.y, a.tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  __shared__ int s_ok;
+  if (wave == 0) {
+    const int b = b_lo + lane;
+    const bool mine = b < b_hi - 1;  // every block with work but this one
+    bool seen = !mine;
+    int spin = 0;
+    for (;;) {
+      if (!seen) seen = __hip_atomic_load(gt + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.tag;
+      if (__all(seen) || ++spin >= kAttnSpinLimit) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (mine) __hip_atomic_store(gt + b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool ok = __all(seen);
+    if (lane == 0) s_ok = ok;
   }
   __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  float r = red[0];
-#pragma unroll
-  for (int i = 1; i < kCombineThreads / 64; ++i) r = is_max ? fmaxf(r, red[i]) : r + red[i];
-  return r;
+  if (!s_ok) {
+    for (int rr = 0; rr < nr; ++rr)
+      *reinterpret_cast<uint32_t*>(a.out + (static_cast<size_t>(r0 + rr) * a.Hq + hkv * kGq + wave) * kHd +
+                                   2 * lane) = 0x7fc07fc0u;
+    return;
+  }
+  for (int rr = 0; rr < nr; ++rr) combine_wave(a, r0 + rr, hkv * kGq + wave);
 }
+
+// The combine as its own launch (the split launch without tags): one
+// workgroup per (row, 4 heads), one wave per head.
+constexpr int kCombineThreads = kGq * 64;
 
 __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(AttnArgs a) {
-  constexpr int kPer = kAttnMaxSplits / kAttnWaves / 2;  // blocks summed per lane (max)
-  __shared__ float s_w[kAttnMaxSplits / kAttnWaves];
-  __shared__ float s_red[kCombineThreads / 64];
-  __shared__ float s_half[kHd];
   // The arguments fetched in one scalar round trip.
   asm volatile("" ::"s"(a.d_pos), "s"(a.row_pos), "s"(a.part_ml), "s"(a.part_o), "s"(a.out),
                "s"(a.nblk), "s"(a.tps), "s"(a.stride), "s"(a.window), "s"(a.kv_base), "s"(a.Hq));
-  const int h = blockIdx.x, row = blockIdx.y;
-  const int len = a.row_pos != nullptr ? a.row_pos[row] + 1
-                                       : (a.d_pos != nullptr ? *a.d_pos : a.kv_base) + row + 1;
-  const int span = kAttnWaves * a.tps * kTile;  // positions per split block
-  const int used = min((min(max(len, 0), a.stride) + span - 1) / span, a.nblk);
-  const int s0 = a.window > 0 ? max(0, len - a.window) / span : 0;
-  const size_t base = (static_cast<size_t>(row) * a.Hq + h) * a.nblk;
-  const int t = threadIdx.x;
-  const int d = t & (kHd - 1), half = t >> 7;
-  // One round of loads: this lane's (m, l) and its half's partial outputs.
-  const float2 ml = s0 + t < used ? a.part_ml[base + s0 + t] : make_float2(-INFINITY, 0.0f);
-  float ov[kPer];
-#pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int sb = s0 + half + 2 * j;
-    ov[j] = sb < used ? a.part_o[(base + sb) * kHd + d] : 0.0f;
-  }
-  const float M = block_reduce(ml.x, true, s_red);
-  const float w = s0 + t < used ? expf(ml.x - M) : 0.0f;
-  if (s0 + t < used) s_w[t] = w;
-  const float L = block_reduce(ml.y * w, false, s_red);  // its barriers also publish s_w
-  float acc = 0.0f;
-#pragma unroll
-  for (int j = 0; j < kPer; ++j)
-    if (s0 + half + 2 * j < used) acc += ov[j] * s_w[half + 2 * j];
-  if (half == 1) s_half[d] = acc;
-  __syncthreads();
-  if (half == 0)
-    a.out[(static_cast<size_t>(row) * a.Hq + h) * kHd + d] =
-        static_cast<uint16_t>(f32_to_bf16((acc + s_half[d]) / L));
+  combine_wave(a, blockIdx.y, blockIdx.x * kGq + (threadIdx.x >> 6));
 }
 
 // ---------------------------------------------------------------------------
@@ -1198,6 +1294,37 @@ int attn_splits(int max_len) {
   return (tiles + tps - 1) / tps;
 }
 
+// Combine mode (granite4_set_attn_combine_mode): 0 inside the split launch,
+// 1 as a second launch (the initial mode with G4_ATTN_COMBINE_LAUNCH=1).
+std::atomic<int> g_attn_combine{[] {
+  const char* e = std::getenv("G4_ATTN_COMBINE_LAUNCH");
+  return e != nullptr && e[0] == '1' ? 1 : 0;
+}()};
+
+// Arrival tags: a process-wide counter from a random start, never 0. The
+// slots need only differ from the call's tag before the call: the combining
+// block re-zeroes every slot of its group.
+std::atomic<unsigned> g_attn_tag{static_cast<unsigned>(std::random_device{}())};
+unsigned next_attn_tag() {
+  unsigned t;
+  do t = g_attn_tag.fetch_add(1, std::memory_order_relaxed) + 1u;
+  while (t == 0u);
+  return t;
+}
+
+// Points a at its tag slots (after the partials) and draws the call's tag,
+// or leaves tags null for the two-launch form. Returns whether the combine
+// is fused.
+bool set_combine(AttnArgs& a, int rows) {
+  if (g_attn_combine.load(std::memory_order_relaxed) != 0) {
+    a.tags = nullptr;
+    return false;
+  }
+  a.tags = reinterpret_cast<unsigned*>(a.part_o + static_cast<size_t>(rows) * a.Hq * a.nblk * kHd);
+  a.tag = next_attn_tag();
+  return true;
+}
+
 template <int BITS, int FUSE>
 void launch_attn_bits(const AttnArgs& a, int group, dim3 grid, hipStream_t st) {
   if constexpr (BITS == 16) {
@@ -1312,7 +1439,14 @@ size_t granite4_attn_split_scratch_bytes(int Hq, int rows, int stride) {
   if (Hq <= 0 || rows <= 0 || stride <= 0) return 0;
   const size_t nblk = (attn_splits(stride) + kAttnWaves - 1) / kAttnWaves;
   const size_t slots = static_cast<size_t>(rows) * Hq * nblk;
-  return slots * (sizeof(float2) + kHd * sizeof(float));
+  // Partial (m, l) and output per slot, then the arrival tags (one per
+  // (row group, KV head, block): at most one per slot).
+  return slots * (sizeof(float2) + kHd * sizeof(float) + sizeof(unsigned));
+}
+
+int granite4_set_attn_combine_mode(int mode) {
+  if (mode != 0 && mode != 1) return -1;
+  return g_attn_combine.exchange(mode);
 }
 
 int granite4_attn_paged(const uint16_t* q, int rows, int Hq, int Hk, int d, float scale,
@@ -1359,6 +1493,7 @@ int granite4_attn_paged(const uint16_t* q, int rows, int Hq, int Hk, int d, floa
   // Multi-sequence rows (row_pos) take one wave each; rows of one sequence
   // share a wave in groups of four (their keys are read once per group).
   const int nz = row_pos != nullptr ? rows : (rows + kRowsPerWave - 1) / kRowsPerWave;
+  const bool fused = set_combine(a, rows);
   const dim3 grid(Hk, a.nblk, nz);
   const hipStream_t st = stream();
   switch (bits) {
@@ -1368,7 +1503,8 @@ int granite4_attn_paged(const uint16_t* q, int rows, int Hq, int Hk, int d, floa
     default: launch_attn_bits<5, kAttnPlain>(a, group, grid, st); break;
   }
   if (launch_status("granite4_attn_paged (split)") != 0) return -1;
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(Hq, rows), kCombineThreads, 0, st, a);
+  if (fused) return 0;
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(Hq / kGq, rows), kCombineThreads, 0, st, a);
   return launch_status("granite4_attn_paged (combine)");
 }
 
@@ -1412,6 +1548,7 @@ int attn_decode_append(const uint16_t* q, const uint16_t* k, const uint16_t* v,
   a.part_o = reinterpret_cast<float*>(a.part_ml + static_cast<size_t>(Hq) * a.nblk);
   a.out = out;
   a.ra = ra;
+  const bool fused = set_combine(a, 1);
   const dim3 grid(Hk, a.nblk, 1);
   const hipStream_t st = stream();
   switch (bits) {
@@ -1421,7 +1558,8 @@ int attn_decode_append(const uint16_t* q, const uint16_t* k, const uint16_t* v,
     default: launch_attn_bits<5, M>(a, grp, grid, st); break;
   }
   if (launch_status(what) != 0) return -1;
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(Hq, 1), kCombineThreads, 0, st, a);
+  if (fused) return 0;
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(Hq / kGq, 1), kCombineThreads, 0, st, a);
   return launch_status(what);
 }
 

@@ -116,6 +116,7 @@ _SIG = {
     "granite4_fp8_sync_status": [P, I],
     "granite4_debug_set_sync_spin_limit": [I],
     "granite4_attn_split_scratch_bytes": [I, I, I],
+    "granite4_set_attn_combine_mode": [I],
     "granite4_attn_split": [P, P, P, F, I, I, I, I, P, I, I, P, P, P, P, P, P, I, P, P, I, P, I,
                             P, P, P, I, P, P, I, I, I],
     "granite4_attn_paged": [P, I, I, I, I, F, P, P, P, P, I, I, I, I, P, P, P, P, I, I, P, P],
@@ -241,6 +242,16 @@ def set_fp8_launch_mode(mode):
     prev = _lib.granite4_set_fp8_launch_mode(mode)
     if prev < 0:
         raise ValueError(f"FP8 launch mode {mode}")
+    return prev
+
+
+def set_attn_combine_mode(mode):
+    """granite4_set_attn_combine_mode: 0 = the split blocks' partials combined
+    inside the split launch, 1 = by a second launch. Returns the previous
+    mode."""
+    prev = _lib.granite4_set_attn_combine_mode(mode)
+    if prev < 0:
+        raise ValueError(f"attention combine mode {mode}")
     return prev
 
 

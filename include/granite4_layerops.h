@@ -379,6 +379,16 @@ int granite4_selftest_fp8(float scale, unsigned long long* d_result);
  * stride, or max_len when a call passes one). */
 size_t granite4_attn_split_scratch_bytes(int Hq, int rows, int stride);
 
+/* Where the split blocks' partials are combined (no counterpart in the
+ * reference, which always launches attn_combine_kernel): 0 (the default)
+ * inside the split launch, by the last block of each (row group, KV head) to
+ * finish; 1 as a second launch. Both give identical outputs. The fused form
+ * keeps arrival tags in the scratch that the combining block re-zeroes, so
+ * a scratch buffer must not be shared by calls in flight at once (as for
+ * the partials in either form). Process-wide; returns the previous mode, or
+ * -1 for another value. */
+int granite4_set_attn_combine_mode(int mode);
+
 /* The reference's attn_split (attention_gpu.h:53-60, bools as int). Causal
  * GQA for rows (1..16) query rows q [rows][Hq * d]: row r sits at position
  * p + r (p = *d_pos when d_pos is non-NULL, else kv_base; or row_pos[r] for

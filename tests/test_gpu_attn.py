@@ -404,3 +404,110 @@ def test_attn_decode_append_long_context_repeated(bits, group):
         assert np.isfinite(got).all()
         for a_, b_ in zip(*res):
             np.testing.assert_array_equal(a_, b_)
+
+
+# ------------------------------------------------- combine inside the split launch
+COMBINE_CASES = [
+    dict(name="rows1_int8", bits=8, stride=2000, rows=1, kv_base=1999),
+    dict(name="rows4_k5", bits=5, stride=2000, rows=4, kv_base=1300),
+    dict(name="rows9_bf16", bits=16, stride=3000, rows=9, kv_base=2900),
+    dict(name="window100", bits=16, stride=5000, rows=2, kv_base=4000, window=100),
+    dict(name="window700_int4", bits=4, stride=5000, rows=3, kv_base=4000, window=700),
+    dict(name="long64blocks", bits=8, stride=16384, rows=1, kv_base=16383),
+    dict(name="multi_seq_with_empty", bits=8, stride=1024, rows=5, multi=[-1, 700, 63, 64, 1000]),
+]
+
+
+@pytest.mark.parametrize("case", COMBINE_CASES, ids=[c["name"] for c in COMBINE_CASES])
+def test_attn_combine_in_split_launch_matches_second_launch(case):
+    """The split blocks' partials combined by the last block of each (row
+    group, KV head) inside the split launch (the default) give the same
+    output bits as the combine's own launch (mode 1), including windows
+    (blocks from the window's first), 64 split blocks (four 16-block chunks)
+    and a multi-sequence row with no keys (position -1: its group has no
+    block with work, and block 0 combines nothing in both forms). Each form
+    runs twice on one scratch, the second call finding the first's tags and
+    partials there."""
+    note(f"attn combine forms {case['name']}")
+    bits, stride, rows = case["bits"], case["stride"], case["rows"]
+    ck, cv, ks, vs = make_cache(bits, D, stride, 0xC0 + bits)
+    q = ol.normal_bf16(0xC1 + rows, 0.0, 1.0, rows * HQ * D).reshape(rows, HQ * D)
+    kw = dict(window=case.get("window", 0))
+    if "multi" in case:
+        pages = stride // 16
+        rng = np.random.default_rng(11)
+        kw["row_pos"] = case["multi"]
+        kw["row_pts"] = [ol.row_table(rng.permutation(pages).astype(np.int32), stride)
+                         for _ in case["multi"]]
+    else:
+        kw["kv_base"] = case["kv_base"]
+    outs = {}
+    prev = L.set_attn_combine_mode(0)
+    try:
+        for mode in (1, 0, 1, 0):
+            L.set_attn_combine_mode(mode)
+            outs.setdefault(mode, []).append(run_paged(q, ck, cv, ks, vs, bits, D, stride, **kw))
+    finally:
+        L.set_attn_combine_mode(prev)
+    for o in outs[1][1:] + outs[0]:
+        np.testing.assert_array_equal(o, outs[1][0])
+    if "multi" not in case:  # and both against the oracle
+        pos = [case["kv_base"] + r for r in range(rows)]
+        want = ol.attn_split(q, ck, cv, ks, vs, bits, D, stride, pos, window=kw["window"],
+                             scale=1.0 / 16, Hk=HK)
+        check(outs[0][0], want, vmax(cv, vs, bits), case["name"])
+
+
+def test_attn_combine_in_split_launch_graph_replays():
+    """A captured granite4_attn_paged (device position, paged, int8) replays
+    with one tag baked in: every replay must find the tag slots re-zeroed by
+    the previous call's combining block. Four replays at positions covering
+    2, 20, 32 and 1 split blocks, each followed by an eager call on the same
+    scratch (a fresh tag) and checked against the second-launch form."""
+    note("attn combine graph replays")
+    bits, pages = 8, 512
+    stride = 16 * pages
+    ck, cv, ks, vs = make_cache(bits, D, stride, 0xC7)
+    rng = np.random.default_rng(12)
+    pt = dev(ol.row_table(rng.permutation(pages).astype(np.int32), stride))
+    dk, dv, dks, dvs = dev(ck), dev(cv), dev(ks), dev(vs)
+    q = dev(ol.normal_bf16(0xC8, 0.0, 1.0, HQ * D))
+    pos = torch.zeros(1, dtype=torch.int32, device="cuda")
+    scratch = torch.empty(L.call_size("granite4_attn_split_scratch_bytes", HQ, 1, stride),
+                          dtype=torch.uint8, device="cuda")
+    out = torch.empty(HQ * D, dtype=torch.int16, device="cuda")
+    out_e = torch.empty(HQ * D, dtype=torch.int16, device="cuda")
+
+    def call(o):
+        L.call("granite4_attn_paged", q, 1, HQ, HK, D, 1.0 / 16, dk, dv, dks, dvs, bits, D, stride,
+               0, pos, pt, None, None, 0, 0, scratch, o)
+
+    prev = L.set_attn_combine_mode(0)
+    try:
+        pos.fill_(300)
+        call(out)  # warm-up outside the capture
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        L.use_stream(s)
+        try:
+            with torch.cuda.graph(g, stream=s):
+                call(out)
+        finally:
+            L.use_stream()
+        for p in (300, 5000, 8191, 63):
+            pos.fill_(p)
+            g.replay()
+            torch.cuda.synchronize()
+            got = host(out).copy()
+            call(out_e)  # eager fused call in between (another tag)
+            fused_eager = host(out_e).copy()
+            L.set_attn_combine_mode(1)
+            call(out_e)
+            two = host(out_e).copy()
+            L.set_attn_combine_mode(0)
+            np.testing.assert_array_equal(got, two, err_msg=f"replay at {p}")
+            np.testing.assert_array_equal(fused_eager, two, err_msg=f"eager at {p}")
+    finally:
+        L.set_attn_combine_mode(prev)
+        L.use_stream()
