@@ -47,6 +47,7 @@
 
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <type_traits>
 
 namespace g4 {
@@ -84,7 +85,21 @@ struct GemmArgs {
   float* partials;  // swiglu: [gridDim.x] max |act|
   int mt, nt;       // tile counts along M and N
   bool vec_out;     // 16-byte output rows (pitch and width multiples of 8)
+  bool xcd_order;   // tiles renumbered per XCD (xcd_tile0)
 };
+
+// Workgroups are handed to the 8 XCDs round-robin by id (id % 8), each XCD
+// with its own L2. The first tile of workgroup b is renumbered so that
+// consecutive tile numbers - the M tiles of one weight column, which read the
+// same W rows - run on one XCD and share its L2 instead of each XCD fetching
+// the column: b -> (b % 8) * (g / 8) + b / 8 over the first 8 * floor(g / 8)
+// workgroups (g the grid), the identity on the rest. Tile t + g keeps the
+// same XCD as tile t.
+__device__ __forceinline__ int xcd_tile0(bool on) {
+  const int b = blockIdx.x, g = gridDim.x, full = g & ~7;
+  if (!on || b >= full) return b;
+  return (b & 7) * (full >> 3) + (b >> 3);
+}
 
 __device__ __forceinline__ float epi_scale(const Granite4GemmEpilogue& ep, int n) {
   return n < ep.seg1 ? ep.scale0 : (n < ep.seg2 ? ep.scale1 : ep.scale2);
@@ -337,7 +352,7 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(GemmArgs a) {
   constexpr int kIters = 32 / kRowsPerIter;
   static_assert(4 * 32 * kEP * 4 <= ST * kStage, "epilogue staging fits the stage buffers");
 
-  for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+  for (int tile = xcd_tile0(a.xcd_order); tile < tiles; tile += gridDim.x) {
     const int tm = tile % a.mt, tn = tile / a.mt;
     const int m0 = tm * kGBM;
     v4f acc[4][4];
@@ -489,7 +504,7 @@ __global__ __launch_bounds__(256) void gemm_bf16w_kernel(GemmArgs a) {
   constexpr int kIters = 32 / kRowsPerIter;
   static_assert(4 * 32 * kEP * 4 <= 2 * kBwStage, "epilogue staging fits the stage buffers");
 
-  for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+  for (int tile = xcd_tile0(a.xcd_order); tile < tiles; tile += gridDim.x) {
     const int tm = tile % a.mt, tn = tile / a.mt;
     const int m0 = tm * kGBM;
     v4f acc[4][4];
@@ -570,6 +585,27 @@ bool gemm_args_ok(const uint8_t* A, int lda, const uint8_t* W, int M, int N, int
          static_cast<long long>(M) * lda < (1LL << 40);
 }
 
+// Whether XCD-ordered tiles (xcd_tile0) cut the L2 fills of a launch of g
+// workgroups over mt M tiles. Per round each XCD runs g / 8 tiles; the A rows
+// and W rows it fetches grow with the block of tiles it covers, bm M tiles x
+// bn N tiles, as bm + bn. XCD order gives each XCD whole columns, bm = mt
+// (up to g / 8); the plain order gives it every 8th tile: one M tile (mt <= 8)
+// or mt / 8 of them, spread over g / 8 or g / mt columns. Measured: T = 512
+// gate|up 88 -> 77 us with XCD order (4 x 16 against 1 x 64), T = 8192 the
+// plain order's 8 x 8 beats XCD order's 64 x 1 by 14-17 %. G4_GEMM_XCD=0
+// keeps the plain order everywhere (A/B measurement).
+bool gemm_xcd_order(int mt, unsigned g) {
+  static const bool allowed = [] {
+    const char* e = std::getenv("G4_GEMM_XCD");
+    return !(e != nullptr && e[0] == '0');
+  }();
+  if (!allowed || g < 16) return false;
+  const long long per = g / 8;
+  const long long xbm = mt < per ? mt : per, xbn = (per + mt - 1) / mt;
+  const long long pbm = mt <= 8 ? 1 : mt / 8, pbn = mt <= 8 ? per : (g + mt - 1) / mt;
+  return xbm + xbn < pbm + pbn;
+}
+
 template <int EPI, int TN = kGBN, int ST = kGStages>
 unsigned gemm_grid(long long tiles, int cap) {
   const int resident = resident_blocks(reinterpret_cast<const void*>(gemm_fp8_kernel<EPI, TN, ST>), 256);
@@ -615,7 +651,10 @@ int granite4_gemm_fp8(int out, const uint8_t* A, int lda, const float* d_a_scale
   a.nt = narrow ? (N + 63) / 64 : (N + kGBN - 1) / kGBN;
   const long long tiles = static_cast<long long>(a.mt) * a.nt;
   const hipStream_t st = stream();
-  const auto go = [&](auto kern, unsigned grid) { hipLaunchKernelGGL(kern, grid, 256, 0, st, a); };
+  const auto go = [&](auto kern, unsigned grid) {
+    a.xcd_order = gemm_xcd_order(a.mt, grid);
+    hipLaunchKernelGGL(kern, grid, 256, 0, st, a);
+  };
   // 128 x 64 tiles: six stages where every tile has a CU of its own (one
   // workgroup per CU, 144 KB of LDS), three where two share one (72 KB
   // each), two otherwise.
@@ -673,7 +712,9 @@ int granite4_prefill_gemm(int out, const uint16_t* A, int lda, const uint8_t* W,
     const int resident = resident_blocks(k, 256);
     long long g = tiles;
     if (resident > 0 && g > resident) g = resident;
-    return static_cast<unsigned>(g > 0 ? g : 1);
+    const unsigned gu = static_cast<unsigned>(g > 0 ? g : 1);
+    a.xcd_order = gemm_xcd_order(a.mt, gu);
+    return gu;
   };
   switch (out) {
     case GRANITE4_GEMM_BF16:
@@ -731,6 +772,7 @@ int granite4_gemm_fp8_swiglu(const uint8_t* A, int lda, const float* d_a_scale,
   a.partials = work_partials(d_work);
   const long long tiles = static_cast<long long>(a.mt) * a.nt;
   const unsigned grid = gemm_grid<kEpiSwiglu>(tiles, kMaxPartials);
+  a.xcd_order = gemm_xcd_order(a.mt, grid);
   hipLaunchKernelGGL(gemm_fp8_kernel<kEpiSwiglu>, grid, 256, 0, stream(), a);
   if (launch_status("granite4_gemm_fp8_swiglu") != 0) return -1;
   if (codes == nullptr) return 0;
