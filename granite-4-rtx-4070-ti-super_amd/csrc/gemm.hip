@@ -136,11 +136,11 @@ typedef __attribute__((address_space(3))) void* lds_ptr;
 
 template <int EPI, int TN = kGBN>
 __device__ __forceinline__ void stage_issue(const GemmArgs& a, int m0, int tn, int k0,
-                                            uint8_t* st) {
-  const int wave = threadIdx.x >> 6;
+                                            uint8_t* st, int tid) {
+  const int wave = tid >> 6;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int slot = i * 256 + threadIdx.x;
+    const int slot = i * 256 + tid;
     const int row = slot >> 3, c = (slot & 7) ^ (row & 7);
     const int m = min(m0 + row, a.M - 1);
     __builtin_amdgcn_global_load_lds(a.A + static_cast<size_t>(m) * a.lda + k0 + 16 * c,
@@ -149,7 +149,7 @@ __device__ __forceinline__ void stage_issue(const GemmArgs& a, int m0, int tn, i
   }
 #pragma unroll
   for (int i = 0; i < TN / 32; ++i) {
-    const int slot = i * 256 + threadIdx.x;
+    const int slot = i * 256 + tid;
     const int row = slot >> 3, c = (slot & 7) ^ (row & 7);
     int n = w_row<EPI, TN>(a, tn, row);
     if (n < 0) n = 0;
@@ -234,7 +234,7 @@ __device__ __forceinline__ void stage_wait_n(int later) {
 // output pitch or width is not a multiple of 8, element by element). The
 // residual was prefetched at the tile's start (a load after a store would
 // wait for the store: the vector memory counter covers both).
-template <int EPI, int kIters, int kWCols>
+template <int EPI, int kIters, int kWCols, bool kBarrier = true>
 __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, const v4f (&acc)[4][4],
                                               float a_scale, uint8_t* s_tile, int m0, int col0,
                                               int n_end, const uint4* res, float& amax) {
@@ -244,7 +244,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, const v4f (&acc
   const int fr = lane & 15;
   constexpr int kLanesPerRow = kWCols / 8;
   constexpr int kRowsPerIter = 64 / kLanesPerRow;
-  __builtin_amdgcn_s_barrier();  // every wave is past its last fragment read
+  if (kBarrier) __builtin_amdgcn_s_barrier();  // every wave is past its last fragment read
   float* const sv = reinterpret_cast<float*>(s_tile) + wave * (32 * kEP);
   const Granite4GemmEpilogue& ep = a.ep;
 #pragma unroll
@@ -329,17 +329,30 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, const v4f (&acc
 // wave then owns 64 x 32 outputs (4 x 2 MFMA tiles).
 // ST: pipeline stages (kGStages, or more where one workgroup per CU leaves
 // it the LDS).
-template <int EPI, int TN = kGBN, int ST = kGStages>
-__global__ __launch_bounds__(256) void gemm_fp8_kernel(GemmArgs a) {
+// KS = 2: K split inside the workgroup. Two 4-wave halves (512 threads) run
+// K tiles [0, kh) and [kh, ktiles) through their own ST stages, meeting at
+// every barrier (half 1 idles through its last step when ktiles is odd);
+// half 1 then hands its accumulators to half 0 through LDS, which adds them
+// (the sum of two f32 partial sums) and runs the epilogue. Two waves per
+// SIMD instead of one where a short prompt gives each CU one tile.
+template <int EPI, int TN = kGBN, int ST = kGStages, int KS = 1>
+__global__ __launch_bounds__(256 * KS) void gemm_fp8_kernel(GemmArgs a) {
   static_assert(TN == kGBN || (TN == 64 && EPI != kEpiSwiglu), "tile width");
+  static_assert(KS == 1 || (KS == 2 && EPI != kEpiSwiglu), "split K: plain epilogues only");
   constexpr int kNI = TN / 32;  // MFMA tiles per wave along N
   constexpr int kStage = (kGBM + TN) * kGBK;
-  __shared__ __align__(16) uint8_t s_tile[ST * kStage];
+  __shared__ __align__(16) uint8_t s_tile[KS * ST * kStage];
   constexpr int kLps = 4 + TN / 32;  // loads per thread per stage
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int tid = threadIdx.x & 255;
+  const int half = KS == 2 ? static_cast<int>(threadIdx.x >> 8) : 0;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int ktiles = a.K / kGBK;
+  const int kh = KS == 2 ? (ktiles + 1) / 2 : ktiles;  // steps of the K loop
+  const int kbeg = half * kh;
+  const int kn = KS == 2 ? min(kh, ktiles - kbeg) : ktiles;  // this half's K tiles
+  uint8_t* const sbase = s_tile + half * ST * kStage;
   const int tiles = a.mt * a.nt;
   const int fr = lane & 15;          // fragment row
   const float a_scale = *a.a_scale;
@@ -365,7 +378,7 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(GemmArgs a) {
     const int col0 = EPI == kEpiSwiglu ? tn * 64 + wn * 32 : tn * TN + wn * (TN / 2);
     const int n_end = EPI == kEpiSwiglu ? a.I : a.N;
     uint4 res[EPI == kEpiResidual ? 2 * kIters : 1];
-    if (EPI == kEpiResidual) {
+    if (EPI == kEpiResidual && half == 0) {
 #pragma unroll
       for (int j = 0; j < 2 * kIters; ++j) {
         const int h = j / kIters, it = j % kIters;
@@ -380,19 +393,20 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(GemmArgs a) {
     __syncthreads();  // the previous tile's readers are done with every buffer
 #pragma unroll
     for (int sidx = 0; sidx < ST - 1; ++sidx)
-      if (sidx < ktiles) stage_issue<EPI, TN>(a, m0, tn, sidx * kGBK, s_tile + sidx * kStage);
-    for (int kt = 0; kt < ktiles; ++kt) {
-      // Stages issued after kt so far: min(kStages - 2, ktiles - 1 - kt).
-      const int later = min(ST - 2, ktiles - 1 - kt);
+      if (sidx < kn) stage_issue<EPI, TN>(a, m0, tn, (kbeg + sidx) * kGBK, sbase + sidx * kStage, tid);
+    for (int kt = 0; kt < kh; ++kt) {
+      // Stages issued after kt so far: min(kStages - 2, kn - 1 - kt).
+      const int later = min(ST - 2, kn - 1 - kt);
       stage_wait_n<kLps>(later);
       // Stage kt landed for every wave (each waited for its own loads);
       // stage kt - 1's reads are done (waited before its MFMAs). No fence:
       // a workgroup-scope release would wait for the stages still in flight.
       __builtin_amdgcn_s_barrier();
-      if (kt + ST - 1 < ktiles)
-        stage_issue<EPI, TN>(a, m0, tn, (kt + ST - 1) * kGBK,
-                             s_tile + ((kt + ST - 1) % ST) * kStage);
-      const uint32_t st = lds_addr(s_tile + (kt % ST) * kStage);
+      if (kt + ST - 1 < kn)
+        stage_issue<EPI, TN>(a, m0, tn, (kbeg + kt + ST - 1) * kGBK,
+                             sbase + ((kt + ST - 1) % ST) * kStage, tid);
+      if (KS == 2 && kt >= kn) continue;  // half 1's idle last step (odd ktiles)
+      const uint32_t st = lds_addr(sbase + (kt % ST) * kStage);
       v4u ax[4], ay[4], bx[kNI], by[kNI];
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi) frag_issue(st, wm * 64 + mi * 16 + fr, lane, ax[mi], ay[mi]);
@@ -413,7 +427,27 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(GemmArgs a) {
               frag_of(ax[mi], ay[mi]), frag_of(bx[ni], by[ni]), acc[mi][ni], 0, 0, 0, 0, 0, 0);
     }
 
-    tile_epilogue<EPI, kIters, kWCols>(a, acc, a_scale, s_tile, m0, col0, n_end, res, amax);
+    if constexpr (KS == 2) {
+      // Half 1's accumulators to half 0 through half 1's stage buffers
+      // (16 bytes per lane and MFMA tile, lane-contiguous).
+      __builtin_amdgcn_s_barrier();  // every wave is past its last fragment read
+      v4f* const xa = reinterpret_cast<v4f*>(s_tile + ST * kStage) + wave * (4 * kNI * 64) + lane;
+      if (half == 1) {
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+          for (int ni = 0; ni < kNI; ++ni) xa[(mi * kNI + ni) * 64] = acc[mi][ni];
+      }
+      wave_lds_wait();
+      __builtin_amdgcn_s_barrier();
+      if (half == 1) continue;  // the next tile's first barrier waits for half 0's epilogue
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < kNI; ++ni) acc[mi][ni] += xa[(mi * kNI + ni) * 64];
+    }
+    tile_epilogue<EPI, kIters, kWCols, KS == 1>(a, acc, a_scale, s_tile, m0, col0, n_end, res,
+                                                amax);
   }
   if (EPI == kEpiSwiglu) write_partial(a.partials, amax);
 }
@@ -594,6 +628,16 @@ bool gemm_args_ok(const uint8_t* A, int lda, const uint8_t* W, int M, int N, int
 // gate|up 88 -> 77 us with XCD order (4 x 16 against 1 x 64), T = 8192 the
 // plain order's 8 x 8 beats XCD order's 64 x 1 by 14-17 %. G4_GEMM_XCD=0
 // keeps the plain order everywhere (A/B measurement).
+// K split inside the workgroup (KS = 2) where each CU holds one 128 x 64
+// tile, unless G4_GEMM_KSPLIT=0 (A/B measurement).
+bool gemm_ksplit() {
+  static const bool on = [] {
+    const char* e = std::getenv("G4_GEMM_KSPLIT");
+    return !(e != nullptr && e[0] == '0');
+  }();
+  return on;
+}
+
 bool gemm_xcd_order(int mt, unsigned g) {
   static const bool allowed = [] {
     const char* e = std::getenv("G4_GEMM_XCD");
@@ -606,9 +650,10 @@ bool gemm_xcd_order(int mt, unsigned g) {
   return xbm + xbn < pbm + pbn;
 }
 
-template <int EPI, int TN = kGBN, int ST = kGStages>
+template <int EPI, int TN = kGBN, int ST = kGStages, int KS = 1>
 unsigned gemm_grid(long long tiles, int cap) {
-  const int resident = resident_blocks(reinterpret_cast<const void*>(gemm_fp8_kernel<EPI, TN, ST>), 256);
+  const int resident =
+      resident_blocks(reinterpret_cast<const void*>(gemm_fp8_kernel<EPI, TN, ST, KS>), 256 * KS);
   long long g = tiles;
   if (resident > 0 && g > resident) g = resident;
   if (g > cap) g = cap;
@@ -651,9 +696,9 @@ int granite4_gemm_fp8(int out, const uint8_t* A, int lda, const float* d_a_scale
   a.nt = narrow ? (N + 63) / 64 : (N + kGBN - 1) / kGBN;
   const long long tiles = static_cast<long long>(a.mt) * a.nt;
   const hipStream_t st = stream();
-  const auto go = [&](auto kern, unsigned grid) {
+  const auto go = [&](auto kern, unsigned grid, int threads = 256) {
     a.xcd_order = gemm_xcd_order(a.mt, grid);
-    hipLaunchKernelGGL(kern, grid, 256, 0, st, a);
+    hipLaunchKernelGGL(kern, grid, threads, 0, st, a);
   };
   // 128 x 64 tiles: six stages where every tile has a CU of its own (one
   // workgroup per CU, 144 KB of LDS), three where two share one (72 KB
@@ -662,6 +707,7 @@ int granite4_gemm_fp8(int out, const uint8_t* A, int lda, const float* d_a_scale
   const auto run = [&](auto e_tag) {
     constexpr int E = decltype(e_tag)::value;
     if (!narrow) go(gemm_fp8_kernel<E>, gemm_grid<E>(tiles, INT_MAX));
+    else if (deep == 6 && gemm_ksplit()) go(gemm_fp8_kernel<E, 64, 3, 2>, gemm_grid<E, 64, 3, 2>(tiles, INT_MAX), 512);
     else if (deep == 6) go(gemm_fp8_kernel<E, 64, 6>, gemm_grid<E, 64, 6>(tiles, INT_MAX));
     else if (deep == 3) go(gemm_fp8_kernel<E, 64, 3>, gemm_grid<E, 64, 3>(tiles, INT_MAX));
     else go(gemm_fp8_kernel<E, 64>, gemm_grid<E, 64>(tiles, INT_MAX));

@@ -90,10 +90,13 @@ def run_gemm(kind, A, a_scale, W, scales=(1.0, 1.0, 1.0), segs=None, residual=No
     return host(out)
 
 
-# Fewer than 256 output tiles of 128 x 128 take the 128 x 64 tile form; the
-# last shape (9 x 32 = 288 tiles) the 128 x 128 one.
+# Fewer than 256 output tiles of 128 x 128 take the 128 x 64 tile form, and
+# where those give each CU at most one tile, K split between the two halves of
+# a 512-thread workgroup (K = 128 and 384: an odd count of 128-wide K tiles,
+# half 1 idle in the last step); the 1100-row shape (9 x 32 = 288 tiles) the
+# 128 x 128 form.
 SHAPES = [(1, 128, 128), (70, 136, 256), (128, 256, 512), (300, 520, 1024), (257, 1024, 4096),
-          (1100, 4096, 128)]
+          (1100, 4096, 128), (96, 192, 384)]
 
 
 @pytest.mark.parametrize("M,N,K", SHAPES)
@@ -135,7 +138,8 @@ def test_gemm_fp8_segment_scales():
     assert not bad.any()
 
 
-@pytest.mark.parametrize("M,N,K", [(64, 256, 512), (200, 4096, 4096), (2100, 2048, 256)])
+@pytest.mark.parametrize("M,N,K", [(64, 256, 512), (200, 4096, 4096), (2100, 2048, 256),
+                                   (130, 512, 1408)])
 def test_gemm_fp8_residual_in_place(M, N, K):
     """The O / down projection: hidden = bf16(hidden + rs * y), in place."""
     note(f"gemm_fp8 residual M={M} N={N} K={K}")
