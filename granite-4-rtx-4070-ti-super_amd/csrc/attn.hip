@@ -897,10 +897,10 @@ struct PrefillRaw {
 template <int BITS, int GROUP, int W>
 __device__ __forceinline__ void prefill_pt(const PrefillArgs& a, int j0, int kv_end,
                                            int (&ptk)[PrefillRaw<BITS, GROUP, W>::kKIt],
-                                           int (&ptv)[PrefillRaw<BITS, GROUP, W>::kVIt]) {
+                                           int (&ptv)[PrefillRaw<BITS, GROUP, W>::kVIt], int t) {
   using R = PrefillRaw<BITS, GROUP, W>;
   constexpr int kPrefThreads = R::kPrefThreads;
-  const int t = threadIdx.x, tv = (t + R::kVShift) % kPrefThreads;
+  const int tv = (t + R::kVShift) % kPrefThreads;
   const int last = max(kv_end - 1, 0);
 #pragma unroll
   for (int it = 0; it < R::kKIt; ++it) {
@@ -922,11 +922,11 @@ __device__ __forceinline__ void prefill_load(const PrefillArgs& a, const uint8_t
                                              const float* vscb, int j0, int kv_end,
                                              const int (&ptk)[PrefillRaw<BITS, GROUP, W>::kKIt],
                                              const int (&ptv)[PrefillRaw<BITS, GROUP, W>::kVIt],
-                                             PrefillRaw<BITS, GROUP, W>& raw) {
+                                             PrefillRaw<BITS, GROUP, W>& raw, int t) {
   using R = PrefillRaw<BITS, GROUP, W>;
   constexpr int kPrefThreads = R::kPrefThreads;
   constexpr int kKb = k_row_bytes(BITS);
-  const int t = threadIdx.x, tv = (t + R::kVShift) % kPrefThreads;
+  const int tv = (t + R::kVShift) % kPrefThreads;
   auto valid = [&](int key, int r) {
     return (j0 + key < kv_end && r >= 0 && r < a.stride) ? r : -1;
   };
@@ -968,10 +968,10 @@ __device__ __forceinline__ void prefill_load(const PrefillArgs& a, const uint8_t
 template <int BITS, int GROUP, int W>
 __device__ __forceinline__ void prefill_store(const PrefillRaw<BITS, GROUP, W>& raw, uint16_t* ks,
                                               uint16_t* vs, float* ksc_l, float* vsc_l,
-                                              unsigned* s_valid, float kmul) {
+                                              unsigned* s_valid, float kmul, int t) {
   using R = PrefillRaw<BITS, GROUP, W>;
   constexpr int kPrefThreads = R::kPrefThreads;
-  const int t = threadIdx.x, tv = (t + R::kVShift) % kPrefThreads;
+  const int tv = (t + R::kVShift) % kPrefThreads;
 #pragma unroll
   for (int it = 0; it < R::kKIt; ++it) {
     const int idx = t + it * kPrefThreads;
@@ -1036,21 +1036,31 @@ __device__ __forceinline__ void prefill_store(const PrefillRaw<BITS, GROUP, W>& 
 // CB: column blocks per wave (4 CB positions x 4 heads each); the K and V^T
 // fragments read from LDS serve all CB blocks, and a staged tile serves
 // 16 CB positions.
-template <int BITS, int GROUP, int CB, int W>
+// KSP = 2 (W = 8): the keys split inside the workgroup. Two 4-wave groups own
+// the same 16 positions (waves w and w + 4 the same 4); group k stages and
+// runs tiles j_first + (2 i + k) * 64 through its own two tile buffers, and
+// at the end group 1's (m, l, o) merge into group 0's through LDS
+// (M = max m, each side's o and l scaled by exp(m - M)). Two waves per SIMD
+// where a short prompt gives each CU one 16-position workgroup.
+template <int BITS, int GROUP, int CB, int W, int KSP = 1>
 __global__ __launch_bounds__(W * 64) void attn_prefill_kernel(PrefillArgs a) {
-  constexpr int kPrefWaves = W;
+  static_assert(KSP == 1 || (KSP == 2 && W == 8), "key split: two 4-wave groups");
+  constexpr int kPrefWaves = W / KSP;  // waves owning positions (and staging a tile)
   constexpr bool kQuant = BITS != 16;
   constexpr int kNgrp = kQuant ? kHd / GROUP : 1;
   constexpr int kKb = k_row_bytes(BITS), kVb = v_row_bytes(BITS);
   constexpr int kPos = kPrefWaves * 4 * CB;  // positions per workgroup
-  // Two tile buffers: tile t + 1 is staged into one while tile t is read from
-  // the other, with one barrier per tile.
-  __shared__ __align__(16) uint16_t ks2[2][kTile * kKPitch];
-  __shared__ __align__(16) uint16_t vs2[2][kTile * kVPitch];
-  __shared__ float ksc2[2][kTile * kNgrp], vsc2[2][kTile * kNgrp];
-  __shared__ unsigned valid2[2][kTile];
+  // Two tile buffers per key group: tile t + 1 is staged into one while tile
+  // t is read from the other, with one barrier per tile.
+  __shared__ __align__(16) uint16_t ks2[KSP][2][kTile * kKPitch];
+  __shared__ __align__(16) uint16_t vs2[KSP][2][kTile * kVPitch];
+  __shared__ float ksc2[KSP][2][kTile * kNgrp], vsc2[KSP][2][kTile * kNgrp];
+  __shared__ unsigned valid2[KSP][2][kTile];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int gk = KSP == 2 ? static_cast<int>(threadIdx.x >> 8) : 0;  // key group
+  const int wave = static_cast<int>(threadIdx.x >> 6) & (kPrefWaves - 1);
+  const int tst = threadIdx.x & (kPrefWaves * 64 - 1);  // staging thread within the group
   const int g = lane >> 4, n = lane & 15;
   const int hkv = blockIdx.y;
   const int p0 = blockIdx.x * kPos;
@@ -1101,27 +1111,39 @@ __global__ __launch_bounds__(W * 64) void attn_prefill_kernel(PrefillArgs a) {
   const int wave_pos_min = a.base + wave_row0;
   const int wave_lo_max = a.window > 0 ? max(0, wave_pos_min + 4 * CB - a.window) : 0;
 
-  using Raw = PrefillRaw<BITS, GROUP, W>;
+  constexpr int PW = kPrefWaves;
+  using Raw = PrefillRaw<BITS, GROUP, PW>;
   Raw raw;
   int ptk[Raw::kKIt], ptv[Raw::kVIt];
-  if (j_first < kv_end) {
-    prefill_pt<BITS, GROUP, W>(a, j_first, kv_end, ptk, ptv);
-    prefill_load<BITS, GROUP, W>(a, kbase, vbase, kscb, vscb, j_first, kv_end, ptk, ptv, raw);
-    prefill_pt<BITS, GROUP, W>(a, j_first + kTile, kv_end, ptk, ptv);
-    prefill_store<BITS, GROUP, W>(raw, ks2[0], vs2[0], ksc2[0], vsc2[0], valid2[0], a.scale);
-    if (j_first + kTile < kv_end) {
-      prefill_load<BITS, GROUP, W>(a, kbase, vbase, kscb, vscb, j_first + kTile, kv_end, ptk, ptv, raw);
-      prefill_pt<BITS, GROUP, W>(a, j_first + 2 * kTile, kv_end, ptk, ptv);
+  constexpr int kStep = KSP * kTile;    // between a group's tiles
+  const int jg = j_first + gk * kTile;  // this group's first tile
+  if (jg < kv_end) {
+    prefill_pt<BITS, GROUP, PW>(a, jg, kv_end, ptk, ptv, tst);
+    prefill_load<BITS, GROUP, PW>(a, kbase, vbase, kscb, vscb, jg, kv_end, ptk, ptv, raw, tst);
+    prefill_pt<BITS, GROUP, PW>(a, jg + kStep, kv_end, ptk, ptv, tst);
+    prefill_store<BITS, GROUP, PW>(raw, ks2[gk][0], vs2[gk][0], ksc2[gk][0], vsc2[gk][0],
+                                   valid2[gk][0], a.scale, tst);
+    if (jg + kStep < kv_end) {
+      prefill_load<BITS, GROUP, PW>(a, kbase, vbase, kscb, vscb, jg + kStep, kv_end, ptk, ptv, raw, tst);
+      prefill_pt<BITS, GROUP, PW>(a, jg + 2 * kStep, kv_end, ptk, ptv, tst);
     }
   }
   __syncthreads();
+  // Both groups run the same number of steps (one barrier each); group 1
+  // idles through the last when the tile count is odd.
+  const int steps = kv_end > j_first ? (kv_end - j_first + kStep - 1) / kStep : 0;
   int buf = 0;
-  for (int j0 = j_first; j0 < kv_end; j0 += kTile, buf ^= 1) {
-    const uint16_t* ks = ks2[buf];
-    const uint16_t* vs = vs2[buf];
-    const float* ksc_l = ksc2[buf];
-    const float* vsc_l = vsc2[buf];
-    const unsigned* s_valid = valid2[buf];
+  for (int it = 0; it < steps; ++it, buf ^= 1) {
+    const int j0 = jg + it * kStep;
+    if (KSP == 2 && j0 >= kv_end) {
+      __syncthreads();
+      continue;
+    }
+    const uint16_t* ks = ks2[gk][buf];
+    const uint16_t* vs = vs2[gk][buf];
+    const float* ksc_l = ksc2[gk][buf];
+    const float* vsc_l = vsc2[gk][buf];
+    const unsigned* s_valid = valid2[gk][buf];
     // A tile that every column of this wave sees whole (all keys at or below
     // the wave's first position, at or above its last window start, each with
     // an arena row) takes the form without the mask.
@@ -1247,18 +1269,49 @@ __global__ __launch_bounds__(W * 64) void attn_prefill_kernel(PrefillArgs a) {
     };
     if (full) tile(std::false_type{});
     else tile(std::true_type{});
-    if (j0 + kTile < kv_end) {
-      // Stage the next tile (its bytes were loaded a tile ago) into the other
-      // buffer, whose last readers passed the previous barrier; then load the
-      // bytes of the tile after it and the page-table entries of the third.
-      prefill_store<BITS, GROUP, W>(raw, ks2[buf ^ 1], vs2[buf ^ 1], ksc2[buf ^ 1], vsc2[buf ^ 1],
-                                 valid2[buf ^ 1], a.scale);
-      if (j0 + 2 * kTile < kv_end) {
-        prefill_load<BITS, GROUP, W>(a, kbase, vbase, kscb, vscb, j0 + 2 * kTile, kv_end, ptk, ptv, raw);
-        prefill_pt<BITS, GROUP, W>(a, j0 + 3 * kTile, kv_end, ptk, ptv);
+    if (j0 + kStep < kv_end) {
+      // Stage the group's next tile (its bytes were loaded a tile ago) into
+      // its other buffer, whose last readers passed the previous barrier;
+      // then load the bytes of the tile after it and the page-table entries
+      // of the third.
+      prefill_store<BITS, GROUP, PW>(raw, ks2[gk][buf ^ 1], vs2[gk][buf ^ 1], ksc2[gk][buf ^ 1],
+                                     vsc2[gk][buf ^ 1], valid2[gk][buf ^ 1], a.scale, tst);
+      if (j0 + 2 * kStep < kv_end) {
+        prefill_load<BITS, GROUP, PW>(a, kbase, vbase, kscb, vscb, j0 + 2 * kStep, kv_end, ptk,
+                                      ptv, raw, tst);
+        prefill_pt<BITS, GROUP, PW>(a, j0 + 3 * kStep, kv_end, ptk, ptv, tst);
       }
     }
     __syncthreads();
+  }
+  if constexpr (KSP == 2) {
+    // Group 1's state to group 0 through the tile buffers (free: the loop
+    // ended with a barrier): o lane-contiguous per (wave, cb, nb), then m, l.
+    f32x4_t* xo = reinterpret_cast<f32x4_t*>(&ks2[0][0][0]) + (wave * CB * 8) * 64 + lane;
+    float* xm = reinterpret_cast<float*>(&vs2[0][0][0]) + (wave * CB * 2) * 64 + lane;
+    static_assert(sizeof(ks2) >= sizeof(f32x4_t) * 4 * CB * 8 * 64, "merge area (o)");
+    static_assert(sizeof(vs2) >= sizeof(float) * 4 * CB * 2 * 64, "merge area (m, l)");
+    if (gk == 1) {
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) xo[(cb * 8 + nb) * 64] = o[cb][nb];
+        xm[(cb * 2) * 64] = m[cb];
+        xm[(cb * 2 + 1) * 64] = l[cb];
+      }
+    }
+    __syncthreads();
+    if (gk == 1) return;
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      const float m1 = xm[(cb * 2) * 64], l1 = xm[(cb * 2 + 1) * 64];
+      const float mm = fmaxf(m[cb], m1);
+      const float a0 = m[cb] == -INFINITY ? 0.0f : __expf(m[cb] - mm);
+      const float a1 = m1 == -INFINITY ? 0.0f : __expf(m1 - mm);
+      l[cb] = l[cb] * a0 + l1 * a1;
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) o[cb][nb] = o[cb][nb] * a0 + xo[(cb * 8 + nb) * 64] * a1;
+    }
   }
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) {
@@ -1343,21 +1396,32 @@ void launch_attn_bits(const AttnArgs& a, int group, dim3 grid, hipStream_t st) {
 // cycles per tile), so more registers per wave only cost occupancy.
 constexpr int kPrefillCb = 1;
 
-template <int BITS, int W>
+template <int BITS, int W, int KSP = 1>
 void launch_prefill_w(const PrefillArgs& a, int group, dim3 grid, hipStream_t st) {
   constexpr int CB = kPrefillCb;
   if constexpr (BITS == 16) {
     (void)group;
-    hipLaunchKernelGGL((attn_prefill_kernel<16, kHd, CB, W>), grid, W * 64, 0, st, a);
+    hipLaunchKernelGGL((attn_prefill_kernel<16, kHd, CB, W, KSP>), grid, W * 64, 0, st, a);
   } else {
-    if (group == kHd) hipLaunchKernelGGL((attn_prefill_kernel<BITS, kHd, CB, W>), grid, W * 64, 0, st, a);
-    else if (group == 64) hipLaunchKernelGGL((attn_prefill_kernel<BITS, 64, CB, W>), grid, W * 64, 0, st, a);
-    else hipLaunchKernelGGL((attn_prefill_kernel<BITS, 32, CB, W>), grid, W * 64, 0, st, a);
+    if (group == kHd) hipLaunchKernelGGL((attn_prefill_kernel<BITS, kHd, CB, W, KSP>), grid, W * 64, 0, st, a);
+    else if (group == 64) hipLaunchKernelGGL((attn_prefill_kernel<BITS, 64, CB, W, KSP>), grid, W * 64, 0, st, a);
+    else hipLaunchKernelGGL((attn_prefill_kernel<BITS, 32, CB, W, KSP>), grid, W * 64, 0, st, a);
   }
 }
 
+// The key split for 16-position workgroups unless G4_PREFILL_KSPLIT=0 (A/B
+// measurement).
+bool prefill_ksplit() {
+  static const bool on = [] {
+    const char* e = std::getenv("G4_PREFILL_KSPLIT");
+    return !(e != nullptr && e[0] == '0');
+  }();
+  return on;
+}
+
 // 8-wave workgroups (32 positions each) where they give every CU one, else
-// 4-wave workgroups (16 positions) for twice the workgroups.
+// 16-position workgroups for twice the workgroups: 8 waves splitting the keys
+// between two 4-wave groups, or 4 waves.
 template <int BITS>
 void launch_prefill_bits(const PrefillArgs& a, int group, int Hk, hipStream_t st) {
   const long long wide = static_cast<long long>((a.rows + 8 * 4 * kPrefillCb - 1) / (8 * 4 * kPrefillCb)) * Hk;
@@ -1366,7 +1430,8 @@ void launch_prefill_bits(const PrefillArgs& a, int group, int Hk, hipStream_t st
     launch_prefill_w<BITS, 8>(a, group, grid, st);
   } else {
     const dim3 grid((a.rows + 4 * 4 * kPrefillCb - 1) / (4 * 4 * kPrefillCb), Hk);
-    launch_prefill_w<BITS, 4>(a, group, grid, st);
+    if (prefill_ksplit()) launch_prefill_w<BITS, 8, 2>(a, group, grid, st);
+    else launch_prefill_w<BITS, 4>(a, group, grid, st);
   }
 }
 
