@@ -249,7 +249,10 @@ const bool g_rope_row_kernel = [] {
   return e == nullptr || e[0] != '0';
 }();
 
-constexpr int kRopeRowKernelMinRows = 256;
+// Measured (int8, A/B on one box, per-unit kernel / row kernel, us): 512 rows
+// 5.06 / 5.38, 640 5.62 / 5.98, 768 7.09 / 6.18, 1024 8.20 / 7.25, 4096
+// 23.4 / 18.6.
+constexpr int kRopeRowKernelMinRows = 704;
 
 // Validated launch of the fused kernel (d == 128) or the generic one.
 int launch_rope_append(RopeArgs a, int bits, int group, const char* what) {
@@ -264,9 +267,9 @@ int launch_rope_append(RopeArgs a, int bits, int group, const char* what) {
     const long long blocks = (units + (kBlock / 16) - 1) / (kBlock / 16);
     const unsigned grid = static_cast<unsigned>(blocks);
     const int upl = (a.units_per_row + 15) / 16;
-    // Per-token workgroups for long inputs; few rows (decode, T = 8) keep one
-    // unit per lane group, which spreads them over more workgroups (T=8: 24
-    // instead of 8, 2.7 vs 3.3 us).
+    // Per-token workgroups for long inputs; fewer rows (decode, T = 8, up to
+    // about 700 rows) keep one unit per lane group, which spreads them over
+    // more workgroups (T=8: 24 instead of 8, 2.7 vs 3.3 us).
     if (g_rope_row_kernel && upl <= 4 && a.rows >= kRopeRowKernelMinRows) {
       switch (bits) {
         case 16: launch_row_bits<16>(a, 128, upl); break;

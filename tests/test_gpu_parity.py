@@ -433,12 +433,12 @@ def _oracle_arena(bits, group, Hk, stride, fill=0xEE):
             np.zeros(Hk * stride * ng, np.float32), np.zeros(Hk * stride * ng, np.float32))
 
 
-@pytest.mark.parametrize("rows", [40, 300])
+@pytest.mark.parametrize("rows", [40, 300, 800])
 @pytest.mark.parametrize("bits", [16, 8, 4, 5])
 def test_prefill_rope_split_append_paged(tables, bits, rows):
     """The reference's prefill launchers: f32-rotated K quantised, random page table,
-    untouched rows keep their 0xEE fill (test_kernels.cu:730-801). 40 rows take the
-    one-unit-per-lane-group kernel, 300 the per-token one."""
+    untouched rows keep their 0xEE fill (test_kernels.cu:730-801). 40 and 300 rows take
+    the one-unit-per-lane-group kernel, 800 the per-token one (from 704 rows)."""
     note(f"prefill split append bits={bits} rows={rows}")
     c, s, dc, ds = tables
     Hq, Hk, base = 32, 8, 100
@@ -460,15 +460,16 @@ def test_prefill_rope_split_append_paged(tables, bits, rows):
     _arena_compare(arena, want, bits, 128, Hk, stride)
 
 
-@pytest.mark.parametrize("rows", [64, 300])
+@pytest.mark.parametrize("rows", [64, 800])
 @pytest.mark.parametrize("bits,group", [(8, 128), (8, 32), (4, 32), (5, 32), (5, 64), (16, 128)])
 def test_rope_append_fused_entry(tables, bits, group, rows):
     """granite4_rope_append at config-4 positions (57344..), group scales, per-row arena rows
-    (64 rows: one unit per lane group; 300: one workgroup per token)."""
+    (64 rows: one unit per lane group; 800: one workgroup per token)."""
     note(f"rope_append bits={bits} group={group} rows={rows}")
     c, s, dc, ds = tables
     Hq, Hk = 32, 8
-    stride = 512
+    stride = 1024  # arena rows: a permutation of [0, stride), one per token row (rows <= stride)
+    assert rows <= stride
     qkv = _qkv(rows, 0x77 + bits + group)
     d_qkv = dev(qkv)
     q, k, v = d_qkv[:, :Hq * 128], d_qkv[:, Hq * 128:(Hq + Hk) * 128], d_qkv[:, (Hq + Hk) * 128:]
