@@ -30,7 +30,10 @@
 // summed, for group scales); p = exp(logit - m) in f32 against the split's
 // running maximum m, l sums the unrounded p, and the value product uses
 // bf16(p * v_scale) (or bf16(p)) against the V codes (values). The combine
-// kernel rescales the splits' (m, l, o) and writes bf16(sum o w / sum l w).
+// rescales the splits' (m, l, o) and writes bf16(sum o w / sum l w): by
+// default the last split block of each (row group, KV head) does it inside
+// the split launch (combine_wave), else a second launch (attn_combine_kernel)
+// with the same arithmetic.
 // The MFMA accumulates in f32 in its own order; the tests hold the result to
 // the oracle's sequential f32 evaluation within stated bf16 tolerances.
 #include "g4_common.h"
