@@ -134,6 +134,14 @@ __device__ __forceinline__ int b_row(int wn, int ni) {
 // valid row instead (their results are never stored).
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
+// Chunk position of 16-byte chunk c of tile row r: c ^ chunk_swz(r).
+__device__ __forceinline__ int chunk_swz(int r) { return r & 7; }
+// The bf16-A kernel's A rows: c ^ ((r >> 1) & 7). Measured against r & 7
+// (A/B on one box): T=8192 down + residual 1716 -> 1611 us, T=512 215.6 ->
+// 203 us; the FP8 kernel's fragments show no difference (bank-conflict
+// counts equal, times within 1.5 %).
+__device__ __forceinline__ int bw_chunk_swz(int r) { return (r >> 1) & 7; }
+
 template <int EPI, int TN = kGBN>
 __device__ __forceinline__ void stage_issue(const GemmArgs& a, int m0, int tn, int k0,
                                             uint8_t* st, int tid) {
@@ -141,7 +149,7 @@ __device__ __forceinline__ void stage_issue(const GemmArgs& a, int m0, int tn, i
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int slot = i * 256 + tid;
-    const int row = slot >> 3, c = (slot & 7) ^ (row & 7);
+    const int row = slot >> 3, c = (slot & 7) ^ chunk_swz(row);
     const int m = min(m0 + row, a.M - 1);
     __builtin_amdgcn_global_load_lds(a.A + static_cast<size_t>(m) * a.lda + k0 + 16 * c,
                                      (lds_ptr)(st + (i * 256 + wave * 64) * 16), 16,
@@ -150,7 +158,7 @@ __device__ __forceinline__ void stage_issue(const GemmArgs& a, int m0, int tn, i
 #pragma unroll
   for (int i = 0; i < TN / 32; ++i) {
     const int slot = i * 256 + tid;
-    const int row = slot >> 3, c = (slot & 7) ^ (row & 7);
+    const int row = slot >> 3, c = (slot & 7) ^ chunk_swz(row);
     int n = w_row<EPI, TN>(a, tn, row);
     if (n < 0) n = 0;
     __builtin_amdgcn_global_load_lds(a.W + static_cast<size_t>(n) * a.K + k0 + 16 * c,
@@ -180,8 +188,8 @@ __device__ __forceinline__ void lds_reads_done() { asm volatile("s_waitcnt lgkmc
 __device__ __forceinline__ void frag_issue(uint32_t region, int r, int lane, v4u& x, v4u& y) {
   const int c0 = 2 * (lane >> 4);
   const uint32_t row = region + static_cast<uint32_t>(r * kGBK);
-  x = lds_read16(row + 16u * static_cast<uint32_t>(c0 ^ (r & 7)));
-  y = lds_read16(row + 16u * static_cast<uint32_t>((c0 + 1) ^ (r & 7)));
+  x = lds_read16(row + 16u * static_cast<uint32_t>(c0 ^ chunk_swz(r)));
+  y = lds_read16(row + 16u * static_cast<uint32_t>((c0 + 1) ^ chunk_swz(r)));
 }
 
 __device__ __forceinline__ v8i frag_of(const v4u& x, const v4u& y) {
@@ -460,7 +468,7 @@ __global__ __launch_bounds__(256 * KS) void gemm_fp8_kernel(GemmArgs a) {
 //
 // Same tiling, persistent grid and epilogue as gemm_fp8_kernel; K advances
 // 64 elements per stage. A stage holds A as 128 rows x 128 bytes (the bf16
-// k-slice, eight 16-byte chunks XOR-swizzled by row) and W raw as 128 rows
+// k-slice, eight 16-byte chunks XOR-swizzled by (row / 2) % 8) and W raw as 128 rows
 // x 64 bytes (four chunks, swizzled by row % 4), both filled by
 // direct-to-LDS loads. Each wave converts its W fragments from e4m3 to bf16
 // as it reads them (exact: an e4m3 value has at most 4 significant bits, so
@@ -482,7 +490,7 @@ __device__ __forceinline__ void bw_stage_issue(const GemmArgs& a, int m0, int tn
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int slot = i * 256 + threadIdx.x;
-    const int row = slot >> 3, c = (slot & 7) ^ (row & 7);
+    const int row = slot >> 3, c = (slot & 7) ^ bw_chunk_swz(row);
     const int m = min(m0 + row, a.M - 1);
     const int k = k0 + 8 * c < a.K ? k0 + 8 * c : 0;  // past K: a valid chunk, unused
     __builtin_amdgcn_global_load_lds(A + static_cast<size_t>(m) * a.lda + k,
@@ -583,7 +591,7 @@ __global__ __launch_bounds__(256) void gemm_bf16w_kernel(GemmArgs a) {
         for (int mi = 0; mi < 4; ++mi) {
           const int r = wm * 64 + mi * 16 + fr;
           ax[mi] = lds_read16(st + static_cast<uint32_t>(r * kBwARow) +
-                              16u * static_cast<uint32_t>(ca ^ (r & 7)));
+                              16u * static_cast<uint32_t>(ca ^ bw_chunk_swz(r)));
         }
 #pragma unroll
         for (int ni = 0; ni < 4; ++ni) {
