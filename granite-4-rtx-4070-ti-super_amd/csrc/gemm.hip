@@ -469,7 +469,7 @@ __global__ __launch_bounds__(256 * KS) void gemm_fp8_kernel(GemmArgs a) {
 // Same tiling, persistent grid and epilogue as gemm_fp8_kernel; K advances
 // 64 elements per stage. A stage holds A as 128 rows x 128 bytes (the bf16
 // k-slice, eight 16-byte chunks XOR-swizzled by (row / 2) % 8) and W raw as 128 rows
-// x 64 bytes (four chunks, swizzled by row % 4), both filled by
+// x 64 bytes (four chunks, swizzled by (row / 2) % 4), both filled by
 // direct-to-LDS loads. Each wave converts its W fragments from e4m3 to bf16
 // as it reads them (exact: an e4m3 value has at most 4 significant bits, so
 // its bf16 is the top half of its f32): one conversion and one byte permute
@@ -499,7 +499,7 @@ __device__ __forceinline__ void bw_stage_issue(const GemmArgs& a, int m0, int tn
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int slot = i * 256 + threadIdx.x;
-    const int row = slot >> 2, c = (slot & 3) ^ (row & 3);
+    const int row = slot >> 2, c = (slot & 3) ^ ((row >> 1) & 3);
     int n = w_row<EPI>(a, tn, row);
     if (n < 0) n = 0;
     const int k = k0 + 16 * c < a.K ? k0 + 16 * c : 0;
@@ -597,7 +597,7 @@ __global__ __launch_bounds__(256) void gemm_bf16w_kernel(GemmArgs a) {
         for (int ni = 0; ni < 4; ++ni) {
           const int r = wn * 64 + ni * 16 + fr;
           bq[ni] = lds_read8(sw + static_cast<uint32_t>(r * kBwWRow) +
-                             16u * static_cast<uint32_t>(cw ^ (r & 3)) + wh);
+                             16u * static_cast<uint32_t>(cw ^ ((r >> 1) & 3)) + wh);
         }
         lds_reads_done();
 #pragma unroll
