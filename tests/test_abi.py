@@ -71,6 +71,18 @@ def test_argument_validation_returns_minus_one():
     assert lib.granite4_debug_set_sync_spin_limit(-1) == -1
 
 
+def test_mode_switches_return_previous_and_reject_others():
+    """The process-wide launch switches (FP8 single launch, attention combine
+    in the split launch) return the previous mode and reject other values;
+    host-only, no device call."""
+    for setter in (L.lib.granite4_set_fp8_launch_mode, L.lib.granite4_set_attn_combine_mode):
+        prev = setter(1)
+        assert prev in (0, 1)
+        assert setter(2) == -1 and setter(-1) == -1
+        assert setter(0) == 1
+        assert setter(prev) == 0
+
+
 def test_row_table_host_matches_oracle_and_golden():
     G = np.load(ol.os.path.join(ol.ROOT, "tests", "golden", "golden.npz"))
     for s in range(G["pt_blocks"].shape[0]):
