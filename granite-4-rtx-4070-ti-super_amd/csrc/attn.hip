@@ -61,6 +61,11 @@ enum : int { kAttnPlain = 0, kAttnRopeAppend = 1, kAttnAppend = 2 };
 constexpr int kAttnWaves = 4;  // splits per workgroup, merged before the combine
 constexpr int kAttnSpinLimit = 1 << 20;  // polls before the combining block gives up
 constexpr int kVPitch = kHd + 16;  // LDS V row pitch (bf16): 288 B, rows 8 banks apart
+// Waves per SIMD the split kernel is compiled for: two for the quantised
+// pools (so a grid of more blocks than CUs keeps two blocks on each); the
+// bf16 kernel keeps one (its K and V tiles in flight take more registers
+// than half a SIMD's, and two would spill).
+constexpr int attn_waves_per_eu(int bits) { return bits == 16 ? 1 : 2; }
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -266,12 +271,16 @@ __device__ __forceinline__ unsigned long long f2_bits(float x, float y) {
 }
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// The split blocks [s0, used) whose partials make up row `row`: the blocks up
-// to the row's causal length (clamped to the arena), from the block holding
+// Causal length of row `row` (unclamped): its position + 1.
+__device__ __forceinline__ int combine_len(const AttnArgs& a, int row) {
+  return a.row_pos != nullptr ? a.row_pos[row] + 1
+                              : (a.d_pos != nullptr ? *a.d_pos : a.kv_base) + row + 1;
+}
+
+// The split blocks [s0, used) whose partials make up a row of causal length
+// len: the blocks up to len (clamped to the arena), from the block holding
 // the window's first key.
-__device__ __forceinline__ void combine_range(const AttnArgs& a, int row, int& s0, int& used) {
-  const int len = a.row_pos != nullptr ? a.row_pos[row] + 1
-                                       : (a.d_pos != nullptr ? *a.d_pos : a.kv_base) + row + 1;
+__device__ __forceinline__ void combine_range(const AttnArgs& a, int len, int& s0, int& used) {
   const int span = kAttnWaves * a.tps * kTile;  // positions per split block
   used = min((min(max(len, 0), a.stride) + span - 1) / span, a.nblk);
   s0 = a.window > 0 ? max(0, len - a.window) / span : 0;
@@ -283,22 +292,27 @@ __device__ __forceinline__ void combine_range(const AttnArgs& a, int row, int& s
 // and out = bf16(sum o_b w_b / L), both sums in block order. Lane j holds
 // block s0 + j's (m, l) (at most 64 blocks: kAttnMaxSplits / kAttnWaves);
 // each lane owns dims 2 lane and 2 lane + 1, whose partials are loaded 16
-// blocks at a time.
-__device__ void combine_wave(const AttnArgs& a, int row, int h) {
+// blocks at a time. (32 at a time, one round trip up to 32 blocks, measured
+// 0.1-0.3 us faster at 17 blocks and 0.2-0.5 us slower at 1-16 and 32.)
+//
+// len: the row's causal length (combine_len), known before the call: loaded
+// here, after the partials' loads, its wait would also wait for all of them
+// (memory loads complete in order), one more round trip.
+__device__ void combine_wave(const AttnArgs& a, int row, int h, int len) {
   static_assert(kAttnMaxSplits / kAttnWaves <= 64, "one (m, l) per lane");
   const int lane = threadIdx.x & 63;
   constexpr int kChunk = 16;
   const size_t rbase = (static_cast<size_t>(row) * a.Hq + h) * a.nblk;
   const float* prow = a.part_o + rbase * kHd + 2 * lane;
-  // The first chunk and the (m, l) loads go out with the row's length, not
-  // after it, from block 0; a window that starts the row's blocks later
+  // The first chunk and the (m, l) loads go out before the row's block range
+  // is known, from block 0; a window that starts the row's blocks later
   // loads them again from its first block.
   unsigned long long ov[kChunk];
 #pragma unroll
   for (int j = 0; j < kChunk; ++j) ov[j] = ld_dev_u64(prow + static_cast<size_t>(min(j, a.nblk - 1)) * kHd);
   unsigned long long mlb = ld_dev_u64(a.part_ml + rbase + min(lane, a.nblk - 1));
   int s0, used;
-  combine_range(a, row, s0, used);
+  combine_range(a, len, s0, used);
   if (s0 > 0) {
     const int sc = min(s0, a.nblk - 1), lc = max(min(used, a.nblk) - 1, sc);
 #pragma unroll
@@ -341,13 +355,16 @@ __device__ void combine_wave(const AttnArgs& a, int row, int h) {
 // the append's registers.
 // parameter so that the plain kernels carry none of its registers.
 template <int BITS, int GROUP, int MODE>
-__global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu(attn_waves_per_eu(BITS))))
+void attn_split_kernel(AttnArgs a) {
   constexpr bool kQuant = BITS != 16;
   constexpr int kNgrp = kQuant ? kHd / GROUP : 1;
   constexpr int kKb = k_row_bytes(BITS), kVb = v_row_bytes(BITS);
-  // Per wave: its V tile (reused for the end-of-block merge) and scales.
+  // Per wave: its V tile (reused for the end-of-block merge); each row's K and
+  // V scales sit in the row's padding (dims 128..143: 8 floats), so the
+  // block's LDS stays under half a CU's and two blocks fit on one.
   __shared__ __align__(16) uint16_t vl_all[kAttnWaves][kTile * kVPitch];
-  __shared__ float ksc_all[kAttnWaves][kTile * kNgrp], vsc_all[kAttnWaves][kTile * kNgrp];
+  static_assert(2 * kNgrp * sizeof(float) <= (kVPitch - kHd) * sizeof(uint16_t), "scales in the pad");
 
   // The kernel arguments of the prologue fetched together (one scalar-cache
   // miss instead of a chain of them before the position is even requested).
@@ -356,8 +373,10 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
                "s"(a.q), "s"(a.k), "s"(a.v), "s"(a.Hq));
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   uint16_t* vl = vl_all[wave];
-  float* ksc_l = ksc_all[wave];
-  float* vsc_l = vsc_all[wave];
+  // Scale slots of key `key`, group gi: floats 64 + gi (K) and 68 + gi (V) of its row.
+  float* const vlf = reinterpret_cast<float*>(vl);
+  auto ksc_at = [&](int key, int gi) -> float& { return vlf[key * (kVPitch / 2) + kHd / 2 + gi]; };
+  auto vsc_at = [&](int key, int gi) -> float& { return vlf[key * (kVPitch / 2) + kHd / 2 + 4 + gi]; };
   const int g = lane >> 4;   // lane group: keys 4 g + i of each 16-key block
   const int n = lane & 15;   // query column: row n / 4, head n % 4
   const int hkv = blockIdx.x, split = blockIdx.y * kAttnWaves + wave;
@@ -613,8 +632,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
     if constexpr (kQuant) {
 #pragma unroll
       for (int gi = 0; gi < kNgrp; ++gi) {
-        ksc_l[lane * kNgrp + gi] = prow >= 0 ? ksr[gi] : 0.0f;
-        vsc_l[lane * kNgrp + gi] = prow >= 0 ? vsr[gi] : 0.0f;
+        ksc_at(lane, gi) = prow >= 0 ? ksr[gi] : 0.0f;
+        vsc_at(lane, gi) = prow >= 0 ? vsr[gi] : 0.0f;
       }
     }
     wave_lds_sync();  // V tile and scales in LDS
@@ -631,7 +650,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
         for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s], qb[s], acc, 0, 0, 0);
         if constexpr (kQuant) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) acc[i] = acc[i] * ksc_l[(16 * mb + 4 * g + i) * kNgrp];
+          for (int i = 0; i < 4; ++i) acc[i] = acc[i] * ksc_at(16 * mb + 4 * g + i, 0);
         }
       } else {
         constexpr int kSteps = GROUP / 32;
@@ -642,7 +661,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
           for (int s = gi * kSteps; s < (gi + 1) * kSteps; ++s)
             part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s], qb[s], part, 0, 0, 0);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) acc[i] += part[i] * ksc_l[(16 * mb + 4 * g + i) * kNgrp + gi];
+          for (int i = 0; i < 4; ++i) acc[i] += part[i] * ksc_at(16 * mb + 4 * g + i, gi);
         }
       }
       // logit = bf16(scale * dot), two per hardware conversion (equal to the
@@ -689,7 +708,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const int mb = 2 * s + (j >> 2), i = j & 3;
-          const float sc = kQuant ? vsc_l[(16 * mb + 4 * g + i) * kNgrp + gi] : 1.0f;
+          const float sc = kQuant ? vsc_at(16 * mb + 4 * g + i, gi) : 1.0f;
           pv[j] = e[mb][i] * sc;
         }
         pb[gi] = as_bf16x8(pack_bf16_hw(pv[0], pv[1]), pack_bf16_hw(pv[2], pv[3]),
@@ -820,7 +839,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
                                    2 * lane) = 0x7fc07fc0u;
     return;
   }
-  for (int rr = 0; rr < nr; ++rr) combine_wave(a, r0 + rr, hkv * kGq + wave);
+  for (int rr = 0; rr < nr; ++rr)
+    combine_wave(a, r0 + rr, hkv * kGq + wave, a.row_pos != nullptr ? row_pos0 + 1 : base + r0 + rr + 1);
 }
 
 // The combine as its own launch (the split launch without tags): one
@@ -831,7 +851,8 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(AttnArgs 
   // The arguments fetched in one scalar round trip.
   asm volatile("" ::"s"(a.d_pos), "s"(a.row_pos), "s"(a.part_ml), "s"(a.part_o), "s"(a.out),
                "s"(a.nblk), "s"(a.tps), "s"(a.stride), "s"(a.window), "s"(a.kv_base), "s"(a.Hq));
-  combine_wave(a, blockIdx.y, blockIdx.x * kGq + (threadIdx.x >> 6));
+  const int len = combine_len(a, blockIdx.y);  // loaded before the partials
+  combine_wave(a, blockIdx.y, blockIdx.x * kGq + (threadIdx.x >> 6), len);
 }
 
 // ---------------------------------------------------------------------------
