@@ -61,11 +61,10 @@ enum : int { kAttnPlain = 0, kAttnRopeAppend = 1, kAttnAppend = 2 };
 constexpr int kAttnWaves = 4;  // splits per workgroup, merged before the combine
 constexpr int kAttnSpinLimit = 1 << 20;  // polls before the combining block gives up
 constexpr int kVPitch = kHd + 16;  // LDS V row pitch (bf16): 288 B, rows 8 banks apart
-// Waves per SIMD the split kernel is compiled for: two for the quantised
-// pools (so a grid of more blocks than CUs keeps two blocks on each); the
-// bf16 kernel keeps one (its K and V tiles in flight take more registers
-// than half a SIMD's, and two would spill).
-constexpr int attn_waves_per_eu(int bits) { return bits == 16 ? 1 : 2; }
+// Waves per SIMD the split kernel is compiled for: two (so a grid of more
+// blocks than CUs keeps two blocks on each), except the bf16 decode-append
+// forms, whose appended row's registers on top of the K tile would spill.
+constexpr int attn_waves_per_eu(int bits, int mode) { return bits == 16 && mode != 0 ? 1 : 2; }
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -205,6 +204,42 @@ __device__ __forceinline__ void v_load(const uint8_t* vbase, int prow,
     const int pr = __shfl(prow, key);
     // Unconditional (row 0 for keys without a row); v_store zeroes those.
     raw[i] = *reinterpret_cast<const u32x4_t*>(vbase + static_cast<size_t>(pr >= 0 ? pr : 0) * VS::kRowB + 16 * c);
+  }
+}
+
+// bf16 V tiles go from global memory straight to LDS (global_load_lds, 16
+// bytes per lane): no registers hold them, so the bf16 kernel fits two waves
+// per SIMD. The tile is 64 rows of 256 bytes without padding; the 16-byte
+// chunk c of row r sits at chunk c ^ 2 (r & 7), so that the transposed reads
+// of 16 consecutive rows (32 bytes each) spread over all 64 banks (two
+// passes, as with the padded layout). Load i writes rows 4 i .. 4 i + 3.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+__device__ __forceinline__ int v_swz(int row) { return 2 * (row & 7); }
+__device__ __forceinline__ void v_dma_bf16(const uint8_t* vbase, int prow, uint16_t* vl) {
+  const int lane = threadIdx.x & 63;
+  uint8_t* dst = reinterpret_cast<uint8_t*>(vl);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int row = 4 * i + (lane >> 4), c = (lane & 15) ^ v_swz(row);
+    const int pr = __shfl(prow, row);
+    // Unconditional (row 0 for keys without a row); v_fix_bf16 zeroes those.
+    __builtin_amdgcn_global_load_lds(vbase + static_cast<size_t>(pr >= 0 ? pr : 0) * 256 + 16 * c,
+                                     (lds_ptr_t)(dst + 1024 * i), 16, 0, 0);
+  }
+}
+// After the loads have landed: rows without an arena row become 0, and row
+// jnew (>= 0: the key appended in this launch) takes the bytes at src.
+__device__ __forceinline__ void v_fix_bf16(uint16_t* vl, unsigned long long valid, int jnew,
+                                           const uint8_t* src) {
+  if (valid == ~0ull && jnew < 0) return;
+  const int lane = threadIdx.x & 63;
+  uint8_t* dst = reinterpret_cast<uint8_t*>(vl);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int row = 4 * i + (lane >> 4), c = (lane & 15) ^ v_swz(row);
+    u32x4_t* d = reinterpret_cast<u32x4_t*>(dst + 1024 * i + 16 * lane);
+    if (row == jnew) *d = *reinterpret_cast<const u32x4_t*>(src + 16 * c);
+    else if (!((valid >> row) & 1ull)) *d = u32x4_t{0u, 0u, 0u, 0u};
   }
 }
 
@@ -355,7 +390,7 @@ __device__ void combine_wave(const AttnArgs& a, int row, int h, int len) {
 // the append's registers.
 // parameter so that the plain kernels carry none of its registers.
 template <int BITS, int GROUP, int MODE>
-__global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu(attn_waves_per_eu(BITS))))
+__global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu(attn_waves_per_eu(BITS, MODE))))
 void attn_split_kernel(AttnArgs a) {
   constexpr bool kQuant = BITS != 16;
   constexpr int kNgrp = kQuant ? kHd / GROUP : 1;
@@ -545,8 +580,11 @@ void attn_split_kernel(AttnArgs a) {
         *reinterpret_cast<float4*>(nsn + 4) = *reinterpret_cast<const float4*>(sp + 4);
       }
     }
+    constexpr bool kVDma = BITS == 16;  // V straight to LDS
     u32x4_t vraw[VStage<BITS>::kSteps];
-    v_load<BITS>(vbase, prow, vraw);
+    if constexpr (kVDma) v_dma_bf16(vbase, prow, vl);
+    else v_load<BITS>(vbase, prow, vraw);
+    int vnew = -1;  // the appended key's row in the tile (its V from LDS)
     u32x4_t kraw[4][4];
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) {
@@ -610,11 +648,15 @@ void attn_split_kernel(AttnArgs a) {
             }
           }
         }
-        using VS = VStage<BITS>;
+        if constexpr (kVDma) {
+          vnew = j;
+        } else {
+          using VS = VStage<BITS>;
 #pragma unroll
-        for (int i = 0; i < VS::kSteps; ++i) {
-          const int key = i * (64 / VS::kChunks) + lane / VS::kChunks, c = lane % VS::kChunks;
-          if (key == j) vraw[i] = *reinterpret_cast<const u32x4_t*>(mir_v[wave] + 16 * c);
+          for (int i = 0; i < VS::kSteps; ++i) {
+            const int key = i * (64 / VS::kChunks) + lane / VS::kChunks, c = lane % VS::kChunks;
+            if (key == j) vraw[i] = *reinterpret_cast<const u32x4_t*>(mir_v[wave] + 16 * c);
+          }
         }
         if constexpr (kQuant) {
           if (lane == j) {
@@ -628,7 +670,14 @@ void attn_split_kernel(AttnArgs a) {
       }
     }
     const unsigned long long kvalid = __ballot(prow >= 0);
-    v_store<BITS>(vraw, vl, kvalid);
+    if constexpr (kVDma) {
+      // Every load of the tile has landed (the K loads, issued after the V
+      // tile's, are needed next anyway); then the tile's fix-ups.
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      v_fix_bf16(vl, kvalid, vnew, mir_v[wave]);
+    } else {
+      v_store<BITS>(vraw, vl, kvalid);
+    }
     if constexpr (kQuant) {
 #pragma unroll
       for (int gi = 0; gi < kNgrp; ++gi) {
@@ -715,12 +764,16 @@ void attn_split_kernel(AttnArgs a) {
                            pack_bf16_hw(pv[4], pv[5]), pack_bf16_hw(pv[6], pv[7]));
       }
       const int kk = n >> 2, dd = 4 * (n & 3);
-      const uint16_t* r1 = vl + (32 * s + 4 * g + kk) * kVPitch + dd;
-      const uint16_t* r2 = r1 + 16 * kVPitch;
+      const int vrow = 32 * s + 4 * g + kk;  // and vrow + 16 (same swizzle)
+      const uint16_t* r1 = vl + vrow * (kVDma ? kHd : kVPitch) + dd;
+      const uint16_t* r2 = r1 + 16 * (kVDma ? kHd : kVPitch);
+      const int vt = vrow & 7;
 #pragma unroll
       for (int nb = 0; nb < 8; ++nb) {
-        const u32x2_t lo = lds_read_tr(r1 + 16 * nb);
-        const u32x2_t hi = lds_read_tr(r2 + 16 * nb);
+        // bf16 (swizzled): dims 16 nb + dd.. sit in chunk pair nb ^ (row & 7).
+        const int co = kVDma ? 16 * (nb ^ vt) : 16 * nb;
+        const u32x2_t lo = lds_read_tr(r1 + co);
+        const u32x2_t hi = lds_read_tr(r2 + co);
         const bf16x8_t va = as_bf16x8(lo.x, lo.y, hi.x, hi.y);
         const int gi = kQuant ? (16 * nb) / GROUP : 0;
         o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[gi], o[nb], 0, 0, 0);
