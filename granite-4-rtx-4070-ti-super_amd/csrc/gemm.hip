@@ -182,6 +182,17 @@ __device__ __forceinline__ v4u lds_read16(uint32_t addr) {
   return v;
 }
 __device__ __forceinline__ void lds_reads_done() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// Waits until at most N of the wave's LDS reads are still in flight.
+template <int N>
+__device__ __forceinline__ void lds_reads_left() {
+  if constexpr (N == 0) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  else if constexpr (N == 1) asm volatile("s_waitcnt lgkmcnt(1)" ::: "memory");
+  else if constexpr (N == 2) asm volatile("s_waitcnt lgkmcnt(2)" ::: "memory");
+  else if constexpr (N == 3) asm volatile("s_waitcnt lgkmcnt(3)" ::: "memory");
+  else if constexpr (N == 4) asm volatile("s_waitcnt lgkmcnt(4)" ::: "memory");
+  else if constexpr (N == 6) asm volatile("s_waitcnt lgkmcnt(6)" ::: "memory");
+  else static_assert(N < 0, "add the count");
+}
 
 // Fragment of tile row r of a region at LDS address `region`: chunks
 // 2 * (lane / 16) and + 1 of the row, as two 16-byte reads.
@@ -416,23 +427,32 @@ __global__ __launch_bounds__(256 * KS) void gemm_fp8_kernel(GemmArgs a) {
       if (KS == 2 && kt >= kn) continue;  // half 1's idle last step (odd ktiles)
       const uint32_t st = lds_addr(sbase + (kt % ST) * kStage);
       v4u ax[4], ay[4], bx[kNI], by[kNI];
-#pragma unroll
-      for (int mi = 0; mi < 4; ++mi) frag_issue(st, wm * 64 + mi * 16 + fr, lane, ax[mi], ay[mi]);
+      // B's fragments first, then A's row blocks in order: row block mi's
+      // MFMAs start once its two reads (and B's) have landed, while the
+      // later blocks' reads are still in flight (LDS reads complete in order).
 #pragma unroll
       for (int ni = 0; ni < kNI; ++ni)
         frag_issue(st + kGBM * kGBK, b_row<EPI, TN>(wn, ni) + fr, lane, bx[ni], by[ni]);
-      lds_reads_done();
-      // The fragments pass through the wait: no use can move above it.
 #pragma unroll
-      for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(ax[j]), "+v"(ay[j]));
+      for (int mi = 0; mi < 4; ++mi) frag_issue(st, wm * 64 + mi * 16 + fr, lane, ax[mi], ay[mi]);
 #pragma unroll
-      for (int j = 0; j < kNI; ++j) asm volatile("" : "+v"(bx[j]), "+v"(by[j]));
+      for (int mi = 0; mi < 4; ++mi) {
+        if (mi == 0) lds_reads_left<6>();
+        else if (mi == 1) lds_reads_left<4>();
+        else if (mi == 2) lds_reads_left<2>();
+        else lds_reads_left<0>();
+        // The fragments pass through the wait: no use can move above it.
+        asm volatile("" : "+v"(ax[mi]), "+v"(ay[mi]));
+        if (mi == 0) {
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
+          for (int j = 0; j < kNI; ++j) asm volatile("" : "+v"(bx[j]), "+v"(by[j]));
+        }
 #pragma unroll
         for (int ni = 0; ni < kNI; ++ni)
           acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
               frag_of(ax[mi], ay[mi]), frag_of(bx[ni], by[ni]), acc[mi][ni], 0, 0, 0, 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);  // keep the block's MFMAs ahead of the next wait
+      }
     }
 
     if constexpr (KS == 2) {
@@ -530,7 +550,7 @@ __device__ __forceinline__ bf16x8_g fp8x8_to_bf16(uint2 q) {
   return __builtin_bit_cast(bf16x8_g, u);
 }
 
-template <int EPI>
+template <int EPI, bool kLateRes = false>
 __global__ __launch_bounds__(256) void gemm_bf16w_kernel(GemmArgs a) {
   __shared__ __align__(16) uint8_t s_tile[2 * kBwStage];
   const int lane = threadIdx.x & 63;
@@ -556,8 +576,14 @@ __global__ __launch_bounds__(256) void gemm_bf16w_kernel(GemmArgs a) {
       for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     const int col0 = tn * kGBN + wn * 64;
     const int n_end = a.N;
+    // The residual of the tile's outputs: loaded at the tile's start (its wait
+    // overlaps the first stage's), or, kLateRes, after the K loop. Held across
+    // the loop its 32 registers leave one wave per SIMD: with more tiles than
+    // CUs (T=8192 down + residual: 1437 -> 1150 us) the second wave is worth
+    // more than the round trip; with one tile per workgroup (T=512: 175 vs
+    // 189 us) it is not.
     uint4 res[EPI == kEpiResidual ? 2 * kIters : 1];
-    if (EPI == kEpiResidual) {
+    const auto load_res = [&] {
 #pragma unroll
       for (int j = 0; j < 2 * kIters; ++j) {
         const int h = j / kIters, it = j % kIters;
@@ -567,7 +593,8 @@ __global__ __launch_bounds__(256) void gemm_bf16w_kernel(GemmArgs a) {
                      ? *reinterpret_cast<const uint4*>(a.ep.residual + static_cast<size_t>(m) * a.ep.ldc + n)
                      : make_uint4(0u, 0u, 0u, 0u);
       }
-    }
+    };
+    if (EPI == kEpiResidual && !kLateRes) load_res();
 
     __syncthreads();  // the previous tile's readers are done with both buffers
     bw_stage_issue<EPI>(a, m0, tn, 0, s_tile);
@@ -587,33 +614,44 @@ __global__ __launch_bounds__(256) void gemm_bf16w_kernel(GemmArgs a) {
         const int ca = 4 * s + (lane >> 4);            // A chunk: elements 32 s + 8 (lane / 16)
         const int cw = 2 * s + (lane >> 5);            // W chunk: bytes 32 s + 8 (lane / 16)
         const uint32_t wh = 8u * static_cast<uint32_t>((lane >> 4) & 1);
-#pragma unroll
-        for (int mi = 0; mi < 4; ++mi) {
-          const int r = wm * 64 + mi * 16 + fr;
-          ax[mi] = lds_read16(st + static_cast<uint32_t>(r * kBwARow) +
-                              16u * static_cast<uint32_t>(ca ^ bw_chunk_swz(r)));
-        }
+        // W's fragments first, then A's row blocks in order: row block mi's
+        // MFMAs start once its read (and W's) have landed, while the later
+        // blocks' reads are still in flight (LDS reads complete in order).
 #pragma unroll
         for (int ni = 0; ni < 4; ++ni) {
           const int r = wn * 64 + ni * 16 + fr;
           bq[ni] = lds_read8(sw + static_cast<uint32_t>(r * kBwWRow) +
                              16u * static_cast<uint32_t>(cw ^ ((r >> 1) & 3)) + wh);
         }
-        lds_reads_done();
-#pragma unroll
-        for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(ax[j]), "+v"(bq[j]));
-        bf16x8_g bf[4];
-#pragma unroll
-        for (int ni = 0; ni < 4; ++ni) bf[ni] = fp8x8_to_bf16(bq[ni]);
 #pragma unroll
         for (int mi = 0; mi < 4; ++mi) {
+          const int r = wm * 64 + mi * 16 + fr;
+          ax[mi] = lds_read16(st + static_cast<uint32_t>(r * kBwARow) +
+                              16u * static_cast<uint32_t>(ca ^ bw_chunk_swz(r)));
+        }
+        bf16x8_g bf[4];
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi) {
+          if (mi == 0) lds_reads_left<3>();
+          else if (mi == 1) lds_reads_left<2>();
+          else if (mi == 2) lds_reads_left<1>();
+          else lds_reads_left<0>();
+          asm volatile("" : "+v"(ax[mi]));
+          if (mi == 0) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(bq[j]));
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) bf[ni] = fp8x8_to_bf16(bq[ni]);
+          }
           const bf16x8_g af = __builtin_bit_cast(bf16x8_g, ax[mi]);
 #pragma unroll
           for (int ni = 0; ni < 4; ++ni)
             acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bf[ni], acc[mi][ni], 0, 0, 0);
+          __builtin_amdgcn_sched_barrier(0);  // keep the block's MFMAs ahead of the next wait
         }
       }
     }
+    if (EPI == kEpiResidual && kLateRes) load_res();
     tile_epilogue<EPI, kIters, kWCols>(a, acc, 1.0f, s_tile, m0, col0, n_end, res, amax);
   }
 }
@@ -781,11 +819,18 @@ int granite4_prefill_gemm(int out, const uint16_t* A, int lda, const uint8_t* W,
                          grid(reinterpret_cast<const void*>(gemm_bf16w_kernel<kEpiF32>)), 256, 0, st,
                          a);
       break;
-    default:
-      hipLaunchKernelGGL(gemm_bf16w_kernel<kEpiResidual>,
-                         grid(reinterpret_cast<const void*>(gemm_bf16w_kernel<kEpiResidual>)), 256,
-                         0, st, a);
+    default: {
+      // More tiles than the early-residual form keeps resident: the late form.
+      const void* early = reinterpret_cast<const void*>(gemm_bf16w_kernel<kEpiResidual, false>);
+      const int resident = resident_blocks(early, 256);
+      if (resident > 0 && tiles > resident) {
+        const void* late = reinterpret_cast<const void*>(gemm_bf16w_kernel<kEpiResidual, true>);
+        hipLaunchKernelGGL((gemm_bf16w_kernel<kEpiResidual, true>), grid(late), 256, 0, st, a);
+      } else {
+        hipLaunchKernelGGL((gemm_bf16w_kernel<kEpiResidual, false>), grid(early), 256, 0, st, a);
+      }
       break;
+    }
   }
   return launch_status("granite4_prefill_gemm");
 }
