@@ -191,6 +191,10 @@ __device__ __forceinline__ void lds_reads_left() {
   else if constexpr (N == 3) asm volatile("s_waitcnt lgkmcnt(3)" ::: "memory");
   else if constexpr (N == 4) asm volatile("s_waitcnt lgkmcnt(4)" ::: "memory");
   else if constexpr (N == 6) asm volatile("s_waitcnt lgkmcnt(6)" ::: "memory");
+  else if constexpr (N == 8) asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
+  else if constexpr (N == 9) asm volatile("s_waitcnt lgkmcnt(9)" ::: "memory");
+  else if constexpr (N == 10) asm volatile("s_waitcnt lgkmcnt(10)" ::: "memory");
+  else if constexpr (N == 11) asm volatile("s_waitcnt lgkmcnt(11)" ::: "memory");
   else static_assert(N < 0, "add the count");
 }
 
@@ -551,7 +555,7 @@ __device__ __forceinline__ bf16x8_g fp8x8_to_bf16(uint2 q) {
 }
 
 template <int EPI, bool kLateRes = false>
-__global__ __launch_bounds__(256) void gemm_bf16w_kernel(GemmArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_bf16w_kernel(GemmArgs a) {
   __shared__ __align__(16) uint8_t s_tile[2 * kBwStage];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -606,44 +610,57 @@ __global__ __launch_bounds__(256) void gemm_bf16w_kernel(GemmArgs a) {
       const uint32_t st = lds_addr(s_tile + (kt & 1) * kBwStage);
       const uint32_t sw = st + kGBM * kBwARow;
       const int halves = a.K - kt * kBwK >= kBwK ? 2 : 1;  // wave-uniform
+      // Both 32-element halves' reads go out first (W's fragments, then A's
+      // row blocks, per half), and each row block's MFMAs start once its
+      // reads have landed: the second half's reads overlap the first half's
+      // MFMAs (LDS reads complete in order).
+      v4u ax[2][4];
+      uint2 bq[2][4];
+      const uint32_t wh = 8u * static_cast<uint32_t>((lane >> 4) & 1);
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         if (s >= halves) break;
-        v4u ax[4];
-        uint2 bq[4];
         const int ca = 4 * s + (lane >> 4);            // A chunk: elements 32 s + 8 (lane / 16)
         const int cw = 2 * s + (lane >> 5);            // W chunk: bytes 32 s + 8 (lane / 16)
-        const uint32_t wh = 8u * static_cast<uint32_t>((lane >> 4) & 1);
-        // W's fragments first, then A's row blocks in order: row block mi's
-        // MFMAs start once its read (and W's) have landed, while the later
-        // blocks' reads are still in flight (LDS reads complete in order).
 #pragma unroll
         for (int ni = 0; ni < 4; ++ni) {
           const int r = wn * 64 + ni * 16 + fr;
-          bq[ni] = lds_read8(sw + static_cast<uint32_t>(r * kBwWRow) +
-                             16u * static_cast<uint32_t>(cw ^ ((r >> 1) & 3)) + wh);
+          bq[s][ni] = lds_read8(sw + static_cast<uint32_t>(r * kBwWRow) +
+                                16u * static_cast<uint32_t>(cw ^ ((r >> 1) & 3)) + wh);
         }
 #pragma unroll
         for (int mi = 0; mi < 4; ++mi) {
           const int r = wm * 64 + mi * 16 + fr;
-          ax[mi] = lds_read16(st + static_cast<uint32_t>(r * kBwARow) +
-                              16u * static_cast<uint32_t>(ca ^ bw_chunk_swz(r)));
+          ax[s][mi] = lds_read16(st + static_cast<uint32_t>(r * kBwARow) +
+                                 16u * static_cast<uint32_t>(ca ^ bw_chunk_swz(r)));
         }
+      }
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        if (s >= halves) break;
+        const bool more = s == 0 && halves == 2;  // the second half's 8 reads are behind
         bf16x8_g bf[4];
 #pragma unroll
         for (int mi = 0; mi < 4; ++mi) {
-          if (mi == 0) lds_reads_left<3>();
-          else if (mi == 1) lds_reads_left<2>();
-          else if (mi == 2) lds_reads_left<1>();
-          else lds_reads_left<0>();
-          asm volatile("" : "+v"(ax[mi]));
+          if (more) {
+            if (mi == 0) lds_reads_left<11>();
+            else if (mi == 1) lds_reads_left<10>();
+            else if (mi == 2) lds_reads_left<9>();
+            else lds_reads_left<8>();
+          } else {
+            if (mi == 0) lds_reads_left<3>();
+            else if (mi == 1) lds_reads_left<2>();
+            else if (mi == 2) lds_reads_left<1>();
+            else lds_reads_left<0>();
+          }
+          asm volatile("" : "+v"(ax[s][mi]));
           if (mi == 0) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(bq[j]));
+            for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(bq[s][j]));
 #pragma unroll
-            for (int ni = 0; ni < 4; ++ni) bf[ni] = fp8x8_to_bf16(bq[ni]);
+            for (int ni = 0; ni < 4; ++ni) bf[ni] = fp8x8_to_bf16(bq[s][ni]);
           }
-          const bf16x8_g af = __builtin_bit_cast(bf16x8_g, ax[mi]);
+          const bf16x8_g af = __builtin_bit_cast(bf16x8_g, ax[s][mi]);
 #pragma unroll
           for (int ni = 0; ni < 4; ++ni)
             acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bf[ni], acc[mi][ni], 0, 0, 0);
