@@ -227,19 +227,16 @@ __device__ __forceinline__ void v_dma_bf16(const uint8_t* vbase, int prow, uint1
                                      (lds_ptr_t)(dst + 1024 * i), 16, 0, 0);
   }
 }
-// After the loads have landed: rows without an arena row become 0, and row
-// jnew (>= 0: the key appended in this launch) takes the bytes at src.
-__device__ __forceinline__ void v_fix_bf16(uint16_t* vl, unsigned long long valid, int jnew,
-                                           const uint8_t* src) {
-  if (valid == ~0ull && jnew < 0) return;
+// After the loads have landed: rows without an arena row become 0.
+__device__ __forceinline__ void v_fix_bf16(uint16_t* vl, unsigned long long valid) {
+  if (valid == ~0ull) return;
   const int lane = threadIdx.x & 63;
   uint8_t* dst = reinterpret_cast<uint8_t*>(vl);
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const int row = 4 * i + (lane >> 4), c = (lane & 15) ^ v_swz(row);
-    u32x4_t* d = reinterpret_cast<u32x4_t*>(dst + 1024 * i + 16 * lane);
-    if (row == jnew) *d = *reinterpret_cast<const u32x4_t*>(src + 16 * c);
-    else if (!((valid >> row) & 1ull)) *d = u32x4_t{0u, 0u, 0u, 0u};
+    const int row = 4 * i + (lane >> 4);
+    if (!((valid >> row) & 1ull))
+      *reinterpret_cast<u32x4_t*>(dst + 1024 * i + 16 * lane) = u32x4_t{0u, 0u, 0u, 0u};
   }
 }
 
@@ -588,7 +585,6 @@ void attn_split_kernel(AttnArgs a) {
     u32x4_t vraw[VStage<BITS>::kSteps];
     if constexpr (kVDma) v_dma_bf16(vbase, prow, vl);
     else v_load<BITS>(vbase, prow, vraw);
-    int vnew = -1;  // the appended key's row in the tile (its V from LDS)
     u32x4_t kraw[4][4];
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) {
@@ -652,9 +648,7 @@ void attn_split_kernel(AttnArgs a) {
             }
           }
         }
-        if constexpr (kVDma) {
-          vnew = j;
-        } else {
+        if constexpr (!kVDma) {  // the append forms stage V through registers
           using VS = VStage<BITS>;
 #pragma unroll
           for (int i = 0; i < VS::kSteps; ++i) {
@@ -678,7 +672,7 @@ void attn_split_kernel(AttnArgs a) {
       // Every load of the tile has landed (the K loads, issued after the V
       // tile's, are needed next anyway); then the tile's fix-ups.
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      v_fix_bf16(vl, kvalid, vnew, mir_v[wave]);
+      v_fix_bf16(vl, kvalid);
     } else {
       v_store<BITS>(vraw, vl, kvalid);
     }
