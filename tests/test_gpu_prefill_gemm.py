@@ -103,10 +103,13 @@ def test_prefill_gemm_f32_out(M, N, K):
     assert np.all(err <= bound(A, W, sc, None) + np.abs(y) * 2.0 ** -23)
 
 
-def test_prefill_gemm_residual_in_place():
+# 200 x 256: 4 tiles, the residual prefetched at each tile's start; 2100 x
+# 4096: 544 tiles, more than the 512 workgroups resident at two per CU, so the
+# form that loads the residual after the K loop runs.
+@pytest.mark.parametrize("M,N,K", [(200, 256, 512), (2100, 4096, 128)])
+def test_prefill_gemm_residual_in_place(M, N, K):
     """kResidual, the O / down projection: hidden = bf16(hidden + rs * y), in place."""
-    note("prefill_gemm residual")
-    M, N, K = 200, 256, 512
+    note(f"prefill_gemm residual M={M} N={N} K={K}")
     A, W = inputs(M, N, K, 0xA1)
     res = ol.normal_bf16(0xA3, 0.0, 1.0, M * N).reshape(M, N)
     sc = (0.02, 0.02, 0.02)
