@@ -122,6 +122,16 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(uint32_t a, uint32_t b, uint32_t c
 __device__ __forceinline__ uint32_t int_pair_bf16(int a, int b) {
   return pack_bf16_hw(static_cast<float>(a), static_cast<float>(b));
 }
+// The int4 codes at bits [b, b + 4) and [b + 4, b + 8) of x, as their
+// values code - 8, in bf16: the code xor 8 read as a signed 4-bit field is
+// code - 8, so each value is one sign-extending field extract (xs = x ^
+// 0x88888888, once per word) instead of an extract and a subtraction.
+__device__ __forceinline__ int sfield4(uint32_t xs, int b) {
+  return static_cast<int>(xs << (28 - b)) >> 28;
+}
+__device__ __forceinline__ uint32_t int4_pair_bf16(uint32_t xs, int b) {
+  return int_pair_bf16(sfield4(xs, b), sfield4(xs, b + 4));
+}
 
 // Row bytes of the K / V caches per format.
 __host__ __device__ constexpr int k_row_bytes(int bits) {
@@ -165,6 +175,10 @@ __device__ __forceinline__ bf16x8_t k_raw_bf16(const u32x4_t& r) {
       w[e] = int_pair_bf16(static_cast<int8_t>(x >> sh), static_cast<int8_t>(x >> (sh + 8)));
     }
     return as_bf16x8(w[0], w[1], w[2], w[3]);
+  } else if constexpr (BITS == 4) {
+    const uint32_t xs = r.x ^ 0x88888888u;
+    return as_bf16x8(int4_pair_bf16(xs, 0), int4_pair_bf16(xs, 8), int4_pair_bf16(xs, 16),
+                     int4_pair_bf16(xs, 24));
   } else {
     constexpr int off = BITS == 5 ? 16 : 8;
     uint32_t w[4];
@@ -270,8 +284,7 @@ __device__ __forceinline__ void v_store(const u32x4_t (&raw)[VStage<BITS>::kStep
       for (int e = 0; e < 16; ++e) {
         const uint32_t x = u[e >> 2];
         const int b = 8 * (e & 3);
-        w[e] = int_pair_bf16(static_cast<int>((x >> b) & 0xFu) - 8,
-                             static_cast<int>((x >> (b + 4)) & 0xFu) - 8);
+        w[e] = int4_pair_bf16(x ^ 0x88888888u, b);
       }
       uint16_t* dst = vl + key * kVPitch + 32 * c;
 #pragma unroll
@@ -1097,8 +1110,7 @@ __device__ __forceinline__ void prefill_store(const PrefillRaw<BITS, GROUP, W>& 
       for (int e = 0; e < 16; ++e) {
         const uint32_t x = u[e >> 2];
         const int b = 8 * (e & 3);
-        w[e] = int_pair_bf16(static_cast<int>((x >> b) & 0xFu) - 8,
-                             static_cast<int>((x >> (b + 4)) & 0xFu) - 8);
+        w[e] = int4_pair_bf16(x ^ 0x88888888u, b);
       }
       uint16_t* dst = vs + key * kVPitch + 32 * c;
 #pragma unroll
