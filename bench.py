@@ -33,6 +33,7 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 H, I, HQ, HK, D = 4096, 12800, 32, 8, 128
 VOCAB = 100352
 PEAK_GBS = 8000.0  # MI355X HBM3E
+ROTATE_BYTES = 320e6  # distinct bytes per timed replay: more than the 256 MB Infinity Cache
 
 # Algorithmic bytes per token (BASELINE.md section 3 / the survey's 8(d)).
 B_EMBED = 4 * H + 4
@@ -198,21 +199,36 @@ def main():
         op_swiglu_fp8(s)
         op_rope(s)
 
-    def measure_ops(T, nsets, bits, group, pos0, rope_key, steps, warmup):
+    def rotation(b, steps):
+        """Input sets for an op of b bytes per call such that one replay of
+        the timed graph touches more than ROTATE_BYTES distinct bytes of the
+        op's own buffers (more than the 256 MB Infinity Cache holds), and
+        the graph's call count: every set once per replay, at least `steps`
+        calls."""
+        n = max(2, -(-int(ROTATE_BYTES) // int(b)))
+        return n, n * max(1, -(-steps // n))
+
+    def measure_ops(T, bits, group, pos0, rope_key, steps, warmup):
+        ops = (("embed", op_embed, B_EMBED * T),
+               ("add_rmsnorm_fp8", op_norm_fp8, B_NORM_FP8 * T + per_launch_extra("norm_fp8")),
+               ("swiglu_fp8", op_swiglu_fp8, B_SWIGLU_FP8 * T + per_launch_extra("swiglu_fp8")),
+               (f"rope_append_{rope_key}", op_rope, B_ROPE[rope_key] * T))
+        step_bytes = sum(b for _, _, b in ops)
+        nsets = max(rotation(b, steps)[0] for _, _, b in ops + (("step", None, step_bytes),))
         sets = prefill_sets(T, nsets, bits, group, pos0)
         out = {}
-        for name, fn, b in (("embed", op_embed, B_EMBED * T),
-                            ("add_rmsnorm_fp8", op_norm_fp8, B_NORM_FP8 * T + per_launch_extra("norm_fp8")),
-                            ("swiglu_fp8", op_swiglu_fp8, B_SWIGLU_FP8 * T + per_launch_extra("swiglu_fp8")),
-                            (f"rope_append_{rope_key}", op_rope, B_ROPE[rope_key] * T)):
-            ms = timed(fn, steps, warmup, sets)
+        for name, fn, b in ops:
+            n, calls = rotation(b, steps)
+            ms = timed(fn, calls, warmup, sets[:n])
             gbs = b / (ms * 1e-3) / 1e9
             out[name] = {"us": round(ms * 1e3, 3), "bytes": int(b), "GBps": round(gbs, 1),
-                         "frac_peak": round(gbs / PEAK_GBS, 4)}
-        step_bytes = sum(v["bytes"] for v in out.values())
-        ms = timed(op_step, steps, warmup, sets)
+                         "frac_peak": round(gbs / PEAK_GBS, 4), "sets": n,
+                         "rotated_MB": round(n * b / 1e6, 1)}
+        n, calls = rotation(step_bytes, steps)
+        ms = timed(op_step, calls, warmup, sets[:n])
         out["step"] = {"us": round(ms * 1e3, 3), "bytes": int(step_bytes),
-                       "GBps": round(step_bytes / (ms * 1e-3) / 1e9, 1)}
+                       "GBps": round(step_bytes / (ms * 1e-3) / 1e9, 1), "sets": n,
+                       "rotated_MB": round(n * step_bytes / 1e6, 1)}
         del sets
         torch.cuda.empty_cache()
         return out
@@ -221,9 +237,9 @@ def main():
 
     if args.only:
         if args.only == "t512":
-            r = measure_ops(512, 8, 8, 128, 0, 8, args.steps, args.warmup)
+            r = measure_ops(512, 8, 128, 0, 8, args.steps, args.warmup)
         elif args.only == "t8192":
-            r = measure_ops(8192, 2, 5, 32, 57344, "k5v4g32", args.steps, args.warmup)
+            r = measure_ops(8192, 5, 32, 57344, "k5v4g32", args.steps, args.warmup)
         elif args.only == "probe":
             r = bench_probe(torch, L, stream, timed)
         elif args.only == "t1":
@@ -231,8 +247,7 @@ def main():
         elif args.only == "floor":
             r = bench_floor(torch, L, timed, work)
         elif args.only == "tN":
-            r = measure_ops(args.T, max(2, min(8, 4096 // args.T)), 8, 128, 0, 8, args.steps,
-                            args.warmup)
+            r = measure_ops(args.T, 8, 128, 0, 8, args.steps, args.warmup)
         elif args.only == "decode_gemv":
             r = bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream)
         elif args.only == "decode":
@@ -252,7 +267,7 @@ def main():
 
     # ---------------------------------------------------------------- headline: T = 512
     log("config 3: prefill T=512 (embed + add_rmsnorm_fp8 + swiglu_fp8 + rope_int8)")
-    c3 = measure_ops(512, 8, 8, 128, 0, 8, args.steps, args.warmup)
+    c3 = measure_ops(512, 8, 128, 0, 8, args.steps, args.warmup)
     log(json.dumps(c3))
     result_extra["prefill_T512"] = c3
 
@@ -280,7 +295,7 @@ def main():
                                                  stream, timed, args)
         log(json.dumps(result_extra["decode_T8"]))
         log("config 4: prefill T=8192, RoPE at 57344.., K5V4 group 32")
-        result_extra["prefill_T8192"] = measure_ops(8192, 2, 5, 32, 57344, "k5v4g32",
+        result_extra["prefill_T8192"] = measure_ops(8192, 5, 32, 57344, "k5v4g32",
                                                     max(5, args.steps // 2), 2)
         log(json.dumps(result_extra["prefill_T8192"]))
         log("config 5: bandwidth stress, 40 layers x T=32768, bf16")

@@ -37,10 +37,9 @@ int launch_status(const char* what) {
 }
 
 namespace {
-std::atomic<int> g_fp8_mode{[] {
-  const char* e = std::getenv("G4_FP8_SINGLE_LAUNCH");
-  return e != nullptr && e[0] == '0' ? 1 : 0;
-}()};
+// 0: single launch with one grid synchronisation where the grid is resident;
+// 1: two launches (granite4_set_fp8_launch_mode).
+std::atomic<int> g_fp8_mode{0};
 }  // namespace
 
 int fp8_launch_mode() { return g_fp8_mode.load(std::memory_order_relaxed); }

@@ -59,7 +59,6 @@ constexpr int kRowsPerWave = 4;  // query rows per wave (x 4 heads = 16 MFMA row
 constexpr int kAttnMaxSplits = 256;
 enum : int { kAttnPlain = 0, kAttnRopeAppend = 1, kAttnAppend = 2 };
 constexpr int kAttnWaves = 4;  // splits per workgroup, merged before the combine
-constexpr int kAttnSpinLimit = 1 << 20;  // polls before the combining block gives up
 constexpr int kVPitch = kHd + 16;  // LDS V row pitch (bf16): 288 B, rows 8 banks apart
 // Waves per SIMD the split kernel is compiled for: two (so a grid of more
 // blocks than CUs keeps two blocks on each), except the bf16 decode-append
@@ -93,6 +92,8 @@ struct AttnArgs {
   // a second launch (attn_combine_kernel) combines.
   unsigned* tags;
   unsigned tag;
+  unsigned* err;  // sticky error word (1: a combining block's wait gave up)
+  int spin_limit; // polls before the combining block gives up
   // Decode append (one row at *d_pos): q, k, v are the raw bf16 projections
   // (ra.q / ra.k / ra.v); q is rotated in registers, and the wave whose split
   // holds the position rotates and quantises that position's K / V row (the
@@ -887,14 +888,24 @@ void attn_split_kernel(AttnArgs a) {
     const bool mine = b < b_hi - 1;  // every block with work but this one
     bool seen = !mine;
     int spin = 0;
-    for (;;) {
+    // A spin limit of 0 (the test hook) gives up before polling, so the
+    // outcome does not depend on timing.
+    const bool forced = a.spin_limit <= 0;
+    while (!forced) {
       if (!seen) seen = __hip_atomic_load(gt + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.tag;
-      if (__all(seen) || ++spin >= kAttnSpinLimit) break;
+      if (__all(seen) || ++spin >= a.spin_limit) break;
       __builtin_amdgcn_s_sleep(1);
     }
-    if (mine) __hip_atomic_store(gt + b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const bool ok = __all(seen);
-    if (lane == 0) s_ok = ok;
+    // Only slots seen carrying the tag are cleared: an unseen block may
+    // still store its tag after a give-up, so its slot is left alone, and
+    // the give-up is recorded in the sticky error word for the host, which
+    // then zero-fills the scratch before the next call.
+    if (mine && seen) __hip_atomic_store(gt + b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool ok = !forced && __all(seen);
+    if (lane == 0) {
+      s_ok = ok;
+      if (!ok) __hip_atomic_store(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
   __syncthreads();
   if (!s_ok) {
@@ -1435,11 +1446,8 @@ int attn_splits(int max_len) {
 }
 
 // Combine mode (granite4_set_attn_combine_mode): 0 inside the split launch,
-// 1 as a second launch (the initial mode with G4_ATTN_COMBINE_LAUNCH=1).
-std::atomic<int> g_attn_combine{[] {
-  const char* e = std::getenv("G4_ATTN_COMBINE_LAUNCH");
-  return e != nullptr && e[0] == '1' ? 1 : 0;
-}()};
+// 1 as a second launch.
+std::atomic<int> g_attn_combine{0};
 
 // Arrival tags: a process-wide counter from a random start, never 0. The
 // slots need only differ from the call's tag before the call: the combining
@@ -1450,6 +1458,18 @@ unsigned next_attn_tag() {
   do t = g_attn_tag.fetch_add(1, std::memory_order_relaxed) + 1u;
   while (t == 0u);
   return t;
+}
+
+// Scratch layout: a 256-byte head holding the sticky error word, then the
+// partials (m, l) [rows][Hq][nblk], the partial outputs [rows][Hq][nblk][128]
+// and the arrival tags.
+constexpr size_t kAttnScratchHead = 256;
+
+void set_scratch(AttnArgs& a, void* scratch, int rows) {
+  a.err = static_cast<unsigned*>(scratch);
+  a.spin_limit = fp8_sync_spin_limit();
+  a.part_ml = reinterpret_cast<float2*>(static_cast<char*>(scratch) + kAttnScratchHead);
+  a.part_o = reinterpret_cast<float*>(a.part_ml + static_cast<size_t>(rows) * a.Hq * a.nblk);
 }
 
 // Points a at its tag slots (after the partials) and draws the call's tag,
@@ -1496,16 +1516,6 @@ void launch_prefill_w(const PrefillArgs& a, int group, dim3 grid, hipStream_t st
   }
 }
 
-// The key split for 16-position workgroups unless G4_PREFILL_KSPLIT=0 (A/B
-// measurement).
-bool prefill_ksplit() {
-  static const bool on = [] {
-    const char* e = std::getenv("G4_PREFILL_KSPLIT");
-    return !(e != nullptr && e[0] == '0');
-  }();
-  return on;
-}
-
 // 8-wave workgroups (32 positions each) where they give every CU one, else
 // 16-position workgroups for twice the workgroups: 8 waves splitting the keys
 // between two 4-wave groups, or 4 waves.
@@ -1517,8 +1527,7 @@ void launch_prefill_bits(const PrefillArgs& a, int group, int Hk, hipStream_t st
     launch_prefill_w<BITS, 8>(a, group, grid, st);
   } else {
     const dim3 grid((a.rows + 4 * 4 * kPrefillCb - 1) / (4 * 4 * kPrefillCb), Hk);
-    if (prefill_ksplit()) launch_prefill_w<BITS, 8, 2>(a, group, grid, st);
-    else launch_prefill_w<BITS, 4>(a, group, grid, st);
+    launch_prefill_w<BITS, 8, 2>(a, group, grid, st);
   }
 }
 
@@ -1593,7 +1602,26 @@ size_t granite4_attn_split_scratch_bytes(int Hq, int rows, int stride) {
   const size_t slots = static_cast<size_t>(rows) * Hq * nblk;
   // Partial (m, l) and output per slot, then the arrival tags (one per
   // (row group, KV head, block): at most one per slot).
-  return slots * (sizeof(float2) + kHd * sizeof(float) + sizeof(unsigned));
+  return kAttnScratchHead + slots * (sizeof(float2) + kHd * sizeof(float) + sizeof(unsigned));
+}
+
+int granite4_attn_sync_status(void* scratch, int clear) {
+  if (scratch == nullptr) return -1;
+  unsigned v = 0;
+  const hipStream_t st = stream();
+  bool ok = hipMemcpyAsync(&v, scratch, sizeof v, hipMemcpyDeviceToHost, st) == hipSuccess &&
+            hipStreamSynchronize(st) == hipSuccess;
+  if (ok && clear && v != 0) {
+    static const unsigned zero = 0;
+    ok = hipMemcpyAsync(scratch, &zero, sizeof zero, hipMemcpyHostToDevice, st) == hipSuccess &&
+         hipStreamSynchronize(st) == hipSuccess;
+  }
+  if (!ok) {
+    std::fprintf(stderr, "granite4: granite4_attn_sync_status: %s\n",
+                 hipGetErrorString(hipGetLastError()));
+    return -1;
+  }
+  return v != 0 ? 1 : 0;
 }
 
 int granite4_set_attn_combine_mode(int mode) {
@@ -1639,8 +1667,7 @@ int granite4_attn_paged(const uint16_t* q, int rows, int Hq, int Hk, int d, floa
   a.row_pos = row_pos;
   a.row_pt = row_pt;
   a.nblk = (a.splits + kAttnWaves - 1) / kAttnWaves;
-  a.part_ml = static_cast<float2*>(scratch);
-  a.part_o = reinterpret_cast<float*>(a.part_ml + static_cast<size_t>(rows) * Hq * a.nblk);
+  set_scratch(a, scratch, rows);
   a.out = out;
   // Multi-sequence rows (row_pos) take one wave each; rows of one sequence
   // share a wave in groups of four (their keys are read once per group).
@@ -1696,8 +1723,7 @@ int attn_decode_append(const uint16_t* q, const uint16_t* k, const uint16_t* v,
   a.d_pos = d_pos;
   a.d_pt = d_pt;
   a.nblk = (a.splits + kAttnWaves - 1) / kAttnWaves;
-  a.part_ml = static_cast<float2*>(scratch);
-  a.part_o = reinterpret_cast<float*>(a.part_ml + static_cast<size_t>(Hq) * a.nblk);
+  set_scratch(a, scratch, 1);
   a.out = out;
   a.ra = ra;
   const bool fused = set_combine(a, 1);

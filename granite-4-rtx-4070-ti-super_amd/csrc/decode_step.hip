@@ -22,32 +22,57 @@
 #include "g4_common.h"
 #include "granite4_layerops.h"
 
+#include <cmath>
+#include <cstdint>
 #include <cstdio>
 
 namespace {
 
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool k_ok(int K) { return K >= 64 && K % 64 == 0 && K <= 16384; }  // the GEMVs' K range
+bool fin(float x) { return std::isfinite(x); }
+
+// Every condition the step's entry points check, tested before the first
+// launch, so that a call either launches nothing (-1) or launches the whole
+// step: a step rejected half-way would already have appended the position's
+// K / V rows in the earlier layers.
 bool model_ok(const Granite4DecodeModel* m) {
-  if (m == nullptr || m->layers <= 0 || m->layer == nullptr || m->H <= 0 || m->H % 64 != 0 ||
-      m->I <= 0 || m->I % 64 != 0 || m->Hq <= 0 || m->Hk <= 0 || m->Hq % m->Hk != 0 ||
+  if (m == nullptr || m->layers <= 0 || m->layer == nullptr || m->Hq <= 0 || m->Hk <= 0 ||
+      m->Hq != 4 * m->Hk || !k_ok(m->H) || !k_ok(m->I) || !k_ok(m->Hq * 128) ||
       m->emb == nullptr || m->vocab <= 0 || m->cos_tbl == nullptr || m->sin_tbl == nullptr ||
-      m->max_pos <= 0 || m->kv_stride <= 0)
+      m->max_pos <= 0 || m->kv_stride <= 0 || !fin(m->eps) || !fin(m->emb_mult) ||
+      !fin(m->resid_mult) || !fin(m->attn_scale) || !fin(m->lm_scale))
     return false;
-  if (m->lm_head != nullptr && m->final_norm == nullptr) return false;
+  if (m->kv_bits != 16 && m->kv_bits != 8 && m->kv_bits != 4 && m->kv_bits != 5) return false;
+  if (m->kv_bits != 16 && m->kv_group != 32 && m->kv_group != 64 && m->kv_group != 128)
+    return false;
+  if (m->lm_head != nullptr && (m->final_norm == nullptr || !al16(m->lm_head))) return false;
+  if (m->final_norm != nullptr && !al16(m->final_norm)) return false;
+  const long long qkv_rows = static_cast<long long>(m->Hq + 2 * m->Hk) * 128;
+  if (qkv_rows * m->H >= (1LL << 40) || static_cast<long long>(m->I) * m->H >= (1LL << 40) ||
+      static_cast<long long>(m->vocab) * m->H >= (1LL << 40))
+    return false;
   for (int l = 0; l < m->layers; ++l) {
     const Granite4DecodeLayer& y = m->layer[l];
-    if (y.attn_norm == nullptr || y.ffn_norm == nullptr || y.wq == nullptr || y.wk == nullptr ||
-        y.wv == nullptr || y.wo == nullptr || y.wg == nullptr || y.wu == nullptr ||
-        y.wd == nullptr || y.cache_k == nullptr || y.cache_v == nullptr ||
+    const void* ptrs[] = {y.attn_norm, y.ffn_norm, y.wq, y.wk, y.wv, y.wo, y.wg, y.wu, y.wd};
+    for (const void* p : ptrs)
+      if (p == nullptr || !al16(p)) return false;
+    if (y.cache_k == nullptr || y.cache_v == nullptr ||
         (m->kv_bits != 16 && (y.k_scale == nullptr || y.v_scale == nullptr)))
       return false;
+    const float sc[] = {y.sq, y.sk, y.sv, y.so, y.sg, y.su, y.sd};
+    for (float x : sc)
+      if (!fin(x)) return false;
   }
   return true;
 }
 
 bool buffers_ok(const Granite4DecodeBuffers* b) {
-  return b != nullptr && b->hidden != nullptr && b->q_rot != nullptr && b->k_rot != nullptr &&
-         b->v != nullptr && b->attn_out != nullptr && b->act != nullptr &&
-         b->attn_scratch != nullptr;
+  if (b == nullptr || b->attn_scratch == nullptr) return false;
+  const void* ptrs[] = {b->hidden, b->q_rot, b->k_rot, b->v, b->attn_out, b->act};
+  for (const void* p : ptrs)
+    if (p == nullptr || !al16(p)) return false;
+  return true;
 }
 
 }  // namespace

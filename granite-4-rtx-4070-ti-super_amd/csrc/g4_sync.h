@@ -34,7 +34,12 @@
 // sticky error word is set to 1 for the host to read
 // (granite4_fp8_sync_status). A spin limit of 0 gives up before polling:
 // workgroup 0 publishes a NaN maximum, so every workgroup of the launch
-// deterministically ends with NaN and the error word set.
+// deterministically ends with NaN and the error word set. After a give-up
+// that is not forced this way, workgroups may disagree (one saw every slot,
+// another gave up), so the whole call's codes and scale are invalid whenever
+// the error word is set. Both forms advance the generation in every call,
+// give-ups included, so the next call on the workspace starts clean without
+// a clear.
 #ifndef G4_SYNC_H
 #define G4_SYNC_H
 
@@ -137,8 +142,10 @@ __device__ __forceinline__ float grid_max(float m, const GridSync& gs, unsigned 
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
       if (lane == 0) {
+        // Workgroup 0 advances the generation also after a give-up, so the
+        // next call's tag differs from every slot this call wrote.
         if (late) __hip_atomic_store(gs.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        else if (blockIdx.x == 0)
+        if (blockIdx.x == 0)
           __hip_atomic_store(gs.gen, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_out = late ? __builtin_nanf("") : v;
       }

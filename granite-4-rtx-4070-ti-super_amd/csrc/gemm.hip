@@ -689,24 +689,9 @@ bool gemm_args_ok(const uint8_t* A, int lda, const uint8_t* W, int M, int N, int
 // (up to g / 8); the plain order gives it every 8th tile: one M tile (mt <= 8)
 // or mt / 8 of them, spread over g / 8 or g / mt columns. Measured: T = 512
 // gate|up 88 -> 77 us with XCD order (4 x 16 against 1 x 64), T = 8192 the
-// plain order's 8 x 8 beats XCD order's 64 x 1 by 14-17 %. G4_GEMM_XCD=0
-// keeps the plain order everywhere (A/B measurement).
-// K split inside the workgroup (KS = 2) where each CU holds one 128 x 64
-// tile, unless G4_GEMM_KSPLIT=0 (A/B measurement).
-bool gemm_ksplit() {
-  static const bool on = [] {
-    const char* e = std::getenv("G4_GEMM_KSPLIT");
-    return !(e != nullptr && e[0] == '0');
-  }();
-  return on;
-}
-
+// plain order's 8 x 8 beats XCD order's 64 x 1 by 14-17 %.
 bool gemm_xcd_order(int mt, unsigned g) {
-  static const bool allowed = [] {
-    const char* e = std::getenv("G4_GEMM_XCD");
-    return !(e != nullptr && e[0] == '0');
-  }();
-  if (!allowed || g < 16) return false;
+  if (g < 16) return false;
   const long long per = g / 8;
   const long long xbm = mt < per ? mt : per, xbn = (per + mt - 1) / mt;
   const long long pbm = mt <= 8 ? 1 : mt / 8, pbn = mt <= 8 ? per : (g + mt - 1) / mt;
@@ -770,8 +755,7 @@ int granite4_gemm_fp8(int out, const uint8_t* A, int lda, const float* d_a_scale
   const auto run = [&](auto e_tag) {
     constexpr int E = decltype(e_tag)::value;
     if (!narrow) go(gemm_fp8_kernel<E>, gemm_grid<E>(tiles, INT_MAX));
-    else if (deep == 6 && gemm_ksplit()) go(gemm_fp8_kernel<E, 64, 3, 2>, gemm_grid<E, 64, 3, 2>(tiles, INT_MAX), 512);
-    else if (deep == 6) go(gemm_fp8_kernel<E, 64, 6>, gemm_grid<E, 64, 6>(tiles, INT_MAX));
+    else if (deep == 6) go(gemm_fp8_kernel<E, 64, 3, 2>, gemm_grid<E, 64, 3, 2>(tiles, INT_MAX), 512);
     else if (deep == 3) go(gemm_fp8_kernel<E, 64, 3>, gemm_grid<E, 64, 3>(tiles, INT_MAX));
     else go(gemm_fp8_kernel<E, 64>, gemm_grid<E, 64>(tiles, INT_MAX));
   };

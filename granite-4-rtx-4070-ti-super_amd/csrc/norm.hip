@@ -468,14 +468,8 @@ constexpr int kNormDeepHL = G4_NORM_DEEP_HL;
 // Waves per row. Four waves per 4096-wide row (2 vectors per lane, 54-62
 // VGPRs, full occupancy) measured faster than one wave per row (8 vectors per
 // lane, 142-152 VGPRs, 3 waves per SIMD) at every size: T=8192 FP8 70 vs 76 µs,
-// T=32768 bf16 stress 5.62 vs 5.52 TB/s. G4_NORM_WPR=1|4 overrides (sweeps).
-int pick_wpr(int /*rows*/) {
-  static const int forced = [] {
-    const char* e = std::getenv("G4_NORM_WPR");
-    return e ? std::atoi(e) : 0;
-  }();
-  return forced == 1 ? 1 : 4;
-}
+// T=32768 bf16 stress 5.62 vs 5.52 TB/s. Every width the vector path takes
+// (nvec <= 512) runs four waves per row.
 
 // Grid of a norm launch: one workgroup per row group, capped at kMaxPartials
 // for the FP8 passes (their workgroups loop over row groups).
@@ -494,7 +488,6 @@ template <int MODE>
 int launch_norm(NormArgs& a, const char* what) {
   const int nvec = a.cols / 8;
   const bool vec = norm_vector_path(a.rows, a.cols);
-  const int wpr = pick_wpr(a.rows);
   const hipStream_t st = stream();
   if (MODE == kOutFp8 && vec) {
     a.inv_nvec = 1.0 / nvec;
@@ -502,19 +495,12 @@ int launch_norm(NormArgs& a, const char* what) {
     const long long want = (vectors + 4LL * kBlock - 1) / (4LL * kBlock);
     const unsigned grid = static_cast<unsigned>(want < kPersistBlocks ? want : kPersistBlocks);
     hipLaunchKernelGGL(norm_encode_kernel, grid, kBlock, 0, st, a);
-  } else if (vec && wpr == 4 && nvec <= 4 * 64 * 4) {
+  } else if (vec) {
     const unsigned grid = norm_grid(MODE, a.rows);
     if (MODE == kOutAmax) a.n_partials = static_cast<int>(grid);
     if (nvec <= 256) hipLaunchKernelGGL((norm_kernel<1, 4, MODE>), grid, kBlock, 0, st, a);
     else if (nvec <= 512) hipLaunchKernelGGL((norm_kernel<2, 4, MODE>), grid, kBlock, 0, st, a);
     else hipLaunchKernelGGL((norm_kernel<4, 4, MODE>), grid, kBlock, 0, st, a);
-  } else if (vec) {
-    const unsigned grid = norm_grid(MODE, (a.rows + 3) / 4);
-    if (MODE == kOutAmax) a.n_partials = static_cast<int>(grid);
-    if (nvec <= 64) hipLaunchKernelGGL((norm_kernel<1, 1, MODE>), grid, kBlock, 0, st, a);
-    else if (nvec <= 128) hipLaunchKernelGGL((norm_kernel<2, 1, MODE>), grid, kBlock, 0, st, a);
-    else if (nvec <= 256) hipLaunchKernelGGL((norm_kernel<4, 1, MODE>), grid, kBlock, 0, st, a);
-    else hipLaunchKernelGGL((norm_kernel<8, 1, MODE>), grid, kBlock, 0, st, a);
   } else {
     const unsigned grid = norm_grid(MODE, a.rows);
     if (MODE == kOutAmax) a.n_partials = static_cast<int>(grid);
@@ -549,8 +535,7 @@ bool launch_norm_fp8_fused(const uint16_t* x, const uint16_t* branch, float mult
                            float eps, int rows, int cols, uint16_t* res_out, uint8_t* codes,
                            float* scale, void* work) {
   const int nvec = cols / 8;
-  if (fp8_launch_mode() != 0 || !norm_vector_path(rows, cols) || pick_wpr(rows) != 4 ||
-      nvec > 4 * 64 * 4)
+  if (fp8_launch_mode() != 0 || !norm_vector_path(rows, cols))
     return false;
   NormArgs a{x, branch, mult, w, eps, rows, cols, res_out, nullptr, codes, scale, nullptr, 0,
              nullptr, 0.0};
@@ -620,20 +605,14 @@ static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 constexpr int kMaxDevices = 64;
 
-namespace {
-// Zero-fills n 32-bit words (a kernel rather than hipMemsetAsync, so a
-// caller may capture it in a graph).
-__global__ __launch_bounds__(kBlock) void scratch_clear_kernel(unsigned* p, int n) {
-  for (int i = blockIdx.x * kBlock + threadIdx.x; i < n; i += gridDim.x * kBlock) p[i] = 0u;
-}
-}  // namespace
-
 // The device address of the current device's `scratch` (the host-side name
-// is only a stand-in), looked up once per device with that device current;
-// the first call on a device also zero-fills its synchronisation area on the
-// calling stream (the slots and generation word must start zero). The
-// per-row and partial areas need no clearing: each call writes them before
-// reading them. nullptr (with a message) on failure.
+// is only a stand-in), looked up once per device with that device current.
+// Nothing is launched: the array is zero-initialised when the code object is
+// loaded onto the device, which is the start state the synchronisation area
+// needs (slots, generation and error word), so a first use under graph
+// capture records no clearing node. The per-row and partial areas need no
+// clearing: each call writes them before reading them. nullptr (with a
+// message) on failure.
 void* static_scratch(const char* what) {
   static std::mutex mu;
   static void* ptrs[kMaxDevices] = {};
@@ -653,10 +632,6 @@ void* static_scratch(const char* what) {
                  hipGetErrorString(e));
     return nullptr;
   }
-  constexpr int words = static_cast<int>(kNoAllocScratchBytes / 4);
-  hipLaunchKernelGGL(scratch_clear_kernel, (words + kBlock - 1) / kBlock, kBlock, 0, stream(),
-                     static_cast<unsigned*>(ptr), words);
-  if (launch_status(what) != 0) return nullptr;
   ptrs[dev] = ptr;
   return ptr;
 }

@@ -242,12 +242,7 @@ void launch_fast_bits(const RopeArgs& a, int group, unsigned grid) {
 }  // namespace
 
 // Per-token workgroups (rope_append_row_kernel) or one unit per lane group
-// (rope_append_kernel); both write the same bytes. G4_ROPE_ROW_KERNEL=0 in
-// the environment selects the latter (A/B measurements).
-const bool g_rope_row_kernel = [] {
-  const char* e = std::getenv("G4_ROPE_ROW_KERNEL");
-  return e == nullptr || e[0] != '0';
-}();
+// (rope_append_kernel); both write the same bytes.
 
 // Measured (int8, A/B on one box, per-unit kernel / row kernel, us): 512 rows
 // 5.06 / 5.38, 640 5.62 / 5.98, 768 7.09 / 6.18, 1024 8.20 / 7.25, 4096
@@ -270,7 +265,7 @@ int launch_rope_append(RopeArgs a, int bits, int group, const char* what) {
     // Per-token workgroups for long inputs; fewer rows (decode, T = 8, up to
     // about 700 rows) keep one unit per lane group, which spreads them over
     // more workgroups (T=8: 24 instead of 8, 2.7 vs 3.3 us).
-    if (g_rope_row_kernel && upl <= 4 && a.rows >= kRopeRowKernelMinRows) {
+    if (upl <= 4 && a.rows >= kRopeRowKernelMinRows) {
       switch (bits) {
         case 16: launch_row_bits<16>(a, 128, upl); break;
         case 8: launch_row_bits<8>(a, group, upl); break;

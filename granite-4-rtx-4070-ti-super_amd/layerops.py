@@ -117,6 +117,7 @@ _SIG = {
     "granite4_debug_set_sync_spin_limit": [I],
     "granite4_attn_split_scratch_bytes": [I, I, I],
     "granite4_set_attn_combine_mode": [I],
+    "granite4_attn_sync_status": [P, I],
     "granite4_attn_split": [P, P, P, F, I, I, I, I, P, I, I, P, P, P, P, P, P, I, P, P, I, P, I,
                             P, P, P, I, P, P, I, I, I],
     "granite4_attn_paged": [P, I, I, I, I, F, P, P, P, P, I, I, I, I, P, P, P, P, I, I, P, P],
@@ -255,6 +256,15 @@ def set_attn_combine_mode(mode):
     return prev
 
 
+def attn_sync_status(scratch, clear=False):
+    """granite4_attn_sync_status: 1 if a fused-combine wait on this attention
+    scratch gave up since the last clear (or zero fill), else 0."""
+    rc = _lib.granite4_attn_sync_status(_ptr(scratch), int(bool(clear)))
+    if rc < 0:
+        raise Granite4Error("granite4_attn_sync_status failed")
+    return rc
+
+
 class DecodeStep:
     """granite4_decode_step over torch tensors: `layers` is a list of dicts
     with the Granite4DecodeLayer fields (tensors or pointers, floats for the
@@ -287,7 +297,7 @@ class DecodeStep:
         self.v = torch.empty(Hk * 128, dtype=bf, device=device)
         self.attn_out = torch.empty(Hq * 128, dtype=bf, device=device)
         self.act = torch.empty(I, dtype=bf, device=device)
-        self.scratch = torch.empty(_lib.granite4_attn_split_scratch_bytes(Hq, 1, kv_stride),
+        self.scratch = torch.zeros(_lib.granite4_attn_split_scratch_bytes(Hq, 1, kv_stride),
                                    dtype=torch.uint8, device=device)
         self.buffers = DecodeBuffers(*[_ptr(t) for t in (self.hidden, self.q_rot, self.k_rot,
                                                           self.v, self.attn_out, self.act,

@@ -238,8 +238,7 @@ int granite4_add_rmsnorm(const uint16_t* d_res, const uint16_t* d_branch, float 
 size_t granite4_fp8_work_bytes(int rows);
 /* FP8 launch form for granite4_add_rmsnorm_fp8 / granite4_swiglu_fp8, process
  * wide: 0 (default) = one launch when the tensor fits the registers of one
- * resident grid, else two; 1 = always two launches (also selected at load by
- * the environment variable G4_FP8_SINGLE_LAUNCH=0). Both forms give identical
+ * resident grid, else two; 1 = always two launches. Both forms give identical
  * codes and scales. Returns the previous mode, -1 for another value. No
  * reference counterpart (a tuning switch).
  *
@@ -263,8 +262,9 @@ int granite4_set_fp8_launch_mode(int mode);
  * granite4_add_rmsnorm_fp8_noalloc. No reference counterpart. */
 int granite4_fp8_sync_status(void* d_work, int clear);
 /* Test hook: sets the process-wide poll limit of the single-launch forms'
- * bounded waits (default 2^20) and returns the previous one, -1 for a
- * negative limit. 0 makes every wait give up at once, so a test can drive
+ * bounded waits and of the attention's fused-combine wait (default 2^20)
+ * and returns the previous one, -1 for a negative limit. 0 makes every wait
+ * give up at once, so a test can drive
  * the error path while every kernel still exits normally. No reference
  * counterpart. */
 int granite4_debug_set_sync_spin_limit(int limit);
@@ -388,6 +388,17 @@ size_t granite4_attn_split_scratch_bytes(int Hq, int rows, int stride);
  * the partials in either form). Process-wide; returns the previous mode, or
  * -1 for another value. */
 int granite4_set_attn_combine_mode(int mode);
+
+/* Status of the fused combine's bounded wait on one attention scratch buffer
+ * (no counterpart in the reference, whose combine is always a second
+ * launch): 0 if no combining block gave up waiting since the last clear (or
+ * the zero fill of the scratch), 1 if one did; then that call's outputs are
+ * NaN, and tags of late blocks may remain in the scratch, so zero-fill the
+ * whole scratch before reusing it. clear != 0 resets the error word.
+ * Synchronises the calling thread's stream; -1 on a null scratch or a HIP
+ * error. The error word is the scratch's first 4 bytes, valid once the
+ * scratch was zero-filled after allocation. */
+int granite4_attn_sync_status(void* scratch, int clear);
 
 /* The reference's attn_split (attention_gpu.h:53-60, bools as int). Causal
  * GQA for rows (1..16) query rows q [rows][Hq * d]: row r sits at position

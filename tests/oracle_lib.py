@@ -259,6 +259,23 @@ def row_table(block_table, n, page=16):
     return out
 
 
+def config2_page_tables(rs, n, pool_pages, max_pos=65536):
+    """BASELINE config 2's sessions: n positions drawn from [0, max_pos), each
+    session with a page table over all max_pos / 16 of its pages. Every page
+    maps to a random page of a small pool (repeats allowed, as no other page
+    is written); the n pages that hold the sessions' positions map to n
+    distinct pool pages, so the n rows written never collide. Returns the
+    positions and the per-session row tables (int32 [max_pos])."""
+    pos = rs.integers(0, max_pos, n).astype(np.int32)
+    own = rs.permutation(pool_pages)[:n].astype(np.int32)
+    pts = []
+    for i in range(n):
+        bt = rs.integers(0, pool_pages, max_pos // 16).astype(np.int32)
+        bt[pos[i] // 16] = own[i]
+        pts.append(row_table(bt, max_pos))
+    return pos, pts
+
+
 ATTN_TILE = 64
 ATTN_MAX_SPLITS = 256
 

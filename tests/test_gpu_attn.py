@@ -89,7 +89,7 @@ def check(got, want, vm, what):
 def run_paged(q, ck, cv, ks, vs, bits, group, stride, *, kv_base=0, d_pos=None, d_pt=None,
               row_pos=None, row_pts=None, max_len=0, window=0, scale=1.0 / 16):
     rows = q.shape[0]
-    scratch = torch.empty(L.call_size("granite4_attn_split_scratch_bytes", HQ, rows,
+    scratch = torch.zeros(L.call_size("granite4_attn_split_scratch_bytes", HQ, rows,
                                       max_len if max_len else stride),
                           dtype=torch.uint8, device="cuda")
     out = torch.empty((rows, HQ * D), dtype=torch.int16, device="cuda")
@@ -119,6 +119,53 @@ def test_attn_contiguous(bits, rows):
     pos = [kv_base + r for r in range(rows)]
     want = ol.attn_split(q, ck, cv, ks, vs, bits, D, stride, pos, scale=1.0 / 16, Hk=HK)
     check(got, want, vmax(cv, vs, bits), f"bits {bits} rows {rows}")
+
+
+@pytest.mark.parametrize("bits", [8, 16])
+def test_attn_combine_give_up_is_reported(bits):
+    """The fused combine's bounded wait, forced by the host to give up before
+    polling (spin limit 0, so every kernel still exits normally): the outputs
+    are NaN and the scratch's sticky error word reads 1. After the zero fill
+    the error word asks for, the same scratch gives the oracle's result."""
+    note(f"attn combine give-up bits={bits}")
+    pages = 80
+    stride = 16 * pages
+    ck, cv, ks, vs = make_cache(bits, D, stride, 0xE5 + bits)
+    pt = ol.row_table(np.random.default_rng(7 + bits).permutation(pages).astype(np.int32), stride)
+    q = ol.normal_bf16(0xE6, 0.0, 1.0, HQ * D).reshape(1, HQ * D)
+    pos = dev(np.array([1100], np.int32))
+    scratch = torch.zeros(L.call_size("granite4_attn_split_scratch_bytes", HQ, 1, stride),
+                          dtype=torch.uint8, device="cuda")
+    dks = None if ks is None else dev(ks)
+    dvs = None if vs is None else dev(vs)
+    d_q, d_ck, d_cv, d_pt = dev(q), dev(ck), dev(cv), dev(pt)
+
+    def run():
+        out = torch.empty((1, HQ * D), dtype=torch.int16, device="cuda")
+        L.call("granite4_attn_paged", d_q, 1, HQ, HK, D, 1.0 / 16, d_ck, d_cv, dks, dvs, bits, D,
+               stride, 0, pos, d_pt, None, None, 0, 0, scratch, out)
+        return host(out).view(np.uint16)
+
+    prev_mode = L.set_attn_combine_mode(0)
+    try:
+        assert L.attn_sync_status(scratch) == 0
+        prev = L.set_sync_spin_limit(0)
+        try:
+            bad = run()
+            torch.cuda.synchronize()
+        finally:
+            L.set_sync_spin_limit(prev)
+        assert ((bad & 0x7FFF) > 0x7F80).all(), "every output should be NaN after a give-up"
+        assert L.attn_sync_status(scratch) == 1
+        scratch.zero_()
+        assert L.attn_sync_status(scratch) == 0
+        got = run()
+        assert L.attn_sync_status(scratch) == 0
+    finally:
+        L.set_attn_combine_mode(prev_mode)
+    want = ol.attn_split(q, ck, cv, ks, vs, bits, D, stride, [1100], pts=[pt], scale=1.0 / 16,
+                         Hk=HK)
+    check(got, want, vmax(cv, vs, bits), f"bits {bits} after give-up")
 
 
 @pytest.mark.parametrize("bits", [8, 16])

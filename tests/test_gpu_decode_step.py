@@ -205,7 +205,7 @@ def _close(got, want, what):
     assert within >= 0.95, (what, within)
 
 
-@pytest.mark.parametrize("bits,group", [(16, 128), (8, 128), (5, 32)])
+@pytest.mark.parametrize("bits,group", [(16, 128), (8, 128), (5, 32), (4, 32), (5, 128)])
 def test_decode_step_two_layers(bits, group):
     note(f"decode step bits={bits} group={group}")
     m = Model(bits, group, ctx=300, seed=0xD5 + bits)
@@ -288,3 +288,22 @@ def test_decode_step_rejects_bad_arguments():
     m.step.model.lm_head = None
     with pytest.raises(L.Granite4Error):
         m.step(m.tokens, d_pos, m.pt, None, lg)
+
+
+def test_decode_step_rejects_a_bad_later_layer_before_any_launch():
+    """A bad argument of the second layer (a NaN weight scale) is rejected
+    before anything is launched: no layer's arena is touched, so a caller
+    that fixes the argument and calls again appends the position once."""
+    note("decode step rejects layer 1 before launching")
+    m = Model(8, 128, ctx=40, seed=0xD8)
+    d_pos = torch.tensor([40], dtype=torch.int32, device="cuda")
+    start = [(host(k).copy(), host(v).copy()) for k, v in m.arenas()]
+    hid = host(m.step.hidden).copy()
+    m.step._arr[1].sd = float("nan")
+    with pytest.raises(L.Granite4Error):
+        m.step(m.tokens, d_pos, m.pt)
+    torch.cuda.synchronize()
+    for (k, v), (k0, v0) in zip(m.arenas(), start):
+        np.testing.assert_array_equal(host(k), k0)
+        np.testing.assert_array_equal(host(v), v0)
+    np.testing.assert_array_equal(host(m.step.hidden), hid)

@@ -347,13 +347,10 @@ def test_multi_kv_append_reference_api(bits):
     positions, each through its own random page table; K is written as given
     (no rotation). Untouched arena rows keep their fill."""
     note(f"multi_kv_append bits={bits}")
-    n, pages_per_seq, pool_pages = 8, 8, 64
+    n, pool_pages = 8, 64
     stride = pool_pages * 16
     rs = np.random.default_rng(0x3915 + bits)
-    perm = rs.permutation(pool_pages).astype(np.int32)
-    pos = rs.integers(0, pages_per_seq * 16, n).astype(np.int32)
-    pts = [ol.row_table(perm[i * pages_per_seq:(i + 1) * pages_per_seq], pages_per_seq * 16)
-           for i in range(n)]
+    pos, pts = ol.config2_page_tables(rs, n, pool_pages)
     d_pts = [dev(t) for t in pts]
     m = L.multi_rows_struct()()
     m.n = n

@@ -560,13 +560,11 @@ def test_multi_rope_append(tables, bits):
     note(f"multi rope append bits={bits}")
     c, s, dc, ds = tables
     n, Hq, Hk = 8, 32, 8
-    pages_per_seq, pool_pages = 8, 64
+    pool_pages = 64
     stride = pool_pages * 16
     rs = np.random.default_rng(40 + bits)
-    perm = rs.permutation(pool_pages).astype(np.int32)
-    pos = rs.integers(0, pages_per_seq * 16, n).astype(np.int32)
-    tables_pt = [ol.row_table(perm[i * pages_per_seq:(i + 1) * pages_per_seq], pages_per_seq * 16)
-                 for i in range(n)]
+    pos, tables_pt = ol.config2_page_tables(rs, n, pool_pages)
+    assert pos.max() >= 32768, "the draw should reach the upper half of [0, 65536)"
     d_pts = [dev(t) for t in tables_pt]
     M = L.multi_rows_struct()
     m = M()
@@ -631,54 +629,68 @@ def test_out_of_range_rows_are_skipped(tables):
 
 
 # ----------------------------------------------------------------------------- grid-sync failure
-@pytest.mark.parametrize("op,rows", [("norm", 512), ("norm", 8192), ("swiglu", 512),
-                                     ("swiglu", 2048)])
-def test_fp8_single_launch_wait_give_up_is_reported(op, rows):
+@pytest.mark.parametrize("clear", [True, False])
+@pytest.mark.parametrize("op,rows", [("norm", 8), ("norm", 512), ("norm", 8192), ("swiglu", 8),
+                                     ("swiglu", 512), ("swiglu", 2048)])
+def test_fp8_single_launch_wait_give_up_is_reported(op, rows, clear):
     """The single-launch FP8 forms' bounded wait, forced by the host to give
     up at once (spin limit 0: workgroup 0 publishes a NaN maximum without
-    polling, so every kernel exits normally): the scale is NaN, the sticky
-    error word reads 1 until cleared, and after the clear the same workspace
-    gives correct results again."""
-    note(f"fp8 sync give-up {op} rows={rows}")
+    polling, so every kernel exits normally): the scale is NaN and the sticky
+    error word reads 1 until cleared. The next call on the same workspace is
+    correct whether or not the caller cleared it first, also on other inputs
+    than the failed call's (8 rows is the one-hop synchronisation, whose
+    slots would otherwise still carry the next tag)."""
+    note(f"fp8 sync give-up {op} rows={rows} clear={clear}")
     work = L.fp8_workspace()
     assert L.fp8_sync_status(work) == 0
     if op == "norm":
         cols = 4096
-        x = dev(_hidden(rows, cols, 0xD1))
+        xs = [dev(_hidden(rows, cols, 0xD1)), dev(_hidden(rows, cols, 0xD4))]
         w_h = ol.normal_bf16(0xD2, 1.0, 0.1, cols)
         w = dev(w_h)
         codes = torch.empty((rows, cols), dtype=torch.uint8, device="cuda")
 
-        def run(scale):
-            L.call("granite4_add_rmsnorm_fp8", x, None, 1.0, w, 1e-5, rows, cols, None, codes,
-                   scale, work)
+        def run(i, scale, wk):
+            L.call("granite4_add_rmsnorm_fp8", xs[i], None, 1.0, w, 1e-5, rows, cols, None, codes,
+                   scale, wk)
     else:
         I_ = 12800
-        gu = dev(ol.normal_bf16(0xD3, 0.0, 1.0, rows * 2 * I_).reshape(rows, 2 * I_))
+        gus = [dev(ol.normal_bf16(0xD3, 0.0, 1.0, rows * 2 * I_).reshape(rows, 2 * I_)),
+               dev(ol.normal_bf16(0xD5, 0.0, 3.0, rows * 2 * I_).reshape(rows, 2 * I_))]
         codes = torch.empty((rows, I_), dtype=torch.uint8, device="cuda")
 
-        def run(scale):
-            L.call("granite4_swiglu_fp8", gu, rows, I_, codes, scale, work, None)
+        def run(i, scale, wk):
+            L.call("granite4_swiglu_fp8", gus[i], rows, I_, codes, scale, wk, None)
+    fresh = L.fp8_workspace()
+    want_scale, want_codes = [], []
+    for i in range(2):
+        sc = torch.empty(1, dtype=torch.float32, device="cuda")
+        run(i, sc, fresh)
+        want_scale.append(host(sc)[0])
+        want_codes.append(host(codes).copy())
+    assert want_scale[0] != want_scale[1]
     good = torch.empty(1, dtype=torch.float32, device="cuda")
-    run(good)
-    good_codes = host(codes).copy()
+    run(0, good, work)
+    assert host(good)[0] == want_scale[0]
     assert L.fp8_sync_status(work) == 0
     prev = L.set_sync_spin_limit(0)
     try:
         bad = torch.empty(1, dtype=torch.float32, device="cuda")
-        run(bad)
+        run(1, bad, work)
         torch.cuda.synchronize()
     finally:
         L.set_sync_spin_limit(prev)
     assert np.isnan(host(bad)[0])
     assert L.fp8_sync_status(work) == 1
-    assert L.fp8_sync_status(work, clear=True) == 1
-    assert L.fp8_sync_status(work) == 0
-    again = torch.empty(1, dtype=torch.float32, device="cuda")
-    run(again)
-    assert host(again)[0] == host(good)[0]
-    np.testing.assert_array_equal(host(codes), good_codes)
-    assert L.fp8_sync_status(work) == 0
+    if clear:
+        assert L.fp8_sync_status(work, clear=True) == 1
+        assert L.fp8_sync_status(work) == 0
+    for i in (1, 0):
+        again = torch.empty(1, dtype=torch.float32, device="cuda")
+        run(i, again, work)
+        assert host(again)[0] == want_scale[i]
+        np.testing.assert_array_equal(host(codes), want_codes[i])
+    assert L.fp8_sync_status(work) == (0 if clear else 1)
 
 
 @pytest.mark.parametrize("rows", [8, 512, 2048])

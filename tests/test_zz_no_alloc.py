@@ -58,6 +58,49 @@ def _run(name, rows, res, br, w, mult, work=None):
     return host(ro), host(codes), host(scale)[0]
 
 
+def test_noalloc_first_use_under_graph_capture():
+    """The first use of the static scratch in this process happens inside a
+    graph capture (this test runs first in the module, and no other module
+    touches that scratch). The library records nothing but the op itself, so
+    the graph's replays (with eager calls and synchronisations between them)
+    keep the sticky error word that a give-up would set, and every replay
+    equals the workspace entry point's result for its input."""
+    note("noalloc first use under capture")
+    rows = 512
+    w = dev(ol.normal_bf16(0x9D, 1.0, 0.1, COLS))
+    work = L.fp8_workspace()
+    ins = [_inputs(rows, 0xA0 + 3 * i) for i in range(2)]
+    want = [_run("granite4_add_rmsnorm_fp8", rows, r, b, w, 1.0, work) for r, b in ins]
+    src_r = torch.empty_like(ins[0][0])
+    src_b = torch.empty_like(ins[0][1])
+    ro = torch.empty((rows, COLS), dtype=torch.int16, device="cuda")
+    codes = torch.empty((rows, COLS), dtype=torch.uint8, device="cuda")
+    scale = torch.empty(1, dtype=torch.float32, device="cuda")
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    L.use_stream(s)
+    try:
+        with torch.cuda.graph(g, stream=s):
+            L.call("granite4_add_rmsnorm_fp8_noalloc", src_r, src_b, 1.0, w, 1e-5, rows, COLS, ro,
+                   codes, scale)
+    finally:
+        L.use_stream()
+    for i in (0, 1, 1, 0):
+        src_r.copy_(ins[i][0])
+        src_b.copy_(ins[i][1])
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(host(ro), want[i][0])
+        np.testing.assert_array_equal(host(codes), want[i][1])
+        assert host(scale)[0] == want[i][2]
+        # eager work between replays
+        _run("granite4_add_rmsnorm_fp8_noalloc", 64, ins[1 - i][0][:64], ins[1 - i][1][:64], w,
+             0.5)
+    assert L.fp8_sync_status(None) == 0
+
+
 @pytest.mark.parametrize("mode", [0, 1])
 @pytest.mark.parametrize("sizes", [(512, 200), (8192, 4097), (40, 1)])
 def test_noalloc_matches_workspace_entry(mode, sizes):
