@@ -82,13 +82,18 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline + decode only")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=["t512", "t8192", "decode", "t8", "stress", "tN", "probe", "floor", "t1",
-                                       "attn", "gemm", "decode_gemv"],
+                                       "attn", "gemm", "decode_gemv", "decode_trace"],
                     help="run one configuration and print its detail (profiling runs)")
     ap.add_argument("--T", type=int, default=1024, help="token count for --only tN")
     ap.add_argument("--attn-case", default=None, help="run only this bench_attn case")
     ap.add_argument("--gemm-case", default=None,
                     help="run only this bench_gemm case, as T512:name or T8192:name")
+    ap.add_argument("--trace-summary", default=None, metavar="KERNEL_TRACE_CSV",
+                    help="summarise a rocprofv3 kernel trace of --only decode_trace (no GPU)")
     args = ap.parse_args()
+    if args.trace_summary:
+        print(json.dumps(summarize_decode_trace(args.trace_summary)), flush=True)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the non-GEMM layer ops are "
               "token-parallel; see DESIGN.md for how they would shard). Run with --gpus 1.",
@@ -250,6 +255,9 @@ def main():
             r = measure_ops(args.T, 8, 128, 0, 8, args.steps, args.warmup)
         elif args.only == "decode_gemv":
             r = bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream)
+        elif args.only == "decode_trace":
+            r = bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream,
+                                  trace_replays=25)
         elif args.only == "decode":
             r = {"decode_T1": bench_decode(torch, L, randn, cos_t, sin_t, emb, gamma, stream, args),
                  "decode_T1_with_attention": bench_decode(torch, L, randn, cos_t, sin_t, emb, gamma,
@@ -554,7 +562,8 @@ def graphs_us(torch, L, stream, steps, rounds=5, reps=20):
     return {name: sorted(t)[len(t) // 2] for name, t in times.items()}
 
 
-def bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream, layers=40):
+def bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream, layers=40,
+                      trace_replays=0):
     """Batch-1 decode step with its GEMVs (fp8 weight rows of the 8B model:
     q|k|v 6144 x 4096, o 4096 x 4096, gate and up 12800 x 4096, down 4096 x
     12800; 199 MB per layer, random e4m3 codes), three ways, each replayed as
@@ -747,16 +756,33 @@ def bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream, layers=40
 
     def fused_rope_epilogue():
         # config 1's ops (embed, add+RMSNorm, SwiGLU, RoPE on Q/K) all inside
-        # the decode GEMVs: RoPE in the q|k|v epilogue, no KV write
-        L.call("granite4_embed_at_pos", toks, pos, emb, VOCAB, H, 1.0, hidden)
-        for p in per:
-            L.call("granite4_gemv_rmsnorm_qkv_rope", hidden, gamma, 1e-5, p["wq"], p["wk"],
-                   p["wv"], sc, sc, sc, cos_t, sin_t, 65536, pos, HQ, HK, H, q_rot, k_rot, v)
+        # the decode GEMVs: the embedding in the first q|k|v GEMV's prologue,
+        # RoPE in the q|k|v epilogue, no KV write
+        for i, p in enumerate(per):
+            if i == 0:
+                L.call("granite4_gemv_embed_rmsnorm_qkv_rope", toks, emb, VOCAB, 1.0, hidden, gamma,
+                       1e-5, p["wq"], p["wk"], p["wv"], sc, sc, sc, cos_t, sin_t, 65536, pos, HQ,
+                       HK, H, q_rot, k_rot, v)
+            else:
+                L.call("granite4_gemv_rmsnorm_qkv_rope", hidden, gamma, 1e-5, p["wq"], p["wk"],
+                       p["wv"], sc, sc, sc, cos_t, sin_t, 65536, pos, HQ, HK, H, q_rot, k_rot, v)
             L.call("granite4_gemv_fp8w_resid", attn_out, p["wo"], sc, hidden, 1.0, H, HQ * D,
                    hidden)
             L.call("granite4_gemv_rmsnorm_silu_gate_up", hidden, gamma, 1e-5, p["wg"], p["wu"],
                    sc, sc, I, H, act)
             L.call("granite4_gemv_fp8w_resid", act, p["wd"], sc, hidden, 1.0, H, I, hidden)
+
+    if trace_replays:
+        # Kernel-trace mode: the plain and config-1 steps only, replayed
+        # alternately, for a rocprofv3 kernel trace whose per-step kernel
+        # duration sums (summarize_decode_trace) give the overhead without
+        # the graph-timing noise of the launches around them.
+        t = graphs_us(torch, L, stream, {"plain": plain, "config1": fused_rope_epilogue},
+                      rounds=trace_replays, reps=1)
+        del per
+        torch.cuda.empty_cache()
+        return {"layers": layers, "replays_each": trace_replays, "graph_us": t,
+                "config1_non_gemm_overhead_us": round(t["config1"] - t["plain"], 1)}
 
     t = graphs_us(torch, L, stream, {
         "plain": plain, "plain_attn": plain_attn, "unfused_attn": unfused_attn,
@@ -798,6 +824,53 @@ def bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream, layers=40
                                       "fused": 1 + 5 * layers}},
             "launches_per_step": {"plain": 4 * layers, "unfused": 1 + 7 * layers,
                                   "fused": 1 + 5 * layers}}
+
+
+def summarize_decode_trace(path, layers=40):
+    """Per-step kernel time of the plain and config-1 decode steps from a
+    rocprofv3 kernel trace (CSV) of `bench.py --only decode_trace`.
+
+    A dispatch of gemv_kernel<0, 0, ...> (no prologue, plain output) belongs
+    to the plain step; every other gemv_kernel (norm / embed prologues,
+    residual, SwiGLU and RoPE epilogues) to the config-1 step. Each step is
+    4 * layers dispatches; the k-th group of each class is the k-th replay.
+    The overhead is the config-1 step's summed kernel durations minus the
+    plain step's: the time the fused ops add inside the GEMVs, without the
+    launch gaps (both steps launch 4 * layers kernels)."""
+    import csv
+    rows = []
+    with open(path, newline="") as fh:
+        for rec in csv.DictReader(fh):
+            name = rec.get("Kernel_Name") or rec.get("KernelName") or ""
+            if "gemv_kernel" not in name:
+                continue
+            t0 = int(rec.get("Start_Timestamp") or rec.get("BeginNs"))
+            t1 = int(rec.get("End_Timestamp") or rec.get("EndNs"))
+            rows.append((t0, t1, "gemv_kernel<0, 0," in name or "gemv_kernelILi0ELi0E" in name))
+    rows.sort()
+    per = 4 * layers
+    def med(v):
+        v = sorted(v)
+        return v[len(v) // 2]
+
+    steps, slots = {}, {}
+    for cls, plain in (("plain", True), ("config1", False)):
+        d = [t1 - t0 for t0, t1, p in rows if p == plain]
+        n = len(d) // per
+        steps[cls] = [sum(d[i * per:(i + 1) * per]) / 1e3 for i in range(n)]
+        # the median duration of each of the step's 4 * layers launches over
+        # the replays, summed: robust to the odd slow dispatch
+        slots[cls] = sum(med([d[i * per + j] for i in range(n)]) for j in range(per)) / 1e3
+    n = min(len(steps["plain"]), len(steps["config1"]))
+    diff = sorted(steps["config1"][i] - steps["plain"][i] for i in range(n))
+    return {"replays": n, "layers": layers,
+            "plain_kernel_us_per_step": round(med(steps["plain"]), 1),
+            "config1_kernel_us_per_step": round(med(steps["config1"]), 1),
+            "config1_non_gemm_overhead_us": {
+                "per_launch_medians": round(slots["config1"] - slots["plain"], 2),
+                "median": round(med(diff), 2), "min": round(diff[0], 2),
+                "max": round(diff[-1], 2), "p10": round(diff[n // 10], 2),
+                "p90": round(diff[(9 * n) // 10], 2)}}
 
 
 def bench_multi8(torch, L, randn, cos_t, sin_t, gamma, work, gen, stream, timed, args):

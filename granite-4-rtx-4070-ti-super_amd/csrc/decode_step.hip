@@ -3,8 +3,9 @@
 // layer ops folded into this library's decode GEMVs and attention.
 //
 // Order per step (position *d_pos, token d_tokens[*d_pos]):
-//   hidden = bf16(emb_mult * emb[token])                    embed_at_pos
-//   per layer:
+//   hidden = bf16(emb_mult * emb[token])                    } layer 0: one launch,
+//   q_rot, k_rot, v = RoPE(GEMV(RMSNorm(hidden)))            } gemv_embed_rmsnorm_qkv_rope
+//   per layer (layers > 0 start with):
 //     q_rot, k_rot, v = RoPE(GEMV(RMSNorm(hidden)))          gemv_rmsnorm_qkv_rope
 //     KV append at d_pt[*d_pos]; attn_out = attention       attn_decode_append_rotated
 //     hidden = bf16(hidden + resid_mult * GEMV_o(attn_out))  gemv_fp8w_resid
@@ -13,12 +14,14 @@
 //   hidden_out = RMSNorm(hidden, final_norm)                 (optional)
 //   logits = bf16(lm_scale * GEMV_lm(RMSNorm(hidden)))       (optional)
 //
-// Five launches per layer plus the embedding and the head, all on the
+// Five launches per layer plus the head, all on the
 // calling thread's stream, no allocation and no synchronisation: a caller
 // captures the step once in a HIP graph and replays it per token, advancing
 // *d_pos between replays (capture_decode_graph, forward_gpu.cu:2934-2964).
 // Each launch is one of this library's entry points, so the step's outputs
-// are bit-identical to calling them one by one in this order.
+// are bit-identical to calling them one by one in this order (the first
+// launch is bit-identical to granite4_embed_at_pos then
+// granite4_gemv_rmsnorm_qkv_rope).
 #include "g4_common.h"
 #include "granite4_layerops.h"
 
@@ -39,7 +42,7 @@ bool fin(float x) { return std::isfinite(x); }
 bool model_ok(const Granite4DecodeModel* m) {
   if (m == nullptr || m->layers <= 0 || m->layer == nullptr || m->Hq <= 0 || m->Hk <= 0 ||
       m->Hq != 4 * m->Hk || !k_ok(m->H) || !k_ok(m->I) || !k_ok(m->Hq * 128) ||
-      m->emb == nullptr || m->vocab <= 0 || m->cos_tbl == nullptr || m->sin_tbl == nullptr ||
+      m->emb == nullptr || !al16(m->emb) || m->vocab <= 0 || m->cos_tbl == nullptr || m->sin_tbl == nullptr ||
       m->max_pos <= 0 || m->kv_stride <= 0 || !fin(m->eps) || !fin(m->emb_mult) ||
       !fin(m->resid_mult) || !fin(m->attn_scale) || !fin(m->lm_scale))
     return false;
@@ -89,13 +92,19 @@ int granite4_decode_step(const Granite4DecodeModel* m, const Granite4DecodeBuffe
     return -1;
   }
   const int H = m->H, I = m->I, Hq = m->Hq, Hk = m->Hk, nq = Hq * 128;
-  if (granite4_embed_at_pos(d_tokens, d_pos, m->emb, m->vocab, H, m->emb_mult, b->hidden) != 0)
-    return -1;
   for (int l = 0; l < m->layers; ++l) {
     const Granite4DecodeLayer& y = m->layer[l];
-    if (granite4_gemv_rmsnorm_qkv_rope(b->hidden, y.attn_norm, m->eps, y.wq, y.wk, y.wv, y.sq,
-                                       y.sk, y.sv, m->cos_tbl, m->sin_tbl, m->max_pos, d_pos, Hq,
-                                       Hk, H, b->q_rot, b->k_rot, b->v) != 0 ||
+    const int qkv =
+        l == 0 ? granite4_gemv_embed_rmsnorm_qkv_rope(d_tokens, m->emb, m->vocab, m->emb_mult,
+                                                      b->hidden, y.attn_norm, m->eps, y.wq, y.wk,
+                                                      y.wv, y.sq, y.sk, y.sv, m->cos_tbl,
+                                                      m->sin_tbl, m->max_pos, d_pos, Hq, Hk, H,
+                                                      b->q_rot, b->k_rot, b->v)
+               : granite4_gemv_rmsnorm_qkv_rope(b->hidden, y.attn_norm, m->eps, y.wq, y.wk, y.wv,
+                                                y.sq, y.sk, y.sv, m->cos_tbl, m->sin_tbl,
+                                                m->max_pos, d_pos, Hq, Hk, H, b->q_rot, b->k_rot,
+                                                b->v);
+    if (qkv != 0 ||
         granite4_attn_decode_append_rotated(b->q_rot, b->k_rot, b->v, m->max_pos, d_pos, d_pt,
                                             Hq, Hk, m->attn_scale, y.cache_k, y.cache_v,
                                             y.k_scale, y.v_scale, m->kv_bits, m->kv_group,

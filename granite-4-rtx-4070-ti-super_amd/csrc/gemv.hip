@@ -40,13 +40,24 @@
 namespace g4 {
 namespace {
 
-enum : int { kProNone = 0, kProNorm = 1 };
+// Prologues: none; the RMSNorm of x; the embedding row of the token at
+// *d_pos (x = bf16(emb_mult * emb[token]), also stored to x_out, the
+// residual stream) followed by the RMSNorm.
+enum : int { kProNone = 0, kProNorm = 1, kProEmbedNorm = 2 };
 enum : int { kEpiOut = 0, kEpiResid = 1, kEpiSwiglu = 2, kEpiRope = 3 };
 
 #ifndef G4_GEMV_DEPTH
 #define G4_GEMV_DEPTH 4
 #endif
 constexpr int kDepth = G4_GEMV_DEPTH;     // rows of loads in flight
+// The RoPE forms (768 workgroups for the 8B q|k|v: 3 per CU) issue all 8
+// rows before the norm prologue: one round trip to the weights instead of
+// two. Measured (rocprof kernel durations, 40-layer steps): norm + q|k|v +
+// RoPE 7.47 -> 7.28 us per call; 6 rows in flight 7.47.
+#ifndef G4_GEMV_ROPE_DEPTH
+#define G4_GEMV_ROPE_DEPTH 8
+#endif
+constexpr int kRopeDepth = G4_GEMV_ROPE_DEPTH;
 constexpr int kMaxChunks = 4;             // 1024-byte chunks per wave per row: K <= 16384
 constexpr int kMaxK = 4 * kMaxChunks * 1024;
 
@@ -68,6 +79,12 @@ struct GemvArgs {
   const float* sin_t;
   int max_pos;
   const int* d_pos;
+  // kProEmbedNorm: x is row tokens[*d_pos] of the table x (vocab rows; a
+  // token outside [0, vocab) gives a zero row), times emb_mult.
+  const int32_t* tokens;
+  int vocab;
+  float emb_mult;
+  uint16_t* x_out;
 };
 
 __device__ __forceinline__ uint4 ld_u4_nt(const uint8_t* p) {
@@ -121,17 +138,19 @@ __device__ __forceinline__ void fp8x16_to_f32(const uint4& q, float (&f)[16]) {
 // Weight row r (0 .. kRows - 1) of the workgroup, or nullptr past the end (n:
 // its output index). swiglu: the first half gate rows, the second half the up
 // rows of the same act columns.
-// kEpiRope (kRows = 8): the rotated segments [0, seg2) go 16 blocks per head,
-// block j of a head holding dims 4j .. 4j + 3 (rows r < 4) and their RoPE
-// partners 64 + 4j .. 64 + 4j + 3 (rows r >= 4), so each rotation pair is in
-// one workgroup; the rows past seg2 (v) follow in order.
+// kEpiRope (kRows = 2 half): the rotated segments [0, seg2) go 64 / half
+// blocks per head, block j of a head holding dims half j .. half j + half - 1
+// (rows r < half) and their RoPE partners 64 + half j .. (rows r >= half), so
+// each rotation pair is in one workgroup; the rows past seg2 (v) follow in
+// order.
 template <int EPI, int kRows>
 __device__ __forceinline__ int out_row(const GemvArgs& a, int r) {
   if (EPI == kEpiRope) {
-    const int nrot = a.seg2 / 8;
+    constexpr int half = kRows / 2;
+    const int nrot = a.seg2 / kRows;
     if (static_cast<int>(blockIdx.x) < nrot) {
-      const int h = blockIdx.x / 16, j = blockIdx.x % 16;
-      return h * 128 + 4 * j + (r & 3) + (r >= 4 ? 64 : 0);
+      const int h = blockIdx.x / (64 / half), j = blockIdx.x % (64 / half);
+      return h * 128 + half * j + (r % half) + (r >= half ? 64 : 0);
     }
     return a.seg2 + (blockIdx.x - nrot) * kRows + r;
   }
@@ -161,7 +180,8 @@ __device__ __forceinline__ const uint8_t* row_ptr(const GemvArgs& a, int r, int&
 template <int EPI, int kRows>
 __device__ __forceinline__ int row_offset(const GemvArgs& a, int r) {
   // kEpiRope: head-paired rows in the rotated segments, plain order for v
-  if (EPI == kEpiRope && static_cast<int>(blockIdx.x) < a.seg2 / 8) return (r & 3) + (r >= 4 ? 64 : 0);
+  if (EPI == kEpiRope && static_cast<int>(blockIdx.x) < a.seg2 / kRows)
+    return (r % (kRows / 2)) + (r >= kRows / 2 ? 64 : 0);
   return r;
 }
 
@@ -193,6 +213,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   // miss after another before the first weight load.
   asm volatile("" ::"s"(a.N), "s"(a.K), "s"(a.seg1), "s"(a.seg2), "s"(a.I), "s"(a.w[0]),
                "s"(a.w[1]), "s"(a.w[2]), "s"(a.x), "s"(a.gamma), "s"(a.d_pos));
+  if (PRO == kProEmbedNorm) asm volatile("" ::"s"(a.tokens), "s"(a.vocab), "s"(a.emb_mult), "s"(a.x_out));
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int K = a.K;
   const int kq = K / 4;                 // bytes of each row this wave reads
@@ -249,7 +270,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   // Measured: 8 rows in flight instead of 4 in the 8-row forms cost 14 us
   // per decode step (all 8 in flight before the SwiGLU form's norm: no
   // change, 18.7 vs 18.8 us per call).
-  constexpr int kD = kRows < kDepth ? kRows : kDepth;
+  constexpr int kDep = EPI == kEpiRope ? kRopeDepth : kDepth;
+  constexpr int kD = kRows < kDep ? kRows : kDep;
   uint4 buf[kD][kChunks];
   const auto load_row = [&](int r, uint4 (&dst)[kChunks]) {
 #pragma unroll
@@ -271,17 +293,60 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     asm volatile("v_mov_b32 %0, 0" : "=v"(z));
     rpos = a.d_pos[z];
   }
+  if (PRO == kProEmbedNorm) {
+    // The token's row depends on two loads (position, token): the weight
+    // rows go out first, then the row and gamma.
 #pragma unroll
-  for (int c = 0; c < kChunks; ++c) {
-    xr[c][0] = *reinterpret_cast<const uint4*>(a.x + koff[c]);
-    xr[c][1] = *reinterpret_cast<const uint4*>(a.x + koff[c] + 8);
-    if (PRO == kProNorm) {
+    for (int r = 0; r < kD; ++r) load_row(r, buf[r]);
+    // The token through the scalar cache (its wait counts scalar loads only,
+    // not the weight rows issued above, which a vector load would queue
+    // behind). A negative position reads no token (a zero row).
+    const int pos_s = __builtin_amdgcn_readfirstlane(rpos);
+    int tok = -1;
+    if (pos_s >= 0) {
+      const int32_t* tp = a.tokens + pos_s;
+      asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(tok) : "s"(tp) : "memory");
+    }
+    const bool valid = tok >= 0 && tok < a.vocab;
+    const uint32_t vmask = valid ? 0xffffffffu : 0u;
+    const uint16_t* xrow = a.x + static_cast<size_t>(valid ? tok : 0) * K;
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+      xr[c][0] = *reinterpret_cast<const uint4*>(xrow + koff[c]);
+      xr[c][1] = *reinterpret_cast<const uint4*>(xrow + koff[c] + 8);
       gr[c][0] = *reinterpret_cast<const uint4*>(a.gamma + koff[c]);
       gr[c][1] = *reinterpret_cast<const uint4*>(a.gamma + koff[c] + 8);
     }
-  }
+    // bf16(emb_mult * e) per element, as the embedding kernel computes it;
+    // workgroup 0 stores the row (the residual stream of the step).
 #pragma unroll
-  for (int r = 0; r < kD; ++r) load_row(r, buf[r]);
+    for (int c = 0; c < kChunks; ++c) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        uint32_t w4[4] = {xr[c][h].x, xr[c][h].y, xr[c][h].z, xr[c][h].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          w4[e] = pack_bf16_hw(a.emb_mult * lo_bf16(w4[e]), a.emb_mult * hi_bf16(w4[e])) & vmask;
+        xr[c][h] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+      }
+      if (blockIdx.x == 0 && cin[c]) {
+        *reinterpret_cast<uint4*>(a.x_out + koff[c]) = xr[c][0];
+        *reinterpret_cast<uint4*>(a.x_out + koff[c] + 8) = xr[c][1];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+      xr[c][0] = *reinterpret_cast<const uint4*>(a.x + koff[c]);
+      xr[c][1] = *reinterpret_cast<const uint4*>(a.x + koff[c] + 8);
+      if (PRO == kProNorm) {
+        gr[c][0] = *reinterpret_cast<const uint4*>(a.gamma + koff[c]);
+        gr[c][1] = *reinterpret_cast<const uint4*>(a.gamma + koff[c] + 8);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < kD; ++r) load_row(r, buf[r]);
+  }
   __builtin_amdgcn_sched_barrier(0);
   // kEpiRope: this thread's cos / sin (as output row threadIdx.x % 8), loaded
   // unconditionally from a clamped position, used in the epilogue.
@@ -293,13 +358,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     res_bits = a.residual[n];
   }
   float rc = 0.0f, rsn = 0.0f;
+  static_assert(PRO != kProEmbedNorm || EPI == kEpiRope, "the embed prologue reads *d_pos");
   if (EPI == kEpiRope) {
     const int i = out_row<EPI, kRows>(a, threadIdx.x % kRows) % 128;
     const long long cp = static_cast<long long>(min(max(rpos, 0), a.max_pos - 1)) * 64 + (i & 63);
     rc = a.cos_t[cp];
     rsn = a.sin_t[cp];
   }
-  if (PRO == kProNorm) {
+  if (PRO != kProNone) {
     double ss = 0.0;
 #pragma unroll
     for (int c = 0; c < kChunks; ++c) {
@@ -387,11 +453,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     // the output unwritten, as the append kernels leave q_rot.
     const int seg = n < a.seg1 ? 0 : 1;
     const int base = seg == 0 ? 0 : a.seg1;
-    const int p = r ^ 4;
+    const int p = r ^ (kRows / 2);
     const float tp = (s_part[0][p] + s_part[1][p]) + (s_part[2][p] + s_part[3][p]);
     const float ya = bf16_to_f32(f32_to_bf16(a.s[seg] * tot));
     const float yp = bf16_to_f32(f32_to_bf16(a.s[seg] * tp));
-    const float b = r < 4 ? -yp : yp;
+    const float b = r < kRows / 2 ? -yp : yp;
     if (rpos >= 0 && rpos < a.max_pos) a.o[seg][n - base] = static_cast<uint16_t>(f32_to_bf16(ya * rc + b * rsn));
     return;
   }
@@ -513,6 +579,11 @@ bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Chunks per wave per row: K / 4 bytes in 1024-byte chunks. Rows per
 // workgroup: 16, or 8 when 16 would leave fewer than two workgroups per CU.
+#ifndef G4_GEMV_ROPE_ROWS
+#define G4_GEMV_ROPE_ROWS 8
+#endif
+constexpr int kRopeRows = G4_GEMV_ROPE_ROWS;
+
 template <int PRO, int EPI>
 int launch_gemv(const GemvArgs& a, const char* what) {
   const int ch = (a.K / 4 + 1023) / 1024;
@@ -529,12 +600,13 @@ int launch_gemv(const GemvArgs& a, const char* what) {
   // More workgroups hide the weight stream's latency better; the norm forms
   // keep 8 (with 4 their per-workgroup row norm costs more than it hides:
   // q|k|v 7.18 -> 7.39), as the RoPE form must (head-paired rows).
-  const int rows = PRO == kProNone && EPI != kEpiRope && EPI != kEpiSwiglu && outputs < 8192 ? 4 : 8;
+  const int rows = EPI == kEpiRope ? kRopeRows
+                   : (PRO == kProNone && EPI != kEpiSwiglu && outputs < 8192 ? 4 : 8);
   const unsigned grid = static_cast<unsigned>(EPI == kEpiSwiglu ? (a.I + rows / 2 - 1) / (rows / 2)
                                                                  : (a.N + rows - 1) / rows);
   const hipStream_t st = stream();
   const auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, 256, 0, st, a); };
-  if constexpr (PRO == kProNone && EPI != kEpiRope && EPI != kEpiSwiglu) {
+  if constexpr ((PRO == kProNone && EPI != kEpiSwiglu) || EPI == kEpiRope) {
     if (rows == 4) {
       if (ch <= 1) go(gemv_kernel<PRO, EPI, 1, 4>);
       else if (ch == 2) go(gemv_kernel<PRO, EPI, 2, 4>);
@@ -620,6 +692,54 @@ int gemv_qkv_rope(int pro, const uint16_t* x, const uint16_t* gamma, float eps,
   a.d_pos = d_pos;
   return pro == kProNorm ? launch_gemv<kProNorm, kEpiRope>(a, what)
                          : launch_gemv<kProNone, kEpiRope>(a, what);
+}
+
+// The first layer's q|k|v with the embedding of the step's token as the
+// prologue (kProEmbedNorm): gemv_qkv_rope's arguments plus the table.
+int gemv_embed_qkv_rope(const int32_t* tokens, const uint16_t* emb, int vocab, float emb_mult,
+                        uint16_t* hidden_out, const uint16_t* gamma, float eps, const uint8_t* wq,
+                        const uint8_t* wk, const uint8_t* wv, float sq, float sk, float sv,
+                        const float* cos_t, const float* sin_t, int max_pos, const int* d_pos,
+                        int Hq, int Hk, int K, uint16_t* q_rot, uint16_t* k_rot, uint16_t* v,
+                        const char* what) {
+  if (tokens == nullptr || emb == nullptr || !al16(emb) || vocab <= 0 || !std::isfinite(emb_mult) ||
+      hidden_out == nullptr || !al16(hidden_out) || gamma == nullptr || !al16(gamma) ||
+      !std::isfinite(eps) || !gemv_k_ok(K) || Hq <= 0 || Hk <= 0 || cos_t == nullptr ||
+      sin_t == nullptr || max_pos <= 0 || d_pos == nullptr || wq == nullptr || wk == nullptr ||
+      wv == nullptr || !al16(wq) || !al16(wk) || !al16(wv) || q_rot == nullptr ||
+      k_rot == nullptr || v == nullptr || !std::isfinite(sq) || !std::isfinite(sk) ||
+      !std::isfinite(sv) || static_cast<long long>(Hq + 2 * Hk) * 128 * K >= (1LL << 40) ||
+      static_cast<long long>(vocab) * K >= (1LL << 40)) {
+    std::fprintf(stderr, "granite4: %s: invalid arguments\n", what);
+    return -1;
+  }
+  GemvArgs a{};
+  a.x = emb;
+  a.gamma = gamma;
+  a.eps = eps;
+  a.w[0] = wq;
+  a.w[1] = wk;
+  a.w[2] = wv;
+  a.s[0] = sq;
+  a.s[1] = sk;
+  a.s[2] = sv;
+  a.o[0] = q_rot;
+  a.o[1] = k_rot;
+  a.o[2] = v;
+  a.seg1 = Hq * 128;
+  a.seg2 = (Hq + Hk) * 128;
+  a.N = (Hq + 2 * Hk) * 128;
+  a.K = K;
+  a.inv_k = (K & (K - 1)) == 0 ? 1.0 / K : 0.0;
+  a.cos_t = cos_t;
+  a.sin_t = sin_t;
+  a.max_pos = max_pos;
+  a.d_pos = d_pos;
+  a.tokens = tokens;
+  a.vocab = vocab;
+  a.emb_mult = emb_mult;
+  a.x_out = hidden_out;
+  return launch_gemv<kProEmbedNorm, kEpiRope>(a, what);
 }
 
 int gemv_swiglu(int pro, const uint16_t* x, const uint16_t* gamma, float eps, const uint8_t* wg,
@@ -715,6 +835,19 @@ int granite4_gemv_qkv_rope(const uint16_t* d_a, const uint8_t* d_wq, const uint8
   return gemv_qkv_rope(kProNone, d_a, nullptr, 0.0f, d_wq, d_wk, d_wv, sq, sk, sv, cos_tbl,
                        sin_tbl, max_pos, d_pos, Hq, Hk, K, d_q_rot, d_k_rot, d_v,
                        "granite4_gemv_qkv_rope");
+}
+
+int granite4_gemv_embed_rmsnorm_qkv_rope(const int32_t* d_tokens, const uint16_t* d_emb,
+                                         int vocab, float emb_mult, uint16_t* d_hidden_out,
+                                         const uint16_t* d_gamma, float eps, const uint8_t* d_wq,
+                                         const uint8_t* d_wk, const uint8_t* d_wv, float sq,
+                                         float sk, float sv, const float* cos_tbl,
+                                         const float* sin_tbl, int max_pos, const int* d_pos,
+                                         int Hq, int Hk, int K, uint16_t* d_q_rot,
+                                         uint16_t* d_k_rot, uint16_t* d_v) {
+  return gemv_embed_qkv_rope(d_tokens, d_emb, vocab, emb_mult, d_hidden_out, d_gamma, eps, d_wq,
+                             d_wk, d_wv, sq, sk, sv, cos_tbl, sin_tbl, max_pos, d_pos, Hq, Hk, K,
+                             d_q_rot, d_k_rot, d_v, "granite4_gemv_embed_rmsnorm_qkv_rope");
 }
 
 int granite4_gemv_rmsnorm_qkv_rope(const uint16_t* d_x, const uint16_t* d_gamma, float eps,

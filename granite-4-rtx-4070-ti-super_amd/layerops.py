@@ -171,6 +171,8 @@ _SIG = {
     "granite4_gemv_qkv": [P, P, P, P, F, F, F, I, I, I, I, P, P, P],
     "granite4_gemv_rmsnorm_qkv": [P, P, F, P, P, P, F, F, F, I, I, I, I, P, P, P],
     "granite4_gemv_rmsnorm_qkv_rope": [P, P, F, P, P, P, F, F, F, P, P, I, P, I, I, I, P, P, P],
+    "granite4_gemv_embed_rmsnorm_qkv_rope": [P, P, I, F, P, P, F, P, P, P, F, F, F, P, P, I, P, I, I,
+                                             I, P, P, P],
     "granite4_gemv_qkv_rope": [P, P, P, P, F, F, F, P, P, I, P, I, I, I, P, P, P],
     "granite4_kernel_silu_gate_up": [P, P, P, F, F, I, I, P],
     "granite4_gemv_rmsnorm_silu_gate_up": [P, P, F, P, P, F, F, I, I, P],
@@ -189,6 +191,8 @@ _RESTYPE = {"granite4_get_stream": P, "granite4_fp8_work_bytes": Z,
             "granite4_attn_split_scratch_bytes": Z, "granite4_kv_pool_create": P,
             "granite4_kv_ctrl_create": P}
 for _name, _args in _SIG.items():
+    if os.environ.get("G4_LAYEROPS_LIB") and not hasattr(_lib, _name):
+        continue  # another build under A/B measurement may predate this entry point
     _fn = getattr(_lib, _name)
     _fn.argtypes = _args
     if _name in _RESTYPE:

@@ -632,6 +632,23 @@ int granite4_gemv_qkv_rope(const uint16_t* d_a, const uint8_t* d_wq, const uint8
                            const float* sin_tbl, int max_pos, const int* d_pos, int Hq, int Hk,
                            int K, uint16_t* d_q_rot, uint16_t* d_k_rot, uint16_t* d_v);
 
+/* Replaces: the decode step's embedding (forward_gpu.cu:2100, embed of the
+ * token d_tokens[*d_pos]) + granite4_gemv_rmsnorm_qkv_rope of the first
+ * layer, in one launch: x = bf16(emb_mult * emb[token]) (a zero row for a
+ * token outside [0, vocab) or a negative position) is the GEMV's input row,
+ * stored to d_hidden_out (the residual stream the step continues with).
+ * Outputs bit-identical to granite4_embed_at_pos then
+ * granite4_gemv_rmsnorm_qkv_rope. No reference counterpart as one call: it
+ * saves the embedding's launch in the decode step. */
+int granite4_gemv_embed_rmsnorm_qkv_rope(const int32_t* d_tokens, const uint16_t* d_emb,
+                                         int vocab, float emb_mult, uint16_t* d_hidden_out,
+                                         const uint16_t* d_gamma, float eps, const uint8_t* d_wq,
+                                         const uint8_t* d_wk, const uint8_t* d_wv, float sq,
+                                         float sk, float sv, const float* cos_tbl,
+                                         const float* sin_tbl, int max_pos, const int* d_pos,
+                                         int Hq, int Hk, int K, uint16_t* d_q_rot,
+                                         uint16_t* d_k_rot, uint16_t* d_v);
+
 /* Replaces: the KV append of the decode step (kv_append_*_kernel,
  * forward_gpu.cu:104-277) followed by granite4_attn_split (rows = 1), in one
  * attention launch, for q and k already rotated (granite4_gemv_rmsnorm_qkv_rope):
@@ -713,7 +730,9 @@ typedef struct Granite4DecodeBuffers {
  * attention, O GEMV + residual, RMSNorm + gate/up GEMV + SwiGLU, down GEMV +
  * residual; then d_hidden_out = RMSNorm(hidden, final_norm) and d_logits =
  * bf16(lm_scale * lm_head . RMSNorm(hidden)) where given (NULL skips them).
- * 5 launches per layer + 1-3. Asynchronous on the calling thread's stream,
+ * 5 launches per layer + 0-2 (the embedding is the prologue of the first
+ * layer's q|k|v launch, granite4_gemv_embed_rmsnorm_qkv_rope). Asynchronous
+ * on the calling thread's stream,
  * no allocation: capturable once in a HIP graph and replayed per token with
  * *d_pos advanced between replays. Outputs are bit-identical to calling
  * granite4_embed_at_pos, granite4_gemv_rmsnorm_qkv_rope,

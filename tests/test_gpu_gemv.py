@@ -260,3 +260,54 @@ def test_rmsnorm_qkv_rope_then_append_attention(bits, group, pos_v, max_pos):
         np.testing.assert_array_equal(a, b)
     if pos_v < max_pos:
         assert np.any(outs[1][0] != 0)  # q_rot was written
+
+
+@pytest.mark.parametrize("mult,tok_kind", [(12.0, "valid"), (1.0, "valid"), (0.37, "invalid"),
+                                           (12.0, "negative_pos")])
+def test_embed_rmsnorm_qkv_rope_fused(mult, tok_kind):
+    """The first layer's q|k|v launch with the embedding as its prologue
+    (granite4_gemv_embed_rmsnorm_qkv_rope): hidden, q_rot, k_rot and v
+    bit-identical to granite4_embed_at_pos then granite4_gemv_rmsnorm_qkv_rope,
+    for embedding multipliers 12 and 1, a token outside the vocabulary (a zero
+    row: the norm of zeros gives zero outputs) and a negative position (no
+    token read; q_rot / k_rot not written, as the rotation skips positions
+    outside the table)."""
+    print(f"embed + rmsnorm qkv rope mult={mult} {tok_kind}", flush=True)
+    K, Hq, Hk, D, vocab = 4096, 32, 8, 128, 5000
+    emb = dev(ol.normal_bf16(0xE1, 0.0, 0.05, vocab * K).reshape(vocab, K))
+    gamma = dev(ol.normal_bf16(0xE2, 1.0, 0.1, K))
+    Wq, Wk, Wv = (dev(ol.fp8_codes(0xE3 + i, (n, K), std=0.5)) for i, n in
+                  enumerate((Hq * D, Hk * D, Hk * D)))
+    sc = (0.004, 0.005, 0.006)
+    cos_t, sin_t = ol.rope_tables(1e7, D, 8192)
+    dcos, dsin = dev(cos_t), dev(sin_t)
+    toks = np.random.default_rng(3).integers(0, vocab, 8192).astype(np.int32)
+    p = 4321 if tok_kind != "negative_pos" else -3
+    if tok_kind == "invalid":
+        toks[p] = vocab + 7
+    d_tok = dev(toks)
+    pos = dev(np.array([p], np.int32))
+    outs = []
+    for fused in (False, True):
+        hid = torch.full((K,), 0x1234, dtype=torch.int16, device="cuda")
+        q_rot = torch.zeros(Hq * D, dtype=torch.int16, device="cuda")
+        k_rot = torch.zeros(Hk * D, dtype=torch.int16, device="cuda")
+        v = empty16(Hk * D)
+        if fused:
+            L.call("granite4_gemv_embed_rmsnorm_qkv_rope", d_tok, emb, vocab, mult, hid, gamma,
+                   1e-5, Wq, Wk, Wv, *sc, dcos, dsin, 8192, pos, Hq, Hk, K, q_rot, k_rot, v)
+        else:
+            if p >= 0:
+                L.call("granite4_embed_at_pos", d_tok, pos, emb, vocab, K, mult, hid)
+            else:
+                hid.zero_()  # the fused form reads no token at a negative position
+            L.call("granite4_gemv_rmsnorm_qkv_rope", hid, gamma, 1e-5, Wq, Wk, Wv, *sc, dcos, dsin,
+                   8192, pos, Hq, Hk, K, q_rot, k_rot, v)
+        outs.append([host(t) for t in (hid, q_rot, k_rot, v)])
+    for a, b in zip(*outs):
+        np.testing.assert_array_equal(a, b)
+    if tok_kind == "valid":
+        want = np.vectorize(ol.lib.g4o_f32_to_bf16, otypes=[np.uint16])(
+            np.float32(mult) * ol.bf16_to_f32(host(emb)[toks[p]]))
+        np.testing.assert_array_equal(outs[1][0], want)
+        assert np.any(outs[1][1] != 0)
