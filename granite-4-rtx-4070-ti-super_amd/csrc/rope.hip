@@ -733,6 +733,49 @@ int granite4_prefill_rope_split_append_k5v4(const uint16_t* qkv, const float* co
 
 // --- multi-session (forward_gpu.cu:3891-3937) -----------------------------------
 
+}  // extern "C"
+
+namespace g4 {
+namespace {
+// embed_multi_v8_kernel (forward_gpu.cu:370-378): row r is the token of
+// session row r at its position (tok[r][slot], slot = tree ? slot[r] :
+// pos[r]), times the embedding multiplier; a token outside [0, vocab)
+// gives a zero row, as granite4_embed_rows.
+__global__ __launch_bounds__(kBlock) void multi_embed_kernel(const GpuMultiRows* mr,
+                                                             const uint16_t* emb, int vocab,
+                                                             int H, float mult, uint16_t* out) {
+  const int r = blockIdx.y;
+  const int j = 8 * (blockIdx.x * kBlock + threadIdx.x);
+  if (j >= H) return;
+  const int slot = mr->tree ? mr->slot[r] : mr->pos[r];
+  const int32_t* tp = mr->tok[r];
+  const int tok = tp != nullptr && slot >= 0 ? tp[slot] : -1;
+  const bool valid = tok >= 0 && tok < vocab;
+  V8 v{{0u, 0u, 0u, 0u}};
+  if (valid) {
+    v = ld8_nt(emb + static_cast<long long>(tok) * H + j);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v.w[e] = pack_bf16_hw(mult * lo_bf16(v.w[e]), mult * hi_bf16(v.w[e]));
+  }
+  st8_nt(out + static_cast<long long>(r) * H + j, v);
+}
+}  // namespace
+}  // namespace g4
+
+extern "C" {
+
+int granite4_multi_embed(const GpuMultiRows* d_rows, int rows, const uint16_t* emb, int vocab,
+                         int H, float mult, uint16_t* out) {
+  if (d_rows == nullptr || emb == nullptr || out == nullptr || rows < 1 ||
+      rows > kMaxVerifyRows || vocab <= 0 || H <= 0 || H % 8 != 0 || !std::isfinite(mult)) {
+    std::fprintf(stderr, "granite4: granite4_multi_embed: invalid arguments\n");
+    return -1;
+  }
+  hipLaunchKernelGGL(multi_embed_kernel, dim3((H / 8 + kBlock - 1) / kBlock, rows), kBlock, 0,
+                     stream(), d_rows, emb, vocab, H, mult, out);
+  return launch_status("granite4_multi_embed");
+}
+
 int granite4_multi_rope(const uint16_t* x, const float* cos_tbl, const float* sin_tbl,
                         const GpuMultiRows* d_rows, int rows, int heads, int d, uint16_t* out) {
   if (x == nullptr || cos_tbl == nullptr || sin_tbl == nullptr || out == nullptr ||

@@ -74,6 +74,16 @@ class DecodeBuffers(_c.Structure):
     _fields_ = [("hidden", P), ("q_rot", P), ("k_rot", P), ("v", P), ("attn_out", P),
                 ("act", P), ("attn_scratch", P)]
 
+
+class BatchBuffers(_c.Structure):
+    """Granite4BatchBuffers (include/granite4_layerops.h)."""
+    _fields_ = [("max_rows", I), ("hidden", P), ("normed", P), ("qkv", P), ("q_rot", P),
+                ("attn", P), ("act", P), ("gu", P), ("codes", P), ("act_codes", P),
+                ("scales", P), ("fp8_work", P), ("attn_scratch", P)]
+
+
+OPS_BF16, OPS_FP8 = 0, 1
+
 _SIG = {
     "granite4_set_stream": [P],
     "granite4_get_stream": [],
@@ -179,6 +189,11 @@ _SIG = {
     "granite4_gemv_rmsnorm_qkv_rope_append": [P, P, F, P, P, P, F, F, F, P, P, I, P, P, I, I, I, I,
                                               P, P, P, P, P, I],
     "granite4_decode_step": [_c.POINTER(DecodeModel), _c.POINTER(DecodeBuffers), P, P, P, P, P],
+    "granite4_prefill_layers": [_c.POINTER(DecodeModel), _c.POINTER(BatchBuffers), P, I, I, P, I,
+                                P, P],
+    "granite4_decode_step_multi": [_c.POINTER(DecodeModel), _c.POINTER(BatchBuffers), P, I, I, P,
+                                   P],
+    "granite4_multi_embed": [P, I, P, I, I, F, P],
     "granite4_host_fp8_encode": [P, _c.c_size_t, F, P],
     "granite4_host_kv_codes": [P, _c.c_size_t, F, I, P],
     "granite4_selftest_bf16": [P],
@@ -267,6 +282,62 @@ def attn_sync_status(scratch, clear=False):
     if rc < 0:
         raise Granite4Error("granite4_attn_sync_status failed")
     return rc
+
+
+class LayerSteps:
+    """granite4_prefill_layers / granite4_decode_step_multi over torch
+    tensors: the model as DecodeStep takes it (`layers` dicts, keyword model
+    fields); device buffers for up to `max_rows` rows are allocated once.
+    prefill(tokens, start, rows, pt, ops) and multi(d_rows, rows, ops) launch
+    on the current library stream (capturable)."""
+
+    def __init__(self, layers, H, I, Hq, Hk, vocab, emb, cos, sin, max_rows, eps=1e-5,
+                 emb_mult=1.0, resid_mult=1.0, attn_scale=1.0 / 128, final_norm=None,
+                 lm_head=None, lm_scale=1.0, kv_bits=16, kv_group=128, kv_stride=0,
+                 device="cuda"):
+        self._keep = [layers, emb, cos, sin, final_norm, lm_head]
+        arr = (DecodeLayer * len(layers))()
+        for i, ly in enumerate(layers):
+            for f in DecodeStep._LAYER_PTRS:
+                setattr(arr[i], f, _ptr(ly.get(f)))
+            for f in ("sq", "sk", "sv", "so", "sg", "su", "sd"):
+                setattr(arr[i], f, float(ly[f]))
+        self._arr = arr
+        self.model = DecodeModel(len(layers), H, I, Hq, Hk, vocab, eps, emb_mult, resid_mult,
+                                 attn_scale, _ptr(emb), arr, _ptr(final_norm), _ptr(lm_head),
+                                 lm_scale, _ptr(cos), _ptr(sin), cos.shape[0], kv_bits, kv_group,
+                                 kv_stride)
+        bf, R = torch.bfloat16, max_rows
+        nq, nqkv = Hq * 128, (Hq + 2 * Hk) * 128
+        self.hidden = torch.empty((R, H), dtype=bf, device=device)
+        self.normed = torch.empty((R, H), dtype=bf, device=device)
+        self.qkv = torch.empty((R, nqkv), dtype=bf, device=device)
+        self.q_rot = torch.empty((R, nq), dtype=bf, device=device)
+        self.attn = torch.empty((R, nq), dtype=bf, device=device)
+        self.act = torch.empty((R, I), dtype=bf, device=device)
+        self.gu = torch.empty((R, 2 * I), dtype=torch.float32, device=device)
+        self.codes = torch.empty((R, H), dtype=torch.uint8, device=device)
+        self.act_codes = torch.empty((R, I), dtype=torch.uint8, device=device)
+        self.scales = torch.zeros(2, dtype=torch.float32, device=device)
+        self.fp8_work = fp8_workspace(R, device)
+        self.attn_scratch = torch.zeros(
+            _lib.granite4_attn_split_scratch_bytes(Hq, min(R, MAX_VERIFY_ROWS), kv_stride),
+            dtype=torch.uint8, device=device)
+        self.buffers = BatchBuffers(R, *[_ptr(t) for t in (
+            self.hidden, self.normed, self.qkv, self.q_rot, self.attn, self.act, self.gu,
+            self.codes, self.act_codes, self.scales, self.fp8_work, self.attn_scratch)])
+
+    def prefill(self, tokens, start, rows, pt=None, ops=OPS_BF16, hidden_out=None, logits=None):
+        _check(_lib.granite4_prefill_layers(_c.byref(self.model), _c.byref(self.buffers),
+                                            _ptr(tokens), int(start), int(rows), _ptr(pt),
+                                            int(ops), _ptr(hidden_out), _ptr(logits)),
+               "granite4_prefill_layers")
+
+    def multi(self, d_rows, rows, ops=OPS_BF16, hidden_out=None, logits=None):
+        _check(_lib.granite4_decode_step_multi(_c.byref(self.model), _c.byref(self.buffers),
+                                               _ptr(d_rows), int(rows), int(ops),
+                                               _ptr(hidden_out), _ptr(logits)),
+               "granite4_decode_step_multi")
 
 
 class DecodeStep:

@@ -191,6 +191,12 @@ int granite4_multi_rope_append(const uint16_t* q, const uint16_t* k, const uint1
 int granite4_multi_kv_append(const uint16_t* k, const uint16_t* v, int bits, void* cache_k,
                              void* cache_v, float* k_scale, float* v_scale,
                              const GpuMultiRows* d_rows, int rows, int stride, int Hk, int d);
+/* embed_multi_v8_kernel (forward_gpu.cu:370-378, the embedding of
+ * forward_multi_step :2517-2524): out[r] = bf16(mult * emb[tok]) with tok =
+ * d_rows->tok[r][tree ? slot[r] : pos[r]]; a token outside [0, vocab) (or a
+ * NULL token array) writes a zero row. H % 8 == 0, rows <= 16. */
+int granite4_multi_embed(const GpuMultiRows* d_rows, int rows, const uint16_t* emb, int vocab,
+                         int H, float mult, uint16_t* out);
 
 /* ===========================================================================
  * Fused entry points the MI355X build adds (no single reference function;
@@ -742,6 +748,77 @@ typedef struct Granite4DecodeBuffers {
 int granite4_decode_step(const Granite4DecodeModel* model, const Granite4DecodeBuffers* buffers,
                          const int32_t* d_tokens, const int* d_pos, const int* d_pt,
                          uint16_t* d_hidden_out, uint16_t* d_logits);
+
+/* ---------------------------------------------------------------------------
+ * Batched layer sequences: a prompt chunk (forward_prefill) and one decode
+ * position of several sessions (forward_multi_step), over the model of
+ * granite4_decode_step.
+ * ------------------------------------------------------------------------- */
+
+/* Activation forms of the batched sequences: the reference's bf16
+ * activations (GEMMs with a bf16 A), or FP8 e4m3 activations with
+ * per-tensor scales on the RMSNorm and SwiGLU outputs (this library's fused
+ * RMSNorm -> FP8 and gate|up + SwiGLU -> FP8 ops and its FP8 GEMMs). */
+#define GRANITE4_OPS_BF16 0
+#define GRANITE4_OPS_FP8 1
+
+/* Caller-owned device buffers for up to max_rows rows (max_rows <= 16 for
+ * granite4_decode_step_multi): hidden, normed [max_rows][H]; qkv
+ * [max_rows][(Hq + 2 Hk) 128]; q_rot, attn [max_rows][Hq 128]; act
+ * [max_rows][I] (bf16). Bf16 form: gu f32 [max_rows][2I]. FP8 form: codes
+ * [max_rows][H], act_codes [max_rows][I], scales f32 [2], fp8_work
+ * GRANITE4_FP8_WORK_BYTES(max_rows) zero-filled once. The multi step:
+ * attn_scratch granite4_attn_split_scratch_bytes(Hq, max_rows, kv_stride),
+ * zero-filled once. Unused members may be NULL. */
+typedef struct Granite4BatchBuffers {
+  int max_rows;
+  uint16_t* hidden;
+  uint16_t* normed;
+  uint16_t* qkv;
+  uint16_t* q_rot;
+  uint16_t* attn;
+  uint16_t* act;
+  float* gu;
+  uint8_t* codes;
+  uint8_t* act_codes;
+  float* scales;
+  void* fp8_work;
+  void* attn_scratch;
+} Granite4BatchBuffers;
+
+/* Replaces: forward_prefill (forward_gpu.cu:2751-2863) for one chunk:
+ * positions start .. start + rows - 1 of one sequence (tokens
+ * d_tokens[start ..], bounds-checked as granite4_embed_rows), every layer's
+ * K / V appended to its arena through the row table d_pt (NULL: row =
+ * position), causal attention over the pool (granite4_prefill_attn), then
+ * d_hidden_out = RMSNorm(hidden, final_norm) [rows][H] and d_logits =
+ * bf16(lm_scale * lm_head . that) [rows][vocab] where given. ops: one of
+ * GRANITE4_OPS_*. The FP8 form needs the gate and up weights as one
+ * [2I][H] block (wu == wg + I * H). Per layer: 9 launches (bf16; 10 when
+ * q, k and v are not one [nqkv][H] block) or 8 (FP8). Asynchronous, no
+ * allocation; -1 before any launch on invalid arguments. No reference
+ * counterpart as one exported call (the reference's is internal). */
+int granite4_prefill_layers(const Granite4DecodeModel* model, const Granite4BatchBuffers* buffers,
+                            const int32_t* d_tokens, int start, int rows, const int* d_pt,
+                            int ops, uint16_t* d_hidden_out, uint16_t* d_logits);
+
+/* Replaces: forward_multi_step (forward_gpu.cu:2486-2623) up to the logits:
+ * one decode position for each of `rows` (<= 16) sessions of the device
+ * descriptor d_rows (row r: position pos[r], token tok[r][pos[r]], page
+ * table pt[r]; draft-tree descriptors, tree != 0, are not supported).
+ * Embedding (granite4_multi_embed), then per layer: RMSNorm, q / k / v
+ * GEMMs, RoPE + the KV append of every row (granite4_multi_rope_append),
+ * the split-KV attention of the rows at their own positions and page tables
+ * (granite4_attn_paged with row_pos / row_pt), O + residual, RMSNorm, gate /
+ * up + SwiGLU, down + residual; then the optional final norm and logits.
+ * ops: one of GRANITE4_OPS_*. The KV format must have per-row scales (group
+ * 128) or be bf16. Sampling and advancing the positions are the caller's
+ * (the reference's argmax_rows_kernel and multi_scatter_advance_kernel).
+ * Asynchronous, no allocation, graph-capturable; -1 before any launch on
+ * invalid arguments. */
+int granite4_decode_step_multi(const Granite4DecodeModel* model,
+                               const Granite4BatchBuffers* buffers, const GpuMultiRows* d_rows,
+                               int rows, int ops, uint16_t* d_hidden_out, uint16_t* d_logits);
 
 #ifdef __cplusplus
 }  /* extern "C" */
