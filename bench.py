@@ -82,7 +82,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline + decode only")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=["t512", "t8192", "decode", "t8", "stress", "tN", "probe", "floor", "t1",
-                                       "attn", "gemm", "decode_gemv", "decode_trace"],
+                                       "attn", "gemm", "decode_gemv", "decode_trace",
+                                       "layer_steps"],
                     help="run one configuration and print its detail (profiling runs)")
     ap.add_argument("--T", type=int, default=1024, help="token count for --only tN")
     ap.add_argument("--attn-case", default=None, help="run only this bench_attn case")
@@ -255,6 +256,8 @@ def main():
             r = measure_ops(args.T, 8, 128, 0, 8, args.steps, args.warmup)
         elif args.only == "decode_gemv":
             r = bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream)
+        elif args.only == "layer_steps":
+            r = bench_layer_steps(torch, L, gen, cos_t, sin_t, emb, gamma, stream)
         elif args.only == "decode_trace":
             r = bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream,
                                   trace_replays=25)
@@ -924,6 +927,91 @@ def bench_multi8(torch, L, randn, cos_t, sin_t, gamma, work, gen, stream, timed,
         out[name + "_us"] = round(timed(fn, 200, 20, sets) * 1e3, 3)
     out["layer_us"] = round(2 * out["add_rmsnorm_fp8_us"] + out["swiglu_fp8_us"] +
                             out["multi_rope_append_int8_us"], 3)
+    return out
+
+
+def bench_layer_steps(torch, L, gen, cos_t, sin_t, emb, gamma, stream):
+    """The engine's batched layer sequences through their single calls:
+    granite4_prefill_layers (forward_prefill, one chunk) per layer at T=512
+    (config 3: int8 KV, positions 0..511) and T=8192 (config 4: K5V4 group
+    32, positions 57344..65535, attending to every earlier position), and granite4_decode_step_multi
+    (forward_multi_step) for config 2's 8 sessions at random positions in
+    [0, 65536) over 40 layers (int8 KV, each session's page table over its
+    own 4096 pages of the pool). Both activation forms; random fp8 weights of
+    the 8B shapes (q|k|v and gate|up one block each). Each timed as a HIP
+    graph (graphs_us)."""
+    dev = "cuda"
+
+    def codes(*shape):
+        c = torch.randint(0, 0x7F, shape, generator=gen, device=dev, dtype=torch.int32)
+        sign = torch.randint(0, 2, shape, generator=gen, device=dev, dtype=torch.int32) << 7
+        return (c | sign).to(torch.uint8)
+
+    def layers(n, bits, group, stride):
+        out = []
+        for _ in range(n):
+            wqkv = codes((HQ + 2 * HK) * D, H)
+            wgu = codes(2 * I, H)
+            a = L.KvArena(bits, HK, stride, group=group)
+            out.append({"attn_norm": gamma, "ffn_norm": gamma, "wq": wqkv[:HQ * D],
+                        "wk": wqkv[HQ * D:(HQ + HK) * D], "wv": wqkv[(HQ + HK) * D:],
+                        "wo": codes(H, HQ * D), "wg": wgu[:I], "wu": wgu[I:], "wd": codes(H, I),
+                        "sq": 1 / 512, "sk": 1 / 512, "sv": 1 / 512, "so": 1 / 512,
+                        "sg": 1 / 512, "su": 1 / 512, "sd": 1 / 512, "cache_k": a.k,
+                        "cache_v": a.v, "k_scale": a.k_scale, "v_scale": a.v_scale, "_a": a})
+        return out
+
+    out = {}
+    toks = torch.randint(0, VOCAB, (65536,), dtype=torch.int32, device=dev, generator=gen)
+    nl = 4
+    for T, bits, group, pos0, key in ((512, 8, 128, 0, "T512_int8"),
+                                      (8192, 5, 32, 57344, "T8192_k5v4g32")):
+        # one sequence, arena row = position: the chunk at pos0 attends to
+        # all pos0 earlier positions (zero-filled codes and scales)
+        stride, pt = pos0 + T, None
+        ly = layers(nl, bits, group, stride)
+        st = L.LayerSteps(ly, H, I, HQ, HK, VOCAB, emb, cos_t, sin_t, T, eps=1e-5,
+                          resid_mult=0.22, kv_bits=bits, kv_group=group, kv_stride=stride)
+        t = graphs_us(torch, L, stream, {
+            "fp8": lambda: st.prefill(toks, pos0, T, pt, L.OPS_FP8),
+            "bf16": lambda: st.prefill(toks, pos0, T, pt, L.OPS_BF16)}, rounds=3, reps=3)
+        out[f"prefill_{key}"] = {"layers_timed": nl,
+                                 "fp8_us_per_layer": round(t["fp8"] / nl, 1),
+                                 "bf16_us_per_layer": round(t["bf16"] / nl, 1)}
+        del st, ly
+        torch.cuda.empty_cache()
+    n, pages_per = 8, 4096
+    pool_pages = n * pages_per
+    stride = pool_pages * 16
+    ly = layers(40, 8, 128, stride)
+    rs = np.random.default_rng(5)
+    pos = rs.integers(0, 65536, n).astype(np.int32)
+    perm = torch.randperm(pool_pages, generator=gen, device=dev).to(torch.int64)
+    pts = [(perm[i * pages_per:(i + 1) * pages_per, None] * 16 +
+            torch.arange(16, device=dev)[None, :]).reshape(-1).to(torch.int32).contiguous()
+           for i in range(n)]
+    tok_rows = [torch.randint(0, VOCAB, (65536,), dtype=torch.int32, device=dev, generator=gen)
+                for _ in range(n)]
+    M = L.multi_rows_struct()()
+    M.n = n
+    for i in range(n):
+        M.pos[i] = int(pos[i])
+        M.pt[i] = pts[i].data_ptr()
+        M.tok[i] = tok_rows[i].data_ptr()
+    d_m = torch.from_numpy(np.frombuffer(bytes(M), np.uint8).copy()).to(dev)
+    st = L.LayerSteps(ly, H, I, HQ, HK, VOCAB, emb, cos_t, sin_t, n, eps=1e-5, resid_mult=0.22,
+                      kv_bits=8, kv_group=128, kv_stride=stride)
+    t = graphs_us(torch, L, stream, {"fp8": lambda: st.multi(d_m, n, L.OPS_FP8),
+                                     "bf16": lambda: st.multi(d_m, n, L.OPS_BF16)},
+                  rounds=3, reps=3)
+    ctx = int(pos.sum()) + n
+    out["decode_T8_multi_40_layers"] = {
+        "sessions": n, "positions": [int(p) for p in pos], "fp8_us": round(t["fp8"], 1),
+        "bf16_us": round(t["bf16"], 1),
+        "weight_GB": round(40 * ((HQ + 2 * HK) * D * H + 2 * I * H + H * HQ * D + H * I) / 1e9, 2),
+        "kv_read_GB": round(40 * ctx * HK * 2 * (D + 4) / 1e9, 2)}
+    del st, ly
+    torch.cuda.empty_cache()
     return out
 
 
