@@ -83,7 +83,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=["t512", "t8192", "decode", "t8", "stress", "tN", "probe", "floor", "t1",
                                        "attn", "gemm", "decode_gemv", "decode_trace",
-                                       "layer_steps"],
+                                       "layer_steps", "fp8_trace"],
                     help="run one configuration and print its detail (profiling runs)")
     ap.add_argument("--T", type=int, default=1024, help="token count for --only tN")
     ap.add_argument("--attn-case", default=None, help="run only this bench_attn case")
@@ -256,6 +256,8 @@ def main():
             r = measure_ops(args.T, 8, 128, 0, 8, args.steps, args.warmup)
         elif args.only == "decode_gemv":
             r = bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream)
+        elif args.only == "fp8_trace":
+            r = bench_fp8_trace(torch, L, randn, gamma)
         elif args.only == "layer_steps":
             r = bench_layer_steps(torch, L, gen, cos_t, sin_t, emb, gamma, stream)
         elif args.only == "decode_trace":
@@ -927,6 +929,51 @@ def bench_multi8(torch, L, randn, cos_t, sin_t, gamma, work, gen, stream, timed,
         out[name + "_us"] = round(timed(fn, 200, 20, sets) * 1e3, 3)
     out["layer_us"] = round(2 * out["add_rmsnorm_fp8_us"] + out["swiglu_fp8_us"] +
                             out["multi_rope_append_int8_us"], 3)
+    return out
+
+
+def bench_fp8_trace(torch, L, randn, gamma):
+    """Per-workgroup timestamps of the single-launch FP8 kernels, from a
+    measurement build of the library (build.py --define G4_TRACE_FP8, loaded
+    with G4_LAYEROPS_LIB): µs after the first workgroup's start, [min,
+    median, max] over the workgroups, of the last of 4 calls. Marks: start,
+    first part held, all held / streamed once, grid maximum known, (swiglu:
+    held part encoded), end."""
+    work = L.fp8_workspace(65536)
+    off = L.fp8_work_bytes(0)
+    out = {}
+
+    def marks(n):
+        torch.cuda.synchronize()
+        tr = work[off:off + 8 * 8 * 1024].view(torch.int64).cpu().numpy().reshape(-1, 8)[:, :n]
+        tr = tr[tr[:, 0] > 0]
+        if len(tr) == 0:
+            return "no marks: load a build made with --define G4_TRACE_FP8"
+        rel = (tr - tr[:, 0].min()) / 100.0
+        return {"workgroups": len(tr),
+                "marks_us": [[round(float(np.min(rel[:, i])), 1), round(float(np.median(rel[:, i])), 1),
+                              round(float(np.max(rel[:, i])), 1)] for i in range(n)]}
+
+    gu = [randn((8192, 2 * I)) for _ in range(2)]
+    codes = torch.empty((8192, I), dtype=torch.uint8, device="cuda")
+    scale = torch.empty(1, dtype=torch.float32, device="cuda")
+    for i in range(4):
+        if i == 3:
+            work[off:].zero_()
+        L.call("granite4_swiglu_fp8", gu[i % 2], 8192, I, codes, scale, work, None)
+    out["swiglu_fp8_T8192"] = marks(6)
+    del gu, codes
+    for T in (8192, 4096, 512):
+        xs = [randn((T, H)) for _ in range(2)]
+        br = randn((T, H))
+        ro = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+        c = torch.empty((T, H), dtype=torch.uint8, device="cuda")
+        for i in range(4):
+            if i == 3:
+                work[off:].zero_()
+            L.call("granite4_add_rmsnorm_fp8", xs[i % 2], br, 1.0, gamma, 1e-5, T, H, ro, c, scale,
+                   work)
+        out[f"add_rmsnorm_fp8_T{T}"] = marks(5)
     return out
 
 

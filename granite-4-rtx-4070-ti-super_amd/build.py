@@ -74,7 +74,13 @@ if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=8)
     ap.add_argument("--out", default=LIB, help="output library path")
+    ap.add_argument("--define", action="append", default=[],
+                    help="extra preprocessor definition (measurement builds, e.g. G4_TRACE_FP8)")
+    ap.add_argument("--build-dir", default=None, help="object directory (default _build/)")
     a = ap.parse_args()
+    HIPFLAGS += [f"-D{d}" for d in a.define]
+    if a.build_dir:
+        BUILD = os.path.abspath(a.build_dir)
     try:
         build(a.jobs, out=os.path.abspath(a.out))
     except RuntimeError as e:

@@ -45,6 +45,21 @@ __host__ __device__ inline unsigned* work_err(void* w) {
 __host__ __device__ inline unsigned long long* work_result(void* w) {
   return reinterpret_cast<unsigned long long*>(static_cast<char*>(w) + kWorkGenOff + 128);
 }
+// Measurement builds (-DG4_TRACE_FP8, never the shipped library): the
+// single-launch FP8 kernels store s_memrealtime (100 MHz) at fixed points,
+// 8 slots per workgroup, into the workspace's per-row area
+// (bench.py --only fp8_trace reads them back).
+#ifdef G4_TRACE_FP8
+// gs: the launch's GridSync (its generation word sits at kWorkGenOff).
+#define G4_TRACE_MARK(gs, i)                                                               \
+  if (threadIdx.x == 0)                                                                    \
+  reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>((gs).gen) - kWorkGenOff +  \
+                                        kWorkRowOff)[blockIdx.x * 8 + (i)] =               \
+      __builtin_amdgcn_s_memrealtime()
+#else
+#define G4_TRACE_MARK(gs, i)
+#endif
+
 __host__ __device__ inline float* work_row_r(void* w) {
   return reinterpret_cast<float*>(static_cast<char*>(w) + kWorkRowOff);
 }

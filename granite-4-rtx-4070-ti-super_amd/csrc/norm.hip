@@ -370,6 +370,7 @@ void norm_fp8_fused_kernel(NormArgs a, GridSync gs) {
                "s"(a.res_out), "s"(a.eps), "s"(gs.gen), "s"(gs.slots), "s"(gs.result),
                "s"(gs.blocks));
   __shared__ uint4 s_y[HL > 0 ? HL : 1][VPL][kBlock];
+  G4_TRACE_MARK(gs, 0);
   const unsigned tag = grid_sync_tag(gs);
   V8 y[HR > 0 ? HR : 1][VPL];
   // max |y| on the bf16 bit patterns, two per v_pk_max_u16 (for
@@ -383,6 +384,7 @@ void norm_fp8_fused_kernel(NormArgs a, GridSync gs) {
     if (rg >= a.rows) break;
     NormRow<VPL, 4> t;
     norm_row_front<VPL, 4, true>(a, rg, t);
+    if (h == 0) G4_TRACE_MARK(gs, 1);
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
       V8 yv;
@@ -423,7 +425,9 @@ void norm_fp8_fused_kernel(NormArgs a, GridSync gs) {
       }
     }
   }
+  G4_TRACE_MARK(gs, 2);
   const Fp8Enc f = fp8_scale_of(grid_max(m, gs, tag));
+  G4_TRACE_MARK(gs, 3);
   if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = f.s;
   const int part = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int nvec = a.cols >> 3;
@@ -451,6 +455,7 @@ void norm_fp8_fused_kernel(NormArgs a, GridSync gs) {
   };
   if (f.fast) encode(std::true_type{});
   else encode(std::false_type{});
+  G4_TRACE_MARK(gs, 4);
 }
 
 // Held rows per workgroup of the two single-launch forms: VGPRs only, and

@@ -286,6 +286,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(G4_SW_WP
   asm volatile("" ::"s"(a.gu), "s"(a.rows), "s"(a.I), "s"(a.inv_nv), "s"(a.act), "s"(a.codes),
                "s"(gs.gen), "s"(gs.slots), "s"(gs.result), "s"(gs.blocks));
   __shared__ uint4 s_hold[kHoldL > 0 ? kHoldL : 1][kBlock];
+  G4_TRACE_MARK(gs, 0);
   const unsigned tag = grid_sync_tag(gs);
   const int nv = a.I >> 3;
   const int total = a.rows * nv;
@@ -325,6 +326,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(G4_SW_WP
       }
     }
   }
+  G4_TRACE_MARK(gs, 1);
   // The streamed rest: max only (cached loads: part is still cached when
   // the second sweep comes back to it).
   const int vs = v0 + kHold * step;
@@ -338,7 +340,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(G4_SW_WP
       take(x[j], v + j * step, o);
     }
   }
+  G4_TRACE_MARK(gs, 2);
   const Fp8Enc f = fp8_enc_of(fp8_scale_for(grid_max(m, gs, tag)));
+  G4_TRACE_MARK(gs, 3);
   if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = f.s;
   const auto encode = [&](auto fast_tag) {
     constexpr bool kFast = decltype(fast_tag)::value;
@@ -360,6 +364,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(G4_SW_WP
       const uint2 c = fp8x8_encode_bf16<kFast>(o, f);
       st_u32x2_nt(a.codes + 8LL * v, c.x, c.y);
     }
+    G4_TRACE_MARK(gs, 4);
     for (int v = vs; v < total; v += kStreamU * step) {
       GuRaw<false> x[kStreamU];
 #pragma unroll
@@ -378,6 +383,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(G4_SW_WP
   };
   if (f.fast) encode(std::true_type{});
   else encode(std::false_type{});
+  G4_TRACE_MARK(gs, 5);
 }
 
 // Grid of the held single-launch form (every workgroup resident, one
