@@ -172,7 +172,7 @@ int granite4_rope_tables_free(float* d_cos, float* d_sin) {
 }
 
 int granite4_set_fp8_launch_mode(int mode) {
-  if (mode != 0 && mode != 1) return -1;
+  if (mode != 0 && mode != 1 && mode != 2) return -1;
   return g_fp8_mode.exchange(mode);
 }
 

@@ -79,8 +79,23 @@ int launch_status(const char* what);
 int resident_blocks(const void* kernel, int threads);
 
 // Process-wide FP8 launch mode (granite4_set_fp8_launch_mode): 0 = single
-// launch where the tensor fits, 1 = always two launches.
+// launch where the tensor fits, 1 = always two launches, 2 = single launch
+// through hipLaunchCooperativeKernel.
 int fp8_launch_mode();
+
+// Launches a kernel that synchronises its grid (the single-launch FP8
+// forms): a plain launch, or in FP8 launch mode 2 a cooperative launch, for
+// which the runtime checks that every workgroup can be resident at once.
+template <class K, class... A>
+void launch_grid_sync(K kern, unsigned grid, unsigned block, hipStream_t st, A... args) {
+  if (fp8_launch_mode() == 2) {
+    void* p[] = {static_cast<void*>(&args)...};
+    (void)hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kern), dim3(grid), dim3(block),
+                                     p, 0, st);
+    return;
+  }
+  hipLaunchKernelGGL(kern, grid, block, 0, st, args...);
+}
 
 // The current device's static FP8 scratch (granite4_add_rmsnorm_fp8_noalloc):
 // its device address, set up on first use; nullptr on failure.

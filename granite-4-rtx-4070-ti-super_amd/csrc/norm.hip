@@ -525,7 +525,7 @@ bool launch_fused_vpl(const NormArgs& a, const GridSync& gs, int nvec) {
     const unsigned grid = static_cast<unsigned>(a.rows < cap ? a.rows : cap);
     GridSync g = gs;
     g.blocks = static_cast<int>(grid);
-    hipLaunchKernelGGL(kern, grid, kBlock, 0, stream(), a, g);
+    launch_grid_sync(kern, grid, kBlock, stream(), a, g);
     return true;
   };
   if (nvec <= 256) return go(norm_fp8_fused_kernel<1, HR, HL>);
@@ -540,7 +540,7 @@ bool launch_norm_fp8_fused(const uint16_t* x, const uint16_t* branch, float mult
                            float eps, int rows, int cols, uint16_t* res_out, uint8_t* codes,
                            float* scale, void* work) {
   const int nvec = cols / 8;
-  if (fp8_launch_mode() != 0 || !norm_vector_path(rows, cols))
+  if (fp8_launch_mode() == 1 || !norm_vector_path(rows, cols))
     return false;
   NormArgs a{x, branch, mult, w, eps, rows, cols, res_out, nullptr, codes, scale, nullptr, 0,
              nullptr, 0.0};

@@ -242,7 +242,7 @@ __global__ __launch_bounds__(kFusedThreads) void swiglu_fp8_fused_kernel(SwArgs 
 // measured against 1024-thread workgroups on one per CU, T=512 14.0 vs
 // 14.8 us and T=8 5.9 vs 7.4 us.
 unsigned fused_grid(long long vectors) {
-  if (fp8_launch_mode() != 0) return 0;
+  if (fp8_launch_mode() == 1) return 0;
   const int resident = resident_blocks(reinterpret_cast<const void*>(swiglu_fp8_fused_kernel),
                                        kFusedThreads);
   const int cap = resident < kMaxPartials ? resident : kMaxPartials;
@@ -390,7 +390,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(G4_SW_WP
 // partial slot each), or 0 when the device cannot hold a useful grid or the
 // indices would overflow.
 unsigned hold_grid(long long vectors) {
-  if (fp8_launch_mode() != 0) return 0;
+  if (fp8_launch_mode() == 1) return 0;
   const int resident = resident_blocks(reinterpret_cast<const void*>(swiglu_fp8_hold_kernel), kBlock);
   const int grid = resident < kMaxPartials ? resident : kMaxPartials;
   if (grid < kCUs) return 0;
@@ -512,7 +512,7 @@ int granite4_swiglu_fp8(const uint16_t* d_gu, int rows, int I, uint8_t* d_codes,
     f.scale_out = d_scale;
     const GridSync gs{work_slots(d_work), work_gen(d_work), work_result(d_work),
                       static_cast<int>(fgrid), work_err(d_work), fp8_sync_spin_limit()};
-    hipLaunchKernelGGL(swiglu_fp8_fused_kernel, fgrid, kFusedThreads, 0, stream(), f, gs);
+    launch_grid_sync(swiglu_fp8_fused_kernel, fgrid, kFusedThreads, stream(), f, gs);
     return launch_status("granite4_swiglu_fp8");
   }
   const unsigned hgrid = hold_grid(vectors);
@@ -523,7 +523,7 @@ int granite4_swiglu_fp8(const uint16_t* d_gu, int rows, int I, uint8_t* d_codes,
     h.scale_out = d_scale;
     const GridSync gs{work_slots(d_work), work_gen(d_work), work_result(d_work),
                       static_cast<int>(hgrid), work_err(d_work), fp8_sync_spin_limit()};
-    hipLaunchKernelGGL(swiglu_fp8_hold_kernel, hgrid, kBlock, 0, stream(), h, gs);
+    launch_grid_sync(swiglu_fp8_hold_kernel, hgrid, kBlock, stream(), h, gs);
     return launch_status("granite4_swiglu_fp8");
   }
   const unsigned grid = grid_for(vectors, kMaxPartials);

@@ -244,9 +244,13 @@ int granite4_add_rmsnorm(const uint16_t* d_res, const uint16_t* d_branch, float 
 size_t granite4_fp8_work_bytes(int rows);
 /* FP8 launch form for granite4_add_rmsnorm_fp8 / granite4_swiglu_fp8, process
  * wide: 0 (default) = one launch when the tensor fits the registers of one
- * resident grid, else two; 1 = always two launches. Both forms give identical
- * codes and scales. Returns the previous mode, -1 for another value. No
- * reference counterpart (a tuning switch).
+ * resident grid, else two; 1 = always two launches; 2 = as 0, with the single
+ * launch made through hipLaunchCooperativeKernel, so that the runtime
+ * guarantees the co-residency instead of the occupancy query (measured on
+ * MI355X: about 92 us more per launch than mode 0, in a HIP graph or not, and
+ * graph-capturable). Every form gives identical codes and scales. Returns the
+ * previous mode, -1 for another value. No reference counterpart (a tuning
+ * switch).
  *
  * The single-launch form's workgroups meet once inside the launch, so it
  * needs every workgroup of its grid resident at the same time. The library
@@ -260,11 +264,12 @@ size_t granite4_fp8_work_bytes(int rows);
 int granite4_set_fp8_launch_mode(int mode);
 /* Reads the workspace's sticky synchronisation-error word: 0 if no
  * single-launch FP8 call on d_work gave up waiting since the last clear, 1
- * if one did (its scale is NaN), -1 on a HIP error. clear != 0 resets the
- * word and the workspace's synchronisation slots to their zero-filled start
- * (a wait that gave up can leave a slot tagged for a later call; until the
- * clear, later calls on the workspace are not reliable). Synchronises the calling thread's stream (not for use inside graph
- * capture). d_work NULL reads the current device's static scratch of
+ * if one did (that call's codes and scale are invalid; its scale is NaN where
+ * the give-up reached workgroup 0), -1 on a HIP error. Every call advances
+ * the workspace's generation, give-ups included, so later calls are correct
+ * without a clear. clear != 0 resets the word and the synchronisation slots
+ * to their zero-filled start. Synchronises the calling thread's stream (not
+ * for use inside graph capture). d_work NULL reads the current device's static scratch of
  * granite4_add_rmsnorm_fp8_noalloc. No reference counterpart. */
 int granite4_fp8_sync_status(void* d_work, int clear);
 /* Test hook: sets the process-wide poll limit of the single-launch forms'

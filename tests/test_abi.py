@@ -75,11 +75,13 @@ def test_mode_switches_return_previous_and_reject_others():
     """The process-wide launch switches (FP8 single launch, attention combine
     in the split launch) return the previous mode and reject other values;
     host-only, no device call."""
-    for setter in (L.lib.granite4_set_fp8_launch_mode, L.lib.granite4_set_attn_combine_mode):
+    for setter, top in ((L.lib.granite4_set_fp8_launch_mode, 2),
+                        (L.lib.granite4_set_attn_combine_mode, 1)):
         prev = setter(1)
-        assert prev in (0, 1)
-        assert setter(2) == -1 and setter(-1) == -1
-        assert setter(0) == 1
+        assert prev in range(top + 1)
+        assert setter(top + 1) == -1 and setter(-1) == -1
+        assert setter(top) == 1
+        assert setter(0) == top
         assert setter(prev) == 0
 
 

@@ -747,3 +747,64 @@ def test_add_rmsnorm_fp8_nan_row_is_ignored_by_the_scale(rows):
             L.set_fp8_launch_mode(prev)
         _fp8_check(host(codes), host(scale)[0], host(no))
         assert np.isfinite(host(scale)[0]) and host(scale)[0] > 0
+
+
+@pytest.mark.parametrize("op,rows", [("norm", 8), ("norm", 512), ("norm", 8192), ("swiglu", 8),
+                                     ("swiglu", 512), ("swiglu", 8192)])
+def test_fp8_cooperative_launch_mode(op, rows):
+    """FP8 launch mode 2 (the single-launch forms through
+    hipLaunchCooperativeKernel): codes and scale identical to mode 0, eagerly
+    and as a captured graph replayed twice on other inputs."""
+    note(f"fp8 cooperative launch {op} rows={rows}")
+    work = L.fp8_workspace()
+    if op == "norm":
+        cols = 4096
+        xs = [dev(_hidden(rows, cols, 0xC1 + i)) for i in range(2)]
+        w = dev(ol.normal_bf16(0xC3, 1.0, 0.1, cols))
+        src = torch.empty_like(xs[0])
+        codes = torch.empty((rows, cols), dtype=torch.uint8, device="cuda")
+
+        def run(x, scale):
+            L.call("granite4_add_rmsnorm_fp8", x, None, 1.0, w, 1e-5, rows, cols, None, codes,
+                   scale, work)
+    else:
+        I_ = 12800
+        xs = [dev(ol.normal_bf16(0xC4 + i, 0.0, 1.0 + i, rows * 2 * I_).reshape(rows, 2 * I_))
+              for i in range(2)]
+        src = torch.empty_like(xs[0])
+        codes = torch.empty((rows, I_), dtype=torch.uint8, device="cuda")
+
+        def run(x, scale):
+            L.call("granite4_swiglu_fp8", x, rows, I_, codes, scale, work, None)
+    want = []
+    for x in xs:
+        sc = torch.empty(1, dtype=torch.float32, device="cuda")
+        run(x, sc)
+        want.append((host(codes).copy(), host(sc)[0]))
+    prev = L.set_fp8_launch_mode(2)
+    try:
+        for x, (c, s) in zip(xs, want):
+            sc = torch.empty(1, dtype=torch.float32, device="cuda")
+            run(x, sc)
+            np.testing.assert_array_equal(host(codes), c)
+            assert host(sc)[0] == s
+        sc = torch.empty(1, dtype=torch.float32, device="cuda")
+        stream = torch.cuda.Stream()
+        g = torch.cuda.CUDAGraph()
+        torch.cuda.synchronize()
+        L.use_stream(stream)
+        try:
+            with torch.cuda.graph(g, stream=stream):
+                run(src, sc)
+        finally:
+            L.use_stream()
+        for i in (1, 0):
+            src.copy_(xs[i])
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(host(codes), want[i][0])
+            assert host(sc)[0] == want[i][1]
+    finally:
+        L.set_fp8_launch_mode(prev)
+    assert L.fp8_sync_status(work) == 0
