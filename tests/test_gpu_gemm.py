@@ -286,3 +286,32 @@ def test_norm_fp8_feeds_gemm_through_device_scale_graph_replay():
         bad, d = bf16_ok(host(out), y, abs_bound(c, W, s * w_s))
         note(f"  replay {rep}: scale {s:.6g}, max ulp {d.max()}")
         assert not bad.any()
+
+
+@pytest.mark.parametrize("M", [512, 8192])
+def test_gemm_fp8_swiglu_fp8_8b_shape(M):
+    """The gate|up + SwiGLU -> FP8 GEMM at the 8B shape (I 12800, K 4096):
+    codes and scale of the reference quantiser on the act the GEMM stored,
+    the same in every FP8 launch mode."""
+    note(f"gemm_fp8_swiglu 8B shape M={M}")
+    I, K = 12800, 4096
+    dA = dev(ol.fp8_codes(0x7C, (M, K)))
+    dW = dev(ol.fp8_codes(0x7D, (2 * I, K), std=0.5))
+    a_s, gs, us = 0.04, 0.006, 0.009
+    work = L.fp8_workspace(rows=16)
+    res = []
+    for mode in (0, 1):
+        prev = L.set_fp8_launch_mode(mode)
+        try:
+            act, codes, scale = L.gemm_fp8_swiglu(
+                dA, a_s, dW, gs, us, work, act=torch.empty((M, I), dtype=torch.int16, device="cuda"))
+            res.append((host(act).copy(), host(codes).copy(), host(scale)[0]))
+        finally:
+            L.set_fp8_launch_mode(prev)
+    np.testing.assert_array_equal(res[0][0], res[1][0])
+    np.testing.assert_array_equal(res[0][1], res[1][1])
+    assert res[0][2] == res[1][2]
+    want_codes, want_scale = ol.fp8_quantize(res[0][0])
+    assert res[0][2] == np.float32(want_scale)
+    np.testing.assert_array_equal(res[0][1], want_codes)
+    assert L.fp8_sync_status(work) == 0
