@@ -698,6 +698,150 @@ bool gemm_xcd_order(int mt, unsigned g) {
   return xbm + xbn < pbm + pbn;
 }
 
+
+// ---------------------------------------------------------------------------
+// Skinny GEMM, M <= 16 rows (a batched decode step's sessions, a short
+// chunk): the 128-row tiles above would leave 120 of 128 MFMA rows idle and
+// stream each weight tile through LDS. Here a 256-thread workgroup owns 16
+// weight rows (swiglu: 16 gate + the matching 16 up rows) and all M rows,
+// one 16 x 16 MFMA tile; its 4 waves split K into quarters, each streaming
+// its quarter of the 16 rows straight from global memory into the MFMA
+// fragments (lane l: row l % 16, the fragment's bytes at k offset
+// (l / 16) * 32 of a 128-byte fp8 step, or (l / 16) * 8 elements of a
+// 32-element bf16 step), U steps of loads in flight. A rows past M and
+// weight rows past N read row M - 1 / N - 1 (their outputs are not
+// stored). The 4 partial tiles are summed in wave order through LDS, and
+// wave 0 stores the tile with the epilogue of the large kernels (same
+// y = acc * (a_scale * w_scale(n)), residual and SwiGLU arithmetic). The f32
+// sum's order differs from the large kernels' (K in quarters); both are
+// held to the same parity bar.
+// ---------------------------------------------------------------------------
+constexpr int kSkinnyMaxM = 16;
+
+template <bool F8A, int EPI, int U>
+__global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs a) {
+  __shared__ v4f s_acc[2][3][64];  // waves 1..3's partial tiles (gate / up)
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int fr = lane & 15, fq = lane >> 4;
+  constexpr int kStepK = F8A ? 128 : 32;  // k elements per MFMA step
+  const int steps = a.K / kStepK;
+  const int s0 = wave * steps / 4, s1 = (wave + 1) * steps / 4;
+  const int arow = min(fr, a.M - 1);
+  constexpr int kTiles = EPI == kEpiSwiglu ? 2 : 1;
+  const int ncols = EPI == kEpiSwiglu ? a.I : a.N;
+  const int ntile = (ncols + 15) / 16;
+  float amax = 0.0f;
+  const float a_scale = F8A ? *a.a_scale : 1.0f;
+  for (int tile = blockIdx.x; tile < ntile; tile += gridDim.x) {
+    const int c = min(tile * 16 + fr, ncols - 1);
+    // this lane's weight rows: column c (gate row c and up row I + c for swiglu)
+    const uint8_t* wrow[kTiles];
+    wrow[0] = a.W + static_cast<size_t>(c) * a.K;
+    if (EPI == kEpiSwiglu) wrow[kTiles - 1] = a.W + static_cast<size_t>(a.I + c) * a.K;
+    v4f acc[kTiles];
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) acc[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int sb = s0; sb < s1; sb += U) {
+      if constexpr (F8A) {
+        v4u wx[U][kTiles], wy[U][kTiles], ax[U], ay[U];
+        const uint8_t* arow_p = a.A + static_cast<size_t>(arow) * a.lda;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int k = min(sb + u, s1 - 1) * kStepK + 32 * fq;
+#pragma unroll
+          for (int t = 0; t < kTiles; ++t) {
+            wx[u][t] = *reinterpret_cast<const v4u*>(wrow[t] + k);
+            wy[u][t] = *reinterpret_cast<const v4u*>(wrow[t] + k + 16);
+          }
+          ax[u] = *reinterpret_cast<const v4u*>(arow_p + k);
+          ay[u] = *reinterpret_cast<const v4u*>(arow_p + k + 16);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          if (sb + u >= s1) break;
+#pragma unroll
+          for (int t = 0; t < kTiles; ++t)
+            acc[t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                frag_of(ax[u], ay[u]), frag_of(wx[u][t], wy[u][t]), acc[t], 0, 0, 0, 0, 0, 0);
+        }
+      } else {
+        uint2 wq[U][kTiles];
+        v4u ax[U];
+        const uint16_t* arow_p = reinterpret_cast<const uint16_t*>(a.A) + static_cast<size_t>(arow) * a.lda;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int k = min(sb + u, s1 - 1) * kStepK + 8 * fq;
+#pragma unroll
+          for (int t = 0; t < kTiles; ++t) wq[u][t] = *reinterpret_cast<const uint2*>(wrow[t] + k);
+          ax[u] = *reinterpret_cast<const v4u*>(arow_p + k);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          if (sb + u >= s1) break;
+          const bf16x8_g af = __builtin_bit_cast(bf16x8_g, ax[u]);
+#pragma unroll
+          for (int t = 0; t < kTiles; ++t)
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, fp8x8_to_bf16(wq[u][t]), acc[t], 0,
+                                                             0, 0);
+        }
+      }
+    }
+    // the quarters summed in wave order: wave 0 + 1 + 2 + 3
+    if (wave > 0) {
+#pragma unroll
+      for (int t = 0; t < kTiles; ++t) s_acc[t][wave - 1][lane] = acc[t];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+      for (int t = 0; t < kTiles; ++t)
+#pragma unroll
+        for (int w = 0; w < 3; ++w) acc[t] += s_acc[t][w][lane];
+      // lane l holds C[4 (l / 16) + i][16 tile + l % 16]
+      const int n = tile * 16 + fr;
+      const Granite4GemmEpilogue& ep = a.ep;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = 4 * fq + i;
+        if (m >= a.M || n >= ncols) continue;
+        const size_t off = static_cast<size_t>(m) * ep.ldc + n;
+        if constexpr (EPI == kEpiSwiglu) {
+          const float g = acc[0][i] * (a_scale * ep.scale0);
+          const float u = acc[kTiles - 1][i] * (a_scale * ep.scale1);
+          const uint32_t b = pack_bf16_rne(silu_mul(g, u), 0.0f) & 0xffffu;
+          ep.out_bf16[off] = static_cast<uint16_t>(b);
+          amax = fmaxf(amax, bf16_to_f32(static_cast<uint16_t>(b & 0x7fffu)));
+        } else {
+          const float y = acc[0][i] * (a_scale * epi_scale(ep, n));
+          if (EPI == kEpiF32) {
+            ep.out_f32[off] = y;
+          } else if (EPI == kEpiResidual) {
+            const float r = bf16_to_f32(ep.residual[off]);
+            ep.out_bf16[off] = static_cast<uint16_t>(pack_bf16_rne(r + ep.resid_scale * y, 0.0f));
+          } else {
+            ep.out_bf16[off] = static_cast<uint16_t>(pack_bf16_rne(y, 0.0f));
+          }
+        }
+      }
+    }
+    __syncthreads();  // s_acc is reused by the next tile
+  }
+  if (EPI == kEpiSwiglu) write_partial(a.partials, amax);
+}
+
+constexpr int kSkinnyU = 4;
+
+// Launches the skinny kernel for M <= kSkinnyMaxM; grid: one workgroup per
+// 16 output columns, at most `cap` (the partial slots for swiglu).
+template <bool F8A, int EPI>
+unsigned launch_skinny(const GemmArgs& a, int cap) {
+  const int ncols = EPI == kEpiSwiglu ? a.I : a.N;
+  const long long ntile = (ncols + 15) / 16;
+  const unsigned grid = static_cast<unsigned>(ntile < cap ? ntile : cap);
+  hipLaunchKernelGGL((gemm_skinny_kernel<F8A, EPI, kSkinnyU>), grid, 256, 0, stream(), a);
+  return grid;
+}
+
 template <int EPI, int TN = kGBN, int ST = kGStages, int KS = 1>
 unsigned gemm_grid(long long tiles, int cap) {
   const int resident =
@@ -754,7 +898,8 @@ int granite4_gemm_fp8(int out, const uint8_t* A, int lda, const float* d_a_scale
   const int deep = !narrow ? 2 : (tiles <= kCUs ? 6 : (tiles <= 2 * kCUs ? 3 : 2));
   const auto run = [&](auto e_tag) {
     constexpr int E = decltype(e_tag)::value;
-    if (!narrow) go(gemm_fp8_kernel<E>, gemm_grid<E>(tiles, INT_MAX));
+    if (M <= kSkinnyMaxM) launch_skinny<true, E>(a, INT_MAX);
+    else if (!narrow) go(gemm_fp8_kernel<E>, gemm_grid<E>(tiles, INT_MAX));
     else if (deep == 6) go(gemm_fp8_kernel<E, 64, 3, 2>, gemm_grid<E, 64, 3, 2>(tiles, INT_MAX), 512);
     else if (deep == 3) go(gemm_fp8_kernel<E, 64, 3>, gemm_grid<E, 64, 3>(tiles, INT_MAX));
     else go(gemm_fp8_kernel<E, 64>, gemm_grid<E, 64>(tiles, INT_MAX));
@@ -809,6 +954,12 @@ int granite4_prefill_gemm(int out, const uint16_t* A, int lda, const uint8_t* W,
     a.xcd_order = gemm_xcd_order(a.mt, gu);
     return gu;
   };
+  if (M <= kSkinnyMaxM) {
+    if (out == GRANITE4_GEMM_BF16) launch_skinny<false, kEpiBf16>(a, INT_MAX);
+    else if (out == GRANITE4_GEMM_F32) launch_skinny<false, kEpiF32>(a, INT_MAX);
+    else launch_skinny<false, kEpiResidual>(a, INT_MAX);
+    return launch_status("granite4_prefill_gemm");
+  }
   switch (out) {
     case GRANITE4_GEMM_BF16:
       hipLaunchKernelGGL(gemm_bf16w_kernel<kEpiBf16>,
@@ -871,9 +1022,14 @@ int granite4_gemm_fp8_swiglu(const uint8_t* A, int lda, const float* d_a_scale,
   a.vec_out = true;
   a.partials = work_partials(d_work);
   const long long tiles = static_cast<long long>(a.mt) * a.nt;
-  const unsigned grid = gemm_grid<kEpiSwiglu>(tiles, kMaxPartials);
-  a.xcd_order = gemm_xcd_order(a.mt, grid);
-  hipLaunchKernelGGL(gemm_fp8_kernel<kEpiSwiglu>, grid, 256, 0, stream(), a);
+  unsigned grid;
+  if (M <= kSkinnyMaxM) {
+    grid = launch_skinny<true, kEpiSwiglu>(a, kMaxPartials);
+  } else {
+    grid = gemm_grid<kEpiSwiglu>(tiles, kMaxPartials);
+    a.xcd_order = gemm_xcd_order(a.mt, grid);
+    hipLaunchKernelGGL(gemm_fp8_kernel<kEpiSwiglu>, grid, 256, 0, stream(), a);
+  }
   if (launch_status("granite4_gemm_fp8_swiglu") != 0) return -1;
   if (codes == nullptr) return 0;
   return launch_encode_bf16(act, M, I, work_partials(d_work), static_cast<int>(grid), codes, d_scale)

@@ -95,8 +95,11 @@ def run_gemm(kind, A, a_scale, W, scales=(1.0, 1.0, 1.0), segs=None, residual=No
 # a 512-thread workgroup (K = 128 and 384: an odd count of 128-wide K tiles,
 # half 1 idle in the last step); the 1100-row shape (9 x 32 = 288 tiles) the
 # 128 x 128 form.
+# M <= 16 takes the skinny kernel (16-column workgroups, K in quarters: 384 gives
+# quarters of 0, 1, 1 and 1 steps), M = 17 the tiled one.
 SHAPES = [(1, 128, 128), (70, 136, 256), (128, 256, 512), (300, 520, 1024), (257, 1024, 4096),
-          (1100, 4096, 128), (96, 192, 384)]
+          (1100, 4096, 128), (96, 192, 384), (8, 136, 4096), (16, 520, 384), (17, 520, 384),
+          (5, 4096, 12800)]
 
 
 @pytest.mark.parametrize("M,N,K", SHAPES)
@@ -139,7 +142,7 @@ def test_gemm_fp8_segment_scales():
 
 
 @pytest.mark.parametrize("M,N,K", [(64, 256, 512), (200, 4096, 4096), (2100, 2048, 256),
-                                   (130, 512, 1408)])
+                                   (130, 512, 1408), (8, 4096, 12800), (1, 256, 512)])
 def test_gemm_fp8_residual_in_place(M, N, K):
     """The O / down projection: hidden = bf16(hidden + rs * y), in place."""
     note(f"gemm_fp8 residual M={M} N={N} K={K}")
@@ -155,7 +158,8 @@ def test_gemm_fp8_residual_in_place(M, N, K):
     assert not bad.any()
 
 
-@pytest.mark.parametrize("M,I,K", [(1, 64, 128), (100, 328, 512), (257, 1280, 4096)])
+@pytest.mark.parametrize("M,I,K", [(1, 64, 128), (100, 328, 512), (257, 1280, 4096),
+                                   (8, 1280, 4096), (16, 328, 512)])
 def test_gemm_fp8_swiglu_fused(M, I, K):
     """gate|up GEMM + SwiGLU (+ FP8) in one GEMM epilogue vs the oracle GEMM
     followed by the reference's f32 SwiGLU (g4o_silu_mul_f32)."""

@@ -81,7 +81,7 @@ def inputs(M, N, K, seed):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 8, 32), (37, 40, 96), (130, 264, 256), (300, 520, 512),
-                                   (64, 128, 4128)])
+                                   (64, 128, 4128), (8, 136, 4096), (16, 40, 96), (3, 520, 12800)])
 def test_prefill_gemm_bf16_out(M, N, K):
     note(f"prefill_gemm bf16 M={M} N={N} K={K}")
     A, W = inputs(M, N, K, 0x81 + M)
@@ -92,7 +92,7 @@ def test_prefill_gemm_bf16_out(M, N, K):
     note(f"  bit-exact fraction {exact:.4f}")
 
 
-@pytest.mark.parametrize("M,N,K", [(33, 72, 160), (256, 384, 1024)])
+@pytest.mark.parametrize("M,N,K", [(33, 72, 160), (256, 384, 1024), (8, 72, 160)])
 def test_prefill_gemm_f32_out(M, N, K):
     note(f"prefill_gemm f32 M={M} N={N} K={K}")
     A, W = inputs(M, N, K, 0x91 + M)
@@ -106,7 +106,7 @@ def test_prefill_gemm_f32_out(M, N, K):
 # 200 x 256: 4 tiles, the residual prefetched at each tile's start; 2100 x
 # 4096: 544 tiles, more than the 512 workgroups resident at two per CU, so the
 # form that loads the residual after the K loop runs.
-@pytest.mark.parametrize("M,N,K", [(200, 256, 512), (2100, 4096, 128)])
+@pytest.mark.parametrize("M,N,K", [(200, 256, 512), (2100, 4096, 128), (8, 4096, 4096)])
 def test_prefill_gemm_residual_in_place(M, N, K):
     """kResidual, the O / down projection: hidden = bf16(hidden + rs * y), in place."""
     note(f"prefill_gemm residual M={M} N={N} K={K}")
@@ -125,12 +125,13 @@ def test_prefill_gemm_residual_in_place(M, N, K):
     assert not ((d > 2) & (err > bnd + np.abs(want_f) * 2.0 ** -7)).any()
 
 
+@pytest.mark.parametrize("M", [21, 7])
 @pytest.mark.parametrize("N,ldc", [(38, 38), (38, 40), (18, 22)])
-def test_prefill_gemm_even_widths_and_pitches(N, ldc):
+def test_prefill_gemm_even_widths_and_pitches(N, ldc, M):
     """The reference accepts any even N and ldc: outputs not 16-byte aligned
     per row are written element by element, columns past N untouched."""
-    note(f"prefill_gemm N={N} ldc={ldc}")
-    M, K = 21, 64
+    note(f"prefill_gemm N={N} ldc={ldc} M={M}")
+    K = 64
     A, W = inputs(M, N, K, 0xB1 + N + ldc)
     full = torch.full((M, ldc), 0x7E7E, dtype=torch.int16, device="cuda")
     ep = L.GemmEpilogue(0.05, 0.05, 0.05, N, N, full.data_ptr(), None, None, 1.0, ldc)
