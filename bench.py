@@ -83,7 +83,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=["t512", "t8192", "decode", "t8", "stress", "tN", "probe", "floor", "t1",
                                        "attn", "gemm", "decode_gemv", "decode_trace",
-                                       "layer_steps", "fp8_trace"],
+                                       "layer_steps", "multi_step", "fp8_trace"],
                     help="run one configuration and print its detail (profiling runs)")
     ap.add_argument("--T", type=int, default=1024, help="token count for --only tN")
     ap.add_argument("--attn-case", default=None, help="run only this bench_attn case")
@@ -260,6 +260,8 @@ def main():
             r = bench_fp8_trace(torch, L, randn, gamma)
         elif args.only == "layer_steps":
             r = bench_layer_steps(torch, L, gen, cos_t, sin_t, emb, gamma, stream)
+        elif args.only == "multi_step":
+            r = bench_layer_steps(torch, L, gen, cos_t, sin_t, emb, gamma, stream, prefill=False)
         elif args.only == "decode_trace":
             r = bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream,
                                   trace_replays=25)
@@ -977,7 +979,7 @@ def bench_fp8_trace(torch, L, randn, gamma):
     return out
 
 
-def bench_layer_steps(torch, L, gen, cos_t, sin_t, emb, gamma, stream):
+def bench_layer_steps(torch, L, gen, cos_t, sin_t, emb, gamma, stream, prefill=True):
     """The engine's batched layer sequences through their single calls:
     granite4_prefill_layers (forward_prefill, one chunk) per layer at T=512
     (config 3: int8 KV, positions 0..511) and T=8192 (config 4: K5V4 group
@@ -986,7 +988,7 @@ def bench_layer_steps(torch, L, gen, cos_t, sin_t, emb, gamma, stream):
     [0, 65536) over 40 layers (int8 KV, each session's page table over its
     own 4096 pages of the pool). Both activation forms; random fp8 weights of
     the 8B shapes (q|k|v and gate|up one block each). Each timed as a HIP
-    graph (graphs_us)."""
+    graph (graphs_us). prefill=False times the multi-session step only."""
     dev = "cuda"
 
     def codes(*shape):
@@ -1012,7 +1014,7 @@ def bench_layer_steps(torch, L, gen, cos_t, sin_t, emb, gamma, stream):
     toks = torch.randint(0, VOCAB, (65536,), dtype=torch.int32, device=dev, generator=gen)
     nl = 4
     for T, bits, group, pos0, key in ((512, 8, 128, 0, "T512_int8"),
-                                      (8192, 5, 32, 57344, "T8192_k5v4g32")):
+                                      (8192, 5, 32, 57344, "T8192_k5v4g32"))[:2 if prefill else 0]:
         # one sequence, arena row = position: the chunk at pos0 attends to
         # all pos0 earlier positions (zero-filled codes and scales)
         stride, pt = pos0 + T, None

@@ -1598,7 +1598,11 @@ int granite4_prefill_attention(const uint16_t* q_rot, const uint16_t* cache_k,
 
 size_t granite4_attn_split_scratch_bytes(int Hq, int rows, int stride) {
   if (Hq <= 0 || rows <= 0 || stride <= 0) return 0;
-  const size_t nblk = (attn_splits(stride) + kAttnWaves - 1) / kAttnWaves;
+  // Enough for every split layout a call over this arena may take (max_len
+  // <= stride): the split count is not monotone in the length (256 tiles
+  // give 256 splits, 257 give 129), so the bound is min(tiles, 256).
+  const int tiles = (stride + kTile - 1) / kTile;
+  const size_t nblk = ((tiles < kAttnMaxSplits ? tiles : kAttnMaxSplits) + kAttnWaves - 1) / kAttnWaves;
   const size_t slots = static_cast<size_t>(rows) * Hq * nblk;
   // Partial (m, l) and output per slot, then the arrival tags (one per
   // (row group, KV head, block): at most one per slot).

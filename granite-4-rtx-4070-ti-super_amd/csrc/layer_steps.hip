@@ -257,6 +257,11 @@ int granite4_decode_step_multi(const Granite4DecodeModel* m, const Granite4Batch
                                                     offsetof(GpuMultiRows, pos));
   const int* const* row_pt = reinterpret_cast<const int* const*>(
       reinterpret_cast<const char*>(d_rows) + offsetof(GpuMultiRows, pt));
+  // The attention's split layout follows the longest sequence the model
+  // takes, max_pos (the reference's multi step passes g->max_pos,
+  // forward_gpu.cu:2567-2580); a pool shorter than that (which the reference
+  // rejects) takes its own length.
+  const int split_len = m->max_pos <= m->kv_stride ? m->max_pos : 0;
   // q, k, v as three row blocks of the qkv buffer (the multi append's layout).
   uint16_t* q = b->qkv;
   uint16_t* k = q + static_cast<size_t>(rows) * nq;
@@ -272,7 +277,8 @@ int granite4_decode_step_multi(const Granite4DecodeModel* m, const Granite4Batch
                                    m->kv_stride, b->q_rot) != 0 ||
         granite4_attn_paged(b->q_rot, rows, Hq, Hk, 128, m->attn_scale, y.cache_k, y.cache_v,
                             y.k_scale, y.v_scale, m->kv_bits, 128, m->kv_stride, 0, nullptr,
-                            nullptr, row_pos, row_pt, 0, 0, b->attn_scratch, b->attn) != 0 ||
+                            nullptr, row_pos, row_pt, split_len, 0, b->attn_scratch,
+                            b->attn) != 0 ||
         layer_tail(m, y, b, rows, fp8) != 0) {
       std::fprintf(stderr, "granite4: granite4_decode_step_multi: layer %d failed\n", l);
       return -1;

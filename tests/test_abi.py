@@ -85,6 +85,23 @@ def test_mode_switches_return_previous_and_reject_others():
         assert setter(prev) == 0
 
 
+def test_attn_scratch_covers_every_layout_up_to_the_arena():
+    """granite4_attn_split_scratch_bytes(Hq, rows, stride) holds the partials
+    of any split layout a call over that arena may take (max_len <= stride):
+    the split count is not monotone (256 tiles give 256 splits of one tile,
+    257 tiles 129 splits of two), so a 257-tile arena sized by its own layout
+    would be too small for a call laid out by max_len = 256 tiles."""
+    f = L.lib.granite4_attn_split_scratch_bytes
+    f.restype = ctypes.c_size_t
+    per_slot = 8 + 128 * 4 + 4  # (m, l), the partial output, the arrival tag
+    for stride, splits in ((64, 1), (16384, 256), (16448, 256), (20480, 256), (524288, 256),
+                           (1000, 16)):
+        nblk = (splits + 3) // 4
+        assert f(32, 8, stride) == 256 + 8 * 32 * nblk * per_slot, stride
+    for stride in range(64, 40000, 640):
+        assert f(32, 1, stride) >= f(32, 1, min(stride, 16384))
+
+
 def test_row_table_host_matches_oracle_and_golden():
     G = np.load(ol.os.path.join(ol.ROOT, "tests", "golden", "golden.npz"))
     for s in range(G["pt_blocks"].shape[0]):

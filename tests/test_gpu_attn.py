@@ -252,6 +252,34 @@ def test_attn_multi_sequence_rows():
     check(got, want, vmax(cv, vs, bits), "multi-sequence")
 
 
+@pytest.mark.parametrize("bits,group", [(8, 128), (5, 32), (4, 64)])
+def test_attn_multi_sequence_layout_from_max_len(bits, group):
+    """The multi-session step's form over a pool longer than the sequences:
+    stride 20480 (320 tiles: 2 tiles per split) with the layout taken from
+    max_len 8192 (1 tile per split), 6 sessions with their own page tables at
+    positions up to 8191 (a tile's first and last key, a split's last key).
+    Against the oracle with the same layout, and each row bit for bit the
+    single-sequence call (device position and page table) with the same
+    max_len."""
+    note(f"attn multi-sequence max_len bits={bits} group={group}")
+    pages, max_len = 1280, 8192
+    stride = 16 * pages
+    ck, cv, ks, vs = make_cache(bits, group, stride, 0xDA + bits)
+    rng = np.random.default_rng(0xDB)
+    pos = [8191, 64, 4095, 127, 0, 6000]
+    pts = [ol.row_table(rng.permutation(pages).astype(np.int32), stride) for _ in pos]
+    q = ol.normal_bf16(0xDC, 0.0, 1.0, len(pos) * HQ * D).reshape(len(pos), HQ * D)
+    got = run_paged(q, ck, cv, ks, vs, bits, group, stride, row_pos=pos, row_pts=pts,
+                    max_len=max_len)
+    want = ol.attn_split(q, ck, cv, ks, vs, bits, group, stride, pos, pts=pts, scale=1.0 / 16,
+                         Hk=HK, max_len=max_len)
+    check(got, want, vmax(cv, vs, bits), "multi-sequence, layout from max_len")
+    for r, p in enumerate(pos):
+        one = run_paged(q[r:r + 1], ck, cv, ks, vs, bits, group, stride,
+                        d_pos=dev(np.array([p], np.int32)), d_pt=dev(pts[r]), max_len=max_len)
+        np.testing.assert_array_equal(one[0], got[r], err_msg=f"row {r} at {p}")
+
+
 @pytest.mark.parametrize("window", [1, 100, 5000])
 def test_attn_window(window):
     note(f"attn window={window}")

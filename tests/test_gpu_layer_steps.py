@@ -96,6 +96,8 @@ class Model:
         g.manual_seed(seed)
         self.H, self.I, self.Hq, self.Hk, self.vocab = H, I, Hq, Hk, vocab
         self.bits, self.group, self.stride = bits, group, stride
+        # the multi step's split layout: max_pos when the pool holds that many rows
+        self.split_len = max_pos if max_pos <= stride else 0
         self.eps, self.emb_mult, self.rs, self.att, self.lm_scale = 1e-5, 12.0, 0.22, 1 / 128, 1 / 64
         nq, nk = Hq * 128, Hk * 128
 
@@ -299,7 +301,7 @@ def _multi_one_by_one(m, d_m, n, fp8):
                st.q_rot)
         L.call("granite4_attn_paged", st.q_rot, n, m.Hq, m.Hk, 128, m.att, ly["cache_k"],
                ly["cache_v"], ly["k_scale"], ly["v_scale"], m.bits, 128, m.stride, 0, None, None,
-               row_pos, row_pt, 0, 0, st.attn_scratch, st.attn)
+               row_pos, row_pt, m.split_len, 0, st.attn_scratch, st.attn)
     one_by_one(m, n, fp8, first, attention)
 
 
@@ -345,7 +347,7 @@ def test_decode_step_multi_matches_one_by_one_and_oracle(ops):
                                k_round_bf16=True, cache_k=ck, cache_v=cv, k_scale=ks,
                                v_scale=vs)[0]
         return ol.attn_split(q_rot, ck, cv, ks, vs, 8, 128, m.stride, pos, pts=pts,
-                             scale=m.att, Hk=m.Hk)
+                             scale=m.att, Hk=m.Hk, max_len=m.split_len)
     hid, logits = oracle_layers(m, x, fp8, arenas, attention)
     _close(host(hid2), hid, "final-normed hidden", fp8)
     _close(host(log2), logits, "logits", fp8)
