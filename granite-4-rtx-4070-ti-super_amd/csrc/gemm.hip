@@ -723,7 +723,7 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs a) {
   __shared__ v4f s_acc[2][3][64];  // waves 1..3's partial tiles (gate / up)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int fr = lane & 15, fq = lane >> 4;
-  constexpr int kStepK = F8A ? 128 : 32;  // k elements per MFMA step
+  constexpr int kStepK = 128;  // k elements per step (bf16 A: four MFMAs)
   const int steps = a.K / kStepK;
   const int s0 = wave * steps / 4, s1 = (wave + 1) * steps / 4;
   const int arow = min(fr, a.M - 1);
@@ -765,24 +765,51 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs a) {
                 frag_of(ax[u], ay[u]), frag_of(wx[u][t], wy[u][t]), acc[t], 0, 0, 0, 0, 0, 0);
         }
       } else {
-        uint2 wq[U][kTiles];
-        v4u ax[U];
+        // A step's 128 k elements as four MFMAs: lane group fq reads the
+        // 32 contiguous weight bytes 32 fq .. 32 fq + 31 of the step (and the
+        // same 32 activations), and feeds bytes 8 j .. 8 j + 7 to MFMA j as
+        // its k slot fq. A and B take the same k assignment, so each MFMA sums
+        // products of matching k; the four cover the step.
+        v4u wx[U][kTiles], wy[U][kTiles], ax[U][4];
         const uint16_t* arow_p = reinterpret_cast<const uint16_t*>(a.A) + static_cast<size_t>(arow) * a.lda;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          const int k = min(sb + u, s1 - 1) * kStepK + 8 * fq;
+          const int k = min(sb + u, s1 - 1) * kStepK + 32 * fq;
 #pragma unroll
-          for (int t = 0; t < kTiles; ++t) wq[u][t] = *reinterpret_cast<const uint2*>(wrow[t] + k);
-          ax[u] = *reinterpret_cast<const v4u*>(arow_p + k);
+          for (int t = 0; t < kTiles; ++t) {
+            wx[u][t] = *reinterpret_cast<const v4u*>(wrow[t] + k);
+            wy[u][t] = *reinterpret_cast<const v4u*>(wrow[t] + k + 16);
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j) ax[u][j] = *reinterpret_cast<const v4u*>(arow_p + k + 8 * j);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
           if (sb + u >= s1) break;
-          const bf16x8_g af = __builtin_bit_cast(bf16x8_g, ax[u]);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const bf16x8_g af = __builtin_bit_cast(bf16x8_g, ax[u][j]);
+#pragma unroll
+            for (int t = 0; t < kTiles; ++t) {
+              const v4u& wv = j < 2 ? wx[u][t] : wy[u][t];
+              const uint2 wq = (j & 1) ? make_uint2(wv[2], wv[3]) : make_uint2(wv[0], wv[1]);
+              acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, fp8x8_to_bf16(wq), acc[t], 0, 0, 0);
+            }
+          }
+        }
+      }
+    }
+    if constexpr (!F8A) {
+      // K % 128: the remaining 32-element steps, by the last wave.
+      if (wave == 3) {
+        const uint16_t* arow_p = reinterpret_cast<const uint16_t*>(a.A) + static_cast<size_t>(arow) * a.lda;
+        for (int k0 = steps * kStepK; k0 < a.K; k0 += 32) {
+          const int k = k0 + 8 * fq;
+          const bf16x8_g af = __builtin_bit_cast(bf16x8_g, *reinterpret_cast<const v4u*>(arow_p + k));
 #pragma unroll
           for (int t = 0; t < kTiles; ++t)
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, fp8x8_to_bf16(wq[u][t]), acc[t], 0,
-                                                             0, 0);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                af, fp8x8_to_bf16(*reinterpret_cast<const uint2*>(wrow[t] + k)), acc[t], 0, 0, 0);
         }
       }
     }
