@@ -86,6 +86,11 @@ struct GemmArgs {
   int mt, nt;       // tile counts along M and N
   bool vec_out;     // 16-byte output rows (pitch and width multiples of 8)
   bool xcd_order;   // tiles renumbered per XCD (xcd_tile0)
+  // Skinny kBf16 only (gemm_rows_split): when seg_out[0] is set, column n of
+  // segment s (ep.seg1 / ep.seg2 bounds) goes to seg_out[s][m * seg_ld[s] +
+  // n - start of s] instead of ep.out_bf16.
+  uint16_t* seg_out[3];
+  int seg_ld[3];
 };
 
 // Workgroups are handed to the 8 XCDs round-robin by id (id % 8), each XCD
@@ -845,6 +850,11 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs a) {
           } else if (EPI == kEpiResidual) {
             const float r = bf16_to_f32(ep.residual[off]);
             ep.out_bf16[off] = static_cast<uint16_t>(pack_bf16_rne(r + ep.resid_scale * y, 0.0f));
+          } else if (a.seg_out[0] != nullptr) {
+            const int sg = n < ep.seg1 ? 0 : (n < ep.seg2 ? 1 : 2);
+            const int n0 = sg == 0 ? 0 : (sg == 1 ? ep.seg1 : ep.seg2);
+            a.seg_out[sg][static_cast<size_t>(m) * a.seg_ld[sg] + n - n0] =
+                static_cast<uint16_t>(pack_bf16_rne(y, 0.0f));
           } else {
             ep.out_bf16[off] = static_cast<uint16_t>(pack_bf16_rne(y, 0.0f));
           }
@@ -880,6 +890,43 @@ unsigned gemm_grid(long long tiles, int cap) {
 }
 
 }  // namespace
+
+// One skinny GEMM (M <= 16) over a weight block of three row segments
+// (ep.seg1, ep.seg2 bounds, scale0..2 their scales) with each segment's bf16
+// output in a buffer of its own: the batched decode step's q|k|v, whose
+// three row blocks the multi-row RoPE append reads. fp8: A is e4m3 codes with
+// the device scale a_scale (granite4_gemm_fp8's operands), else bf16
+// (granite4_prefill_gemm's). Not exported: layer_steps.hip calls it.
+int gemm_rows_split(bool fp8, const void* A, int lda, const float* a_scale, const uint8_t* W,
+                    int M, int N, int K, const Granite4GemmEpilogue& ep, uint16_t* const out[3],
+                    const int ld[3]) {
+  const bool ok = fp8 ? gemm_args_ok(static_cast<const uint8_t*>(A), lda, W, M, N, K) && a_scale != nullptr
+                      : (A != nullptr && W != nullptr && K > 0 && K % 32 == 0 && lda >= K && lda % 8 == 0 &&
+                         aligned16(A) && aligned16(W));
+  if (!ok || M <= 0 || M > kSkinnyMaxM || N <= 0 || ep.seg1 <= 0 || ep.seg2 < ep.seg1 ||
+      ep.seg2 > N || out[0] == nullptr || out[1] == nullptr || out[2] == nullptr ||
+      ld[0] < ep.seg1 || ld[1] < ep.seg2 - ep.seg1 || ld[2] < N - ep.seg2) {
+    std::fprintf(stderr, "granite4: gemm_rows_split: invalid arguments\n");
+    return -1;
+  }
+  GemmArgs a{};
+  a.A = static_cast<const uint8_t*>(A);
+  a.lda = lda;
+  a.a_scale = a_scale;
+  a.W = W;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.ep = ep;
+  for (int i = 0; i < 3; ++i) {
+    a.seg_out[i] = out[i];
+    a.seg_ld[i] = ld[i];
+  }
+  if (fp8) launch_skinny<true, kEpiBf16>(a, INT_MAX);
+  else launch_skinny<false, kEpiBf16>(a, INT_MAX);
+  return launch_status("gemm_rows_split");
+}
+
 }  // namespace g4
 
 using namespace g4;

@@ -38,6 +38,13 @@
 #include <cstdint>
 #include <cstdio>
 
+namespace g4 {
+// gemm.hip: the skinny GEMM (rows <= 16) with a bf16 output per row segment.
+int gemm_rows_split(bool fp8, const void* A, int lda, const float* a_scale, const uint8_t* W,
+                    int M, int N, int K, const Granite4GemmEpilogue& ep, uint16_t* const out[3],
+                    const int ld[3]);
+}  // namespace g4
+
 namespace {
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -112,6 +119,8 @@ Granite4GemmEpilogue epi_resid(float s, uint16_t* hidden, float rs, int ldc) {
   return e;
 }
 
+constexpr int kSkinnyRows = 16;
+
 // q|k|v of `rows` rows into [rows][ldq] (q at column 0, k at nq, v at
 // nq + nk) or into three buffers (q_out / k_out / v_out with their own
 // pitches); one GEMM when the three weight matrices are one [nqkv][H] block.
@@ -130,6 +139,17 @@ int qkv_gemm(const Granite4DecodeModel* m, const Granite4DecodeLayer& y,
   if (one) {
     const Granite4GemmEpilogue e = epi_bf16(y.sq, y.sk, y.sv, nq, nq + nk, q_out, ldq);
     return gemm(y.wq, nq + 2 * nk, e);
+  }
+  const bool contiguous_w = y.wk == y.wq + static_cast<size_t>(nq) * H &&
+                            y.wv == y.wk + static_cast<size_t>(nk) * H;
+  if (contiguous_w && rows <= kSkinnyRows) {
+    // one launch, three output buffers
+    const Granite4GemmEpilogue e = epi_bf16(y.sq, y.sk, y.sv, nq, nq + nk, q_out, ldq);
+    uint16_t* const outs[3] = {q_out, k_out, v_out};
+    const int lds[3] = {ldq, ldk, ldv};
+    return fp8 ? g4::gemm_rows_split(true, b->codes, H, b->scales, y.wq, rows, nq + 2 * nk, H, e, outs, lds)
+               : g4::gemm_rows_split(false, b->normed, H, nullptr, y.wq, rows, nq + 2 * nk, H, e, outs,
+                                 lds);
   }
   const Granite4GemmEpilogue eq = epi_bf16(y.sq, y.sq, y.sq, INT32_MAX, INT32_MAX, q_out, ldq);
   const Granite4GemmEpilogue ek = epi_bf16(y.sk, y.sk, y.sk, INT32_MAX, INT32_MAX, k_out, ldk);
