@@ -707,30 +707,30 @@ bool gemm_xcd_order(int mt, unsigned g) {
 // ---------------------------------------------------------------------------
 // Skinny GEMM, M <= 16 rows (a batched decode step's sessions, a short
 // chunk): the 128-row tiles above would leave 120 of 128 MFMA rows idle and
-// stream each weight tile through LDS. Here a 256-thread workgroup owns 16
+// stream each weight tile through LDS. Here a workgroup of NW waves owns 16
 // weight rows (swiglu: 16 gate + the matching 16 up rows) and all M rows,
-// one 16 x 16 MFMA tile; its 4 waves split K into quarters, each streaming
-// its quarter of the 16 rows straight from global memory into the MFMA
+// one 16 x 16 MFMA tile; its NW waves split K into NW parts, each streaming
+// its part of the 16 rows straight from global memory into the MFMA
 // fragments (lane l: row l % 16, the fragment's bytes at k offset
-// (l / 16) * 32 of a 128-byte fp8 step, or (l / 16) * 8 elements of a
-// 32-element bf16 step), U steps of loads in flight. A rows past M and
+// (l / 16) * 32 of a 128-element step, for bf16 activations split over
+// four MFMAs), U steps of loads in flight. A rows past M and
 // weight rows past N read row M - 1 / N - 1 (their outputs are not
-// stored). The 4 partial tiles are summed in wave order through LDS, and
+// stored). The NW partial tiles are summed in wave order through LDS, and
 // wave 0 stores the tile with the epilogue of the large kernels (same
 // y = acc * (a_scale * w_scale(n)), residual and SwiGLU arithmetic). The f32
-// sum's order differs from the large kernels' (K in quarters); both are
+// sum's order differs from the large kernels' (K in NW parts); both are
 // held to the same parity bar.
 // ---------------------------------------------------------------------------
 constexpr int kSkinnyMaxM = 16;
 
-template <bool F8A, int EPI, int U>
-__global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs a) {
-  __shared__ v4f s_acc[2][3][64];  // waves 1..3's partial tiles (gate / up)
+template <bool F8A, int EPI, int U, int NW>
+__global__ __launch_bounds__(NW * 64) void gemm_skinny_kernel(GemmArgs a) {
+  __shared__ v4f s_acc[2][NW - 1][64];  // waves 1..NW-1's partial tiles (gate / up)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int fr = lane & 15, fq = lane >> 4;
   constexpr int kStepK = 128;  // k elements per step (bf16 A: four MFMAs)
   const int steps = a.K / kStepK;
-  const int s0 = wave * steps / 4, s1 = (wave + 1) * steps / 4;
+  const int s0 = wave * steps / NW, s1 = (wave + 1) * steps / NW;
   const int arow = min(fr, a.M - 1);
   constexpr int kTiles = EPI == kEpiSwiglu ? 2 : 1;
   const int ncols = EPI == kEpiSwiglu ? a.I : a.N;
@@ -806,7 +806,7 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs a) {
     }
     if constexpr (!F8A) {
       // K % 128: the remaining 32-element steps, by the last wave.
-      if (wave == 3) {
+      if (wave == NW - 1) {
         const uint16_t* arow_p = reinterpret_cast<const uint16_t*>(a.A) + static_cast<size_t>(arow) * a.lda;
         for (int k0 = steps * kStepK; k0 < a.K; k0 += 32) {
           const int k = k0 + 8 * fq;
@@ -828,7 +828,7 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs a) {
 #pragma unroll
       for (int t = 0; t < kTiles; ++t)
 #pragma unroll
-        for (int w = 0; w < 3; ++w) acc[t] += s_acc[t][w][lane];
+        for (int w = 0; w < NW - 1; ++w) acc[t] += s_acc[t][w][lane];
       // lane l holds C[4 (l / 16) + i][16 tile + l % 16]
       const int n = tile * 16 + fr;
       const Granite4GemmEpilogue& ep = a.ep;
@@ -863,10 +863,19 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs a) {
     }
     __syncthreads();  // s_acc is reused by the next tile
   }
-  if (EPI == kEpiSwiglu) write_partial(a.partials, amax);
+  if (EPI == kEpiSwiglu && wave == 0) {
+    // only wave 0 stores outputs, so it alone holds the workgroup's max |act|
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    if (lane == 0) a.partials[blockIdx.x] = amax;
+  }
 }
 
 constexpr int kSkinnyU = 4;
+// Waves per skinny workgroup. Measured on the 40-layer batched decode step
+// (FP8 / bf16 ms): 4 waves 8.94-9.20 / 9.38-9.64, 8 waves 8.89-8.90 /
+// 9.41, 16 waves 8.96-8.97 / 9.87.
+constexpr int kSkinnyWaves = 8;
 
 // Launches the skinny kernel for M <= kSkinnyMaxM; grid: one workgroup per
 // 16 output columns, at most `cap` (the partial slots for swiglu).
@@ -875,7 +884,7 @@ unsigned launch_skinny(const GemmArgs& a, int cap) {
   const int ncols = EPI == kEpiSwiglu ? a.I : a.N;
   const long long ntile = (ncols + 15) / 16;
   const unsigned grid = static_cast<unsigned>(ntile < cap ? ntile : cap);
-  hipLaunchKernelGGL((gemm_skinny_kernel<F8A, EPI, kSkinnyU>), grid, 256, 0, stream(), a);
+  hipLaunchKernelGGL((gemm_skinny_kernel<F8A, EPI, kSkinnyU, kSkinnyWaves>), grid, kSkinnyWaves * 64, 0, stream(), a);
   return grid;
 }
 
