@@ -181,18 +181,22 @@ __device__ __forceinline__ bf16x8_t k_raw_bf16(const u32x4_t& r) {
     return as_bf16x8(int4_pair_bf16(xs, 0), int4_pair_bf16(xs, 8), int4_pair_bf16(xs, 16),
                      int4_pair_bf16(xs, 24));
   } else {
-    constexpr int off = BITS == 5 ? 16 : 8;
+    // K5: the eight 5-bit codes assembled bytewise, four at a time: the low
+    // nibbles (dims c + 2 e) and the high nibbles (c + 2 e + 1) masked out of
+    // x, and the high-bit plane's bits 2 e (+ 1) moved to bit 4 of byte e by
+    // one 24-bit multiply (bit 2 e of t times 2^4 + 2^10 + 2^16 + 2^22 lands
+    // on 8 e + 4; the other products miss bits 4, 12, 20 and 28 and carry
+    // into none of them). Each byte then converts to f32 in one instruction
+    // (v_cvt_f32_ubyte*) and value = code - 16 exactly.
+    static_assert(BITS == 5, "k_raw_bf16: bf16, int8, int4 or K5");
+    constexpr uint32_t kSpread = (1u << 4) | (1u << 10) | (1u << 16) | (1u << 22);
+    const uint32_t lo = (r.x & 0x0F0F0F0Fu) | (__umul24(r.y & 0x55u, kSpread) & 0x10101010u);
+    const uint32_t hi = ((r.x >> 4) & 0x0F0F0F0Fu) | (__umul24((r.y >> 1) & 0x55u, kSpread) & 0x10101010u);
     uint32_t w[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      int lo = static_cast<int>((r.x >> (8 * e)) & 0xFu);
-      int hi = static_cast<int>((r.x >> (8 * e + 4)) & 0xFu);
-      if constexpr (BITS == 5) {
-        lo |= static_cast<int>((r.y >> (2 * e)) & 1u) << 4;
-        hi |= static_cast<int>((r.y >> (2 * e + 1)) & 1u) << 4;
-      }
-      w[e] = int_pair_bf16(lo - off, hi - off);
-    }
+    for (int e = 0; e < 4; ++e)
+      w[e] = pack_bf16_hw(static_cast<float>((lo >> (8 * e)) & 0xFFu) - 16.0f,
+                          static_cast<float>((hi >> (8 * e)) & 0xFFu) - 16.0f);
     return as_bf16x8(w[0], w[1], w[2], w[3]);
   }
 }
