@@ -261,28 +261,19 @@ unsigned fused_grid(long long vectors) {
 // only the streamed rest. HBM traffic per element: 4 B read + 1 B written
 // + 4 B re-read for the streamed fraction only (the two-launch form
 // re-reads everything: 9 B).
-#ifndef G4_SW_HR
-#define G4_SW_HR 18
-#endif
-#ifndef G4_SW_HL
-#define G4_SW_HL 9
-#endif
-#ifndef G4_SW_SU
-#define G4_SW_SU 2
-#endif
-#ifndef G4_SW_HB
-#define G4_SW_HB 4
-#endif
-#ifndef G4_SW_WPE
-#define G4_SW_WPE 4
-#endif
-constexpr int kHoldR = G4_SW_HR;
-constexpr int kHoldL = G4_SW_HL;
+// Held vectors per lane (VGPRs, LDS), held loads and streamed loads in
+// flight per lane, waves per SIMD. Measured at T=8192 (µs, one box, four
+// interleaved rounds): (18, 9, 4, 2, 4) 131.9-137.3, (22, 9, 2, 1, 4)
+// 129.9-132.3; earlier sweeps: (24, 9, 2, 2) 149, (20, 9, 3, 2) 137,
+// (28, 13, 3 waves) 132, (36, 16, 2 waves) 143-148.
+constexpr int kHoldR = 22;
+constexpr int kHoldL = 9;
 constexpr int kHold = kHoldR + kHoldL;
-constexpr int kHoldBatch = G4_SW_HB;  // held vectors' loads in flight per lane
-constexpr int kStreamU = G4_SW_SU;  // streamed vectors' loads in flight per lane
+constexpr int kHoldBatch = 2;  // held vectors' loads in flight per lane
+constexpr int kStreamU = 1;    // streamed vectors' loads in flight per lane
+constexpr int kHoldWavesPerEu = 4;
 
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(G4_SW_WPE))) void swiglu_fp8_hold_kernel(SwArgs a, GridSync gs) {
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kHoldWavesPerEu))) void swiglu_fp8_hold_kernel(SwArgs a, GridSync gs) {
   asm volatile("" ::"s"(a.gu), "s"(a.rows), "s"(a.I), "s"(a.inv_nv), "s"(a.act), "s"(a.codes),
                "s"(gs.gen), "s"(gs.slots), "s"(gs.result), "s"(gs.blocks));
   __shared__ uint4 s_hold[kHoldL > 0 ? kHoldL : 1][kBlock];
