@@ -26,10 +26,12 @@
 //                 then 16 + 4 g + i), the same for both operands.
 //
 // Numerics (the reference's tensor-core path): logit = bf16(scale * dot) with
-// dot = q . k (bf16 K) or q . codes * k_scale (quantised K; per group, then
-// summed, for group scales); p = exp(logit - m) in f32 against the split's
-// running maximum m, l sums the unrounded p, and the value product uses
-// bf16(p * v_scale) (or bf16(p)) against the V codes (values). The combine
+// dot = q . k (bf16 K) or q . codes * k_scale (one scale per row); p =
+// exp(logit - m) in f32 against the split's running maximum m, l sums the
+// unrounded p, and the value product uses bf16(p * v_scale) (or bf16(p))
+// against the V codes (values). Scale groups of 32 / 64 (not a reference
+// format) read each element as bf16(code * scale_g) and take the bf16 path
+// (kv_deq). The combine
 // rescales the splits' (m, l, o) and writes bf16(sum o w / sum l w): by
 // default the last split block of each (row group, KV head) does it inside
 // the split launch (combine_wave), else a second launch (attn_combine_kernel)
@@ -201,6 +203,67 @@ __device__ __forceinline__ bf16x8_t k_raw_bf16(const u32x4_t& r) {
   }
 }
 
+// Scale groups smaller than a row (32 or 64: this build's extension; the
+// reference keeps one scale per row): the attention reads each element
+// dequantised, bf16(code * scale_g), and then runs the bf16 path (logits
+// bf16(scale * q . k), unscaled bf16 probabilities). One scale per row keeps
+// the reference's form: codes in the products, the row's scales on the dot
+// and on p.
+template <int BITS, int GROUP>
+constexpr bool kv_deq() { return BITS != 16 && GROUP < kHd; }
+
+// The eight K elements of a quantised row as f32 codes.
+template <int BITS>
+__device__ __forceinline__ void k_raw_f32(const u32x4_t& r, float (&f)[8]) {
+  if constexpr (BITS == 8) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = static_cast<float>(static_cast<int8_t>((e < 4 ? r.x : r.y) >> (8 * (e & 3))));
+  } else if constexpr (BITS == 4) {
+    const uint32_t xs = r.x ^ 0x88888888u;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = static_cast<float>(sfield4(xs, 4 * e));
+  } else {
+    static_assert(BITS == 5, "k_raw_f32: int8, int4 or K5");
+    constexpr uint32_t kSpread = (1u << 4) | (1u << 10) | (1u << 16) | (1u << 22);
+    const uint32_t lo = (r.x & 0x0F0F0F0Fu) | (__umul24(r.y & 0x55u, kSpread) & 0x10101010u);
+    const uint32_t hi = ((r.x >> 4) & 0x0F0F0F0Fu) | (__umul24((r.y >> 1) & 0x55u, kSpread) & 0x10101010u);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      f[2 * e] = static_cast<float>((lo >> (8 * e)) & 0xFFu) - 16.0f;
+      f[2 * e + 1] = static_cast<float>((hi >> (8 * e)) & 0xFFu) - 16.0f;
+    }
+  }
+}
+// ... dequantised with the elements' group scale: bf16(code * s).
+template <int BITS>
+__device__ __forceinline__ bf16x8_t k_raw_deq(const u32x4_t& r, float s) {
+  float f[8];
+  k_raw_f32<BITS>(r, f);
+  return as_bf16x8(pack_bf16_hw(f[0] * s, f[1] * s), pack_bf16_hw(f[2] * s, f[3] * s),
+                   pack_bf16_hw(f[4] * s, f[5] * s), pack_bf16_hw(f[6] * s, f[7] * s));
+}
+// One 16-byte V chunk (int8: 16 values, int4: 32), dequantised with scale s,
+// as bf16 pairs w[0 .. 8 or 16).
+template <int BITS>
+__device__ __forceinline__ void v_chunk_deq(const u32x4_t& u, float s, uint32_t (&w)[BITS == 8 ? 8 : 16]) {
+  if constexpr (BITS == 8) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t x = u[e >> 1];
+      const int sh = 16 * (e & 1);
+      w[e] = pack_bf16_hw(static_cast<float>(static_cast<int8_t>(x >> sh)) * s,
+                          static_cast<float>(static_cast<int8_t>(x >> (sh + 8))) * s);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const uint32_t xs = u[e >> 2] ^ 0x88888888u;
+      const int b = 8 * (e & 3);
+      w[e] = pack_bf16_hw(static_cast<float>(sfield4(xs, b)) * s, static_cast<float>(sfield4(xs, b + 4)) * s);
+    }
+  }
+}
+
 // V staging: each step moves one 16-byte chunk per lane of the tile's rows
 // (bf16: 4 keys x 16 chunks per step, 16 steps; int8: 8 keys x 8 chunks, 8
 // steps; int4: 16 keys x 4 chunks, 4 steps) from the pool into a row-major
@@ -256,6 +319,29 @@ __device__ __forceinline__ void v_fix_bf16(uint16_t* vl, unsigned long long vali
     const int row = 4 * i + (lane >> 4);
     if (!((valid >> row) & 1ull))
       *reinterpret_cast<u32x4_t*>(dst + 1024 * i + 16 * lane) = u32x4_t{0u, 0u, 0u, 0u};
+  }
+}
+
+// v_store for scale groups smaller than a row: each chunk dequantised with
+// its key's group scale, scale_of(key, group) (keys without a row: 0).
+template <int BITS, int GROUP, typename F>
+__device__ __forceinline__ void v_store_deq(const u32x4_t (&raw)[VStage<BITS>::kSteps], uint16_t* vl,
+                                            unsigned long long valid, F scale_of) {
+  using VS = VStage<BITS>;
+  static_assert(BITS == 8 || BITS == 4 || BITS == 5, "quantised V");
+  constexpr int kDims = kHd / VS::kChunks;  // dims per chunk (16 or 32), within one group
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < VS::kSteps; ++i) {
+    const int key = i * (64 / VS::kChunks) + lane / VS::kChunks, c = lane % VS::kChunks;
+    const float sc = ((valid >> key) & 1ull) ? scale_of(key, (kDims * c) / GROUP) : 0.0f;
+    uint32_t w[BITS == 8 ? 8 : 16];
+    v_chunk_deq<BITS>(raw[i], sc, w);
+    uint16_t* dst = vl + key * kVPitch + kDims * c;
+#pragma unroll
+    for (int e = 0; e < kDims / 8; ++e)
+      *reinterpret_cast<u32x4_t*>(dst + 8 * e) = u32x4_t{w[4 * e], w[4 * e + 1], w[4 * e + 2], w[4 * e + 3]};
+    __builtin_amdgcn_sched_barrier(0);  // one step's values live at a time
   }
 }
 
@@ -409,6 +495,9 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
 void attn_split_kernel(AttnArgs a) {
   constexpr bool kQuant = BITS != 16;
   constexpr int kNgrp = kQuant ? kHd / GROUP : 1;
+  constexpr bool kDeq = kv_deq<BITS, GROUP>();  // elements dequantised before the products
+  constexpr bool kQB = kQuant && !kDeq;         // the products see codes and row scales
+  constexpr int kNgrpB = kQB ? kNgrp : 1;       // P packs per key
   constexpr int kKb = k_row_bytes(BITS), kVb = v_row_bytes(BITS);
   // Per wave: its V tile (reused for the end-of-block merge); each row's K and
   // V scales sit in the row's padding (dims 128..143: 8 floats), so the
@@ -686,48 +775,48 @@ void attn_split_kernel(AttnArgs a) {
       }
     }
     const unsigned long long kvalid = __ballot(prow >= 0);
+    const auto store_scales = [&] {
+      if constexpr (kQuant) {
+#pragma unroll
+        for (int gi = 0; gi < kNgrp; ++gi) {
+          ksc_at(lane, gi) = prow >= 0 ? ksr[gi] : 0.0f;
+          vsc_at(lane, gi) = prow >= 0 ? vsr[gi] : 0.0f;
+        }
+      }
+    };
     if constexpr (kVDma) {
       // Every load of the tile has landed (the K loads, issued after the V
       // tile's, are needed next anyway); then the tile's fix-ups.
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       v_fix_bf16(vl, kvalid);
+    } else if constexpr (kDeq) {
+      store_scales();
+      wave_lds_sync();  // the scales, read per key below
+      v_store_deq<BITS, GROUP>(vraw, vl, kvalid, vsc_at);
     } else {
       v_store<BITS>(vraw, vl, kvalid);
     }
-    if constexpr (kQuant) {
-#pragma unroll
-      for (int gi = 0; gi < kNgrp; ++gi) {
-        ksc_at(lane, gi) = prow >= 0 ? ksr[gi] : 0.0f;
-        vsc_at(lane, gi) = prow >= 0 ? vsr[gi] : 0.0f;
-      }
-    }
+    if constexpr (!kDeq) store_scales();
     wave_lds_sync();  // V tile and scales in LDS
     // S^T = K Q^T per 16-key block mb: lane l holds keys 16 mb + 4 g + i.
     float sv[4][4];
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) {
       bf16x8_t ka[4];
+      if constexpr (kDeq) {
+        // this lane's A row, key 16 mb + n, dims 32 s + 8 g ..: group 32 s / GROUP
 #pragma unroll
-      for (int s = 0; s < 4; ++s) ka[s] = k_raw_bf16<BITS>(kraw[mb][s]);
-      f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-      if constexpr (!kQuant || GROUP == kHd) {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s], qb[s], acc, 0, 0, 0);
-        if constexpr (kQuant) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[i] = acc[i] * ksc_at(16 * mb + 4 * g + i, 0);
-        }
+        for (int s = 0; s < 4; ++s) ka[s] = k_raw_deq<BITS>(kraw[mb][s], ksc_at(16 * mb + n, (32 * s) / GROUP));
       } else {
-        constexpr int kSteps = GROUP / 32;
 #pragma unroll
-        for (int gi = 0; gi < kNgrp; ++gi) {
-          f32x4_t part = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int s = 0; s < 4; ++s) ka[s] = k_raw_bf16<BITS>(kraw[mb][s]);
+      }
+      f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-          for (int s = gi * kSteps; s < (gi + 1) * kSteps; ++s)
-            part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s], qb[s], part, 0, 0, 0);
+      for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s], qb[s], acc, 0, 0, 0);
+      if constexpr (kQB) {  // one scale per row
 #pragma unroll
-          for (int i = 0; i < 4; ++i) acc[i] += part[i] * ksc_at(16 * mb + 4 * g + i, gi);
-        }
+        for (int i = 0; i < 4; ++i) acc[i] = acc[i] * ksc_at(16 * mb + 4 * g + i, 0);
       }
       // logit = bf16(scale * dot), two per hardware conversion (equal to the
       // integer rounding for every non-NaN value)
@@ -766,14 +855,14 @@ void attn_split_kernel(AttnArgs a) {
     // (j < 4) or 32 s + 16 + 4 g + j - 4.
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      bf16x8_t pb[kNgrp];
+      bf16x8_t pb[kNgrpB];
 #pragma unroll
-      for (int gi = 0; gi < kNgrp; ++gi) {
+      for (int gi = 0; gi < kNgrpB; ++gi) {
         float pv[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const int mb = 2 * s + (j >> 2), i = j & 3;
-          const float sc = kQuant ? vsc_at(16 * mb + 4 * g + i, gi) : 1.0f;
+          const float sc = kQB ? vsc_at(16 * mb + 4 * g + i, gi) : 1.0f;
           pv[j] = e[mb][i] * sc;
         }
         pb[gi] = as_bf16x8(pack_bf16_hw(pv[0], pv[1]), pack_bf16_hw(pv[2], pv[3]),
@@ -791,7 +880,7 @@ void attn_split_kernel(AttnArgs a) {
         const u32x2_t lo = lds_read_tr(r1 + co);
         const u32x2_t hi = lds_read_tr(r2 + co);
         const bf16x8_t va = as_bf16x8(lo.x, lo.y, hi.x, hi.y);
-        const int gi = kQuant ? (16 * nb) / GROUP : 0;
+        const int gi = kQB ? (16 * nb) / GROUP : 0;
         o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[gi], o[nb], 0, 0, 0);
       }
     }
@@ -982,6 +1071,7 @@ struct PrefillRaw {
   static constexpr int kPrefThreads = W * 64;
   static constexpr bool kQuant = BITS != 16;
   static constexpr int kNgrp = kQuant ? kHd / GROUP : 1;
+  static constexpr bool kDeq = kv_deq<BITS, GROUP>();  // staged dequantised
   static constexpr int kKElems = BITS == 16 ? 8 : BITS == 8 ? 16 : 32;  // per K chunk
   static constexpr int kKRowChunks = kHd / kKElems;
   static constexpr int kKIt = (kTile * kKRowChunks + kPrefThreads - 1) / (kPrefThreads);
@@ -993,6 +1083,7 @@ struct PrefillRaw {
   u32x4_t k[kKIt][kKElems / 8];
   u32x4_t v[kVIt];
   float ksc[kKIt][kNgrp], vsc[kKIt][kNgrp];
+  float vsd[kDeq ? kVIt : 1];  // kDeq: each V chunk's group scale
   int kr[kKIt], vr[kVIt];  // arena rows (-1: no row)
 };
 
@@ -1065,6 +1156,9 @@ __device__ __forceinline__ void prefill_load(const PrefillArgs& a, const uint8_t
     raw.vr[it] = pr;
     raw.v[it] = *reinterpret_cast<const u32x4_t*>(
         vbase + static_cast<size_t>(pr >= 0 ? pr : 0) * VStage<BITS>::kRowB + 16 * c);
+    if constexpr (R::kDeq)
+      raw.vsd[it] = vscb[static_cast<size_t>(pr >= 0 ? pr : 0) * R::kNgrp +
+                         (c * (kHd / R::kVRowChunks)) / GROUP];
   }
 }
 
@@ -1084,12 +1178,21 @@ __device__ __forceinline__ void prefill_store(const PrefillRaw<BITS, GROUP, W>& 
     uint16_t* dst = ks + key * kKPitch + c;
 #pragma unroll
     for (int h = 0; h < R::kKElems / 8; ++h) {
-      const bf16x8_t kv = pr >= 0 ? k_raw_bf16<BITS>(raw.k[it][h])
-                                  : __builtin_bit_cast(bf16x8_t, u32x4_t{0u, 0u, 0u, 0u});
+      bf16x8_t kv = __builtin_bit_cast(bf16x8_t, u32x4_t{0u, 0u, 0u, 0u});
+      if constexpr (R::kDeq) {
+        // the chunk's group scale, selected without indexing registers at run time
+        const int gsel = (c + 8 * h) / GROUP;
+        float sk = raw.ksc[it][0];
+#pragma unroll
+        for (int gi = 1; gi < R::kNgrp; ++gi) sk = gi == gsel ? raw.ksc[it][gi] : sk;
+        if (pr >= 0) kv = k_raw_deq<BITS>(raw.k[it][h], sk);
+      } else {
+        if (pr >= 0) kv = k_raw_bf16<BITS>(raw.k[it][h]);
+      }
       *reinterpret_cast<bf16x8_t*>(dst + 8 * h) = kv;
     }
     if (c == 0) {
-      if constexpr (R::kQuant) {
+      if constexpr (R::kQuant && !R::kDeq) {
 #pragma unroll
         for (int gi = 0; gi < R::kNgrp; ++gi) {
           ksc_l[key * R::kNgrp + gi] = pr >= 0 ? raw.ksc[it][gi] * kmul : 0.0f;
@@ -1106,7 +1209,15 @@ __device__ __forceinline__ void prefill_store(const PrefillRaw<BITS, GROUP, W>& 
     const int key = idx / R::kVRowChunks, c = idx % R::kVRowChunks;
     const uint32_t z = BITS == 16 || BITS == 8 ? 0u : 0x88888888u;
     const u32x4_t u = raw.vr[it] >= 0 ? raw.v[it] : u32x4_t{z, z, z, z};
-    if constexpr (BITS == 16) {
+    if constexpr (R::kDeq) {
+      constexpr int kDims = kHd / R::kVRowChunks;
+      uint32_t w[BITS == 8 ? 8 : 16];
+      v_chunk_deq<BITS>(u, raw.vr[it] >= 0 ? raw.vsd[it] : 0.0f, w);
+      uint16_t* dst = vs + key * kVPitch + kDims * c;
+#pragma unroll
+      for (int e = 0; e < kDims / 8; ++e)
+        *reinterpret_cast<u32x4_t*>(dst + 8 * e) = u32x4_t{w[4 * e], w[4 * e + 1], w[4 * e + 2], w[4 * e + 3]};
+    } else if constexpr (BITS == 16) {
       *reinterpret_cast<u32x4_t*>(vs + key * kVPitch + 8 * c) = u;
     } else if constexpr (BITS == 8) {
       uint32_t w[8];
@@ -1150,6 +1261,8 @@ __global__ __launch_bounds__(W * 64) void attn_prefill_kernel(PrefillArgs a) {
   constexpr int kPrefWaves = W / KSP;  // waves owning positions (and staging a tile)
   constexpr bool kQuant = BITS != 16;
   constexpr int kNgrp = kQuant ? kHd / GROUP : 1;
+  constexpr bool kQB = kQuant && !kv_deq<BITS, GROUP>();  // codes and row scales in the products
+  constexpr int kNgrpB = kQB ? kNgrp : 1;
   constexpr int kKb = k_row_bytes(BITS), kVb = v_row_bytes(BITS);
   constexpr int kPos = kPrefWaves * 4 * CB;  // positions per workgroup
   // Two tile buffers per key group: tile t + 1 is staged into one while tile
@@ -1260,36 +1373,24 @@ __global__ __launch_bounds__(W * 64) void attn_prefill_kernel(PrefillArgs a) {
 #pragma unroll
         for (int s = 0; s < 4; ++s)
           ka[s] = *reinterpret_cast<const bf16x8_t*>(ks + (16 * mb + n) * kKPitch + 32 * s + 8 * g);
-        float ksv[4][kNgrp];
+        float ksv[4][kNgrpB];
         bool kv_ok[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int key = 16 * mb + 4 * g + i;
           kv_ok[i] = kMask ? s_valid[key] != 0u : true;
 #pragma unroll
-          for (int gi = 0; gi < kNgrp; ++gi) ksv[i][gi] = kQuant ? ksc_l[key * kNgrp + gi] : 1.0f;
+          for (int gi = 0; gi < kNgrpB; ++gi) ksv[i][gi] = kQB ? ksc_l[key * kNgrp + gi] : 1.0f;
         }
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb) {
           // dot * scale: the staged K scales carry the logit scale.
           f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-          if constexpr (!kQuant || GROUP == kHd) {
+          // (one scale per row: the staged scales carry the logit scale)
 #pragma unroll
-            for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s], qb[cb][s], acc, 0, 0, 0);
+          for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s], qb[cb][s], acc, 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[i] = acc[i] * (kQuant ? ksv[i][0] : a.scale);
-          } else {
-            constexpr int kSteps = GROUP / 32;
-#pragma unroll
-            for (int gi = 0; gi < kNgrp; ++gi) {
-              f32x4_t part = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-              for (int s = gi * kSteps; s < (gi + 1) * kSteps; ++s)
-                part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s], qb[cb][s], part, 0, 0, 0);
-#pragma unroll
-              for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(part[i], ksv[i][gi], acc[i]);
-            }
-          }
+          for (int i = 0; i < 4; ++i) acc[i] = acc[i] * (kQB ? ksv[i][0] : a.scale);
           const uint32_t lg01 = pack_bf16_hw(acc[0], acc[1]);
           const uint32_t lg23 = pack_bf16_hw(acc[2], acc[3]);
           const float lg[4] = {lo_bf16(lg01), hi_bf16(lg01), lo_bf16(lg23), hi_bf16(lg23)};
@@ -1335,22 +1436,22 @@ __global__ __launch_bounds__(W * 64) void attn_prefill_kernel(PrefillArgs a) {
       }
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        float vsv[8][kNgrp];
+        float vsv[8][kNgrpB];
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj) {
           const int key = 16 * (2 * s + (jj >> 2)) + 4 * g + (jj & 3);
 #pragma unroll
-          for (int gi = 0; gi < kNgrp; ++gi) vsv[jj][gi] = kQuant ? vsc_l[key * kNgrp + gi] : 1.0f;
+          for (int gi = 0; gi < kNgrpB; ++gi) vsv[jj][gi] = kQB ? vsc_l[key * kNgrp + gi] : 1.0f;
         }
-        bf16x8_t pb[CB][kNgrp];
+        bf16x8_t pb[CB][kNgrpB];
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
-          for (int gi = 0; gi < kNgrp; ++gi) {
+          for (int gi = 0; gi < kNgrpB; ++gi) {
             float pv[8];
 #pragma unroll
             for (int jj = 0; jj < 8; ++jj)
-              pv[jj] = kQuant ? e[cb][2 * s + (jj >> 2)][jj & 3] * vsv[jj][gi] : e[cb][2 * s + (jj >> 2)][jj & 3];
+              pv[jj] = kQB ? e[cb][2 * s + (jj >> 2)][jj & 3] * vsv[jj][gi] : e[cb][2 * s + (jj >> 2)][jj & 3];
             pb[cb][gi] = as_bf16x8(pack_bf16_hw(pv[0], pv[1]), pack_bf16_hw(pv[2], pv[3]),
                                    pack_bf16_hw(pv[4], pv[5]), pack_bf16_hw(pv[6], pv[7]));
           }
@@ -1362,7 +1463,7 @@ __global__ __launch_bounds__(W * 64) void attn_prefill_kernel(PrefillArgs a) {
           const u32x2_t lo2 = lds_read_tr(r1 + 16 * nb);
           const u32x2_t hi2 = lds_read_tr(r2 + 16 * nb);
           const bf16x8_t va = as_bf16x8(lo2.x, lo2.y, hi2.x, hi2.y);
-          const int gi = kQuant ? (16 * nb) / GROUP : 0;
+          const int gi = kQB ? (16 * nb) / GROUP : 0;
 #pragma unroll
           for (int cb = 0; cb < CB; ++cb)
             o[cb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[cb][gi], o[cb][nb], 0, 0, 0);

@@ -449,7 +449,8 @@ int granite4_prefill_attention(const uint16_t* q_rot, const uint16_t* cache_k,
                                const int* d_pt, int k5, int window);
 
 /* granite4_prefill_attention for every pool format of this library (bits 16
- * / 8 / 4 / 5, group 32 / 64 / 128 scales). New entry point. */
+ * / 8 / 4 / 5, group 32 / 64 / 128 scales; groups of 32 / 64 read as
+ * granite4_attn_paged reads them). New entry point. */
 int granite4_prefill_attn(const uint16_t* q_rot, int rows, int Hq, int Hk, int d, float scale,
                           const void* cache_k, const void* cache_v, const float* k_scale,
                           const float* v_scale, int bits, int group, int stride, int base_pos,
@@ -458,7 +459,10 @@ int granite4_prefill_attn(const uint16_t* q_rot, int rows, int Hq, int Hk, int d
 /* The same attention for any pool format of this library, including the
  * group scales of granite4_rope_append: bits 16 / 8 / 4 / 5 (K5 K + int4 V),
  * group 32 / 64 / 128 (scales [Hk][stride][128 / group]; ignored for bf16).
- * New entry point (the reference's attention reads per-row scales only). */
+ * New entry point (the reference's attention reads per-row scales only).
+ * Group 128 keeps the reference's numerics (codes in the products, the row
+ * scales on the dot and on p); groups of 32 / 64 are the bf16 attention over
+ * the cache dequantised element by element, bf16(code * scale_g). */
 int granite4_attn_paged(const uint16_t* q, int rows, int Hq, int Hk, int d, float scale,
                         const void* cache_k, const void* cache_v, const float* k_scale,
                         const float* v_scale, int bits, int group, int stride, int kv_base,

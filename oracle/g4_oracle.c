@@ -473,6 +473,16 @@ static float kv_elem(const uint8_t* row, int bits, int is_k, int d, int i) {
   }
 }
 
+/* Element i of a cached row as the attention reads it: the code (or bf16
+ * value), or for scale groups smaller than the row (this build's group-32 /
+ * 64 pools) the element dequantised to bf16, bf16(code * scale_g). */
+static float kv_att(const uint8_t* row, int bits, int is_k, int d, int i, const float* sc,
+                    int group) {
+  const float c = kv_elem(row, bits, is_k, d, i);
+  if (bits == 16 || group >= d) return c;
+  return g4o_bf16_to_f32(g4o_f32_to_bf16(c * sc[i / group]));
+}
+
 void g4o_attn_split(const uint16_t* q, int rows, int Hq, int Hk, int d, float scale,
                     const void* cache_k, const void* cache_v, const float* k_scale,
                     const float* v_scale, int bits, int group, int stride, const int* pos,
@@ -480,7 +490,7 @@ void g4o_attn_split(const uint16_t* q, int rows, int Hq, int Hk, int d, float sc
   const int G = Hq / Hk, ngrp = d / group, tile = 64, span = tps * tile;
   const int kb = kv_row_bytes(bits, d, 1), vb = kv_row_bytes(bits, d, 0);
   const int quant = bits != 16;
-  float qf[1024], oacc[1024], acc[1024], logit[64], pbf[64 * 32];
+  float qf[1024], oacc[1024], acc[1024], logit[64], pbf[64];
   float *ms = NULL, *ls = NULL, *os = NULL;
   for (int r = 0; r < rows; ++r) {
     const int len = pos[r] + 1;
@@ -516,16 +526,13 @@ void g4o_attn_split(const uint16_t* q, int rows, int Hq, int Hk, int d, float sc
               continue;
             }
             const uint8_t* krow = (const uint8_t*)cache_k + ((size_t)hk * stride + arow) * kb;
+            const float* ks = quant ? k_scale + ((size_t)hk * stride + arow) * ngrp : NULL;
             float dot = 0.0f;
-            if (!quant) {
-              for (int i = 0; i < d; ++i) dot += qf[i] * kv_elem(krow, bits, 1, d, i);
+            if (!quant || ngrp > 1) {
+              for (int i = 0; i < d; ++i) dot += qf[i] * kv_att(krow, bits, 1, d, i, ks, group);
             } else {
-              const float* ks = k_scale + ((size_t)hk * stride + arow) * ngrp;
-              for (int g = 0; g < ngrp; ++g) {
-                float part = 0.0f;
-                for (int i = g * group; i < (g + 1) * group; ++i) part += qf[i] * kv_elem(krow, bits, 1, d, i);
-                dot += part * ks[g];
-              }
+              for (int i = 0; i < d; ++i) dot += qf[i] * kv_elem(krow, bits, 1, d, i);
+              dot *= ks[0];
             }
             logit[j] = g4o_bf16_to_f32(g4o_f32_to_bf16(scale * dot));
             if (logit[j] > mx) mx = logit[j];
@@ -540,17 +547,16 @@ void g4o_attn_split(const uint16_t* q, int rows, int Hq, int Hk, int d, float sc
             const int p = t0 + j;
             const int valid = logit[j] != -INFINITY;
             const int arow = valid ? (pt != NULL && pt[r] != NULL ? pt[r][p] : p) : 0;
-            for (int g = 0; g < ngrp; ++g) {
-              const float sv = quant && valid ? v_scale[((size_t)hk * stride + arow) * ngrp + g] : 1.0f;
-              pbf[j * ngrp + g] = g4o_bf16_to_f32(g4o_f32_to_bf16(e * sv));
-            }
+            const float sv = quant && ngrp == 1 && valid ? v_scale[(size_t)hk * stride + arow] : 1.0f;
+            pbf[j] = g4o_bf16_to_f32(g4o_f32_to_bf16(e * sv));
           }
           for (int j = 0; j < tile; ++j) {
             if (logit[j] == -INFINITY) continue;
             const int p = t0 + j;
             const int arow = pt != NULL && pt[r] != NULL ? pt[r][p] : p;
             const uint8_t* vrow = (const uint8_t*)cache_v + ((size_t)hk * stride + arow) * vb;
-            for (int i = 0; i < d; ++i) oacc[i] += pbf[j * ngrp + i / group] * kv_elem(vrow, bits, 0, d, i);
+            const float* vs = quant ? v_scale + ((size_t)hk * stride + arow) * ngrp : NULL;
+            for (int i = 0; i < d; ++i) oacc[i] += pbf[j] * kv_att(vrow, bits, 0, d, i, vs, group);
           }
         }
         ms[sp] = m;
@@ -583,7 +589,7 @@ static void attn_tiles(const float* qf, int hk, float scale, const void* cache_k
                        float* m_out, float* l_out, float* oacc) {
   const int ngrp = d / group, tile = 64, quant = bits != 16;
   const int kb = kv_row_bytes(bits, d, 1), vb = kv_row_bytes(bits, d, 0);
-  float logit[64], pbf[64 * 32];
+  float logit[64], pbf[64];
   float m = -INFINITY, l = 0.0f;
   for (int i = 0; i < d; ++i) oacc[i] = 0.0f;
   for (int t0 = t_first; t0 < t_end; t0 += tile) {
@@ -596,16 +602,13 @@ static void attn_tiles(const float* qf, int hk, float scale, const void* cache_k
       }
       const int arow = pt != NULL ? pt[p] : p;
       const uint8_t* krow = (const uint8_t*)cache_k + ((size_t)hk * stride + arow) * kb;
+      const float* ks = quant ? k_scale + ((size_t)hk * stride + arow) * ngrp : NULL;
       float dot = 0.0f;
-      if (!quant) {
-        for (int i = 0; i < d; ++i) dot += qf[i] * kv_elem(krow, bits, 1, d, i);
+      if (!quant || ngrp > 1) {
+        for (int i = 0; i < d; ++i) dot += qf[i] * kv_att(krow, bits, 1, d, i, ks, group);
       } else {
-        const float* ks = k_scale + ((size_t)hk * stride + arow) * ngrp;
-        for (int g = 0; g < ngrp; ++g) {
-          float part = 0.0f;
-          for (int i = g * group; i < (g + 1) * group; ++i) part += qf[i] * kv_elem(krow, bits, 1, d, i);
-          dot += part * ks[g];
-        }
+        for (int i = 0; i < d; ++i) dot += qf[i] * kv_elem(krow, bits, 1, d, i);
+        dot *= ks[0];
       }
       logit[j] = g4o_bf16_to_f32(g4o_f32_to_bf16(scale * dot));
       if (logit[j] > mx) mx = logit[j];
@@ -619,16 +622,15 @@ static void attn_tiles(const float* qf, int hk, float scale, const void* cache_k
       l += e;
       const int valid = logit[j] != -INFINITY;
       const int arow = valid ? (pt != NULL ? pt[t0 + j] : t0 + j) : 0;
-      for (int g = 0; g < ngrp; ++g) {
-        const float sv = quant && valid ? v_scale[((size_t)hk * stride + arow) * ngrp + g] : 1.0f;
-        pbf[j * ngrp + g] = g4o_bf16_to_f32(g4o_f32_to_bf16(e * sv));
-      }
+      const float sv = quant && ngrp == 1 && valid ? v_scale[(size_t)hk * stride + arow] : 1.0f;
+      pbf[j] = g4o_bf16_to_f32(g4o_f32_to_bf16(e * sv));
     }
     for (int j = 0; j < tile; ++j) {
       if (logit[j] == -INFINITY) continue;
       const int arow = pt != NULL ? pt[t0 + j] : t0 + j;
       const uint8_t* vrow = (const uint8_t*)cache_v + ((size_t)hk * stride + arow) * vb;
-      for (int i = 0; i < d; ++i) oacc[i] += pbf[j * ngrp + i / group] * kv_elem(vrow, bits, 0, d, i);
+      const float* vs = quant ? v_scale + ((size_t)hk * stride + arow) * ngrp : NULL;
+      for (int i = 0; i < d; ++i) oacc[i] += pbf[j] * kv_att(vrow, bits, 0, d, i, vs, group);
     }
   }
   *m_out = m;

@@ -123,12 +123,15 @@ void g4o_rope_append(const uint16_t* q, long q_stride, const uint16_t* k, long k
  * g4o_rope_append's. Positions are cut into 64-position tiles and
  * the tiles into splits of tps tiles; each split keeps its own online
  * softmax, and the splits are combined, as the kernels do:
- *   logit  = bf16(scale * dot), dot = q . k (bf16 K) or sum over scale groups
- *            of (q . codes) * k_scale (quantised K; one group = the
- *            reference's per-row scale)
+ *   logit  = bf16(scale * dot), dot = q . k (bf16 K), (q . codes) * k_scale
+ *            (quantised K with the reference's one scale per row, group =
+ *            d), or q . bf16(code * k_scale_g) (scale groups of 32 or 64,
+ *            this build's extension: each element dequantised to bf16 with
+ *            its group's scale, then the bf16 path)
  *   p      = exp(logit - m) (f32, m = the split's running maximum), summed
  *            unrounded into l; the value product uses bf16(p * v_scale)
- *            (quantised V) or bf16(p) (bf16 V) against the code / value
+ *            against the code (one scale per row), or bf16(p) against the
+ *            bf16 value (bf16 V; scale groups: bf16(code * v_scale_g))
  *   out    = bf16(sum_s o_s w_s / sum_s l_s w_s), w_s = exp(m_s - max_s m_s).
  * Sums run in f32 in key / dim order. */
 void g4o_attn_split(const uint16_t* q, int rows, int Hq, int Hk, int d, float scale,
@@ -142,8 +145,8 @@ void g4o_attn_split(const uint16_t* q, int rows, int Hq, int Hk, int d, float sc
  * q [rows][Hq][d] sit at positions base_pos + r and attend to positions
  * [lo, base_pos + r] (lo as g4o_attn_split's window rule) through pt (NULL:
  * row = position), in one pass of 64-position tiles from position 0: the
- * same logits, online softmax and bf16(p * v_scale) value product as
- * g4o_attn_split, and out = bf16(o * (1 / l)). */
+ * same logits, online softmax and value product as g4o_attn_split, and
+ * out = bf16(o * (1 / l)). */
 void g4o_prefill_attn(const uint16_t* q, int rows, int Hq, int Hk, int d, float scale,
                       const void* cache_k, const void* cache_v, const float* k_scale,
                       const float* v_scale, int bits, int group, int stride, int base_pos,

@@ -2,7 +2,8 @@
 granite4_attn_split) against the oracle's g4o_attn_split on the same caches.
 
 The kernel follows the oracle's structure exactly (64-position tiles, the same
-splits, bf16 logits, bf16(p * v_scale) in the value product, the same
+splits, bf16 logits, bf16(p * v_scale) in the value product for one scale
+per row, the dequantised bf16 path for scale groups of 32 / 64, the same
 combine); what differs is the order of the f32 sums inside the MFMA and the
 hardware exponential. Bar, per output element: within 2 bf16 steps of the
 oracle's value, or within 2^-8 of max |V| where the output nearly cancels

@@ -172,24 +172,36 @@ def test_attn_quantised_pow2_scales_equal_bf16_on_dequantised(bits):
     np.testing.assert_array_equal(a, b)
 
 
-def test_attn_group_scales_close_to_dequantised_bf16():
-    """Group-32 scales (this build's extension): the quantised path with
-    per-group power-of-two scales matches the bf16 path on the dequantised
-    values within the f32 re-association of the per-group partial dots."""
-    Hq, Hk, n, grp = 8, 2, 120, 32
-    rng = np.random.default_rng(77)
-    ck = rng.integers(0, 256, Hk * n * 80, dtype=np.uint8)
-    cv = rng.integers(0, 256, Hk * n * 64, dtype=np.uint8)
-    ks = (2.0 ** rng.integers(-8, -3, Hk * n * 4)).astype(np.float32)
-    vs = (2.0 ** rng.integers(-6, -1, Hk * n * 4)).astype(np.float32)
-    kf = _dequant_rows(ck, 5, True, Hk * n) * np.repeat(ks.reshape(-1, 4), grp, axis=1)
-    vf = _dequant_rows(cv, 5, False, Hk * n) * np.repeat(vs.reshape(-1, 4), grp, axis=1)
-    q = _rand_q(0xA9, 2, Hq)
-    pos = [n - 1, 40]
-    a = ol.attn_split(q, ck, cv, ks, vs, 5, grp, n, pos, Hk=Hk)
-    b = ol.attn_split(q, ol.f32_to_bf16(kf).view(np.uint8), ol.f32_to_bf16(vf).view(np.uint8),
-                      None, None, 16, D, n, pos, Hk=Hk)
-    assert _ulps(a, b).max() <= 2
+@pytest.mark.parametrize("bits,grp", [(5, 32), (4, 32), (8, 64), (4, 64)])
+def test_attn_group_scales_are_the_bf16_path_on_dequantised_values(bits, grp):
+    """Scale groups of 32 or 64 (this build's extension; the reference has one
+    scale per row): the attention reads each element as bf16(code * scale_g)
+    and then runs the bf16 path, so for any scales (not only powers of two)
+    it equals the bf16 attention over that dequantised cache bit for bit, in
+    the split and in the prefill form."""
+    Hq, Hk, n = 8, 2, 130
+    ng = D // grp
+    rng = np.random.default_rng(77 + bits + grp)
+    kb, vb = ol.KV_ROW_BYTES[bits]
+    ck = rng.integers(0, 256, Hk * n * kb, dtype=np.uint8)
+    cv = rng.integers(0, 256, Hk * n * vb, dtype=np.uint8)
+    ks = (rng.random(Hk * n * ng, dtype=np.float32) * 0.05 + 0.001).astype(np.float32)
+    vs = (rng.random(Hk * n * ng, dtype=np.float32) * 0.2 + 0.01).astype(np.float32)
+    if bits == 8:
+        ks *= np.float32(0.1)
+    kf = _dequant_rows(ck, bits, True, Hk * n) * np.repeat(ks.reshape(-1, ng), grp, axis=1)
+    vf = _dequant_rows(cv, bits, False, Hk * n) * np.repeat(vs.reshape(-1, ng), grp, axis=1)
+    kbf, vbf = ol.f32_to_bf16(kf).view(np.uint8), ol.f32_to_bf16(vf).view(np.uint8)
+    assert not np.array_equal(ol.bf16_to_f32(ol.f32_to_bf16(kf)), kf)  # the rounding matters
+    q = _rand_q(0xA9 + bits, 3, Hq)
+    pos = [n - 1, 40, 64]
+    a = ol.attn_split(q, ck, cv, ks, vs, bits, grp, n, pos, Hk=Hk)
+    b = ol.attn_split(q, kbf, vbf, None, None, 16, D, n, pos, Hk=Hk)
+    np.testing.assert_array_equal(a, b)
+    qp = _rand_q(0xAA + bits, 20, Hq)
+    a = ol.prefill_attn(qp, ck, cv, ks, vs, bits, grp, n, 100, Hk=Hk)
+    b = ol.prefill_attn(qp, kbf, vbf, None, None, 16, D, n, 100, Hk=Hk)
+    np.testing.assert_array_equal(a, b)
 
 
 @pytest.mark.parametrize("kv_len,tps", [(500, 1), (500, 3), (2000, 1), (2000, 8)])
