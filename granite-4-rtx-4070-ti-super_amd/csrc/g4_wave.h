@@ -86,6 +86,23 @@ __device__ __forceinline__ float wave_max(float v) {
                fmaxf(readlane_f32(v, 32), readlane_f32(v, 48)));
 }
 
+// Issue priority from progress: a wave that has done `done` of its `total`
+// work items takes priority 3 (none done) down to 0 (the last quarter). The
+// SIMD's arbiter picks the highest priority first and the oldest wave among
+// equals, so without this the first-dispatched of the workgroups sharing a
+// CU runs ahead and the last finishes late, leaving the CU's tail with too
+// few waves to keep its loads in flight. done / total: the first active
+// lane's values are used.
+__device__ __forceinline__ void wave_priority_by_progress(int done, int total) {
+  done = __builtin_amdgcn_readfirstlane(done);
+  total = __builtin_amdgcn_readfirstlane(total);
+  const int q = total > 0 ? (4 * done) / total : 4;
+  if (q <= 0) __builtin_amdgcn_s_setprio(3);
+  else if (q == 1) __builtin_amdgcn_s_setprio(2);
+  else if (q == 2) __builtin_amdgcn_s_setprio(1);
+  else __builtin_amdgcn_s_setprio(0);
+}
+
 }  // namespace g4
 
 #endif  // G4_WAVE_H

@@ -100,6 +100,15 @@ __device__ __forceinline__ uint32_t act_pair(const GuRaw<F32IN>& x, int p) {
   return pack_bf16_hw(silu_mul(g0, u0), silu_mul(g1, u1));
 }
 
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>), in order.
+template <int N, int I = 0, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<N, I + 1>(f);
+  }
+}
+
 // Vectors (of gate and of up) in flight per lane.
 constexpr int kSwU = 2;
 
@@ -257,8 +266,12 @@ unsigned fused_grid(long long vectors) {
 // persistent grid (every workgroup resident, at most kMaxPartials of them)
 // in which each lane holds its first kHoldR vectors of act in VGPRs and the
 // next kHoldL in LDS, and streams the rest once for max |act|. After the
-// grid synchronisation it encodes what it holds, then re-reads and encodes
-// only the streamed rest. HBM traffic per element: 4 B read + 1 B written
+// grid synchronisation it encodes what it holds, interleaved with the
+// re-read and encode of only the streamed rest. Every wave sets its issue
+// priority from its progress (wave_priority_by_progress), which keeps the
+// four workgroups sharing a CU within a quarter of their work of each other
+// (the oldest otherwise runs ahead and the youngest ends the launch late).
+// HBM traffic per element: 4 B read + 1 B written
 // + 4 B re-read for the streamed fraction only (the two-launch form
 // re-reads everything: 9 B).
 // Held vectors per lane (VGPRs, LDS), held loads and streamed loads in
@@ -272,6 +285,12 @@ constexpr int kHold = kHoldR + kHoldL;
 constexpr int kHoldBatch = 2;  // held vectors' loads in flight per lane
 constexpr int kStreamU = 1;    // streamed vectors' loads in flight per lane
 constexpr int kHoldWavesPerEu = 4;
+// Held vectors encoded per streamed re-read after the grid maximum (0: all
+// held first). With the issue priority by progress in both sweeps, measured
+// at T=8192 (one box, two rounds, us): mix 2 123.5-124.5; held first 128.7;
+// mix 2 or 3 with the priority in the first sweep only 128.8-129.3; neither
+// (the previous form) 128.9-129.5.
+constexpr int kMix = 2;
 
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kHoldWavesPerEu))) void swiglu_fp8_hold_kernel(SwArgs a, GridSync gs) {
   asm volatile("" ::"s"(a.gu), "s"(a.rows), "s"(a.I), "s"(a.inv_nv), "s"(a.act), "s"(a.codes),
@@ -297,8 +316,12 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kHoldWav
     }
   };
   uint32_t w[kHoldR][4];
+  // Vectors per lane over both parts (held, then streamed), for the issue
+  // priority by progress.
+  const int per_lane = (total + step - 1) / step;
 #pragma unroll
   for (int k0 = 0; k0 < kHold; k0 += kHoldBatch) {
+    wave_priority_by_progress(k0, per_lane);
     GuRaw<false> x[kHoldBatch];
 #pragma unroll
     for (int j = 0; j < kHoldBatch; ++j)
@@ -321,7 +344,8 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kHoldWav
   // The streamed rest: max only (cached loads: part is still cached when
   // the second sweep comes back to it).
   const int vs = v0 + kHold * step;
-  for (int v = vs; v < total; v += kStreamU * step) {
+  for (int v = vs, i = kHold; v < total; v += kStreamU * step, i += kStreamU) {
+    wave_priority_by_progress(i, per_lane);
     GuRaw<false> x[kStreamU];
 #pragma unroll
     for (int j = 0; j < kStreamU; ++j) x[j] = load_gu<false, false>(a, min(v + j * step, total - 1), nv);
@@ -332,44 +356,68 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kHoldWav
     }
   }
   G4_TRACE_MARK(gs, 2);
+  __builtin_amdgcn_s_setprio(0);
   const Fp8Enc f = fp8_enc_of(fp8_scale_for(grid_max(m, gs, tag)));
   G4_TRACE_MARK(gs, 3);
   if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = f.s;
   const auto encode = [&](auto fast_tag) {
     constexpr bool kFast = decltype(fast_tag)::value;
-#pragma unroll
-    for (int k = 0; k < kHold; ++k) {
-      const int v = v0 + k * step;
-      if (v >= total) break;
+    // One 64-bit base and a uniform offset per held vector (64-bit indices
+    // per vector kept live across the grid maximum would spill).
+    uint8_t* const cbase = a.codes + 8LL * v0;
+    const auto streamed = [&](const GuRaw<false>& x, int v) {
       uint32_t o[4];
-      if (k < kHoldR) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = w[k < kHoldR ? k : 0][e];
+      for (int e = 0; e < 4; ++e) o[e] = act_pair<false>(x, e);
+      const uint2 c = fp8x8_encode_bf16<kFast>(o, f);
+      st_u32x2_nt(a.codes + 8LL * v, c.x, c.y);
+    };
+    // The held vectors' encode (stores only) interleaved with the re-read of
+    // the streamed rest: after every kMix held vectors (whose registers are
+    // then free) the previous streamed vector is encoded and the next one's
+    // load issued, so a load is in flight while the held codes are written.
+    int vn = vs;
+    GuRaw<false> xs;
+    const auto held = [&](auto kc) {
+      constexpr int k = decltype(kc)::value;
+      if (k >= kHold) return;
+      if (k % 4 == 0) wave_priority_by_progress(k, per_lane);
+      if (v0 >= total - k * step) return;
+      uint32_t o[4];
+      if constexpr (k < kHoldR) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = w[k][e];
       } else {
-        const uint4 h = s_hold[k >= kHoldR ? k - kHoldR : 0][threadIdx.x];
+        const uint4 h = s_hold[k - kHoldR][threadIdx.x];
         o[0] = h.x;
         o[1] = h.y;
         o[2] = h.z;
         o[3] = h.w;
       }
       const uint2 c = fp8x8_encode_bf16<kFast>(o, f);
-      st_u32x2_nt(a.codes + 8LL * v, c.x, c.y);
+      st_u32x2_nt(cbase + 8LL * k * step, c.x, c.y);
+    };
+    constexpr int kGroup = kMix > 0 ? kMix : kHold;
+    static_for<(kHold + kGroup - 1) / kGroup>([&](auto gc) {
+      constexpr int g = decltype(gc)::value;
+      static_for<kGroup>([&](auto kc) { held(std::integral_constant<int, g * kGroup + decltype(kc)::value>{}); });
+      if constexpr (kMix > 0) {
+        if constexpr (g > 0) {
+          if (vn < total) streamed(xs, vn);
+          vn += step;
+        }
+        xs = load_gu<false, true>(a, min(vn, total - 1), nv);
+      }
+    });
+    if constexpr (kMix > 0) {
+      if (vn < total) streamed(xs, vn);
+      vn += step;
     }
     G4_TRACE_MARK(gs, 4);
-    for (int v = vs; v < total; v += kStreamU * step) {
-      GuRaw<false> x[kStreamU];
-#pragma unroll
-      for (int j = 0; j < kStreamU; ++j) x[j] = load_gu<false, true>(a, min(v + j * step, total - 1), nv);
-#pragma unroll
-      for (int j = 0; j < kStreamU; ++j) {
-        const int vj = v + j * step;
-        if (vj >= total) break;
-        uint32_t o[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = act_pair<false>(x[j], e);
-        const uint2 c = fp8x8_encode_bf16<kFast>(o, f);
-        st_u32x2_nt(a.codes + 8LL * vj, c.x, c.y);
-      }
+    for (int v = vn, i = kHold; v < total; v += step, ++i) {
+      wave_priority_by_progress(i, per_lane);
+      const GuRaw<false> x = load_gu<false, true>(a, v, nv);
+      streamed(x, v);
     }
   };
   if (f.fast) encode(std::true_type{});
