@@ -378,13 +378,10 @@ void norm_fp8_fused_kernel(NormArgs a, GridSync gs) {
   // numeric order); a lane that saw a NaN pattern (above 0x7f80 once the
   // sign is cleared) recomputes its maximum with fmaxf, which skips NaN.
   u16x2_t mk = {0, 0};
-  // Rows this workgroup holds (for the issue priority by progress).
-  const int nheld = (a.rows - static_cast<int>(blockIdx.x) + gridDim.x - 1) / gridDim.x;
 #pragma unroll
   for (int h = 0; h < HR + HL; ++h) {
     const int rg = blockIdx.x + h * gridDim.x;  // uniform over the workgroup
     if (rg >= a.rows) break;
-    wave_priority_by_progress(h, nheld);
     NormRow<VPL, 4> t;
     norm_row_front<VPL, 4, true>(a, rg, t);
     if (h == 0) G4_TRACE_MARK(gs, 1);
@@ -429,7 +426,6 @@ void norm_fp8_fused_kernel(NormArgs a, GridSync gs) {
     }
   }
   G4_TRACE_MARK(gs, 2);
-  __builtin_amdgcn_s_setprio(0);
   const Fp8Enc f = fp8_scale_of(grid_max(m, gs, tag));
   G4_TRACE_MARK(gs, 3);
   if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = f.s;
