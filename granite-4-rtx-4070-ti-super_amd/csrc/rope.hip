@@ -387,12 +387,17 @@ int launch_embed(const int32_t* tokens, int start, const int* d_pos, int rows,
     return -1;
   }
   const hipStream_t st = stream();
-  // H = 4096 below 4096 rows: two whole rows per workgroup (measured at
-  // T=512: 3.09 vs 3.31 us; at T=8192 the vector-per-lane grid is faster,
-  // 22.7 vs 23.5 us).
-  if (d_pos == nullptr && H == 4096 && rows < 4096) {
-    hipLaunchKernelGGL((embed_rows_kernel<2, 2>), dim3((rows + 1) / 2), kBlock, 0, st, tokens,
-                       start, rows, emb, vocab, mult, out);
+  // H = 4096: whole rows per workgroup, two below 4096 rows (measured at
+  // T=512: 3.09 vs 3.31 us for the vector-per-lane grid), one from 4096 rows
+  // (T=8192, A/B over two rounds on one box: one row 23.72, two 24.48, four
+  // 24.18-24.26, the vector-per-lane grid 24.12-24.13 us).
+  if (d_pos == nullptr && H == 4096) {
+    if (rows < 4096)
+      hipLaunchKernelGGL((embed_rows_kernel<2, 2>), dim3((rows + 1) / 2), kBlock, 0, st, tokens,
+                         start, rows, emb, vocab, mult, out);
+    else
+      hipLaunchKernelGGL((embed_rows_kernel<2, 1>), dim3(rows), kBlock, 0, st, tokens, start,
+                         rows, emb, vocab, mult, out);
     return launch_status(what);
   }
   if (H % 8 == 0) {
