@@ -113,6 +113,26 @@ def test_embed_invalid_token_zero_row_and_decode_pos():
     np.testing.assert_array_equal(host(one)[0], emb[63])
 
 
+@pytest.mark.parametrize("rows", [4095, 4096, 8193])
+def test_embed_whole_row_workgroups_invalid_tokens(rows):
+    """The whole-row workgroup forms (two rows each below 4096 rows, one from
+    4096): tokens outside [0, vocab) give zero rows at every position,
+    including the odd last row, and the rest match the oracle."""
+    note(f"embed whole rows invalid rows={rows}")
+    vocab, H = 300, 4096
+    emb = ol.normal_bf16(0xE4, 0.0, 0.02, vocab * H).reshape(vocab, H)
+    tok = (ol.u32(0xE5 + rows, rows) % vocab).astype(np.int32)
+    bad = np.array([0, 1, rows // 2, rows - 2, rows - 1])
+    tok[bad[::2]] = -7
+    tok[bad[1::2]] = vocab
+    out = torch.full((rows, H), 77, dtype=torch.int16, device="cuda")
+    L.call("granite4_embed_rows", dev(tok), rows, dev(emb), vocab, H, 0.75, out)
+    o = host(out)
+    assert not o[bad].any()
+    good = np.setdiff1d(np.arange(rows), bad)
+    np.testing.assert_array_equal(o[good], ol.embed_rows(tok[good], emb, 0.75))
+
+
 # ----------------------------------------------------------------------------- rmsnorm
 def _hidden(rows, cols, seed, outliers=True):
     x = ol.normal_bf16(seed, 0.0, 1.0, rows * cols).reshape(rows, cols)
