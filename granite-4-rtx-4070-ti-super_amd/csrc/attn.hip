@@ -1602,15 +1602,19 @@ void launch_attn_bits(const AttnArgs& a, int group, dim3 grid, hipStream_t st) {
   }
 }
 
-// Column blocks per wave. Measured (T=512 int8 / T=8192 at 57344 K5V4): CB = 1
-// 33.7 us / 38.2 ms, CB = 2 45.1 us / 49.2 ms, CB = 4 69.0 us / 42.2 ms - the
-// kernel is VALU-bound (softmax, bf16 logit rounding, P packing ~3x the MFMA
-// cycles per tile), so more registers per wave only cost occupancy.
-constexpr int kPrefillCb = 1;
+// Column blocks per wave: CB = 2 (each wave 8 positions x the 4 query heads,
+// 64 positions per 8-wave workgroup) where those workgroups still give every
+// CU one, else CB = 1. Two column blocks halve the staging (code -> bf16
+// conversion, the VALU-heaviest part) per MFMA; with fewer workgroups the
+// occupancy they cost matters more. Measured (8 KV heads, one box, us): int8
+// from position 0, CB = 1 / 2: T=1024 46.3 / 50.5 (CB = 2 there runs the
+// key-split form), 2048 161.9 / 122.8, 4096 462.5 / 444.1, 8192 1475 / 1274;
+// K5V4 group 32 at 57344..: T=2048 4288 / 3482, 4096 8583 / 7102, 8192 18357
+// / 14779. (Before the group-32 tiles were staged dequantised: CB = 1 / 2 / 4
+// at T=512 int8 33.7 / 45.1 / 69.0 us, at T=8192 K5V4 38.2 / 49.2 / 42.2 ms.)
 
-template <int BITS, int W, int KSP = 1>
+template <int BITS, int W, int KSP = 1, int CB = 1>
 void launch_prefill_w(const PrefillArgs& a, int group, dim3 grid, hipStream_t st) {
-  constexpr int CB = kPrefillCb;
   if constexpr (BITS == 16) {
     (void)group;
     hipLaunchKernelGGL((attn_prefill_kernel<16, kHd, CB, W, KSP>), grid, W * 64, 0, st, a);
@@ -1621,18 +1625,19 @@ void launch_prefill_w(const PrefillArgs& a, int group, dim3 grid, hipStream_t st
   }
 }
 
-// 8-wave workgroups (32 positions each) where they give every CU one, else
-// 16-position workgroups for twice the workgroups: 8 waves splitting the keys
-// between two 4-wave groups, or 4 waves.
+// 8-wave workgroups of 64 positions (CB = 2) or 32 (CB = 1) where they give
+// every CU one, else 16-position workgroups for twice the workgroups: 8 waves
+// splitting the keys between two 4-wave groups.
 template <int BITS>
 void launch_prefill_bits(const PrefillArgs& a, int group, int Hk, hipStream_t st) {
-  const long long wide = static_cast<long long>((a.rows + 8 * 4 * kPrefillCb - 1) / (8 * 4 * kPrefillCb)) * Hk;
-  if (wide >= kCUs) {
-    const dim3 grid((a.rows + 8 * 4 * kPrefillCb - 1) / (8 * 4 * kPrefillCb), Hk);
-    launch_prefill_w<BITS, 8>(a, group, grid, st);
+  const long long blocks64 = static_cast<long long>((a.rows + 63) / 64) * Hk;
+  const long long blocks32 = static_cast<long long>((a.rows + 31) / 32) * Hk;
+  if (blocks64 >= kCUs) {
+    launch_prefill_w<BITS, 8, 1, 2>(a, group, dim3((a.rows + 63) / 64, Hk), st);
+  } else if (blocks32 >= kCUs) {
+    launch_prefill_w<BITS, 8, 1, 1>(a, group, dim3((a.rows + 31) / 32, Hk), st);
   } else {
-    const dim3 grid((a.rows + 4 * 4 * kPrefillCb - 1) / (4 * 4 * kPrefillCb), Hk);
-    launch_prefill_w<BITS, 8, 2>(a, group, grid, st);
+    launch_prefill_w<BITS, 8, 2, 1>(a, group, dim3((a.rows + 15) / 16, Hk), st);
   }
 }
 

@@ -357,16 +357,19 @@ def test_prefill_attn_paged(bits, group, window):
     check(got, want, vmax(cv, vs, bits), f"prefill paged bits {bits} group {group} w {window}")
 
 
-@pytest.mark.parametrize("bits,group,window", [(5, 32, 0), (8, 128, 300)])
-def test_prefill_attn_long_prompt_eight_wave_form(bits, group, window):
-    """1100 rows (8-wave workgroups of 32 positions: enough of them for every
-    CU, where shorter prompts take 4-wave ones), paged, at base 60. Three
-    32-row ranges checked against the oracle run on those rows alone (a row's
-    output depends only on its position and the pool)."""
-    note(f"prefill attn long prompt bits={bits} group={group} window={window}")
-    pages = 80
+@pytest.mark.parametrize("rows", [1100, 2100])
+@pytest.mark.parametrize("bits,group,window", [(5, 32, 0), (8, 128, 300), (16, 128, 0)])
+def test_prefill_attn_long_prompt_eight_wave_form(bits, group, window, rows):
+    """1100 rows (8-wave workgroups of 32 positions, one column block per
+    wave: enough of them for every CU, where shorter prompts take the
+    key-split form) and 2100 rows (64 positions, two column blocks per wave,
+    the last workgroup partly past the end), paged, at base 60. Three 32-row
+    ranges checked against the oracle run on those rows alone (a row's output
+    depends only on its position and the pool)."""
+    note(f"prefill attn long prompt rows={rows} bits={bits} group={group} window={window}")
+    base = 60
+    pages = (base + rows + 15) // 16 + 4
     stride = 16 * pages
-    base, rows = 60, 1100
     ck, cv, ks, vs = make_cache(bits, group, stride, 0xF4 + bits)
     rng = np.random.default_rng(bits + 99)
     pt = ol.row_table(rng.permutation(pages).astype(np.int32), stride)
