@@ -1277,8 +1277,15 @@ __global__ __launch_bounds__(W * 64) void attn_prefill_kernel(PrefillArgs a) {
   const int wave = static_cast<int>(threadIdx.x >> 6) & (kPrefWaves - 1);
   const int tst = threadIdx.x & (kPrefWaves * 64 - 1);  // staging thread within the group
   const int g = lane >> 4, n = lane & 15;
-  const int hkv = blockIdx.y;
-  const int p0 = blockIdx.x * kPos;
+  // Longest rows first: the dispatch order (x fastest) walks every KV head of
+  // the last position block, then of the one before it, so the longest causal
+  // rows start first and the shortest end the launch. Measured (int8 from
+  // position 0, against position blocks in order): T=4096 451 -> 270 us,
+  // T=8192 1349 -> 966 us; K5V4 T=8192 at 57344 14.79 -> 14.01 ms; T <= 2048
+  // unchanged (one round of workgroups).
+  const int lin = blockIdx.x + blockIdx.y * gridDim.x;
+  const int hkv = lin % gridDim.y;
+  const int p0 = (gridDim.x - 1 - lin / gridDim.y) * kPos;
   const int hq = hkv * kGq + (n & 3);
   int r[CB], my_pos[CB], my_lo[CB];
   bool live[CB];
