@@ -234,13 +234,36 @@ __device__ __forceinline__ void k_raw_f32(const u32x4_t& r, float (&f)[8]) {
     }
   }
 }
+// Unsigned codes held one per byte of lo (dims 2 e) and hi (dims 2 e + 1),
+// dequantised as bf16((code - bias) * s): fma(code, s, -bias * s) is the same
+// f32 (code * s - bias * s is exactly (code - bias) * s, and both round it
+// once; bias * s is exact), one instruction instead of a subtraction and a
+// multiply.
+__device__ __forceinline__ bf16x8_t bytes_deq(uint32_t lo, uint32_t hi, float s, float nbs) {
+  uint32_t w[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    w[e] = pack_bf16_hw(fmaf(static_cast<float>((lo >> (8 * e)) & 0xFFu), s, nbs),
+                        fmaf(static_cast<float>((hi >> (8 * e)) & 0xFFu), s, nbs));
+  return as_bf16x8(w[0], w[1], w[2], w[3]);
+}
+
 // ... dequantised with the elements' group scale: bf16(code * s).
 template <int BITS>
 __device__ __forceinline__ bf16x8_t k_raw_deq(const u32x4_t& r, float s) {
-  float f[8];
-  k_raw_f32<BITS>(r, f);
-  return as_bf16x8(pack_bf16_hw(f[0] * s, f[1] * s), pack_bf16_hw(f[2] * s, f[3] * s),
-                   pack_bf16_hw(f[4] * s, f[5] * s), pack_bf16_hw(f[6] * s, f[7] * s));
+  if constexpr (BITS == 5) {
+    constexpr uint32_t kSpread = (1u << 4) | (1u << 10) | (1u << 16) | (1u << 22);
+    const uint32_t lo = (r.x & 0x0F0F0F0Fu) | (__umul24(r.y & 0x55u, kSpread) & 0x10101010u);
+    const uint32_t hi = ((r.x >> 4) & 0x0F0F0F0Fu) | (__umul24((r.y >> 1) & 0x55u, kSpread) & 0x10101010u);
+    return bytes_deq(lo, hi, s, -16.0f * s);
+  } else if constexpr (BITS == 4) {
+    return bytes_deq(r.x & 0x0F0F0F0Fu, (r.x >> 4) & 0x0F0F0F0Fu, s, -8.0f * s);
+  } else {
+    float f[8];
+    k_raw_f32<BITS>(r, f);
+    return as_bf16x8(pack_bf16_hw(f[0] * s, f[1] * s), pack_bf16_hw(f[2] * s, f[3] * s),
+                     pack_bf16_hw(f[4] * s, f[5] * s), pack_bf16_hw(f[6] * s, f[7] * s));
+  }
 }
 // One 16-byte V chunk (int8: 16 values, int4: 32), dequantised with scale s,
 // as bf16 pairs w[0 .. 8 or 16).
@@ -255,11 +278,15 @@ __device__ __forceinline__ void v_chunk_deq(const u32x4_t& u, float s, uint32_t 
                           static_cast<float>(static_cast<int8_t>(x >> (sh + 8))) * s);
     }
   } else {
+    // bf16((code - 8) * s) per nibble, the low nibble of byte b first
+    const float nbs = -8.0f * s;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const uint32_t xs = u[e >> 2] ^ 0x88888888u;
-      const int b = 8 * (e & 3);
-      w[e] = pack_bf16_hw(static_cast<float>(sfield4(xs, b)) * s, static_cast<float>(sfield4(xs, b + 4)) * s);
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t lo = u[q] & 0x0F0F0F0Fu, hi = (u[q] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        w[4 * q + b] = pack_bf16_hw(fmaf(static_cast<float>((lo >> (8 * b)) & 0xFFu), s, nbs),
+                                    fmaf(static_cast<float>((hi >> (8 * b)) & 0xFFu), s, nbs));
     }
   }
 }
