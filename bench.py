@@ -569,6 +569,56 @@ def graphs_us(torch, L, stream, steps, rounds=5, reps=20):
     return {name: sorted(t)[len(t) // 2] for name, t in times.items()}
 
 
+def paired_diff_us(torch, L, stream, base, other, pairs=25, reps=8):
+    """µs per step of other() minus base(), each captured once as a HIP
+    graph: `pairs` back-to-back pairs of timed blocks of `reps` replays (the
+    order inside a pair alternating), the difference taken within each pair.
+    Returns the median, 10th and 90th percentile of the per-pair differences
+    and the median step times."""
+    graphs = []
+    cap = torch.cuda.Stream()
+    for step in (base, other):
+        g = torch.cuda.CUDAGraph()
+        cap.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(cap):
+            L.use_stream(cap)
+            step()
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=cap):
+                step()
+        L.use_stream(stream)
+        torch.cuda.synchronize()
+        graphs.append(g)
+
+    def block(g):
+        g.replay()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e3
+
+    diffs, tb, to = [], [], []
+    for i in range(pairs):
+        if i % 2 == 0:
+            b = block(graphs[0])
+            o = block(graphs[1])
+        else:
+            o = block(graphs[1])
+            b = block(graphs[0])
+        diffs.append(o - b)
+        tb.append(b)
+        to.append(o)
+    del graphs
+    q = np.percentile(diffs, [10, 50, 90])
+    return {"median_us": round(float(q[1]), 1), "p10_us": round(float(q[0]), 1),
+            "p90_us": round(float(q[2]), 1), "pairs": pairs, "reps": reps,
+            "base_us": round(float(np.median(tb)), 1), "other_us": round(float(np.median(to)), 1)}
+
+
 def bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream, layers=40,
                       trace_replays=0):
     """Batch-1 decode step with its GEMVs (fp8 weight rows of the 8B model:
@@ -802,6 +852,10 @@ def bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream, layers=40
     t_fused_attn_ropeattn, t_fused_attn = t["fused_attn_ropeattn"], t["fused_attn"]
     t_unfused, t_qkv_rope_kernel = t["unfused"], t["qkv_rope_kernel"]
     t_fused_norope, t_fused = t["fused_norope"], t["fused"]
+    # Config 1's overhead again as paired differences (plain and config-1
+    # step timed back to back, 25 pairs): the median is steadier than the
+    # difference of two separately taken medians.
+    paired = paired_diff_us(torch, L, stream, plain, fused_rope_epilogue)
     wbytes = layers * (HQ * D + 2 * HK * D + 2 * I) * H + layers * H * (HQ * D + I)
     del per
     torch.cuda.empty_cache()
@@ -812,7 +866,9 @@ def bench_decode_gemv(torch, L, gen, cos_t, sin_t, emb, gamma, stream, layers=40
             "non_gemm_overhead_unfused_us": round(t_unfused - t_plain, 1),
             "non_gemm_overhead_fused_us": round(t_fused - t_plain, 1),
             "config1_fused_us": round(t_rope_epi, 1),
-            "config1_non_gemm_overhead_us": round(t_rope_epi - t_plain, 1),
+            "config1_non_gemm_overhead_us": paired["median_us"],
+            "config1_non_gemm_overhead_paired": paired,
+            "config1_non_gemm_overhead_rounds_us": round(t_rope_epi - t_plain, 1),
             "fused_gemvs_without_rope_us": round(t_fused_norope, 1),
             "rope_append_launches_us": round(t_fused - t_fused_norope, 1),
             "fused_qkv_rope_one_launch_us": round(t_qkv_rope_kernel, 1),
