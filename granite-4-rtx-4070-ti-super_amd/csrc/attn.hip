@@ -1282,6 +1282,8 @@ __device__ __forceinline__ void prefill_store(const PrefillRaw<BITS, GROUP, W>& 
 // at the end group 1's (m, l, o) merge into group 0's through LDS
 // (M = max m, each side's o and l scaled by exp(m - M)). Two waves per SIMD
 // where a short prompt gives each CU one 16-position workgroup.
+constexpr float kLog2E = 1.44269504088896341f;
+
 template <int BITS, int GROUP, int CB, int W, int KSP = 1>
 __global__ __launch_bounds__(W * 64) void attn_prefill_kernel(PrefillArgs a) {
   static_assert(KSP == 1 || (KSP == 2 && W == 8), "key split: two 4-wave groups");
@@ -1459,12 +1461,18 @@ __global__ __launch_bounds__(W * 64) void attn_prefill_kernel(PrefillArgs a) {
 #pragma unroll
           for (int nb = 0; nb < 8; ++nb) o[cb][nb] *= alpha;
         }
+        // exp(e - mx) as exp2(e log2(e) - mx log2(e)): one FMA feeds the
+        // hardware exponential instead of a subtraction and a multiply (the
+        // argument's error is the rounding of mx log2(e), of the same order as
+        // that of (e - mx) log2(e)); T=8192 K5V4 13.63 -> 13.18 ms.
+        const float nml = -mx * kLog2E;
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            if constexpr (kMask) e[cb][mb][i] = mx == -INFINITY ? 0.0f : __expf(e[cb][mb][i] - mx);
-            else e[cb][mb][i] = __expf(e[cb][mb][i] - mx);
+            const float p = __builtin_amdgcn_exp2f(fmaf(e[cb][mb][i], kLog2E, nml));
+            if constexpr (kMask) e[cb][mb][i] = mx == -INFINITY ? 0.0f : p;
+            else e[cb][mb][i] = p;
             l[cb] += e[cb][mb][i];
           }
       }
