@@ -121,6 +121,8 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(uint32_t a, uint32_t b, uint32_t c
   return __builtin_bit_cast(bf16x8_t, u);
 }
 
+constexpr float kLog2E = 1.44269504088896341f;
+
 // Exact bf16 pair of two small integers (|x| <= 127).
 __device__ __forceinline__ uint32_t int_pair_bf16(int a, int b) {
   return pack_bf16_hw(static_cast<float>(a), static_cast<float>(b));
@@ -1282,8 +1284,6 @@ __device__ __forceinline__ void prefill_store(const PrefillRaw<BITS, GROUP, W>& 
 // at the end group 1's (m, l, o) merge into group 0's through LDS
 // (M = max m, each side's o and l scaled by exp(m - M)). Two waves per SIMD
 // where a short prompt gives each CU one 16-position workgroup.
-constexpr float kLog2E = 1.44269504088896341f;
-
 template <int BITS, int GROUP, int CB, int W, int KSP = 1>
 __global__ __launch_bounds__(W * 64) void attn_prefill_kernel(PrefillArgs a) {
   static_assert(KSP == 1 || (KSP == 2 && W == 8), "key split: two 4-wave groups");
